@@ -1,0 +1,290 @@
+/*
+ * smoe.h — C ABI of libsmoe, the MI355X (gfx950) routed-expert MoE path.
+ *
+ * This is the drop-in boundary that replaces the reference's Metal
+ * kernel crate (crates/streammoe-metal, `Kernels` + `KernelCall`) and the
+ * engine's MoE encoders (crates/streammoe/src/riir/moe/expert_forward.rs)
+ * for the routed-expert hot path. Each entry point below cites the
+ * reference interface it replaces as path:line, relative to the
+ * reference repository root. Short prefixes:
+ *   metal/lib.rs      = crates/streammoe-metal/src/lib.rs
+ *   expert_forward.rs = crates/streammoe/src/riir/moe/expert_forward.rs
+ *   gpu_matvec.rs     = crates/streammoe/src/riir/backend/gpu/gpu_matvec.rs
+ *   moe_router.rs     = crates/streammoe/src/riir/moe/moe_router.rs
+ *   shaders.metal     = crates/streammoe/shaders/shaders.metal
+ *
+ * Conventions (the reference's contract, restated for a C caller):
+ *   - Every pointer named as device memory is a device address on the
+ *     handle's GPU (hipMalloc, or any allocator of that device).
+ *     Host-memory arguments are marked "host".
+ *   - Every compute entry point only ENQUEUES work on the handle's
+ *     stream and returns; nothing is allocated on the hot path
+ *     (scratch is reserved at smoe_create / smoe_reserve). Call
+ *     smoe_sync (or synchronise the stream) before reading results.
+ *   - Argument errors return a status code and enqueue nothing (the
+ *     reference panics or returns ExpertForwardError / CpuMatvecError;
+ *     here nothing panics).
+ *   - A handle is not thread-safe (the reference's Ctx is Send + !Sync,
+ *     crates/streammoe/src/lib.rs:23-28): one handle per engine context.
+ *   - Quantized weights use the MLX affine layout: 4-bit = 8 codes per
+ *     little-endian u32, low nibble first; packed 3-bit = 8 codes per
+ *     3 bytes, code i at bits 3i..3i+3 of a little-endian 24-bit pack;
+ *     bf16 scale and bias per `group` inputs; w = q * scale + bias
+ *     (crates/streammoe/src/riir/variants.rs:401-486).
+ */
+#ifndef SMOE_H
+#define SMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SMOE_MAX_K 16 /* expert_forward.rs:117 (MAX_K) */
+
+typedef enum {
+  SMOE_OK = 0,
+  SMOE_ERR_INVALID_ARG = 1,         /* null pointer / zero dimension / bad enum */
+  SMOE_ERR_BAD_K = 2,               /* k outside 1..=SMOE_MAX_K or > n_experts (ExpertForwardError::BadK) */
+  SMOE_ERR_IN_DIM_NOT_MULTIPLE = 3, /* in_dim not a multiple of the group (CpuMatvecError::InDimNotMultiple) */
+  SMOE_ERR_UNSUPPORTED_BITS = 4,    /* bits not 4 or 3 */
+  SMOE_ERR_UNSUPPORTED_GROUP = 5,   /* group not 32, 64 or 128 */
+  SMOE_ERR_UNSUPPORTED_SHAPE = 6,   /* a dimension this build has no kernel for */
+  SMOE_ERR_MISALIGNED = 7,          /* weight/scale region not aligned (CpuMatvecError::Misaligned) */
+  SMOE_ERR_SCRATCH_TOO_SMALL = 8,   /* shapes exceed the reserved scratch; call smoe_reserve */
+  SMOE_ERR_WORKSPACE_TOO_SMALL = 9, /* caller workspace smaller than *_workspace_size */
+  SMOE_ERR_HIP = 10,                /* a HIP runtime call failed (launch, memset, sync) */
+  SMOE_ERR_NO_DEVICE = 11           /* no gfx950 device at that ordinal */
+} smoe_status;
+
+typedef struct smoe_handle smoe_handle;
+
+/* Human-readable text of a status code (static storage). */
+const char* smoe_strerror(int status);
+
+/* Version of this ABI: bumped on any signature change. */
+uint32_t smoe_abi_version(void);
+
+/* ------------------------------------------------------------------ */
+/* Context                                                             */
+/* ------------------------------------------------------------------ */
+
+/* Create a handle on GPU `device`, enqueueing on `stream` (a
+ * hipStream_t; NULL = the default stream). Reserves the decode scratch
+ * for hidden <= 4096, inter <= 2048, n_experts <= 1024 and one token.
+ * Replaces Kernels::new (metal/lib.rs:538-665) together with
+ * MoeBuffers::new_for (expert_forward.rs:432-528). */
+int smoe_create(int device, void* stream, smoe_handle** out);
+
+/* Release the handle and its scratch. */
+int smoe_destroy(smoe_handle* h);
+
+/* Change the stream later launches go to (hipStream_t). */
+int smoe_set_stream(smoe_handle* h, void* stream);
+
+/* Grow the decode scratch (allocates; never call on a hot path or under
+ * graph capture). Shapes above the reservation return
+ * SMOE_ERR_SCRATCH_TOO_SMALL from the compute entry points. */
+int smoe_reserve(smoe_handle* h, uint32_t max_hidden, uint32_t max_inter, uint32_t max_experts);
+
+/* Block until all work enqueued on the handle's stream has finished.
+ * Replaces MetalContext::commit_and_wait_labeled's wait. */
+int smoe_sync(smoe_handle* h);
+
+/* ------------------------------------------------------------------ */
+/* Quantized weights and dense quantized matvec (qmv)                  */
+/* ------------------------------------------------------------------ */
+
+/* One quantized [out_dim, in_dim] matrix inside a device buffer.
+ * Mirrors QuantWeights (metal/lib.rs:339-351), plus the weight width. */
+typedef struct {
+  const void* base;       /* device */
+  uint64_t packed_offset; /* byte offset of the codes, 16-byte aligned (4-bit) / 4-byte (3-bit) */
+  uint64_t scales_offset; /* byte offset of bf16 scales [out_dim, in_dim/group], 2-byte aligned */
+  uint64_t biases_offset; /* byte offset of bf16 biases, same shape */
+  uint32_t group_size;    /* 32, 64 or 128 */
+  uint32_t bits;          /* 4, or 3 for the packed 3-bit layout */
+} smoe_qweights;
+
+/* y[r] = sum_c (q[r,c] * s[r,c/g] + b[r,c/g]) * x[c] for r < out_dim,
+ * fp32 accumulation. x: device f32[in_dim]; y: device f32[out_dim].
+ * Replaces encode_matvec (gpu_matvec.rs:116-159) and its kernel
+ * dequant_matvec_4bit_qmv (shaders.metal:366-423); used for the LM head
+ * (crates/streammoe/src/riir/io/gpu_lm_head.rs:130-193). */
+int smoe_qmv(smoe_handle* h, const smoe_qweights* w, const float* x, float* y, uint32_t out_dim,
+             uint32_t in_dim);
+
+/* Greedy argmax of a device f32[n] (first index wins on ties) into a
+ * device int32. The LM head's token pick. */
+int smoe_argmax(smoe_handle* h, const float* v, uint32_t n, int32_t* out_index);
+
+/* Dequantize rows [row0, row0 + n_rows) of `w` into device
+ * f32[n_rows, in_dim]: w = fma(q, s, b), one rounding, exactly the value
+ * the reference CPU path forms (crates/streammoe/src/riir/backend/cpu/
+ * cpu_matvec.rs:164-165). Verification entry point: the decode kernels
+ * use the same code-unpacking routine and never materialise w. */
+int smoe_dequant(smoe_handle* h, const smoe_qweights* w, uint32_t in_dim, uint32_t row0,
+                 uint32_t n_rows, float* out);
+
+/* ------------------------------------------------------------------ */
+/* Router                                                              */
+/* ------------------------------------------------------------------ */
+
+/* Per token t < n_tokens: logits = router_w · x[t] (f32 [n_experts,
+ * hidden] router, fp32), softmax, running-minimum top-k (slot order =
+ * replacement order, ties to the earlier expert), then the guarded
+ * renormalisation when `normalize` (norm_topk_prob).
+ * x: device f32[n_tokens, hidden]; idx: device int32[n_tokens, k];
+ * weights: device f32[n_tokens, k]; logits_out: device
+ * f32[n_tokens, n_experts] or NULL.
+ * Replaces the router gate matvec (attn/linear_attn_forward.rs:2093)
+ * plus moe_router_cpu_with (moe_router.rs:165-181) on the host, or on
+ * the GPU moe_softmax_topk + moe_normalize_weights (shaders.metal:
+ * 3556-3690, encoded by moe/gpu_moe_router.rs). */
+int smoe_router(smoe_handle* h, const float* router_w, const float* x, uint32_t n_tokens,
+                uint32_t n_experts, uint32_t hidden, uint32_t k, int normalize, int32_t* idx,
+                float* weights, float* logits_out);
+
+/* Softmax + top-k + optional renorm from precomputed logits
+ * (device f32[n_tokens, n_experts]). Replaces Op::MoeSoftmaxTopK +
+ * Op::MoeNormalizeWeights (backend/mod.rs:473-497; shaders.metal:
+ * 3556-3690). */
+int smoe_softmax_topk(smoe_handle* h, const float* logits, uint32_t n_tokens, uint32_t n_experts,
+                      uint32_t k, int normalize, int32_t* idx, float* weights);
+
+/* Top-k only, on arbitrary scores (no softmax): topk() of
+ * moe_router.rs:83-124 per token. values: device f32[n_tokens, k]. */
+int smoe_topk(smoe_handle* h, const float* scores, uint32_t n_tokens, uint32_t n, uint32_t k,
+              int32_t* idx, float* values);
+
+/* ------------------------------------------------------------------ */
+/* Decode: K routed experts + shared expert + combine (one token)      */
+/* ------------------------------------------------------------------ */
+
+/* Shape of one packed expert blob [gate | up | down], each block
+ * [codes | bf16 scales | bf16 biases] (variants.rs:401-486). */
+typedef struct {
+  uint32_t hidden; /* H: gate/up in_dim, down out_dim */
+  uint32_t inter;  /* I: gate/up out_dim, down in_dim */
+  uint32_t group;  /* quantization group along the input dim */
+  uint32_t bits;   /* 4 or 3 */
+} smoe_expert_shape;
+
+/* Bytes of one expert blob of `shape` (variants.rs:519-528). */
+uint64_t smoe_expert_bytes(const smoe_expert_shape* shape);
+
+/* One routed slot's expert binding: the blob starts at base + offset
+ * (device). Mirrors the engine's (&Buffer, u64) expert bindings
+ * (attn/linear_attn_forward.rs:2461-2470; io/expert_io.rs:578-592). */
+typedef struct {
+  const void* base;
+  uint64_t offset;
+} smoe_binding;
+
+/* hidden_out = h_mid + sum_k weights[k] * FFN_k(input)
+ *              (+ sigmoid(shared_gate_score) * shared_out),
+ * with FFN_k = down(silu(gate(x)) * up(x)) on the k bound experts.
+ * bindings, weights: host arrays of k; input, h_mid, shared_out,
+ * hidden_out: device f32[hidden]. shared_out NULL drops the shared term
+ * (moe_combine_residual_flat_noshared); a NaN shared_gate_score adds
+ * shared_out unscaled (the DeepSeek combine).
+ * Replaces encode_experts_mmap_into (expert_forward.rs:927-986) /
+ * gpu_batched_experts_encode_mmap (:880-915) and the kernels they encode
+ * (dequant_matvec_{4,3}bit_v3_experts, swiglu_fused,
+ * moe_combine_residual_flat[_noshared]; shaders.metal:1091-1388). */
+int smoe_experts_decode(smoe_handle* h, const smoe_expert_shape* shape,
+                        const smoe_binding* bindings, uint32_t k, const float* weights,
+                        const float* input, const float* h_mid, const float* shared_out,
+                        float shared_gate_score, float* hidden_out);
+
+/* One resident MoE layer: experts at base + e * stride (device), an f32
+ * router [n_experts, hidden], an optional always-on 4-bit shared expert
+ * (same hidden and inter as the routed ones) with an optional f32 gate
+ * vector [hidden] (its sigmoid scales the shared output; NULL = unscaled). */
+typedef struct {
+  smoe_expert_shape shape;
+  const void* experts;       /* device, n_experts * stride bytes */
+  uint64_t stride;           /* bytes between experts (>= smoe_expert_bytes) */
+  uint32_t n_experts;
+  uint32_t k;                /* routed experts per token */
+  int32_t normalize;         /* norm_topk_prob */
+  const float* router_w;     /* device f32[n_experts, hidden] */
+  const void* shared_expert; /* device 4-bit blob, or NULL */
+  const float* shared_gate;  /* device f32[hidden], or NULL */
+} smoe_layer;
+
+/* Decode one token through one layer with routing on the device:
+ * router -> top-k -> routed + shared expert FFN -> combine.
+ * input: device f32[hidden] (the post-attention-norm hidden);
+ * h_mid: device f32[hidden] (residual); hidden_out: device f32[hidden];
+ * idx_out / w_out: device int32[k] / f32[k], or NULL.
+ * Replaces finish_post_attention's routing (attn/linear_attn_forward.rs:
+ * 2123-2165) + moe_dispatch_per_token (:2382-2710) without the host
+ * round trip. */
+int smoe_moe_decode_layer(smoe_handle* h, const smoe_layer* layer, const float* input,
+                          const float* h_mid, float* hidden_out, int32_t* idx_out, float* w_out);
+
+/* The same over n_layers layers back to back (the decode layer loop,
+ * crates/streammoe/src/riir/mod.rs:~4030-4180, MoE blocks only):
+ * layer l reads x_l and writes r_{l+1} = r_l + MoE_l(x_l), where
+ * x_0 = input, r_0 = residual and, between layers, x_{l+1} =
+ * RMSNorm(r_{l+1}) * norm_w[l+1] (bf16 weights, eps) when norm_w is not
+ * NULL, else x_{l+1} = r_{l+1}. layers: host array; norm_w: host array
+ * of n_layers device bf16[hidden] pointers, or NULL; residual_io:
+ * device f32[hidden], updated in place; work: device f32[hidden] input
+ * staging (x_l for l > 0). */
+int smoe_moe_decode_layers(smoe_handle* h, const smoe_layer* layers, uint32_t n_layers,
+                           const void* const* norm_w, float eps, const float* input,
+                           float* residual_io, float* work);
+
+/* ------------------------------------------------------------------ */
+/* Prefill: many tokens through one layer's routed experts             */
+/* ------------------------------------------------------------------ */
+
+/* Device workspace bytes smoe_moe_prefill needs for these sizes. */
+uint64_t smoe_moe_prefill_workspace_size(const smoe_expert_shape* shape, uint32_t n_tokens,
+                                         uint32_t n_experts, uint32_t k);
+
+/* out_sum[t] = sum_s weights[t,s] * FFN_{idx[t,s]}(x[t]) for t < n_tokens:
+ * tokens sorted by expert on the device, grouped gate/up GEMM with
+ * in-kernel dequant on bf16/f16 MFMA (fp32 accumulate), SwiGLU, down
+ * GEMM, then a fixed-order per-token combine (no atomics).
+ * x: device, bf16 [n_tokens, hidden] when x_is_bf16 else f32;
+ * idx: device int32[n_tokens, k]; weights: device f32[n_tokens, k];
+ * out_sum: device f32[n_tokens, hidden] (overwritten).
+ * Replaces encode_moe_gather_id_fuse (expert_forward.rs:1874-2042) with
+ * MoeIdMap0Call / MoeGatherIdCall / MoeCombineTopkCall (metal/lib.rs:
+ * 932-1189), and its CPU oracle moe_permute_fuse_cpu
+ * (crates/streammoe/src/riir/moe/moe_cpu.rs:282-339). */
+int smoe_moe_prefill(smoe_handle* h, const smoe_expert_shape* shape, const void* experts,
+                     uint64_t stride, uint32_t n_experts, const int32_t* idx,
+                     const float* weights, const void* x, int x_is_bf16, uint32_t n_tokens,
+                     uint32_t k, float* out_sum, void* workspace, uint64_t workspace_bytes);
+
+/* ------------------------------------------------------------------ */
+/* Seeded synthetic data (bench and test inputs)                       */
+/* ------------------------------------------------------------------ */
+/* Replace the synthetic-data helpers of expert_forward.rs:2257-2347 and
+ * the xorshift generators of the reference's kernel tests: fills device
+ * memory from a counter-based generator, so a given (seed, size) gives
+ * the same bytes on any run. */
+
+/* n_experts blobs at base + e * stride: codes uniform (4-bit: random
+ * u32 words; 3-bit: random 24-bit packs), scales bf16(|N(0, scale_sigma)|),
+ * biases bf16(N(0, bias_sigma)). */
+int smoe_synth_experts(smoe_handle* h, void* base, uint32_t n_experts, uint64_t stride,
+                       const smoe_expert_shape* shape, uint64_t seed, float scale_sigma,
+                       float bias_sigma);
+
+/* Device f32[n] ~ N(0, sigma). */
+int smoe_synth_normal_f32(smoe_handle* h, float* out, uint64_t n, uint64_t seed, float sigma);
+
+/* Device bf16[n] (RNE of N(0, sigma)). */
+int smoe_synth_normal_bf16(smoe_handle* h, uint16_t* out, uint64_t n, uint64_t seed, float sigma);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SMOE_H */

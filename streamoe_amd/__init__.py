@@ -1,0 +1,251 @@
+"""streamoe_amd — MI355X (gfx950) routed-expert MoE hot path.
+
+Host-side mirror of the reference's kernel-crate and expert-encoder
+interface over the C ABI of ``libsmoe.so`` (``include/smoe.h``). Names
+follow the reference:
+
+* ``ExpertLayout``      crates/streammoe/src/riir/variants.rs:401-486
+* ``Kernels``           crates/streammoe-metal/src/lib.rs:538-676 (Kernels::new / encode)
+* ``QuantWeights``      crates/streammoe-metal/src/lib.rs:339-351
+* ``ExpertPayload``     crates/streammoe/src/riir/moe/expert_forward.rs:123-139
+* ``gpu_batched_experts_forward``  expert_forward.rs:718-746
+* ``moe_router``        crates/streammoe/src/riir/moe/moe_router.rs:151-181 (on the GPU)
+
+Device buffers are torch tensors on ``cuda`` (PyTorch is only the
+allocator and stream provider here). Every call goes through libsmoe;
+nothing falls back to a CPU path: importing this package without the
+built library raises ImportError.
+"""
+import ctypes as C
+from dataclasses import dataclass
+
+from . import _abi
+from ._abi import SMOE_MAX_K, SmoeError, check
+
+_lib = _abi.load()
+
+MAX_K = SMOE_MAX_K
+
+
+def _ptr(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+@dataclass(frozen=True)
+class ExpertLayout:
+    """Packed-expert layout `[gate | up | down]`, each block
+    `[codes | bf16 scales | bf16 biases]` (variants.rs:401-486), for any
+    shape: `bits` 4 (8 nibbles per u32, low first) or 3 (8 codes per 3
+    bytes, little-endian 24-bit pack)."""
+
+    hidden: int
+    inter: int
+    bits: int = 4
+    group: int = 64
+
+    def row_bytes(self, in_dim):
+        return in_dim * self.bits // 8
+
+    @property
+    def weight_bytes(self):
+        return self.inter * self.row_bytes(self.hidden)
+
+    @property
+    def scale_bytes(self):
+        return self.inter * (self.hidden // self.group) * 2
+
+    @property
+    def block_bytes(self):
+        return self.weight_bytes + 2 * self.scale_bytes
+
+    @property
+    def expert_size(self):
+        return 3 * self.block_bytes
+
+    def offsets(self, block):
+        """(codes, scales, biases) byte offsets of block 0=gate, 1=up, 2=down."""
+        w = block * self.block_bytes
+        s = w + self.weight_bytes
+        return w, s, s + self.scale_bytes
+
+    @classmethod
+    def from_expert_size(cls, size, hidden, inter, group=64):
+        """ExpertLayout::from_expert_size: the layout whose expert is `size` bytes."""
+        for bits in (4, 3):
+            lay = cls(hidden, inter, bits, group)
+            if lay.expert_size == size:
+                return lay
+        return None
+
+    def shape(self):
+        return _abi.ExpertShape(self.hidden, self.inter, self.group, self.bits)
+
+
+@dataclass
+class QuantWeights:
+    """One quantized [out_dim, in_dim] matrix inside a device tensor."""
+
+    buffer: object  # torch tensor on the device
+    packed_offset: int
+    scales_offset: int
+    biases_offset: int
+    group_size: int = 64
+    bits: int = 4
+
+    def c(self):
+        return _abi.QWeights(self.buffer.data_ptr(), self.packed_offset, self.scales_offset,
+                             self.biases_offset, self.group_size, self.bits)
+
+
+@dataclass
+class ExpertPayload:
+    """Per-token host inputs of a K-expert dispatch (expert_forward.rs:123-139)."""
+
+    h_post: object
+    h_mid: object
+    shared_out: object
+    expert_weights: object
+    shared_gate_score: float
+
+
+class Kernels:
+    """A libsmoe handle on one GPU: Kernels::new plus the MoeBuffers scratch.
+
+    ``stream`` is a torch.cuda.Stream (default: torch's current stream)."""
+
+    def __init__(self, device=0, stream=None):
+        import torch
+
+        self._torch = torch
+        self.device = device
+        h = C.c_void_p()
+        s = (stream or torch.cuda.current_stream(device)).cuda_stream
+        check(_lib.smoe_create(device, C.c_void_p(s), C.byref(h)), "smoe_create")
+        self.h = h
+
+    def close(self):
+        if self.h:
+            _lib.smoe_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def sync(self):
+        check(_lib.smoe_sync(self.h), "smoe_sync")
+
+    def reserve(self, max_hidden, max_inter, max_experts):
+        check(_lib.smoe_reserve(self.h, max_hidden, max_inter, max_experts), "smoe_reserve")
+
+    # -- dense quantized matvec (encode_matvec / QmmCall with one token) ----------
+    def qmv(self, w: QuantWeights, x, y, out_dim, in_dim):
+        wc = w.c()
+        return _lib.smoe_qmv(self.h, C.byref(wc), _ptr(x), _ptr(y), out_dim, in_dim)
+
+    def argmax(self, v, n, out):
+        return _lib.smoe_argmax(self.h, _ptr(v), n, _ptr(out))
+
+    def dequant(self, w: QuantWeights, in_dim, row0, n_rows, out):
+        wc = w.c()
+        return _lib.smoe_dequant(self.h, C.byref(wc), in_dim, row0, n_rows, _ptr(out))
+
+    # -- router ------------------------------------------------------------------
+    def router(self, router_w, x, n_tokens, n_experts, hidden, k, normalize, idx, weights,
+               logits=None):
+        return _lib.smoe_router(self.h, _ptr(router_w), _ptr(x), n_tokens, n_experts, hidden, k,
+                                int(normalize), _ptr(idx), _ptr(weights), _ptr(logits))
+
+    def softmax_topk(self, logits, n_tokens, n_experts, k, normalize, idx, weights):
+        return _lib.smoe_softmax_topk(self.h, _ptr(logits), n_tokens, n_experts, k, int(normalize),
+                                      _ptr(idx), _ptr(weights))
+
+    def topk(self, scores, n_tokens, n, k, idx, values):
+        return _lib.smoe_topk(self.h, _ptr(scores), n_tokens, n, k, _ptr(idx), _ptr(values))
+
+    # -- decode experts (encode_experts_mmap_into) --------------------------------
+    def experts_decode(self, layout: ExpertLayout, bindings, weights, input, h_mid, shared_out,
+                       shared_gate_score, hidden_out):
+        """bindings: list of (tensor, byte_offset); weights: list of floats."""
+        k = len(bindings)
+        b = (_abi.Binding * max(k, 1))(*[_abi.Binding(t.data_ptr(), off) for t, off in bindings])
+        w = (C.c_float * max(k, 1))(*weights)
+        shape = layout.shape()
+        return _lib.smoe_experts_decode(self.h, C.byref(shape), b, k, w, _ptr(input), _ptr(h_mid),
+                                        _ptr(shared_out), C.c_float(shared_gate_score),
+                                        _ptr(hidden_out))
+
+    # -- one resident layer (moe_dispatch_per_token with device routing) --------
+    @staticmethod
+    def layer(layout: ExpertLayout, experts, stride, n_experts, k, normalize, router_w,
+              shared_expert=None, shared_gate=None):
+        return _abi.Layer(layout.shape(), experts.data_ptr(), stride, n_experts, k, int(normalize),
+                          router_w.data_ptr(),
+                          None if shared_expert is None else shared_expert.data_ptr(),
+                          None if shared_gate is None else shared_gate.data_ptr())
+
+    def moe_decode_layer(self, layer, input, h_mid, hidden_out, idx_out=None, w_out=None):
+        return _lib.smoe_moe_decode_layer(self.h, C.byref(layer), _ptr(input), _ptr(h_mid),
+                                          _ptr(hidden_out), _ptr(idx_out), _ptr(w_out))
+
+    def moe_decode_layers(self, layers, norm_w, eps, input, residual_io, work):
+        n = len(layers)
+        arr = (_abi.Layer * n)(*layers)
+        nw = None
+        if norm_w is not None:
+            nw = (C.c_void_p * n)(*[None if t is None else t.data_ptr() for t in norm_w])
+        return _lib.smoe_moe_decode_layers(self.h, arr, n, nw, C.c_float(eps), _ptr(input),
+                                           _ptr(residual_io), _ptr(work))
+
+    # -- prefill (encode_moe_gather_id_fuse) --------------------------------------
+    def moe_prefill_workspace_size(self, layout, n_tokens, n_experts, k):
+        shape = layout.shape()
+        return _lib.smoe_moe_prefill_workspace_size(C.byref(shape), n_tokens, n_experts, k)
+
+    def moe_prefill(self, layout, experts, stride, n_experts, idx, weights, x, x_is_bf16, n_tokens,
+                    k, out_sum, workspace):
+        shape = layout.shape()
+        return _lib.smoe_moe_prefill(self.h, C.byref(shape), _ptr(experts), stride, n_experts,
+                                     _ptr(idx), _ptr(weights), _ptr(x), int(x_is_bf16), n_tokens, k,
+                                     _ptr(out_sum), _ptr(workspace),
+                                     0 if workspace is None else workspace.numel() * workspace.element_size())
+
+    # -- synthetic data ---------------------------------------------------------
+    def synth_experts(self, base, n_experts, stride, layout, seed, scale_sigma=0.02,
+                      bias_sigma=0.01):
+        shape = layout.shape()
+        return _lib.smoe_synth_experts(self.h, _ptr(base), n_experts, stride, C.byref(shape), seed,
+                                       C.c_float(scale_sigma), C.c_float(bias_sigma))
+
+    def synth_normal_f32(self, out, seed, sigma=1.0):
+        return _lib.smoe_synth_normal_f32(self.h, _ptr(out), out.numel(), seed, C.c_float(sigma))
+
+    def synth_normal_bf16(self, out, seed, sigma=1.0):
+        return _lib.smoe_synth_normal_bf16(self.h, _ptr(out), out.numel(), seed, C.c_float(sigma))
+
+
+def gpu_batched_experts_forward(kernels: Kernels, layout: ExpertLayout, actual_k, expert_data,
+                                payload: ExpertPayload):
+    """K expert blobs (host bytes, slot order) through gate/up/SwiGLU/down and
+    the combine; returns the post-combine hidden state (host float32).
+    Mirrors expert_forward.rs:718-746 (stage, dispatch, wait, read back)."""
+    import numpy as np
+    import torch
+
+    if actual_k < 1 or actual_k > MAX_K:
+        raise SmoeError(_abi.CODES["SMOE_ERR_BAD_K"], "gpu_batched_experts_forward")
+    data = np.ascontiguousarray(np.frombuffer(bytes(expert_data), np.uint8))
+    if data.size != actual_k * layout.expert_size:
+        raise SmoeError(_abi.CODES["SMOE_ERR_INVALID_ARG"], "expert_data length")
+    dev = torch.device("cuda", kernels.device)
+    blobs = torch.from_numpy(data).to(dev)
+    f = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev)
+    x, h_mid, shared = f(payload.h_post), f(payload.h_mid), f(payload.shared_out)
+    out = torch.empty(layout.hidden, dtype=torch.float32, device=dev)
+    bindings = [(blobs, s * layout.expert_size) for s in range(actual_k)]
+    check(kernels.experts_decode(layout, bindings, list(payload.expert_weights), x, h_mid, shared,
+                                 payload.shared_gate_score, out), "smoe_experts_decode")
+    kernels.sync()
+    return out.cpu().numpy()

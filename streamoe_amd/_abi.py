@@ -1,0 +1,134 @@
+"""ctypes binding of include/smoe.h (libsmoe.so).
+
+Loading fails loudly when the library has not been built: there is no
+fallback path. Build with ``python -m streamoe_amd.build``.
+"""
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libsmoe.so")
+
+SMOE_MAX_K = 16
+
+STATUS = {
+    0: "SMOE_OK",
+    1: "SMOE_ERR_INVALID_ARG",
+    2: "SMOE_ERR_BAD_K",
+    3: "SMOE_ERR_IN_DIM_NOT_MULTIPLE",
+    4: "SMOE_ERR_UNSUPPORTED_BITS",
+    5: "SMOE_ERR_UNSUPPORTED_GROUP",
+    6: "SMOE_ERR_UNSUPPORTED_SHAPE",
+    7: "SMOE_ERR_MISALIGNED",
+    8: "SMOE_ERR_SCRATCH_TOO_SMALL",
+    9: "SMOE_ERR_WORKSPACE_TOO_SMALL",
+    10: "SMOE_ERR_HIP",
+    11: "SMOE_ERR_NO_DEVICE",
+}
+CODES = {v: k for k, v in STATUS.items()}
+
+
+class SmoeError(RuntimeError):
+    """A non-zero status from libsmoe."""
+
+    def __init__(self, status, where):
+        self.status = status
+        self.name = STATUS.get(status, f"status {status}")
+        super().__init__(f"{where}: {self.name}")
+
+
+class QWeights(C.Structure):
+    _fields_ = [
+        ("base", C.c_void_p),
+        ("packed_offset", C.c_uint64),
+        ("scales_offset", C.c_uint64),
+        ("biases_offset", C.c_uint64),
+        ("group_size", C.c_uint32),
+        ("bits", C.c_uint32),
+    ]
+
+
+class ExpertShape(C.Structure):
+    _fields_ = [
+        ("hidden", C.c_uint32),
+        ("inter", C.c_uint32),
+        ("group", C.c_uint32),
+        ("bits", C.c_uint32),
+    ]
+
+
+class Binding(C.Structure):
+    _fields_ = [("base", C.c_void_p), ("offset", C.c_uint64)]
+
+
+class Layer(C.Structure):
+    _fields_ = [
+        ("shape", ExpertShape),
+        ("experts", C.c_void_p),
+        ("stride", C.c_uint64),
+        ("n_experts", C.c_uint32),
+        ("k", C.c_uint32),
+        ("normalize", C.c_int32),
+        ("router_w", C.c_void_p),
+        ("shared_expert", C.c_void_p),
+        ("shared_gate", C.c_void_p),
+    ]
+
+
+_P = C.c_void_p
+_U32 = C.c_uint32
+_U64 = C.c_uint64
+_I = C.c_int
+
+# name -> (restype, argtypes); the order follows include/smoe.h.
+PROTOTYPES = {
+    "smoe_strerror": (C.c_char_p, [_I]),
+    "smoe_abi_version": (_U32, []),
+    "smoe_create": (_I, [_I, _P, C.POINTER(_P)]),
+    "smoe_destroy": (_I, [_P]),
+    "smoe_set_stream": (_I, [_P, _P]),
+    "smoe_reserve": (_I, [_P, _U32, _U32, _U32]),
+    "smoe_sync": (_I, [_P]),
+    "smoe_qmv": (_I, [_P, C.POINTER(QWeights), _P, _P, _U32, _U32]),
+    "smoe_argmax": (_I, [_P, _P, _U32, _P]),
+    "smoe_dequant": (_I, [_P, C.POINTER(QWeights), _U32, _U32, _U32, _P]),
+    "smoe_router": (_I, [_P, _P, _P, _U32, _U32, _U32, _U32, _I, _P, _P, _P]),
+    "smoe_softmax_topk": (_I, [_P, _P, _U32, _U32, _U32, _I, _P, _P]),
+    "smoe_topk": (_I, [_P, _P, _U32, _U32, _U32, _P, _P]),
+    "smoe_expert_bytes": (_U64, [C.POINTER(ExpertShape)]),
+    "smoe_experts_decode": (_I, [_P, C.POINTER(ExpertShape), C.POINTER(Binding), _U32, C.POINTER(C.c_float),
+                                 _P, _P, _P, C.c_float, _P]),
+    "smoe_moe_decode_layer": (_I, [_P, C.POINTER(Layer), _P, _P, _P, _P, _P]),
+    "smoe_moe_decode_layers": (_I, [_P, C.POINTER(Layer), _U32, C.POINTER(_P), C.c_float, _P, _P, _P]),
+    "smoe_moe_prefill_workspace_size": (_U64, [C.POINTER(ExpertShape), _U32, _U32, _U32]),
+    "smoe_moe_prefill": (_I, [_P, C.POINTER(ExpertShape), _P, _U64, _U32, _P, _P, _P, _I, _U32, _U32, _P, _P,
+                              _U64]),
+    "smoe_synth_experts": (_I, [_P, _P, _U32, _U64, C.POINTER(ExpertShape), _U64, C.c_float, C.c_float]),
+    "smoe_synth_normal_f32": (_I, [_P, _P, _U64, _U64, C.c_float]),
+    "smoe_synth_normal_bf16": (_I, [_P, _P, _U64, _U64, C.c_float]),
+}
+
+_lib = None
+
+
+def load():
+    """Load libsmoe.so once; raise if it is missing."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is not built; run `python -m streamoe_amd.build` (no CPU fallback exists)")
+    lib = C.CDLL(LIB_PATH)
+    for name, (res, args) in PROTOTYPES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def check(status, where):
+    if status != 0:
+        raise SmoeError(status, where)
+    return status

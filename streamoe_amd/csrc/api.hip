@@ -1,0 +1,412 @@
+// api.hip — the C ABI of libsmoe (include/smoe.h): argument validation,
+// the handle's reserved scratch, and dispatch to the kernel launchers.
+#include <math.h>
+#include <string.h>
+
+#include <new>
+
+#include "../../include/smoe.h"
+#include "kernels.h"
+
+using namespace smoe;
+
+struct smoe_handle {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  // Decode scratch (MoeBuffers' flat buffers, expert_forward.rs:379-528).
+  void* mem = nullptr;
+  float* act = nullptr;       // [kMaxSlots, max_inter]
+  float* logits = nullptr;    // [max_experts]
+  float* gate = nullptr;      // [1] shared-expert gate score
+  FfnTable* table = nullptr;  // routing table of the current token
+  uint32_t max_hidden = 0, max_inter = 0, max_experts = 0;
+};
+
+namespace {
+
+constexpr uint32_t kAbiVersion = 1;
+
+int hip_status(hipError_t e) { return e == hipSuccess ? SMOE_OK : SMOE_ERR_HIP; }
+
+bool aligned(const void* p, uint64_t off, uint64_t a) {
+  return (((uintptr_t)p + off) % a) == 0;
+}
+
+int check_group(uint32_t group) {
+  return (group == 32 || group == 64 || group == 128) ? SMOE_OK : SMOE_ERR_UNSUPPORTED_GROUP;
+}
+
+int check_shape(const smoe_expert_shape* s) {
+  if (!s || !s->hidden || !s->inter) return SMOE_ERR_INVALID_ARG;
+  if (s->bits != 4 && s->bits != 3) return SMOE_ERR_UNSUPPORTED_BITS;
+  if (int rc = check_group(s->group)) return rc;
+  if (s->hidden % s->group || s->inter % s->group) return SMOE_ERR_IN_DIM_NOT_MULTIPLE;
+  // Kernel instances: hidden/32 in {32, 64, 128}, inter/32 in {8, 16, 32, 64}.
+  const uint32_t ch = s->hidden / 32, ci = s->inter / 32;
+  if (!(ch == 32 || ch == 64 || ch == 128)) return SMOE_ERR_UNSUPPORTED_SHAPE;
+  if (!(ci == 8 || ci == 16 || ci == 32 || ci == 64)) return SMOE_ERR_UNSUPPORTED_SHAPE;
+  return SMOE_OK;
+}
+
+// A blob's codes must allow the chunk loads: 16 bytes (4-bit), 4 (3-bit).
+bool blob_aligned(const void* p, uint32_t bits) { return aligned(p, 0, bits == 4 ? 16 : 4); }
+
+int reserve(smoe_handle* h, uint32_t H, uint32_t I, uint32_t E) {
+  if (h->mem && H <= h->max_hidden && I <= h->max_inter && E <= h->max_experts) return SMOE_OK;
+  H = H > h->max_hidden ? H : h->max_hidden;
+  I = I > h->max_inter ? I : h->max_inter;
+  E = E > h->max_experts ? E : h->max_experts;
+  const size_t act_b = (size_t)kMaxSlotsHost * I * sizeof(float);
+  const size_t log_b = ((size_t)E * sizeof(float) + 255) & ~(size_t)255;
+  const size_t total = act_b + log_b + 256 + sizeof(FfnTable) + 256;
+  void* mem = nullptr;
+  if (hipSetDevice(h->device) != hipSuccess) return SMOE_ERR_HIP;
+  if (hipMalloc(&mem, total) != hipSuccess) return SMOE_ERR_HIP;
+  if (hipMemset(mem, 0, total) != hipSuccess) {
+    (void)hipFree(mem);
+    return SMOE_ERR_HIP;
+  }
+  if (h->mem) {
+    (void)hipDeviceSynchronize();
+    (void)hipFree(h->mem);
+  }
+  char* p = (char*)mem;
+  h->mem = mem;
+  h->act = (float*)p;
+  h->logits = (float*)(p + act_b);
+  h->gate = (float*)(p + act_b + log_b);
+  h->table = (FfnTable*)(p + act_b + log_b + 256);
+  h->max_hidden = H;
+  h->max_inter = I;
+  h->max_experts = E;
+  return SMOE_OK;
+}
+
+int use_device(smoe_handle* h) { return hipSetDevice(h->device) == hipSuccess ? SMOE_OK : SMOE_ERR_HIP; }
+
+}  // namespace
+
+extern "C" {
+
+const char* smoe_strerror(int status) {
+  switch (status) {
+    case SMOE_OK: return "ok";
+    case SMOE_ERR_INVALID_ARG: return "invalid argument (null pointer, zero size or bad enum)";
+    case SMOE_ERR_BAD_K: return "k out of range: must be 1..=16 and <= n_experts";
+    case SMOE_ERR_IN_DIM_NOT_MULTIPLE: return "input dimension is not a multiple of the group size";
+    case SMOE_ERR_UNSUPPORTED_BITS: return "unsupported weight width (4 or 3 bits)";
+    case SMOE_ERR_UNSUPPORTED_GROUP: return "unsupported group size (32, 64 or 128)";
+    case SMOE_ERR_UNSUPPORTED_SHAPE: return "no kernel instance for this shape";
+    case SMOE_ERR_MISALIGNED: return "weight, scale or activation pointer misaligned";
+    case SMOE_ERR_SCRATCH_TOO_SMALL: return "shape exceeds the reserved scratch (smoe_reserve)";
+    case SMOE_ERR_WORKSPACE_TOO_SMALL: return "workspace smaller than the required size";
+    case SMOE_ERR_HIP: return "HIP runtime error";
+    case SMOE_ERR_NO_DEVICE: return "no gfx950 device at that ordinal";
+    default: return "unknown status";
+  }
+}
+
+uint32_t smoe_abi_version(void) { return kAbiVersion; }
+
+int smoe_create(int device, void* stream, smoe_handle** out) {
+  if (!out) return SMOE_ERR_INVALID_ARG;
+  *out = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) return SMOE_ERR_NO_DEVICE;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess) return SMOE_ERR_HIP;
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) return SMOE_ERR_NO_DEVICE;
+  smoe_handle* h = new (std::nothrow) smoe_handle;
+  if (!h) return SMOE_ERR_HIP;
+  h->device = device;
+  h->stream = (hipStream_t)stream;
+  const int rc = reserve(h, 4096, 2048, 1024);
+  if (rc) {
+    delete h;
+    return rc;
+  }
+  *out = h;
+  return SMOE_OK;
+}
+
+int smoe_destroy(smoe_handle* h) {
+  if (!h) return SMOE_ERR_INVALID_ARG;
+  (void)hipSetDevice(h->device);
+  if (h->mem) {
+    (void)hipStreamSynchronize(h->stream);
+    (void)hipFree(h->mem);
+  }
+  delete h;
+  return SMOE_OK;
+}
+
+int smoe_set_stream(smoe_handle* h, void* stream) {
+  if (!h) return SMOE_ERR_INVALID_ARG;
+  h->stream = (hipStream_t)stream;
+  return SMOE_OK;
+}
+
+int smoe_reserve(smoe_handle* h, uint32_t max_hidden, uint32_t max_inter, uint32_t max_experts) {
+  if (!h) return SMOE_ERR_INVALID_ARG;
+  return reserve(h, max_hidden, max_inter, max_experts);
+}
+
+int smoe_sync(smoe_handle* h) {
+  if (!h) return SMOE_ERR_INVALID_ARG;
+  if (int rc = use_device(h)) return rc;
+  return hip_status(hipStreamSynchronize(h->stream));
+}
+
+static int qview(const smoe_qweights* w, uint32_t in_dim, QView* v) {
+  if (!w || !w->base || !in_dim) return SMOE_ERR_INVALID_ARG;
+  if (w->bits != 4 && w->bits != 3) return SMOE_ERR_UNSUPPORTED_BITS;
+  if (int rc = check_group(w->group_size)) return rc;
+  if (in_dim % w->group_size) return SMOE_ERR_IN_DIM_NOT_MULTIPLE;
+  if (!aligned(w->base, w->packed_offset, w->bits == 4 ? 16 : 4) ||
+      !aligned(w->base, w->scales_offset, 2) || !aligned(w->base, w->biases_offset, 2))
+    return SMOE_ERR_MISALIGNED;
+  const uint8_t* b = (const uint8_t*)w->base;
+  v->codes = b + w->packed_offset;
+  v->scales = (const uint16_t*)(b + w->scales_offset);
+  v->biases = (const uint16_t*)(b + w->biases_offset);
+  v->bits = w->bits;
+  v->group = w->group_size;
+  return SMOE_OK;
+}
+
+int smoe_qmv(smoe_handle* h, const smoe_qweights* w, const float* x, float* y, uint32_t out_dim,
+             uint32_t in_dim) {
+  if (!h || !x || !y || !out_dim) return SMOE_ERR_INVALID_ARG;
+  QView v;
+  if (int rc = qview(w, in_dim, &v)) return rc;
+  if (!aligned(x, 0, 16)) return SMOE_ERR_MISALIGNED;
+  if (int rc = use_device(h)) return rc;
+  bool unsupported = false;
+  const hipError_t e = launch_qmv(v, x, y, out_dim, in_dim, h->stream, &unsupported);
+  if (unsupported) return SMOE_ERR_UNSUPPORTED_SHAPE;
+  return hip_status(e);
+}
+
+int smoe_argmax(smoe_handle* h, const float* v, uint32_t n, int32_t* out_index) {
+  if (!h || !v || !n || !out_index) return SMOE_ERR_INVALID_ARG;
+  if (int rc = use_device(h)) return rc;
+  return hip_status(launch_argmax(v, n, out_index, h->stream));
+}
+
+int smoe_dequant(smoe_handle* h, const smoe_qweights* w, uint32_t in_dim, uint32_t row0,
+                 uint32_t n_rows, float* out) {
+  if (!h || !out || !n_rows) return SMOE_ERR_INVALID_ARG;
+  QView v;
+  if (int rc = qview(w, in_dim, &v)) return rc;
+  if (in_dim % 32) return SMOE_ERR_UNSUPPORTED_SHAPE;
+  if (int rc = use_device(h)) return rc;
+  return hip_status(launch_dequant(v, in_dim, row0, n_rows, out, h->stream));
+}
+
+static int check_router(uint32_t n_tokens, uint32_t n_experts, uint32_t k) {
+  if (!n_tokens || !n_experts) return SMOE_ERR_INVALID_ARG;
+  if (k < 1 || k > SMOE_MAX_K || k > n_experts) return SMOE_ERR_BAD_K;
+  if (n_experts > 1024) return SMOE_ERR_UNSUPPORTED_SHAPE;
+  return SMOE_OK;
+}
+
+int smoe_router(smoe_handle* h, const float* router_w, const float* x, uint32_t n_tokens,
+                uint32_t n_experts, uint32_t hidden, uint32_t k, int normalize, int32_t* idx,
+                float* weights, float* logits_out) {
+  if (!h || !router_w || !x || !idx || !weights || !hidden) return SMOE_ERR_INVALID_ARG;
+  if (int rc = check_router(n_tokens, n_experts, k)) return rc;
+  if (hidden % 4) return SMOE_ERR_UNSUPPORTED_SHAPE;
+  if (!aligned(router_w, 0, 16) || !aligned(x, 0, 16)) return SMOE_ERR_MISALIGNED;
+  float* logits = logits_out;
+  if (!logits) {
+    if ((uint64_t)n_tokens * n_experts > h->max_experts) return SMOE_ERR_SCRATCH_TOO_SMALL;
+    logits = h->logits;
+  }
+  if (int rc = use_device(h)) return rc;
+  hipError_t e = launch_router_logits(router_w, nullptr, x, n_tokens, n_experts, hidden, logits,
+                                      nullptr, h->stream);
+  if (e != hipSuccess) return SMOE_ERR_HIP;
+  RouteOut ro{};
+  ro.idx = idx;
+  ro.weight = weights;
+  return hip_status(launch_topk(logits, n_tokens, n_experts, k, true, normalize != 0, ro, h->stream));
+}
+
+int smoe_softmax_topk(smoe_handle* h, const float* logits, uint32_t n_tokens, uint32_t n_experts,
+                      uint32_t k, int normalize, int32_t* idx, float* weights) {
+  if (!h || !logits || !idx || !weights) return SMOE_ERR_INVALID_ARG;
+  if (int rc = check_router(n_tokens, n_experts, k)) return rc;
+  if (int rc = use_device(h)) return rc;
+  RouteOut ro{};
+  ro.idx = idx;
+  ro.weight = weights;
+  return hip_status(launch_topk(logits, n_tokens, n_experts, k, true, normalize != 0, ro, h->stream));
+}
+
+int smoe_topk(smoe_handle* h, const float* scores, uint32_t n_tokens, uint32_t n, uint32_t k,
+              int32_t* idx, float* values) {
+  if (!h || !scores || !idx || !values) return SMOE_ERR_INVALID_ARG;
+  if (int rc = check_router(n_tokens, n, k)) return rc;
+  if (int rc = use_device(h)) return rc;
+  RouteOut ro{};
+  ro.idx = idx;
+  ro.weight = values;
+  return hip_status(launch_topk(scores, n_tokens, n, k, false, false, ro, h->stream));
+}
+
+uint64_t smoe_expert_bytes(const smoe_expert_shape* s) {
+  if (!s || !s->group) return 0;
+  const uint64_t w = (uint64_t)s->inter * s->hidden * s->bits / 8;
+  const uint64_t sc = (uint64_t)s->inter * (s->hidden / s->group) * 2;
+  return 3 * (w + 2 * sc);
+}
+
+int smoe_experts_decode(smoe_handle* h, const smoe_expert_shape* shape,
+                        const smoe_binding* bindings, uint32_t k, const float* weights,
+                        const float* input, const float* h_mid, const float* shared_out,
+                        float shared_gate_score, float* hidden_out) {
+  if (!h || !bindings || !weights || !input || !h_mid || !hidden_out) return SMOE_ERR_INVALID_ARG;
+  if (int rc = check_shape(shape)) return rc;
+  if (k < 1 || k > SMOE_MAX_K) return SMOE_ERR_BAD_K;
+  if (shape->hidden > h->max_hidden || shape->inter > h->max_inter)
+    return SMOE_ERR_SCRATCH_TOO_SMALL;
+  if (!aligned(input, 0, 16)) return SMOE_ERR_MISALIGNED;
+  FfnTable tab{};
+  for (uint32_t s = 0; s < k; ++s) {
+    if (!bindings[s].base) return SMOE_ERR_INVALID_ARG;
+    const uint8_t* p = (const uint8_t*)bindings[s].base + bindings[s].offset;
+    if (!blob_aligned(p, shape->bits)) return SMOE_ERR_MISALIGNED;
+    tab.blob[s] = p;
+    tab.weight[s] = weights[s];
+  }
+  tab.k = k;
+  tab.has_shared = 0;
+  tab.shared_gate = shared_gate_score;
+  if (int rc = use_device(h)) return rc;
+  const BlobGeom g = blob_geom(shape->hidden, shape->inter, shape->group, shape->bits);
+  bool uns = false;
+  hipError_t e = launch_gateup(g, g, nullptr, tab, k, input, h->act, h->stream, &uns);
+  if (uns) return SMOE_ERR_UNSUPPORTED_SHAPE;
+  if (e != hipSuccess) return SMOE_ERR_HIP;
+  e = launch_down_combine(g, g, nullptr, tab, k, h->act, h_mid, shared_out, hidden_out, h->stream,
+                          &uns);
+  if (uns) return SMOE_ERR_UNSUPPORTED_SHAPE;
+  return hip_status(e);
+}
+
+static int check_layer(smoe_handle* h, const smoe_layer* L) {
+  if (!L || !L->experts || !L->router_w) return SMOE_ERR_INVALID_ARG;
+  if (int rc = check_shape(&L->shape)) return rc;
+  if (int rc = check_router(1, L->n_experts, L->k)) return rc;
+  if (L->stride < smoe_expert_bytes(&L->shape)) return SMOE_ERR_INVALID_ARG;
+  if (!blob_aligned(L->experts, L->shape.bits) || L->stride % (L->shape.bits == 4 ? 16 : 4))
+    return SMOE_ERR_MISALIGNED;
+  if (L->shared_expert && !blob_aligned(L->shared_expert, 4)) return SMOE_ERR_MISALIGNED;
+  if (!aligned(L->router_w, 0, 16) || (L->shared_gate && !aligned(L->shared_gate, 0, 16)))
+    return SMOE_ERR_MISALIGNED;
+  if (L->shape.hidden % 4) return SMOE_ERR_UNSUPPORTED_SHAPE;
+  if (L->shape.hidden > h->max_hidden || L->shape.inter > h->max_inter ||
+      L->n_experts > h->max_experts)
+    return SMOE_ERR_SCRATCH_TOO_SMALL;
+  return SMOE_OK;
+}
+
+static int decode_layer(smoe_handle* h, const smoe_layer* L, const float* input,
+                        const float* h_mid, float* hidden_out, int32_t* idx_out, float* w_out) {
+  const smoe_expert_shape& s = L->shape;
+  hipError_t e = launch_router_logits(L->router_w, L->shared_expert ? L->shared_gate : nullptr,
+                                      input, 1, L->n_experts, s.hidden, h->logits, h->gate,
+                                      h->stream);
+  if (e != hipSuccess) return SMOE_ERR_HIP;
+  RouteOut ro{};
+  ro.idx = idx_out;
+  ro.weight = w_out;
+  ro.table = h->table;
+  ro.experts = (const uint8_t*)L->experts;
+  ro.stride = L->stride;
+  ro.shared_blob = (const uint8_t*)L->shared_expert;
+  ro.gate_scores = (L->shared_expert && L->shared_gate) ? h->gate : nullptr;
+  e = launch_topk(h->logits, 1, L->n_experts, L->k, true, L->normalize != 0, ro, h->stream);
+  if (e != hipSuccess) return SMOE_ERR_HIP;
+  const BlobGeom g = blob_geom(s.hidden, s.inter, s.group, s.bits);
+  const BlobGeom gs = blob_geom(s.hidden, s.inter, s.group, 4);
+  FfnTable tv{};
+  tv.k = L->k;
+  const uint32_t n_slots = L->k + (L->shared_expert ? 1 : 0);
+  bool uns = false;
+  e = launch_gateup(g, gs, h->table, tv, n_slots, input, h->act, h->stream, &uns);
+  if (uns) return SMOE_ERR_UNSUPPORTED_SHAPE;
+  if (e != hipSuccess) return SMOE_ERR_HIP;
+  e = launch_down_combine(g, gs, h->table, tv, n_slots, h->act, h_mid, nullptr, hidden_out,
+                          h->stream, &uns);
+  if (uns) return SMOE_ERR_UNSUPPORTED_SHAPE;
+  return hip_status(e);
+}
+
+int smoe_moe_decode_layer(smoe_handle* h, const smoe_layer* layer, const float* input,
+                          const float* h_mid, float* hidden_out, int32_t* idx_out, float* w_out) {
+  if (!h || !input || !h_mid || !hidden_out) return SMOE_ERR_INVALID_ARG;
+  if (int rc = check_layer(h, layer)) return rc;
+  if (!aligned(input, 0, 16)) return SMOE_ERR_MISALIGNED;
+  if (int rc = use_device(h)) return rc;
+  return decode_layer(h, layer, input, h_mid, hidden_out, idx_out, w_out);
+}
+
+int smoe_moe_decode_layers(smoe_handle* h, const smoe_layer* layers, uint32_t n_layers,
+                           const void* const* norm_w, float eps, const float* input,
+                           float* residual_io, float* work) {
+  if (!h || !layers || !n_layers || !input || !residual_io || !work) return SMOE_ERR_INVALID_ARG;
+  for (uint32_t l = 0; l < n_layers; ++l) {
+    if (int rc = check_layer(h, &layers[l])) return rc;
+    if (layers[l].shape.hidden != layers[0].shape.hidden) return SMOE_ERR_INVALID_ARG;
+    if (norm_w && l > 0 && !norm_w[l]) return SMOE_ERR_INVALID_ARG;
+  }
+  if (!aligned(input, 0, 16) || !aligned(residual_io, 0, 16) || !aligned(work, 0, 16))
+    return SMOE_ERR_MISALIGNED;
+  if (int rc = use_device(h)) return rc;
+  const uint32_t H = layers[0].shape.hidden;
+  for (uint32_t l = 0; l < n_layers; ++l) {
+    const float* x = input;
+    if (l > 0) {
+      if (norm_w) {
+        const hipError_t e =
+            launch_rmsnorm(residual_io, (const uint16_t*)norm_w[l], eps, H, work, h->stream);
+        if (e != hipSuccess) return SMOE_ERR_HIP;
+        x = work;
+      } else {
+        x = residual_io;
+      }
+    }
+    if (int rc = decode_layer(h, &layers[l], x, residual_io, residual_io, nullptr, nullptr))
+      return rc;
+  }
+  return SMOE_OK;
+}
+
+int smoe_synth_experts(smoe_handle* h, void* base, uint32_t n_experts, uint64_t stride,
+                       const smoe_expert_shape* shape, uint64_t seed, float scale_sigma,
+                       float bias_sigma) {
+  if (!h || !base || !n_experts || !shape) return SMOE_ERR_INVALID_ARG;
+  if (shape->bits != 4 && shape->bits != 3) return SMOE_ERR_UNSUPPORTED_BITS;
+  if (!shape->group || shape->hidden % shape->group || shape->inter % shape->group)
+    return SMOE_ERR_IN_DIM_NOT_MULTIPLE;
+  if (stride < smoe_expert_bytes(shape)) return SMOE_ERR_INVALID_ARG;
+  if (int rc = use_device(h)) return rc;
+  const BlobGeom g = blob_geom(shape->hidden, shape->inter, shape->group, shape->bits);
+  return hip_status(launch_synth_experts((uint8_t*)base, n_experts, stride, g, seed, scale_sigma,
+                                         bias_sigma, h->stream));
+}
+
+int smoe_synth_normal_f32(smoe_handle* h, float* out, uint64_t n, uint64_t seed, float sigma) {
+  if (!h || !out || !n) return SMOE_ERR_INVALID_ARG;
+  if (int rc = use_device(h)) return rc;
+  return hip_status(launch_synth_normal_f32(out, n, seed, sigma, h->stream));
+}
+
+int smoe_synth_normal_bf16(smoe_handle* h, uint16_t* out, uint64_t n, uint64_t seed, float sigma) {
+  if (!h || !out || !n) return SMOE_ERR_INVALID_ARG;
+  if (int rc = use_device(h)) return rc;
+  return hip_status(launch_synth_normal_bf16(out, n, seed, sigma, h->stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,188 @@
+// common.h — device helpers shared by the libsmoe kernels (gfx950, wave64).
+//
+// Quantized-weight chunk model used by every decode kernel: one lane owns
+// a "chunk" of 32 consecutive inputs of one weight row. A 4-bit chunk is
+// 16 bytes (4 little-endian u32 words, 8 nibbles each, low nibble first);
+// a packed 3-bit chunk is 12 bytes (four little-endian 24-bit packs, code
+// i at bits 3i..3i+3; MLX's layout). Groups are multiples of 32, so a
+// chunk never straddles a group: it has exactly one (scale, bias).
+//
+// The chunk dot product is computed group-factored:
+//     sum_j (q_j * s + b) * x_j  =  s * sum_j q_j x_j  +  b * sum_j x_j
+// which is one FMA per weight instead of two. The 3-bit and 4-bit paths
+// share every floating-point operation after the codes are unpacked into
+// exact small-integer floats, so a packed 3-bit row gives bit-identical
+// results to the same codes stored as 4-bit nibbles.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace smoe {
+
+constexpr int kWave = 64;
+constexpr int kChunk = 32;  // inputs per lane-chunk
+constexpr int kMaxK = 16;
+constexpr int kMaxSlots = kMaxK + 1;  // routed slots + shared expert
+
+__device__ __forceinline__ float bf16f(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+template <int BITS>
+struct Raw;
+template <>
+struct Raw<4> {
+  uint32_t d[4];
+};
+template <>
+struct Raw<3> {
+  uint32_t d[3];
+};
+
+template <int BITS>
+constexpr int chunk_bytes() {
+  return BITS * kChunk / 8;
+}
+
+// Weights are streamed once per decode step: load them non-temporally so
+// they do not evict the activations and routing data from L2.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ Raw<4> load_raw4(const uint8_t* p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  Raw<4> r;
+  r.d[0] = v.x;
+  r.d[1] = v.y;
+  r.d[2] = v.z;
+  r.d[3] = v.w;
+  return r;
+}
+__device__ __forceinline__ Raw<3> load_raw3(const uint8_t* p) {
+  const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
+  Raw<3> r;
+  r.d[0] = __builtin_nontemporal_load(q + 0);
+  r.d[1] = __builtin_nontemporal_load(q + 1);
+  r.d[2] = __builtin_nontemporal_load(q + 2);
+  return r;
+}
+template <int BITS>
+__device__ __forceinline__ Raw<BITS> load_raw(const uint8_t* p);
+template <>
+__device__ __forceinline__ Raw<4> load_raw<4>(const uint8_t* p) {
+  return load_raw4(p);
+}
+template <>
+__device__ __forceinline__ Raw<3> load_raw<3>(const uint8_t* p) {
+  return load_raw3(p);
+}
+
+// Codes of a chunk as exact floats, in input order j = 0..31.
+__device__ __forceinline__ void unpack(const Raw<4>& r, float (&q)[kChunk]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t lo = r.d[i] & 0x0F0F0F0Fu;         // nibbles 0,2,4,6 in bytes 0..3
+    const uint32_t hi = (r.d[i] >> 4) & 0x0F0F0F0Fu;  // nibbles 1,3,5,7
+    q[8 * i + 0] = (float)(lo & 0xFFu);
+    q[8 * i + 2] = (float)((lo >> 8) & 0xFFu);
+    q[8 * i + 4] = (float)((lo >> 16) & 0xFFu);
+    q[8 * i + 6] = (float)(lo >> 24);
+    q[8 * i + 1] = (float)(hi & 0xFFu);
+    q[8 * i + 3] = (float)((hi >> 8) & 0xFFu);
+    q[8 * i + 5] = (float)((hi >> 16) & 0xFFu);
+    q[8 * i + 7] = (float)(hi >> 24);
+  }
+}
+
+__device__ __forceinline__ void unpack(const Raw<3>& r, float (&q)[kChunk]) {
+#pragma unroll
+  for (int j = 0; j < kChunk; ++j) {
+    const int bit = 3 * j, w = bit >> 5, o = bit & 31;
+    uint32_t v;
+    if (o <= 29)
+      v = __builtin_amdgcn_ubfe(r.d[w], o, 3);
+    else
+      v = __builtin_amdgcn_alignbit(r.d[w + 1], r.d[w], o) & 7u;
+    q[j] = (float)v;
+  }
+}
+
+// Integer code of input j of a chunk (used by the dequant probe).
+__device__ __forceinline__ uint32_t code_at(const Raw<4>& r, int j) {
+  return (r.d[j >> 3] >> ((j & 7) * 4)) & 0xFu;
+}
+__device__ __forceinline__ uint32_t code_at(const Raw<3>& r, int j) {
+  const int bit = 3 * j, w = bit >> 5, o = bit & 31;
+  if (o <= 29) return (r.d[w] >> o) & 7u;
+  return ((r.d[w] >> o) | (r.d[w + 1] << (32 - o))) & 7u;
+}
+
+// sum_j q_j x_j over one chunk: four interleaved FMA chains.
+__device__ __forceinline__ float qdot(const float (&q)[kChunk], const float (&x)[kChunk]) {
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+  for (int j = 0; j < kChunk; j += 4) {
+    a0 = __builtin_fmaf(q[j + 0], x[j + 0], a0);
+    a1 = __builtin_fmaf(q[j + 1], x[j + 1], a1);
+    a2 = __builtin_fmaf(q[j + 2], x[j + 2], a2);
+    a3 = __builtin_fmaf(q[j + 3], x[j + 3], a3);
+  }
+  return (a0 + a1) + (a2 + a3);
+}
+
+__device__ __forceinline__ float xsum(const float (&x)[kChunk]) {
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+  for (int j = 0; j < kChunk; j += 4) {
+    a0 += x[j + 0];
+    a1 += x[j + 1];
+    a2 += x[j + 2];
+    a3 += x[j + 3];
+  }
+  return (a0 + a1) + (a2 + a3);
+}
+
+// Contribution of one chunk: s * sum(q x) + b * sum(x).
+template <int BITS>
+__device__ __forceinline__ float chunk_dot(const Raw<BITS>& raw, const float (&x)[kChunk],
+                                           float xs, float s, float b) {
+  float q[kChunk];
+  unpack(raw, q);
+  return __builtin_fmaf(s, qdot(q, x), b * xs);
+}
+
+// Sum over aligned groups of W lanes (W a power of two <= 64). Every lane of
+// a group ends with the same value: the butterfly adds commute exactly.
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+__device__ __forceinline__ void load_x32(const float* p, float (&x)[kChunk]) {
+  const float4* p4 = reinterpret_cast<const float4*>(p);
+#pragma unroll
+  for (int i = 0; i < kChunk / 4; ++i) {
+    const float4 v = p4[i];
+    x[4 * i + 0] = v.x;
+    x[4 * i + 1] = v.y;
+    x[4 * i + 2] = v.z;
+    x[4 * i + 3] = v.w;
+  }
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  // moe_cpu.rs:213-217: silu = g / (1 + exp(-g)); act = silu * up.
+  const float silu = g / (1.0f + expf(-g));
+  return silu * u;
+}
+
+__device__ __forceinline__ float sigmoidf_ref(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+}  // namespace smoe

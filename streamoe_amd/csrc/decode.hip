@@ -1,0 +1,727 @@
+// decode.hip — single-token kernels of the routed-expert path (gfx950).
+//
+//   k_qmv            dense quantized matvec (LM head), persistent waves,
+//                    x held in registers, loads of the next rows issued
+//                    before the current ones are reduced.
+//   k_router_logits  f32 router GEMV, one block per expert row.
+//   k_topk           softmax + running-minimum top-k + renorm, one wave
+//                    per token, exact slot order of the reference.
+//   k_gateup         fused gate + up + SwiGLU over all routed slots and
+//                    the shared expert; one wave reads whole rows with
+//                    one 16-byte (4-bit) / 12-byte (3-bit) load per lane.
+//   k_down_combine   down projection of every slot for a few output rows
+//                    plus the fixed-order weighted combine and residual,
+//                    no atomics.
+#include "common.h"
+#include "kernels.h"
+
+namespace smoe {
+
+static_assert(sizeof(FfnTable) < 4096, "FfnTable must fit a kernel argument");
+
+BlobGeom blob_geom(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t bits) {
+  BlobGeom g{};
+  g.bits = bits;
+  g.hidden = hidden;
+  g.inter = inter;
+  g.group = group;
+  const uint64_t wb = (uint64_t)inter * hidden * bits / 8;
+  const uint64_t sb = (uint64_t)inter * (hidden / group) * 2;
+  const uint64_t blk = wb + 2 * sb;
+  for (int i = 0; i < 3; ++i) {
+    g.w[i] = i * blk;
+    g.s[i] = i * blk + wb;
+    g.b[i] = i * blk + wb + sb;
+  }
+  return g;
+}
+
+// ---------------------------------------------------------------------------
+// Dense qmv.  CPR = in_dim / 32 chunks per row; a row is read by
+// L = min(CPR, 64) lanes, each owning CPL = CPR / L chunks; a wave covers
+// RPP = 64 / L rows per pass and U passes per step.
+// ---------------------------------------------------------------------------
+template <int BITS, int CPR, int U>
+__global__ __launch_bounds__(256) void k_qmv(const uint8_t* __restrict__ codes,
+                                             const uint16_t* __restrict__ scales,
+                                             const uint16_t* __restrict__ biases,
+                                             const float* __restrict__ x, float* __restrict__ y,
+                                             uint32_t rows, uint32_t group, uint32_t n_waves) {
+  constexpr int L = CPR < kWave ? CPR : kWave;
+  constexpr int CPL = CPR / L;
+  constexpr int RPP = kWave / L;
+  constexpr int CB = chunk_bytes<BITS>();
+  constexpr uint32_t ROW_BYTES = CPR * CB;
+  const int lane = threadIdx.x & 63;
+  const uint32_t wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int lrow = lane / L, lch = lane % L;
+  const uint32_t gpr = CPR * kChunk / group;  // groups per row
+  const uint32_t cpg_shift = __builtin_ctz(group / kChunk);
+
+  float xr[CPL][kChunk];
+  float xs[CPL];
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    load_x32(x + (size_t)(lch + L * i) * kChunk, xr[i]);
+    xs[i] = xsum(xr[i]);
+  }
+
+  constexpr uint32_t STEP_ROWS = RPP * U;
+  const uint32_t n_steps = (rows + STEP_ROWS - 1) / STEP_ROWS;
+  Raw<BITS> cur[U][CPL];
+  float cs[U][CPL], cb[U][CPL];
+
+  auto issue = [&](uint32_t step, Raw<BITS>(&raw)[U][CPL], float(&sv)[U][CPL],
+                   float(&bv)[U][CPL]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      uint32_t row = step * STEP_ROWS + u * RPP + lrow;
+      row = row < rows ? row : rows - 1;
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const uint32_t c = lch + L * i;
+        raw[u][i] = load_raw<BITS>(codes + (size_t)row * ROW_BYTES + c * CB);
+        const size_t gi = (size_t)row * gpr + (c >> cpg_shift);
+        sv[u][i] = bf16f(scales[gi]);
+        bv[u][i] = bf16f(biases[gi]);
+      }
+    }
+  };
+
+  uint32_t step = wave;
+  if (step >= n_steps) return;
+  issue(step, cur, cs, cb);
+  while (true) {
+    const uint32_t next = step + n_waves;
+    Raw<BITS> nxt[U][CPL];
+    float ns[U][CPL], nb[U][CPL];
+    const bool more = next < n_steps;
+    if (more) issue(next, nxt, ns, nb);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float part = 0.f;
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) part += chunk_dot<BITS>(cur[u][i], xr[i], xs[i], cs[u][i], cb[u][i]);
+      const float sum = group_sum<L>(part);
+      const uint32_t row = step * STEP_ROWS + u * RPP + lrow;
+      if (lch == 0 && row < rows) y[row] = sum;
+    }
+    if (!more) break;
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        cur[u][i] = nxt[u][i];
+        cs[u][i] = ns[u][i];
+        cb[u][i] = nb[u][i];
+      }
+    step = next;
+  }
+}
+
+template <int BITS, int CPR>
+static hipError_t qmv_inst(const QView& w, const float* x, float* y, uint32_t rows,
+                           hipStream_t st) {
+  constexpr int L = CPR < kWave ? CPR : kWave;
+  constexpr int RPP = kWave / L;
+  constexpr int U = 4;
+  const uint32_t n_steps = (rows + RPP * U - 1) / (RPP * U);
+  // Persistent grid: up to 8 waves per CU on 256 CUs.
+  uint32_t n_waves = n_steps < 2048u ? n_steps : 2048u;
+  const uint32_t wpb = 4;
+  const uint32_t blocks = (n_waves + wpb - 1) / wpb;
+  n_waves = blocks * wpb;
+  hipLaunchKernelGGL((k_qmv<BITS, CPR, U>), dim3(blocks), dim3(wpb * 64), 0, st, w.codes, w.scales,
+                     w.biases, x, y, rows, w.group, n_waves);
+  return hipGetLastError();
+}
+
+template <int BITS>
+static hipError_t qmv_bits(const QView& w, const float* x, float* y, uint32_t rows,
+                           uint32_t in_dim, hipStream_t st, bool* unsupported) {
+  switch (in_dim / kChunk) {
+    case 16: return qmv_inst<BITS, 16>(w, x, y, rows, st);
+    case 32: return qmv_inst<BITS, 32>(w, x, y, rows, st);
+    case 64: return qmv_inst<BITS, 64>(w, x, y, rows, st);
+    case 128: return qmv_inst<BITS, 128>(w, x, y, rows, st);
+    case 256: return qmv_inst<BITS, 256>(w, x, y, rows, st);
+    default: *unsupported = true; return hipSuccess;
+  }
+}
+
+hipError_t launch_qmv(const QView& w, const float* x, float* y, uint32_t out_dim, uint32_t in_dim,
+                      hipStream_t st, bool* unsupported) {
+  *unsupported = false;
+  if (in_dim % kChunk) {
+    *unsupported = true;
+    return hipSuccess;
+  }
+  return w.bits == 4 ? qmv_bits<4>(w, x, y, out_dim, in_dim, st, unsupported)
+                     : qmv_bits<3>(w, x, y, out_dim, in_dim, st, unsupported);
+}
+
+// ---------------------------------------------------------------------------
+// Dequant probe: out[r, c] = fma(q, s, b) for rows [row0, row0 + n_rows).
+// ---------------------------------------------------------------------------
+template <int BITS>
+__global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ codes,
+                                                 const uint16_t* __restrict__ scales,
+                                                 const uint16_t* __restrict__ biases,
+                                                 uint32_t in_dim, uint32_t group, uint32_t row0,
+                                                 uint32_t n_rows, float* __restrict__ out) {
+  const uint32_t cpr = in_dim / kChunk;
+  const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (uint64_t)n_rows * cpr) return;
+  const uint32_t r = row0 + (uint32_t)(t / cpr), c = (uint32_t)(t % cpr);
+  const Raw<BITS> raw = load_raw<BITS>(codes + (size_t)r * cpr * chunk_bytes<BITS>() +
+                                       (size_t)c * chunk_bytes<BITS>());
+  const size_t gi = (size_t)r * (in_dim / group) + (size_t)c * kChunk / group;
+  const float s = bf16f(scales[gi]), b = bf16f(biases[gi]);
+  float* o = out + (size_t)(r - row0) * in_dim + (size_t)c * kChunk;
+#pragma unroll
+  for (int j = 0; j < kChunk; ++j) o[j] = __builtin_fmaf((float)code_at(raw, j), s, b);
+}
+
+hipError_t launch_dequant(const QView& w, uint32_t in_dim, uint32_t row0, uint32_t n_rows,
+                          float* out, hipStream_t st) {
+  const uint64_t n = (uint64_t)n_rows * (in_dim / kChunk);
+  const uint32_t blocks = (uint32_t)((n + 255) / 256);
+  if (w.bits == 4)
+    hipLaunchKernelGGL(k_dequant<4>, dim3(blocks), dim3(256), 0, st, w.codes, w.scales, w.biases,
+                       in_dim, w.group, row0, n_rows, out);
+  else
+    hipLaunchKernelGGL(k_dequant<3>, dim3(blocks), dim3(256), 0, st, w.codes, w.scales, w.biases,
+                       in_dim, w.group, row0, n_rows, out);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Argmax (first index on ties), one block.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ v, uint32_t n,
+                                                 int32_t* __restrict__ out) {
+  __shared__ float sv[16];
+  __shared__ uint32_t si[16];
+  float best = -INFINITY;
+  uint32_t bi = 0xFFFFFFFFu;
+  for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+    const float x = v[i];
+    if (x > best || bi == 0xFFFFFFFFu) {
+      if (bi == 0xFFFFFFFFu || x > best) {
+        best = x;
+        bi = i;
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ob = __shfl_xor(best, o, 64);
+    const uint32_t oi = __shfl_xor(bi, o, 64);
+    if (ob > best || (ob == best && oi < bi)) {
+      best = ob;
+      bi = oi;
+    }
+  }
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    sv[w] = best;
+    si[w] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < (int)(blockDim.x >> 6); ++i)
+      if (sv[i] > best || (sv[i] == best && si[i] < bi)) {
+        best = sv[i];
+        bi = si[i];
+      }
+    *out = (int32_t)bi;
+  }
+}
+
+hipError_t launch_argmax(const float* v, uint32_t n, int32_t* out, hipStream_t st) {
+  hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, st, v, n, out);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Router logits: one 256-thread block per (expert row, token); row
+// n_experts is the shared-expert gate when gate_w is not null.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_router_logits(const float* __restrict__ W,
+                                                       const float* __restrict__ gate_w,
+                                                       const float* __restrict__ x,
+                                                       uint32_t n_experts, uint32_t hidden,
+                                                       float* __restrict__ logits,
+                                                       float* __restrict__ gate_scores) {
+  __shared__ float red[4];
+  const uint32_t e = blockIdx.x, t = blockIdx.y;
+  const float* row = e < n_experts ? W + (size_t)e * hidden : gate_w;
+  const float* xt = x + (size_t)t * hidden;
+  float acc = 0.f;
+  for (uint32_t c = threadIdx.x * 4; c < hidden; c += 1024) {
+    const f32x4 w4 = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(row + c));
+    const float4 x4 = *reinterpret_cast<const float4*>(xt + c);
+    acc = __builtin_fmaf(w4.x, x4.x, acc);
+    acc = __builtin_fmaf(w4.y, x4.y, acc);
+    acc = __builtin_fmaf(w4.z, x4.z, acc);
+    acc = __builtin_fmaf(w4.w, x4.w, acc);
+  }
+  acc = group_sum<64>(acc);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const float s = (red[0] + red[1]) + (red[2] + red[3]);
+    if (e < n_experts)
+      logits[(size_t)t * n_experts + e] = s;
+    else
+      gate_scores[t] = s;
+  }
+}
+
+hipError_t launch_router_logits(const float* W, const float* gate_w, const float* x,
+                                uint32_t n_tokens, uint32_t n_experts, uint32_t hidden,
+                                float* logits, float* gate_scores, hipStream_t st) {
+  const uint32_t rows = n_experts + (gate_w ? 1 : 0);
+  hipLaunchKernelGGL(k_router_logits, dim3(rows, n_tokens), dim3(256), 0, st, W, gate_w, x,
+                     n_experts, hidden, logits, gate_scores);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Top-k: one wave per token. Lane l holds elements [l*P, l*P + P).
+// Slots live in lanes 0..k-1. The reference scans the scores in index
+// order and replaces the running-minimum slot (lowest slot on ties) with
+// every score strictly greater than it (moe_router.rs:83-124). Scores
+// that do not beat the current minimum can never beat a later one, so
+// the scan jumps straight to the next index whose score beats the
+// current minimum: a ballot over the lanes finds it.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t orderable(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+template <int P>
+__global__ __launch_bounds__(64) void k_topk(const float* __restrict__ scores, uint32_t n,
+                                             uint32_t k, int softmax, int normalize,
+                                             RouteOut out) {
+  const uint32_t t = blockIdx.x;
+  const int lane = threadIdx.x;
+  const float* s = scores + (size_t)t * n;
+  float v[P];
+#pragma unroll
+  for (int e = 0; e < P; ++e) {
+    const uint32_t j = lane * P + e;
+    v[e] = j < n ? s[j] : -INFINITY;
+  }
+  if (softmax) {
+    // moe_router.rs:52-72: max, exp(v - max), sum, * (1 / sum).
+    float m = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < P; ++e) m = fmaxf(m, v[e]);
+    m = wave_max(m);
+    float sum = 0.f;
+#pragma unroll
+    for (int e = 0; e < P; ++e) {
+      const uint32_t j = lane * P + e;
+      v[e] = j < n ? expf(v[e] - m) : 0.f;
+      sum += v[e];
+    }
+    sum = group_sum<64>(sum);
+    const float inv = 1.0f / sum;
+#pragma unroll
+    for (int e = 0; e < P; ++e) {
+      const uint32_t j = lane * P + e;
+      v[e] = j < n ? v[e] * inv : -INFINITY;
+    }
+  }
+  // Slot state (lane < k): value and index; other lanes hold +inf so they
+  // never become the minimum.
+  float sval = lane < (int)k ? -1e30f : INFINITY;
+  int32_t sidx = 0;
+  int32_t pos = -1;
+  while (true) {
+    // Minimum slot: smallest value, lowest slot on ties (slots in lanes 0..15).
+    uint64_t key = ((uint64_t)orderable(sval) << 32) | (uint32_t)lane;
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) {
+      const uint64_t other = __shfl_xor(key, o, 64);
+      key = other < key ? other : key;
+    }
+    key = __shfl(key, 0, 64);
+    const int mlane = (int)(key & 0xFFFFFFFFu);
+    const float mval = __shfl(sval, mlane, 64);
+    // First index > pos whose score beats the minimum.
+    int32_t cand = -1;
+    float cval = 0.f;
+#pragma unroll
+    for (int e = P - 1; e >= 0; --e) {
+      const int32_t j = lane * P + e;
+      if (j > pos && v[e] > mval) {
+        cand = j;
+        cval = v[e];
+      }
+    }
+    const uint64_t ball = __ballot(cand >= 0);
+    if (ball == 0) break;
+    const int first = __ffsll((unsigned long long)ball) - 1;
+    const int32_t j = __shfl(cand, first, 64);
+    const float pj = __shfl(cval, first, 64);
+    if (lane == mlane) {
+      sval = pj;
+      sidx = j;
+    }
+    pos = j;
+  }
+  // normalize_weights, moe_router.rs:130-141: sequential sum in slot order.
+  float w = sval;
+  if (normalize) {
+    float sum = 0.f;
+    for (uint32_t i = 0; i < k; ++i) sum += __shfl(sval, i, 64);
+    if (sum > 0.f) {
+      const float inv = 1.0f / sum;
+      w = sval * inv;
+    }
+  }
+  if (lane < (int)k) {
+    if (out.idx) out.idx[(size_t)t * k + lane] = sidx;
+    if (out.weight) out.weight[(size_t)t * k + lane] = w;
+    if (out.table && t == 0) {
+      out.table->blob[lane] = out.experts + (uint64_t)sidx * out.stride;
+      out.table->weight[lane] = w;
+    }
+  }
+  if (out.table && t == 0 && lane == 0) {
+    out.table->k = k;
+    out.table->has_shared = out.shared_blob != nullptr;
+    if (out.shared_blob) {
+      out.table->blob[k] = out.shared_blob;
+      out.table->weight[k] = 1.0f;
+      out.table->shared_gate = out.gate_scores ? out.gate_scores[0] : __builtin_nanf("");
+    }
+  }
+}
+
+hipError_t launch_topk(const float* scores, uint32_t n_tokens, uint32_t n, uint32_t k,
+                       bool softmax, bool normalize, const RouteOut& out, hipStream_t st) {
+  const uint32_t p = (n + 63) / 64;
+  const int sm = softmax, nm = normalize;
+  if (p <= 1)
+    hipLaunchKernelGGL(k_topk<1>, dim3(n_tokens), dim3(64), 0, st, scores, n, k, sm, nm, out);
+  else if (p <= 2)
+    hipLaunchKernelGGL(k_topk<2>, dim3(n_tokens), dim3(64), 0, st, scores, n, k, sm, nm, out);
+  else if (p <= 4)
+    hipLaunchKernelGGL(k_topk<4>, dim3(n_tokens), dim3(64), 0, st, scores, n, k, sm, nm, out);
+  else if (p <= 8)
+    hipLaunchKernelGGL(k_topk<8>, dim3(n_tokens), dim3(64), 0, st, scores, n, k, sm, nm, out);
+  else
+    hipLaunchKernelGGL(k_topk<16>, dim3(n_tokens), dim3(64), 0, st, scores, n, k, sm, nm, out);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Fused gate/up + SwiGLU.  CPR = hidden / 32. One block = one wave handling
+// RW rows (gate and up) of one slot; the block index enumerates
+// (slot, row tile), slots 0..k-1 routed, slot k the shared expert.
+// ---------------------------------------------------------------------------
+template <int BITS, int CPR, int P>
+__device__ __forceinline__ void gateup_body(const uint8_t* __restrict__ blob, const BlobGeom& g,
+                                            uint32_t row0, const float (&xr)[CPR < 64 ? 1 : CPR / 64][kChunk],
+                                            const float (&xs)[CPR < 64 ? 1 : CPR / 64],
+                                            float* __restrict__ act_slot) {
+  constexpr int L = CPR < kWave ? CPR : kWave;
+  constexpr int CPL = CPR / L;
+  constexpr int RPP = kWave / L;
+  constexpr int CB = chunk_bytes<BITS>();
+  constexpr uint32_t ROW_BYTES = CPR * CB;
+  const int lane = threadIdx.x & 63;
+  const int lrow = lane / L, lch = lane % L;
+  const uint32_t gpr = g.hidden / g.group;
+  const uint32_t cpg_shift = __builtin_ctz(g.group / kChunk);
+  const uint32_t inter = g.inter;
+
+  Raw<BITS> rg[P][CPL], ru[P][CPL];
+  float sg[P][CPL], bg[P][CPL], su[P][CPL], bu[P][CPL];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    uint32_t row = row0 + p * RPP + lrow;
+    row = row < inter ? row : inter - 1;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const uint32_t c = lch + L * i;
+      const size_t off = (size_t)row * ROW_BYTES + c * CB;
+      rg[p][i] = load_raw<BITS>(blob + g.w[0] + off);
+      ru[p][i] = load_raw<BITS>(blob + g.w[1] + off);
+      const size_t gi = ((size_t)row * gpr + (c >> cpg_shift)) * 2;
+      sg[p][i] = bf16f(*reinterpret_cast<const uint16_t*>(blob + g.s[0] + gi));
+      bg[p][i] = bf16f(*reinterpret_cast<const uint16_t*>(blob + g.b[0] + gi));
+      su[p][i] = bf16f(*reinterpret_cast<const uint16_t*>(blob + g.s[1] + gi));
+      bu[p][i] = bf16f(*reinterpret_cast<const uint16_t*>(blob + g.b[1] + gi));
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    float pg = 0.f, pu = 0.f;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      pg += chunk_dot<BITS>(rg[p][i], xr[i], xs[i], sg[p][i], bg[p][i]);
+      pu += chunk_dot<BITS>(ru[p][i], xr[i], xs[i], su[p][i], bu[p][i]);
+    }
+    const float gsum = group_sum<L>(pg);
+    const float usum = group_sum<L>(pu);
+    const uint32_t row = row0 + p * RPP + lrow;
+    if (lch == 0 && row < inter) act_slot[row] = silu_mul(gsum, usum);
+  }
+}
+
+template <int BITS, int CPR, int P>
+__global__ __launch_bounds__(64) void k_gateup(BlobGeom routed, BlobGeom shared,
+                                               const FfnTable* __restrict__ tab_dev,
+                                               FfnTable tab_val, uint32_t tiles_per_slot,
+                                               const float* __restrict__ x,
+                                               float* __restrict__ act) {
+  constexpr int L = CPR < kWave ? CPR : kWave;
+  constexpr int CPL = CPR / L;
+  constexpr int RPP = kWave / L;
+  constexpr uint32_t RW = RPP * P;  // rows per wave
+  const int lane = threadIdx.x & 63;
+  const int lch = lane % L;
+  const uint32_t slot = blockIdx.x / tiles_per_slot;
+  const uint32_t tile = blockIdx.x % tiles_per_slot;
+  const uint32_t k = tab_dev ? tab_dev->k : tab_val.k;
+  const uint8_t* blob = tab_dev ? tab_dev->blob[slot] : tab_val.blob[slot];
+
+  float xr[CPL][kChunk];
+  float xs[CPL];
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    load_x32(x + (size_t)(lch + L * i) * kChunk, xr[i]);
+    xs[i] = xsum(xr[i]);
+  }
+  const uint32_t row0 = tile * RW;
+  if (slot < k) {
+    if (row0 >= routed.inter) return;
+    gateup_body<BITS, CPR, P>(blob, routed, row0, xr, xs, act + (size_t)slot * routed.inter);
+  } else {
+    if (row0 >= shared.inter) return;
+    gateup_body<4, CPR, P>(blob, shared, row0, xr, xs, act + (size_t)slot * routed.inter);
+  }
+}
+
+template <int BITS, int CPR>
+static hipError_t gateup_inst(const BlobGeom& routed, const BlobGeom& shared,
+                              const FfnTable* tab_dev, const FfnTable& tab_val, uint32_t n_slots,
+                              const float* x, float* act, hipStream_t st) {
+  constexpr int L = CPR < kWave ? CPR : kWave;
+  constexpr int RPP = kWave / L;
+  constexpr int P = 4;
+  const uint32_t rw = RPP * P;
+  const uint32_t tiles = (routed.inter + rw - 1) / rw;
+  hipLaunchKernelGGL((k_gateup<BITS, CPR, P>), dim3(tiles * n_slots), dim3(64), 0, st, routed,
+                     shared, tab_dev, tab_val, tiles, x, act);
+  return hipGetLastError();
+}
+
+template <int BITS>
+static hipError_t gateup_bits(const BlobGeom& routed, const BlobGeom& shared,
+                              const FfnTable* tab_dev, const FfnTable& tab_val, uint32_t n_slots,
+                              const float* x, float* act, hipStream_t st, bool* unsupported) {
+  switch (routed.hidden / kChunk) {
+    case 32: return gateup_inst<BITS, 32>(routed, shared, tab_dev, tab_val, n_slots, x, act, st);
+    case 64: return gateup_inst<BITS, 64>(routed, shared, tab_dev, tab_val, n_slots, x, act, st);
+    case 128: return gateup_inst<BITS, 128>(routed, shared, tab_dev, tab_val, n_slots, x, act, st);
+    default: *unsupported = true; return hipSuccess;
+  }
+}
+
+hipError_t launch_gateup(const BlobGeom& routed, const BlobGeom& shared, const FfnTable* tab_dev,
+                         const FfnTable& tab_val, uint32_t n_slots, const float* x, float* act,
+                         hipStream_t st, bool* unsupported) {
+  *unsupported = false;
+  return routed.bits == 4
+             ? gateup_bits<4>(routed, shared, tab_dev, tab_val, n_slots, x, act, st, unsupported)
+             : gateup_bits<3>(routed, shared, tab_dev, tab_val, n_slots, x, act, st, unsupported);
+}
+
+// ---------------------------------------------------------------------------
+// Down + combine.  CPR = inter / 32. One wave = RPP output rows; it loads
+// every slot's chunk of those rows up front, then reduces slot by slot in
+// the reference's order: moe = fma(out_k, w_k, moe) (deferred.rs:458-466),
+// then the shared term and the residual.
+// ---------------------------------------------------------------------------
+template <int BITS, int CPR, int MAXS>
+__global__ __launch_bounds__(64) void k_down_combine(BlobGeom routed, BlobGeom shared,
+                                                     const FfnTable* __restrict__ tab_dev,
+                                                     FfnTable tab_val,
+                                                     const float* __restrict__ act,
+                                                     const float* __restrict__ h_mid,
+                                                     const float* __restrict__ shared_out,
+                                                     float* __restrict__ hidden_out) {
+  constexpr int L = CPR < kWave ? CPR : kWave;
+  constexpr int CPL = CPR / L;
+  constexpr int RPP = kWave / L;
+  constexpr int CB = chunk_bytes<BITS>();
+  constexpr int CB4 = chunk_bytes<4>();
+  constexpr uint32_t ROW_BYTES = CPR * CB;
+  constexpr uint32_t ROW_BYTES4 = CPR * CB4;
+  const int lane = threadIdx.x & 63;
+  const int lrow = lane / L, lch = lane % L;
+  const uint32_t H = routed.hidden, I = routed.inter;
+  const uint32_t gpr = I / routed.group;
+  const uint32_t cpg_shift = __builtin_ctz(routed.group / kChunk);
+  uint32_t row = blockIdx.x * RPP + lrow;
+  const bool valid = row < H;
+  row = valid ? row : H - 1;
+
+  const uint32_t k = tab_dev ? tab_dev->k : tab_val.k;
+  const uint32_t has_shared = tab_dev ? tab_dev->has_shared : tab_val.has_shared;
+
+  Raw<BITS> raw[MAXS][CPL];
+  Raw<4> rsh[CPL];
+  float sv[MAXS][CPL], bv[MAXS][CPL], ssh[CPL], bsh[CPL];
+#pragma unroll
+  for (int s = 0; s < MAXS; ++s) {
+    if (s < (int)k) {
+      const uint8_t* blob = tab_dev ? tab_dev->blob[s] : tab_val.blob[s];
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const uint32_t c = lch + L * i;
+        raw[s][i] = load_raw<BITS>(blob + routed.w[2] + (size_t)row * ROW_BYTES + c * CB);
+        const size_t gi = ((size_t)row * gpr + (c >> cpg_shift)) * 2;
+        sv[s][i] = bf16f(*reinterpret_cast<const uint16_t*>(blob + routed.s[2] + gi));
+        bv[s][i] = bf16f(*reinterpret_cast<const uint16_t*>(blob + routed.b[2] + gi));
+      }
+    }
+  }
+  if (has_shared) {
+    const uint8_t* blob = tab_dev ? tab_dev->blob[k] : tab_val.blob[k];
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const uint32_t c = lch + L * i;
+      rsh[i] = load_raw<4>(blob + shared.w[2] + (size_t)row * ROW_BYTES4 + c * CB4);
+      const size_t gi = ((size_t)row * gpr + (c >> cpg_shift)) * 2;
+      ssh[i] = bf16f(*reinterpret_cast<const uint16_t*>(blob + shared.s[2] + gi));
+      bsh[i] = bf16f(*reinterpret_cast<const uint16_t*>(blob + shared.b[2] + gi));
+    }
+  }
+
+  float moe = 0.f;
+#pragma unroll
+  for (int s = 0; s < MAXS; ++s) {
+    if (s < (int)k) {
+      float part = 0.f;
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        float a[kChunk];
+        load_x32(act + (size_t)s * I + (size_t)(lch + L * i) * kChunk, a);
+        part += chunk_dot<BITS>(raw[s][i], a, xsum(a), sv[s][i], bv[s][i]);
+      }
+      const float o = group_sum<L>(part);
+      const float w = tab_dev ? tab_dev->weight[s] : tab_val.weight[s];
+      moe = __builtin_fmaf(o, w, moe);
+    }
+  }
+  float res;
+  if (has_shared) {
+    float part = 0.f;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      float a[kChunk];
+      load_x32(act + (size_t)k * I + (size_t)(lch + L * i) * kChunk, a);
+      part += chunk_dot<4>(rsh[i], a, xsum(a), ssh[i], bsh[i]);
+    }
+    const float sh = group_sum<L>(part);
+    const float gate = tab_dev ? tab_dev->shared_gate : tab_val.shared_gate;
+    const float sum = __builtin_isnan(gate) ? moe + sh : __builtin_fmaf(sh, sigmoidf_ref(gate), moe);
+    res = h_mid[row] + sum;
+  } else if (shared_out) {
+    const float gate = tab_dev ? tab_dev->shared_gate : tab_val.shared_gate;
+    const float sh = shared_out[row];
+    const float sum = __builtin_isnan(gate) ? moe + sh : __builtin_fmaf(sh, sigmoidf_ref(gate), moe);
+    res = h_mid[row] + sum;
+  } else {
+    res = h_mid[row] + moe;
+  }
+  if (lch == 0 && valid) hidden_out[row] = res;
+}
+
+template <int BITS, int CPR>
+static hipError_t down_inst(const BlobGeom& routed, const BlobGeom& shared,
+                            const FfnTable* tab_dev, const FfnTable& tab_val, uint32_t k,
+                            const float* act, const float* h_mid, const float* shared_out,
+                            float* hidden_out, hipStream_t st) {
+  constexpr int L = CPR < kWave ? CPR : kWave;
+  constexpr int RPP = kWave / L;
+  const uint32_t blocks = (routed.hidden + RPP - 1) / RPP;
+  if (k <= 8)
+    hipLaunchKernelGGL((k_down_combine<BITS, CPR, 8>), dim3(blocks), dim3(64), 0, st, routed,
+                       shared, tab_dev, tab_val, act, h_mid, shared_out, hidden_out);
+  else
+    hipLaunchKernelGGL((k_down_combine<BITS, CPR, 16>), dim3(blocks), dim3(64), 0, st, routed,
+                       shared, tab_dev, tab_val, act, h_mid, shared_out, hidden_out);
+  return hipGetLastError();
+}
+
+template <int BITS>
+static hipError_t down_bits(const BlobGeom& routed, const BlobGeom& shared,
+                            const FfnTable* tab_dev, const FfnTable& tab_val, uint32_t k,
+                            const float* act, const float* h_mid, const float* shared_out,
+                            float* hidden_out, hipStream_t st, bool* unsupported) {
+  switch (routed.inter / kChunk) {
+    case 8: return down_inst<BITS, 8>(routed, shared, tab_dev, tab_val, k, act, h_mid, shared_out, hidden_out, st);
+    case 16: return down_inst<BITS, 16>(routed, shared, tab_dev, tab_val, k, act, h_mid, shared_out, hidden_out, st);
+    case 32: return down_inst<BITS, 32>(routed, shared, tab_dev, tab_val, k, act, h_mid, shared_out, hidden_out, st);
+    case 64: return down_inst<BITS, 64>(routed, shared, tab_dev, tab_val, k, act, h_mid, shared_out, hidden_out, st);
+    default: *unsupported = true; return hipSuccess;
+  }
+}
+
+hipError_t launch_down_combine(const BlobGeom& routed, const BlobGeom& shared,
+                               const FfnTable* tab_dev, const FfnTable& tab_val, uint32_t n_slots,
+                               const float* act, const float* h_mid, const float* shared_out,
+                               float* hidden_out, hipStream_t st, bool* unsupported) {
+  *unsupported = false;
+  (void)n_slots;
+  const uint32_t k = tab_val.k;
+  return routed.bits == 4 ? down_bits<4>(routed, shared, tab_dev, tab_val, k, act, h_mid,
+                                         shared_out, hidden_out, st, unsupported)
+                          : down_bits<3>(routed, shared, tab_dev, tab_val, k, act, h_mid,
+                                         shared_out, hidden_out, st, unsupported);
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm with bf16 weights (rms_norm_bf16_n_tokens_cpu, backend/cpu/mod.rs:
+// 406-430; GPU rms_norm_sum_sq + rms_norm_apply_bf16, shaders.metal:
+// 1454-1530), or a copy when w is null. One block.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(1024) void k_rmsnorm(const float* __restrict__ r,
+                                                  const uint16_t* __restrict__ w, float eps,
+                                                  uint32_t dim, float* __restrict__ x) {
+  __shared__ float red[16];
+  __shared__ float inv_sh;
+  if (w) {
+    float acc = 0.f;
+    for (uint32_t i = threadIdx.x; i < dim; i += blockDim.x) acc += r[i] * r[i];
+    acc = group_sum<64>(acc);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float s = 0.f;
+      for (uint32_t i = 0; i < (blockDim.x >> 6); ++i) s += red[i];
+      inv_sh = 1.0f / sqrtf(s / (float)dim + eps);
+    }
+    __syncthreads();
+    const float inv = inv_sh;
+    for (uint32_t i = threadIdx.x; i < dim; i += blockDim.x) x[i] = r[i] * inv * bf16f(w[i]);
+  } else {
+    for (uint32_t i = threadIdx.x; i < dim; i += blockDim.x) x[i] = r[i];
+  }
+}
+
+hipError_t launch_rmsnorm(const float* r, const uint16_t* w, float eps, uint32_t dim, float* x_out,
+                          hipStream_t st) {
+  hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(1024), 0, st, r, w, eps, dim, x_out);
+  return hipGetLastError();
+}
+
+}  // namespace smoe

@@ -1,0 +1,358 @@
+"""GPU parity of the decode path against the CPU oracle, through the C ABI.
+
+Bars: dequantized values and top-k indices
+bit-exact; matvec / expert outputs within max relative error 1e-3 under
+fp32 accumulation, measured as max|got - want| / max|want| (the
+reference's metric, crates/streammoe/tests/group32_kernels.rs:141-150).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from helpers import expert_pair, gen_expert_blob, gen_quant_matrix, rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3  # max relative error, fp32 accumulation
+
+
+def _torch():
+    import torch
+
+    return torch
+
+
+def dev(a):
+    torch = _torch()
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+
+
+def host(t):
+    _torch().cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def pack_matrix(codes, scales, biases):
+    """One device buffer [codes | scales | biases] with 256-byte aligned regions."""
+    def pad(n):
+        return (n + 255) // 256 * 256
+
+    c = codes.ravel().view(np.uint8)
+    s = scales.ravel().view(np.uint8)
+    b = biases.ravel().view(np.uint8)
+    so = pad(c.size)
+    bo = so + pad(s.size)
+    buf = np.zeros(bo + pad(b.size), np.uint8)
+    buf[:c.size] = c
+    buf[so:so + s.size] = s
+    buf[bo:bo + b.size] = b
+    return dev(buf), 0, so, bo
+
+
+def qweights(codes, scales, biases, group, bits):
+    import streamoe_amd as sa
+
+    buf, po, so, bo = pack_matrix(codes, scales, biases)
+    return sa.QuantWeights(buf, po, so, bo, group, bits)
+
+
+def oracle_matvec(codes, scales, biases, in_dim, out_dim, group, bits, x):
+    if bits == 3:
+        words = np.zeros(out_dim * in_dim // 8, np.uint32)
+        c3 = codes.reshape(-1, 3).astype(np.uint32)
+        p = c3[:, 0] | (c3[:, 1] << 8) | (c3[:, 2] << 16)
+        for i in range(8):
+            words |= ((p >> np.uint32(3 * i)) & np.uint32(7)) << np.uint32(4 * i)
+        packed = words
+    else:
+        packed = codes.view(np.uint32)
+    rc, y = oracle.dequant_matvec_4bit_gs(packed, scales, biases, in_dim, out_dim, group, x)
+    assert rc == 0
+    return y, packed
+
+
+# --- qmv --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("out_dim,in_dim,group,bits", [
+    (512, 2048, 64, 4), (2048, 512, 64, 4), (1000, 1024, 32, 4), (77, 4096, 128, 4),
+    (512, 2048, 64, 3), (2048, 512, 64, 3), (333, 8192, 64, 4), (5, 2048, 64, 4),
+])
+def test_qmv_matches_oracle(kernels, out_dim, in_dim, group, bits):
+    rng = np.random.default_rng(out_dim * 7 + in_dim + bits)
+    codes, s, b = gen_quant_matrix(rng, out_dim, in_dim, group, bits)
+    x = rng.standard_normal(in_dim).astype(np.float32)
+    w = qweights(codes, s, b, group, bits)
+    torch = _torch()
+    y = torch.empty(out_dim, dtype=torch.float32, device="cuda")
+    assert kernels.qmv(w, dev(x), y, out_dim, in_dim) == 0
+    want, _ = oracle_matvec(codes, s, b, in_dim, out_dim, group, bits, x)
+    err = rel_err(host(y), want)
+    print(f"qmv {out_dim}x{in_dim} g{group} {bits}-bit rel_err={err:.3e}")
+    assert err <= TOL
+
+
+def test_lm_head_qwen3_shape_and_argmax(kernels):
+    """Config 1: 151,936 x 2048 4-bit g64 LM head; greedy argmax bit-exact."""
+    V, H, G = 151936, 2048, 64
+    rng = np.random.default_rng(0xC1)
+    codes, s, b = gen_quant_matrix(rng, V, H, G, 4)
+    x = rng.standard_normal(H).astype(np.float32)
+    w = qweights(codes, s, b, G, 4)
+    torch = _torch()
+    y = torch.empty(V, dtype=torch.float32, device="cuda")
+    am = torch.empty(1, dtype=torch.int32, device="cuda")
+    assert kernels.qmv(w, dev(x), y, V, H) == 0
+    assert kernels.argmax(y, V, am) == 0
+    want, _ = oracle_matvec(codes, s, b, H, V, G, 4, x)
+    got = host(y)
+    err = rel_err(got, want)
+    top2 = np.sort(want)[-2:]
+    print(f"lm_head rel_err={err:.3e} argmax gpu={int(host(am)[0])} cpu={oracle.argmax(want)} "
+          f"gap={top2[1] - top2[0]:.3e} max|d|={np.max(np.abs(got - want)):.3e}")
+    assert err <= TOL
+    # The gap between the top two logits exceeds twice the largest deviation,
+    # so the argmax cannot flip: the certified comparison is exact equality.
+    assert top2[1] - top2[0] > 2 * np.max(np.abs(got - want))
+    assert int(host(am)[0]) == oracle.argmax(want)
+
+
+# --- dequant (bit-exact) --------------------------------------------------------------
+
+@pytest.mark.parametrize("bits,group", [(4, 64), (3, 64), (4, 32), (3, 128)])
+def test_dequant_bit_exact(kernels, bits, group):
+    rng = np.random.default_rng(bits * 100 + group)
+    out_dim, in_dim = 64, 1024
+    codes, s, b = gen_quant_matrix(rng, out_dim, in_dim, group, bits)
+    w = qweights(codes, s, b, group, bits)
+    torch = _torch()
+    out = torch.empty((out_dim - 3, in_dim), dtype=torch.float32, device="cuda")
+    assert kernels.dequant(w, in_dim, 3, out_dim - 3, out) == 0
+    _, packed = oracle_matvec(codes, s, b, in_dim, out_dim, group, bits, np.zeros(in_dim, np.float32))
+    want = oracle.dequant_4bit(packed, s, b, in_dim, out_dim, group)[3:]
+    assert np.array_equal(host(out).view(np.uint32), want.view(np.uint32))
+
+
+# --- router -----------------------------------------------------------------------------
+
+def test_topk_bit_exact_on_identical_scores(kernels):
+    """Given the same scores the device top-k reproduces the reference's
+    slot order and values bit for bit, including ties."""
+    torch = _torch()
+    cases = [
+        ([0.1, 0.5, 0.3, 0.9, 0.2], 3),
+        ([1.0, 1.0, 1.0, 1.0], 2),
+        ([2.0, 1.0, 1.0, 3.0], 2),
+        ([1.0, 1.0, 2.0], 2),
+        ([5.0, 4.0, 3.0, 2.0, 1.0], 5),
+        (list(np.arange(300, dtype=np.float32)), 16),        # every index is an event
+        (list(np.arange(300, dtype=np.float32)[::-1]), 16),  # no events after the first k
+        ([-1e31, -2e31, 5.0, -1e31], 2),                     # scores below the -1e30 start
+    ]
+    rng = np.random.default_rng(3)
+    for n in (64, 256, 1024):
+        v = rng.standard_normal(n).astype(np.float32)
+        v[rng.integers(0, n, n // 4)] = 0.25  # many exact ties
+        cases.append((list(v), 8))
+    for scores, k in cases:
+        sc = np.array(scores, np.float32)
+        idx = torch.empty(k, dtype=torch.int32, device="cuda")
+        val = torch.empty(k, dtype=torch.float32, device="cuda")
+        assert kernels.topk(dev(sc), 1, sc.size, k, idx, val) == 0
+        rc, widx, wval = oracle.topk(sc, k)
+        assert rc == 0
+        assert np.array_equal(host(idx), widx), (scores[:8], k)
+        assert np.array_equal(host(val).view(np.uint32), wval.view(np.uint32))
+
+
+@pytest.mark.parametrize("n_tokens,E,k,normalize", [(1, 256, 8, True), (8, 256, 8, True), (64, 64, 8, False),
+                                                      (32, 512, 10, True), (4, 1024, 16, True)])
+def test_router_matches_oracle(kernels, n_tokens, E, k, normalize):
+    """f32 router GEMV + softmax + top-k (+ renorm) per token. Index sets
+    and slot order equal the oracle whenever the k-th / (k+1)-th probability
+    gap exceeds the logit deviation (reported); weights within 1e-5."""
+    torch = _torch()
+    H = 2048
+    rng = np.random.default_rng(E * 31 + n_tokens)
+    W = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
+    X = rng.standard_normal((n_tokens, H)).astype(np.float32)
+    idx = torch.empty((n_tokens, k), dtype=torch.int32, device="cuda")
+    w = torch.empty((n_tokens, k), dtype=torch.float32, device="cuda")
+    logits = torch.empty((n_tokens, E), dtype=torch.float32, device="cuda")
+    assert kernels.router(dev(W), dev(X), n_tokens, E, H, k, normalize, idx, w, logits) == 0
+    gi, gw, gl = host(idx), host(w), host(logits)
+    for t in range(n_tokens):
+        lg = oracle.f32_matvec(W, X[t])
+        assert rel_err(gl[t], lg) < 1e-5
+        probs = oracle.softmax(lg)
+        srt = np.sort(probs)[::-1]
+        gap = srt[k - 1] - srt[k]
+        _, widx, ww = oracle.router(lg, k, normalize)
+        if gap > 1e-5 * srt[0]:
+            assert np.array_equal(gi[t], widx), (t, gap)
+            assert np.max(np.abs(gw[t] - ww)) <= 1e-5 * np.max(np.abs(ww))
+        print(f"router t={t} gap={gap:.3e} match={np.array_equal(gi[t], widx)}")
+
+
+def test_softmax_topk_from_oracle_logits(kernels):
+    """Same logits on both sides: the device softmax differs from libm's
+    by ULPs only, so indices match and weights agree to 1e-6."""
+    torch = _torch()
+    rng = np.random.default_rng(17)
+    E, k, T = 256, 8, 16
+    L = rng.standard_normal((T, E)).astype(np.float32)
+    idx = torch.empty((T, k), dtype=torch.int32, device="cuda")
+    w = torch.empty((T, k), dtype=torch.float32, device="cuda")
+    assert kernels.softmax_topk(dev(L), T, E, k, True, idx, w) == 0
+    gi, gw = host(idx), host(w)
+    for t in range(T):
+        _, widx, ww = oracle.router(L[t], k, True)
+        assert np.array_equal(gi[t], widx)
+        assert np.max(np.abs(gw[t] - ww)) <= 1e-6
+
+
+# --- K-expert decode (bindings API) ----------------------------------------------------
+
+def _experts_case(kernels, H, I, k, bits, with_shared, seed):
+    torch = _torch()
+    rng = np.random.default_rng(seed)
+    blobs = [gen_expert_blob(rng, H, I, 64, bits) for _ in range(k)]
+    arena = dev(np.concatenate(blobs))
+    import streamoe_amd as sa
+
+    lay = sa.ExpertLayout(H, I, bits, 64)
+    x = rng.standard_normal(H).astype(np.float32)
+    h_mid = rng.standard_normal(H).astype(np.float32)
+    shared = (0.1 * rng.standard_normal(H)).astype(np.float32) if with_shared else None
+    wts = (rng.random(k) + 0.1).astype(np.float32)
+    score = 0.3
+    out = torch.empty(H, dtype=torch.float32, device="cuda")
+    rc = kernels.experts_decode(lay, [(arena, s * lay.expert_size) for s in range(k)], list(wts), dev(x),
+                                dev(h_mid), None if shared is None else dev(shared), score, out)
+    assert rc == 0
+    outs = np.stack([oracle.expert_swiglu(b, bits, H, I, 64, x) for b in blobs])
+    want = oracle.combine(outs, wts, h_mid, shared, score if with_shared else float("nan"))
+    return host(out), want
+
+
+@pytest.mark.parametrize("H,I,k,bits,shared", [
+    (2048, 512, 8, 4, True),    # Qwen3.6-A3B
+    (2048, 1024, 8, 4, False),  # OLMoE
+    (2048, 512, 8, 3, True),    # packed 3-bit
+    (2048, 512, 16, 4, True),   # MAX_K
+    (2048, 512, 1, 4, False),
+    (4096, 1024, 10, 4, True),
+    (1024, 256, 4, 3, False),
+])
+def test_experts_decode_matches_oracle(kernels, H, I, k, bits, shared):
+    got, want = _experts_case(kernels, H, I, k, bits, shared, seed=H + I + k + bits)
+    # The expert outputs are small next to h_mid; compare the MoE part too.
+    err = rel_err(got, want)
+    print(f"experts H={H} I={I} k={k} {bits}-bit rel_err={err:.3e}")
+    assert err <= TOL
+
+
+def test_packed_3bit_bit_identical_to_nibbles(kernels):
+    """tests/packed_3bit.rs:65-106: the K-expert decode on packed 3-bit
+    equals the same codes stored as 4-bit nibbles, bit for bit (seed
+    0x3B17_DEC0_0001, A3B shapes, k = 8)."""
+    import streamoe_amd as sa
+
+    rng = oracle.XorShift64s(0x3B17DEC00001)
+    k = 8
+    nib, packed = [], []
+    for _ in range(k):
+        a, b = expert_pair(rng)
+        nib.append(a)
+        packed.append(b)
+    h_post = rng.unit(2048)
+    h_mid = rng.unit(2048)
+    shared_out = (np.float32(0.1) * rng.unit(2048)).astype(np.float32)
+    weights = [np.float32(1.0) / np.float32(i + 2) for i in range(k)]
+    payload = sa.ExpertPayload(h_post, h_mid, shared_out, weights, 0.3)
+    a = sa.gpu_batched_experts_forward(kernels, sa.ExpertLayout(2048, 512, 4, 64), k, np.concatenate(nib), payload)
+    b = sa.gpu_batched_experts_forward(kernels, sa.ExpertLayout(2048, 512, 3, 64), k, np.concatenate(packed), payload)
+    assert np.any(a != 0) and np.all(np.isfinite(a))
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    # And both match the CPU path.
+    outs = np.stack([oracle.expert_swiglu(n, 4, 2048, 512, 64, h_post) for n in nib])
+    want = oracle.combine(outs, np.array(weights, np.float32), h_mid, shared_out, 0.3)
+    assert rel_err(a, want) <= TOL
+
+
+def test_experts_decode_argument_errors(kernels):
+    import streamoe_amd as sa
+    from streamoe_amd import _abi
+
+    torch = _torch()
+    buf = torch.zeros(4 << 20, dtype=torch.uint8, device="cuda")
+    x = torch.zeros(2048, dtype=torch.float32, device="cuda")
+    lay = sa.ExpertLayout(2048, 512, 4, 64)
+    ok = [(buf, 0)]
+    assert kernels.experts_decode(lay, [], [], x, x, None, 0.0, x) == _abi.CODES["SMOE_ERR_BAD_K"]
+    assert kernels.experts_decode(lay, ok * 17, [1.0] * 17, x, x, None, 0.0, x) == _abi.CODES["SMOE_ERR_BAD_K"]
+    assert kernels.experts_decode(lay, [(buf, 8)], [1.0], x, x, None, 0.0, x) == _abi.CODES["SMOE_ERR_MISALIGNED"]
+    assert kernels.experts_decode(sa.ExpertLayout(2048, 512, 5, 64), ok, [1.0], x, x, None, 0.0, x) == \
+        _abi.CODES["SMOE_ERR_UNSUPPORTED_BITS"]
+    assert kernels.experts_decode(sa.ExpertLayout(2048, 512, 4, 48), ok, [1.0], x, x, None, 0.0, x) == \
+        _abi.CODES["SMOE_ERR_UNSUPPORTED_GROUP"]
+    assert kernels.experts_decode(sa.ExpertLayout(2048, 500, 4, 64), ok, [1.0], x, x, None, 0.0, x) == \
+        _abi.CODES["SMOE_ERR_IN_DIM_NOT_MULTIPLE"]
+    w = sa.QuantWeights(buf, 0, 4096, 8192, 64, 4)
+    assert kernels.qmv(w, x, x, 10, 2000) == _abi.CODES["SMOE_ERR_IN_DIM_NOT_MULTIPLE"]
+    w = sa.QuantWeights(buf, 4, 4096, 8192, 64, 4)
+    assert kernels.qmv(w, x, x, 10, 2048) == _abi.CODES["SMOE_ERR_MISALIGNED"]
+    idx = torch.zeros(32, dtype=torch.int32, device="cuda")
+    assert kernels.topk(x, 1, 8, 9, idx, x) == _abi.CODES["SMOE_ERR_BAD_K"]
+    torch.cuda.synchronize()
+
+
+# --- one resident layer with device routing ---------------------------------------------
+
+def _layer_case(kernels, H, I, E, k, bits, normalize, shared, seed):
+    """Returns (gpu hidden, gpu idx, gpu w, oracle hidden, oracle idx, oracle w, gap)."""
+    import streamoe_amd as sa
+
+    torch = _torch()
+    lay = sa.ExpertLayout(H, I, bits, 64)
+    stride = lay.expert_size
+    arena = torch.empty(E * stride, dtype=torch.uint8, device="cuda")
+    assert kernels.synth_experts(arena, E, stride, lay, seed) == 0
+    router_w = torch.empty((E, H), dtype=torch.float32, device="cuda")
+    assert kernels.synth_normal_f32(router_w, seed + 1, 0.02) == 0
+    x = torch.empty(H, dtype=torch.float32, device="cuda")
+    assert kernels.synth_normal_f32(x, seed + 2, 1.0) == 0
+    h_mid = torch.empty(H, dtype=torch.float32, device="cuda")
+    assert kernels.synth_normal_f32(h_mid, seed + 3, 1.0) == 0
+    sh_blob = sh_gate = None
+    if shared:
+        slay = sa.ExpertLayout(H, I, 4, 64)
+        sh_blob = torch.empty(slay.expert_size, dtype=torch.uint8, device="cuda")
+        assert kernels.synth_experts(sh_blob, 1, slay.expert_size, slay, seed + 4) == 0
+        sh_gate = torch.empty(H, dtype=torch.float32, device="cuda")
+        assert kernels.synth_normal_f32(sh_gate, seed + 5, 0.02) == 0
+    L = kernels.layer(lay, arena, stride, E, k, normalize, router_w, sh_blob, sh_gate)
+    out = torch.empty(H, dtype=torch.float32, device="cuda")
+    idx = torch.empty(k, dtype=torch.int32, device="cuda")
+    w = torch.empty(k, dtype=torch.float32, device="cuda")
+    assert kernels.moe_decode_layer(L, x, h_mid, out, idx, w) == 0
+    experts_h = host(arena)
+    oh, oi, ow, logits = oracle.moe_decode_layer(experts_h, stride, H, I, E, k, 64, bits, normalize, host(router_w),
+                                                 host(x), host(h_mid), None if sh_blob is None else host(sh_blob),
+                                                 None if sh_gate is None else host(sh_gate))
+    p = np.sort(oracle.softmax(logits))[::-1]
+    return host(out), host(idx), host(w), oh, oi, ow, p[k - 1] - p[k]
+
+
+@pytest.mark.parametrize("name,H,I,E,k,bits,normalize,shared", [
+    ("olmoe", 2048, 1024, 64, 8, 4, False, False),   # config 0
+    ("a3b", 2048, 512, 256, 8, 4, True, True),       # config 2
+    ("a3b-3bit", 2048, 512, 256, 8, 3, True, True),  # config 3
+    ("k16", 2048, 512, 128, 16, 4, True, True),
+])
+def test_moe_decode_layer_matches_oracle(kernels, name, H, I, E, k, bits, normalize, shared):
+    got, gi, gw, want, wi, ww, gap = _layer_case(kernels, H, I, E, k, bits, normalize, shared, seed=hash(name) & 0xFFFF)
+    err = rel_err(got, want)
+    print(f"layer {name}: idx gpu={list(gi)} cpu={list(wi)} gap={gap:.3e} rel_err={err:.3e}")
+    assert np.array_equal(gi, wi)
+    assert np.max(np.abs(gw - ww)) <= 1e-5 * np.max(np.abs(ww))
+    assert err <= TOL
