@@ -7,7 +7,9 @@ intermediate 512, one always-on 4-bit shared expert with a sigmoid gate,
 affine 4-bit g64 weights (codes uniform, scales bf16 |N(0,.02)|, biases
 bf16 N(0,.01)), f32 router N(0,.02), residual stream N(0,1). Between
 layers the next input is RMSNorm(residual) (unit bf16 weights). One step
-= one token through the 40 layers, replayed from a captured HIP graph.
+= one token through the 40 layers: one persistent launch (the default
+decode path), or one kernel per phase replayed from a HIP graph
+(--path kernels --graph).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2]
 
@@ -79,6 +81,45 @@ def cpu_baseline_decode(c, arena_l0, router_l0, shared_l0, gate_l0, x, seconds):
                        f"oracle/oracle.c on {th} threads")
 
 
+def _sync_status(kern):
+    import streamoe_amd as sa
+
+    return sa._lib.smoe_sync(kern.h)
+
+
+def trace_phases(kern, step, nl, nb=256):
+    """Per-block phase timestamps of the persistent decode (100 MHz
+    s_memrealtime ticks) from one traced step, summarised over layers
+    1..nl-1 in microseconds: mean per-phase durations, and for each handoff
+    the gap between the LAST producer and the FIRST consumer."""
+    import numpy as np
+    import torch
+
+    from streamoe_amd import _abi
+
+    buf = torch.zeros(nl * nb * 8 + nl * 2, dtype=torch.int64, device="cuda")
+    kern.set_option(_abi.SMOE_OPT_TRACE_BUFFER, buf.data_ptr())
+    step()
+    torch.cuda.synchronize()
+    kern.set_option(_abi.SMOE_OPT_TRACE_BUFFER, 0)
+    t = buf.cpu().numpy().astype(np.int64)[:nl * nb * 8].reshape(nl, nb, 8).astype(np.float64) * 0.01
+    if not t.any():
+        return None
+    L = slice(1, nl)
+    d = lambda a, b: round(float((t[L, :, b] - t[L, :, a]).mean()), 3)
+    out = {
+        "x_ready": d(0, 1), "router": d(1, 2), "logits_to_set": d(2, 3), "issue_loads": d(3, 7),
+        "gateup": d(7, 4), "act_wait": d(4, 5), "down_combine": d(5, 6),
+        "layer": round(float(np.diff(t[:, 0, 0])[1:].mean()), 3),
+        "logits_last_pub_to_first_set": round(float((t[L, :, 3].min(1) - t[L, :, 2].max(1)).mean()), 3),
+        "act_last_pub_to_first_ready": round(float((t[L, :, 5].min(1) - t[L, :, 4].max(1)).mean()), 3),
+        "hidden_last_pub_to_first_x": round(float((t[2:, :, 1].min(1) - t[1:-1, :, 6].max(1)).mean()), 3),
+        "spread_gateup_done": round(float((t[L, :, 4].max(1) - t[L, :, 4].min(1)).mean()), 3),
+        "spread_set_ready": round(float((t[L, :, 3].max(1) - t[L, :, 3].min(1)).mean()), 3),
+    }
+    return out
+
+
 def run_decode(args, c):
     import numpy as np
     import torch
@@ -116,12 +157,14 @@ def run_decode(args, c):
     work = torch.empty(H, dtype=torch.float32, device=dev)
     torch.cuda.synchronize()
 
+    kern.set_decode_path({"auto": 0, "kernels": 1, "persistent": 2}[args.path])
+
     def step():
         sa.check(kern.moe_decode_layers(layers, norms, 1e-6, x0, resid, work), "smoe_moe_decode_layers")
 
     stream = torch.cuda.current_stream(dev)
     graph = None
-    if not args.no_graph:
+    if args.graph:
         side = torch.cuda.Stream(dev)
         side.wait_stream(stream)
         with torch.cuda.stream(side):
@@ -152,7 +195,11 @@ def run_decode(args, c):
     ms = e0.elapsed_time(e1)
     ms_per_step = ms / args.steps
     us_layer = ms_per_step * 1e3 / nl
+    sa.check(_sync_status(kern), "smoe_sync")
     assert torch.isfinite(resid).all(), "residual stream is not finite"
+    phases = None
+    if args.trace:
+        phases = trace_phases(kern, step, nl)
 
     nbytes = layer_bytes(c)
     achieved = nbytes / (us_layer * 1e-6) / 1e9
@@ -179,6 +226,8 @@ def run_decode(args, c):
                      "unit_of_work": f"one layer: {nbytes} algorithmic bytes", "kernel": "decode layer (all launches)"},
         "wall_s": round(wall, 3),
     }
+    if phases:
+        out["phases_us"] = phases
     if not args.no_cpu:
         a0 = arenas[0].cpu().numpy()
         r0 = routers[0].cpu().numpy()
@@ -196,7 +245,9 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
-    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--path", default="auto", choices=["auto", "kernels", "persistent"])
+    ap.add_argument("--graph", action="store_true", help="replay the step from a HIP graph (per-phase path)")
+    ap.add_argument("--trace", action="store_true", help="report per-phase times of the persistent decode")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     args = ap.parse_args()

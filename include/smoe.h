@@ -56,8 +56,16 @@ typedef enum {
   SMOE_ERR_SCRATCH_TOO_SMALL = 8,   /* shapes exceed the reserved scratch; call smoe_reserve */
   SMOE_ERR_WORKSPACE_TOO_SMALL = 9, /* caller workspace smaller than *_workspace_size */
   SMOE_ERR_HIP = 10,                /* a HIP runtime call failed (launch, memset, sync) */
-  SMOE_ERR_NO_DEVICE = 11           /* no gfx950 device at that ordinal */
+  SMOE_ERR_NO_DEVICE = 11,          /* no gfx950 device at that ordinal */
+  SMOE_ERR_DEVICE_TIMEOUT = 12      /* a bounded device-side wait expired; outputs are invalid */
 } smoe_status;
+
+/* Handle options (smoe_set_option). */
+typedef enum {
+  SMOE_OPT_DECODE_PATH = 1,  /* 0 auto (default), 1 one kernel per phase, 2 persistent */
+  SMOE_OPT_TRACE_BUFFER = 2  /* device uint64 buffer for per-phase timestamps of the
+                                persistent decode (10 per layer), or 0 = off */
+} smoe_option;
 
 typedef struct smoe_handle smoe_handle;
 
@@ -89,9 +97,15 @@ int smoe_set_stream(smoe_handle* h, void* stream);
  * SMOE_ERR_SCRATCH_TOO_SMALL from the compute entry points. */
 int smoe_reserve(smoe_handle* h, uint32_t max_hidden, uint32_t max_inter, uint32_t max_experts);
 
-/* Block until all work enqueued on the handle's stream has finished.
- * Replaces MetalContext::commit_and_wait_labeled's wait. */
+/* Block until all work enqueued on the handle's stream has finished, then
+ * report (and clear) a device-side timeout of the persistent decode.
+ * Replaces MetalContext::commit_and_wait_labeled's wait and its
+ * command-buffer error check (backend/gpu/metal.rs:343-440). */
 int smoe_sync(smoe_handle* h);
+
+/* Set a handle option (smoe_option). No counterpart in the reference: the
+ * decode-path choice and the phase trace are testing and tuning knobs. */
+int smoe_set_option(smoe_handle* h, int option, int64_t value);
 
 /* ------------------------------------------------------------------ */
 /* Quantized weights and dense quantized matvec (qmv)                  */
@@ -216,7 +230,10 @@ typedef struct {
 } smoe_layer;
 
 /* Decode one token through one layer with routing on the device:
- * router -> top-k -> routed + shared expert FFN -> combine.
+ * router -> top-k -> routed + shared expert FFN -> combine. For the shapes
+ * it has an instance for (hidden 2048; inter 512 with <= 256 experts, or
+ * inter 1024 with <= 64; k <= 8) this is one persistent launch, else one
+ * kernel per phase.
  * input: device f32[hidden] (the post-attention-norm hidden);
  * h_mid: device f32[hidden] (residual); hidden_out: device f32[hidden];
  * idx_out / w_out: device int32[k] / f32[k], or NULL.

@@ -137,6 +137,13 @@ class Kernels:
     def sync(self):
         check(_lib.smoe_sync(self.h), "smoe_sync")
 
+    def set_option(self, option, value):
+        check(_lib.smoe_set_option(self.h, option, value), "smoe_set_option")
+
+    def set_decode_path(self, path):
+        """0 auto, 1 one kernel per phase, 2 persistent (SMOE_OPT_DECODE_PATH)."""
+        self.set_option(_abi.SMOE_OPT_DECODE_PATH, path)
+
     def reserve(self, max_hidden, max_inter, max_experts):
         check(_lib.smoe_reserve(self.h, max_hidden, max_inter, max_experts), "smoe_reserve")
 

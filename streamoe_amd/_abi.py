@@ -1,7 +1,7 @@
 """ctypes binding of include/smoe.h (libsmoe.so).
 
 Loading fails loudly when the library has not been built: there is no
-fallback path. Build with ``python -m streamoe_amd.build``.
+fallback path. Build with ``python streamoe_amd/build.py``.
 """
 import ctypes as C
 import os
@@ -24,7 +24,10 @@ STATUS = {
     9: "SMOE_ERR_WORKSPACE_TOO_SMALL",
     10: "SMOE_ERR_HIP",
     11: "SMOE_ERR_NO_DEVICE",
+    12: "SMOE_ERR_DEVICE_TIMEOUT",
 }
+SMOE_OPT_DECODE_PATH = 1
+SMOE_OPT_TRACE_BUFFER = 2
 CODES = {v: k for k, v in STATUS.items()}
 
 
@@ -89,6 +92,7 @@ PROTOTYPES = {
     "smoe_set_stream": (_I, [_P, _P]),
     "smoe_reserve": (_I, [_P, _U32, _U32, _U32]),
     "smoe_sync": (_I, [_P]),
+    "smoe_set_option": (_I, [_P, _I, C.c_int64]),
     "smoe_qmv": (_I, [_P, C.POINTER(QWeights), _P, _P, _U32, _U32]),
     "smoe_argmax": (_I, [_P, _P, _U32, _P]),
     "smoe_dequant": (_I, [_P, C.POINTER(QWeights), _U32, _U32, _U32, _P]),
@@ -118,7 +122,7 @@ def load():
         return _lib
     if not os.path.exists(LIB_PATH):
         raise ImportError(
-            f"{LIB_PATH} is not built; run `python -m streamoe_amd.build` (no CPU fallback exists)")
+            f"{LIB_PATH} is not built; run `python streamoe_amd/build.py` (no CPU fallback exists)")
     lib = C.CDLL(LIB_PATH)
     for name, (res, args) in PROTOTYPES.items():
         fn = getattr(lib, name)

@@ -1,6 +1,9 @@
 """Build libsmoe.so (HIP, gfx950) in-tree.
 
-    python -m streamoe_amd.build          # or streamoe_amd.build.build()
+    python streamoe_amd/build.py
+
+(Run it as a script: importing the streamoe_amd package loads the built
+library, which a build must not depend on.)
 
 Each translation unit is compiled separately (in parallel) with hipcc for
 gfx950 only, then linked into streamoe_amd/libsmoe.so. Packed-FP32 VALU
@@ -15,7 +18,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libsmoe.so")
-SOURCES = ["api.hip", "decode.hip", "prefill.hip", "synth.hip"]
+SOURCES = ["api.hip", "decode.hip", "persist.hip", "prefill.hip", "synth.hip"]
 HEADERS = ["common.h", "kernels.h", os.path.join("..", "..", "include", "smoe.h")]
 ARCH = "gfx950"
 

@@ -7,6 +7,7 @@
 
 #include "../../include/smoe.h"
 #include "kernels.h"
+#include "persist.h"
 
 using namespace smoe;
 
@@ -19,7 +20,17 @@ struct smoe_handle {
   float* logits = nullptr;    // [max_experts]
   float* gate = nullptr;      // [1] shared-expert gate score
   FfnTable* table = nullptr;  // routing table of the current token
+  // Persistent decode: tagged handoff buffers (epoch << 32 | value).
+  uint64_t* tag_resid = nullptr;  // [max_hidden]
+  uint64_t* tag_logit = nullptr;  // [max_experts + 1]
+  uint64_t* tag_act = nullptr;    // [kMaxSlots * max_inter]
+  uint64_t* tag_route = nullptr;  // [32]
+  uint32_t* err = nullptr;        // device error word
+  uint32_t epoch = 1;             // next unused epoch (0 is never used)
   uint32_t max_hidden = 0, max_inter = 0, max_experts = 0;
+  // Options.
+  int decode_path = 0;  // 0 auto, 1 per-phase kernels, 2 persistent
+  uint64_t* trace = nullptr;
 };
 
 namespace {
@@ -56,9 +67,13 @@ int reserve(smoe_handle* h, uint32_t H, uint32_t I, uint32_t E) {
   H = H > h->max_hidden ? H : h->max_hidden;
   I = I > h->max_inter ? I : h->max_inter;
   E = E > h->max_experts ? E : h->max_experts;
-  const size_t act_b = (size_t)kMaxSlotsHost * I * sizeof(float);
-  const size_t log_b = ((size_t)E * sizeof(float) + 255) & ~(size_t)255;
-  const size_t total = act_b + log_b + 256 + sizeof(FfnTable) + 256;
+  auto al = [](size_t n) { return (n + 255) & ~(size_t)255; };
+  const size_t act_b = al((size_t)kMaxSlotsHost * I * sizeof(float));
+  const size_t log_b = al((size_t)E * sizeof(float));
+  const size_t tab_b = al(sizeof(FfnTable));
+  const size_t tr_b = al((size_t)H * 8), tl_b = al(((size_t)E + 1) * 8);
+  const size_t ta_b = al((size_t)kMaxSlotsHost * I * 8), tro_b = al(32 * 8);
+  const size_t total = act_b + log_b + 256 + tab_b + tr_b + tl_b + ta_b + tro_b + 256;
   void* mem = nullptr;
   if (hipSetDevice(h->device) != hipSuccess) return SMOE_ERR_HIP;
   if (hipMalloc(&mem, total) != hipSuccess) return SMOE_ERR_HIP;
@@ -76,6 +91,17 @@ int reserve(smoe_handle* h, uint32_t H, uint32_t I, uint32_t E) {
   h->logits = (float*)(p + act_b);
   h->gate = (float*)(p + act_b + log_b);
   h->table = (FfnTable*)(p + act_b + log_b + 256);
+  char* q = p + act_b + log_b + 256 + tab_b;
+  h->tag_resid = (uint64_t*)q;
+  q += tr_b;
+  h->tag_logit = (uint64_t*)q;
+  q += tl_b;
+  h->tag_act = (uint64_t*)q;
+  q += ta_b;
+  h->tag_route = (uint64_t*)q;
+  q += tro_b;
+  h->err = (uint32_t*)q;
+  h->epoch = 1;
   h->max_hidden = H;
   h->max_inter = I;
   h->max_experts = E;
@@ -102,6 +128,7 @@ const char* smoe_strerror(int status) {
     case SMOE_ERR_WORKSPACE_TOO_SMALL: return "workspace smaller than the required size";
     case SMOE_ERR_HIP: return "HIP runtime error";
     case SMOE_ERR_NO_DEVICE: return "no gfx950 device at that ordinal";
+    case SMOE_ERR_DEVICE_TIMEOUT: return "a bounded device-side wait expired; outputs are invalid";
     default: return "unknown status";
   }
 }
@@ -154,7 +181,29 @@ int smoe_reserve(smoe_handle* h, uint32_t max_hidden, uint32_t max_inter, uint32
 int smoe_sync(smoe_handle* h) {
   if (!h) return SMOE_ERR_INVALID_ARG;
   if (int rc = use_device(h)) return rc;
-  return hip_status(hipStreamSynchronize(h->stream));
+  if (hipStreamSynchronize(h->stream) != hipSuccess) return SMOE_ERR_HIP;
+  uint32_t e = 0;
+  if (hipMemcpy(&e, h->err, sizeof(e), hipMemcpyDeviceToHost) != hipSuccess) return SMOE_ERR_HIP;
+  if (e) {
+    if (hipMemset(h->err, 0, sizeof(e)) != hipSuccess) return SMOE_ERR_HIP;
+    return SMOE_ERR_DEVICE_TIMEOUT;
+  }
+  return SMOE_OK;
+}
+
+int smoe_set_option(smoe_handle* h, int option, int64_t value) {
+  if (!h) return SMOE_ERR_INVALID_ARG;
+  switch (option) {
+    case SMOE_OPT_DECODE_PATH:
+      if (value < 0 || value > 2) return SMOE_ERR_INVALID_ARG;
+      h->decode_path = (int)value;
+      return SMOE_OK;
+    case SMOE_OPT_TRACE_BUFFER:
+      h->trace = (uint64_t*)(uintptr_t)value;
+      return SMOE_OK;
+    default:
+      return SMOE_ERR_INVALID_ARG;
+  }
 }
 
 static int qview(const smoe_qweights* w, uint32_t in_dim, QView* v) {
@@ -343,12 +392,78 @@ static int decode_layer(smoe_handle* h, const smoe_layer* L, const float* input,
   return hip_status(e);
 }
 
+// One persistent launch over layers[0..n) (n <= kMaxPLayers). Returns
+// SMOE_ERR_UNSUPPORTED_SHAPE when no instance covers the shapes.
+static int decode_persistent(smoe_handle* h, const smoe_layer* layers, uint32_t n,
+                             const void* const* norm_w, float eps, const float* input,
+                             const float* resid_in, float* out, int32_t* idx_out, float* w_out) {
+  const smoe_layer& L0 = layers[0];
+  const smoe_expert_shape& s = L0.shape;
+  PPlan plan;
+  const bool shared = L0.shared_expert != nullptr;
+  if (n > (uint32_t)kMaxPLayers || s.group < 32 ||
+      !persist_plan(s.hidden, s.inter, L0.n_experts, L0.k, s.bits, shared,
+                    idx_out != nullptr || w_out != nullptr, &plan))
+    return SMOE_ERR_UNSUPPORTED_SHAPE;
+  for (uint32_t l = 1; l < n; ++l) {
+    const smoe_layer& L = layers[l];
+    if (L.shape.hidden != s.hidden || L.shape.inter != s.inter || L.shape.group != s.group ||
+        L.shape.bits != s.bits || L.n_experts != L0.n_experts || L.k != L0.k ||
+        (L.shared_expert != nullptr) != shared || (L.shared_gate != nullptr) != (L0.shared_gate != nullptr) ||
+        (L.normalize != 0) != (L0.normalize != 0))
+      return SMOE_ERR_UNSUPPORTED_SHAPE;
+  }
+  PArgs a{};
+  for (uint32_t l = 0; l < n; ++l) {
+    const smoe_layer& L = layers[l];
+    a.L[l].experts = (const uint8_t*)L.experts;
+    a.L[l].router = L.router_w;
+    a.L[l].shared = (const uint8_t*)L.shared_expert;
+    a.L[l].gate = L.shared_gate;
+    a.L[l].norm = (norm_w && l > 0) ? (const uint16_t*)norm_w[l] : nullptr;
+    a.L[l].stride = L.stride;
+  }
+  a.geom_routed = blob_geom(s.hidden, s.inter, s.group, s.bits);
+  a.geom_shared = blob_geom(s.hidden, s.inter, s.group, 4);
+  a.n_layers = n;
+  a.E = L0.n_experts;
+  a.k = L0.k;
+  a.group = s.group;
+  a.normalize = L0.normalize != 0;
+  a.has_shared = shared;
+  a.has_gate = shared && L0.shared_gate != nullptr;
+  a.eps = eps;
+  a.input = input;
+  a.resid_in = resid_in;
+  a.out = out;
+  a.idx_out = idx_out;
+  a.w_out = w_out;
+  a.tag_resid = h->tag_resid;
+  a.tag_logit = h->tag_logit;
+  a.tag_act = h->tag_act;
+  a.err = h->err;
+  a.trace = h->trace;
+  if (h->epoch > 0xFFFFFF00u - n) {
+    // Epoch space exhausted: clear the tags and restart at 1.
+    const size_t bytes = (char*)(h->tag_route + 32) - (char*)h->tag_resid;
+    if (hipMemsetAsync(h->tag_resid, 0, bytes, h->stream) != hipSuccess) return SMOE_ERR_HIP;
+    h->epoch = 1;
+  }
+  a.epoch = h->epoch;
+  h->epoch += n;
+  return hip_status(launch_decode_persistent(a, plan, s.bits, h->stream));
+}
+
 int smoe_moe_decode_layer(smoe_handle* h, const smoe_layer* layer, const float* input,
                           const float* h_mid, float* hidden_out, int32_t* idx_out, float* w_out) {
   if (!h || !input || !h_mid || !hidden_out) return SMOE_ERR_INVALID_ARG;
   if (int rc = check_layer(h, layer)) return rc;
   if (!aligned(input, 0, 16)) return SMOE_ERR_MISALIGNED;
   if (int rc = use_device(h)) return rc;
+  if (h->decode_path != 1) {
+    const int rc = decode_persistent(h, layer, 1, nullptr, 0.f, input, h_mid, hidden_out, idx_out, w_out);
+    if (rc != SMOE_ERR_UNSUPPORTED_SHAPE || h->decode_path == 2) return rc;
+  }
   return decode_layer(h, layer, input, h_mid, hidden_out, idx_out, w_out);
 }
 
@@ -365,6 +480,26 @@ int smoe_moe_decode_layers(smoe_handle* h, const smoe_layer* layers, uint32_t n_
     return SMOE_ERR_MISALIGNED;
   if (int rc = use_device(h)) return rc;
   const uint32_t H = layers[0].shape.hidden;
+  if (h->decode_path != 1) {
+    // Persistent launches of up to kMaxPLayers layers; between chunks the
+    // next chunk's input is RMSNorm(residual).
+    int rc = SMOE_OK;
+    for (uint32_t l0 = 0; l0 < n_layers && rc == SMOE_OK; l0 += kMaxPLayers) {
+      const uint32_t n = n_layers - l0 < (uint32_t)kMaxPLayers ? n_layers - l0 : (uint32_t)kMaxPLayers;
+      const float* x = input;
+      if (l0 > 0) {
+        x = residual_io;
+        if (norm_w) {
+          if (launch_rmsnorm(residual_io, (const uint16_t*)norm_w[l0], eps, H, work, h->stream) != hipSuccess)
+            return SMOE_ERR_HIP;
+          x = work;
+        }
+      }
+      rc = decode_persistent(h, layers + l0, n, norm_w ? norm_w + l0 : nullptr, eps, x, residual_io,
+                             residual_io, nullptr, nullptr);
+    }
+    if (rc != SMOE_ERR_UNSUPPORTED_SHAPE || h->decode_path == 2) return rc;
+  }
   for (uint32_t l = 0; l < n_layers; ++l) {
     const float* x = input;
     if (l > 0) {

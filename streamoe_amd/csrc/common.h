@@ -159,6 +159,45 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// DPP data movement within a wave (gfx9 encodings): row_shr:n = 0x110+n,
+// row_bcast:15 = 0x142, row_bcast:31 = 0x143. Lanes whose source is out of
+// range keep `identity`.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_f(float v, float identity) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(identity), __float_as_int(v), CTRL,
+                                                    ROW_MASK, 0xF, false));
+}
+
+// Sum over aligned groups of W lanes (16, 32 or 64) with DPP prefix steps.
+// The group's total is exact-order deterministic and valid in the group's
+// LAST lane (lane % W == W - 1); other lanes hold partial prefixes.
+template <int W>
+__device__ __forceinline__ float group_sum_last(float v) {
+  static_assert(W == 16 || W == 32 || W == 64, "DPP groups are 16, 32 or 64 lanes");
+  v += dpp_f<0x111>(v, 0.f);
+  v += dpp_f<0x112>(v, 0.f);
+  v += dpp_f<0x114>(v, 0.f);
+  v += dpp_f<0x118>(v, 0.f);
+  if (W >= 32) v += dpp_f<0x142, 0xA>(v, 0.f);
+  if (W == 64) v += dpp_f<0x143, 0xC>(v, 0.f);
+  return v;
+}
+
+// Max over the wave, valid in lane 63.
+__device__ __forceinline__ float wave_max_last(float v) {
+  v = fmaxf(v, dpp_f<0x111>(v, -INFINITY));
+  v = fmaxf(v, dpp_f<0x112>(v, -INFINITY));
+  v = fmaxf(v, dpp_f<0x114>(v, -INFINITY));
+  v = fmaxf(v, dpp_f<0x118>(v, -INFINITY));
+  v = fmaxf(v, dpp_f<0x142, 0xA>(v, -INFINITY));
+  v = fmaxf(v, dpp_f<0x143, 0xC>(v, -INFINITY));
+  return v;
+}
+
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
