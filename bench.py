@@ -7,9 +7,10 @@ intermediate 512, one always-on 4-bit shared expert with a sigmoid gate,
 affine 4-bit g64 weights (codes uniform, scales bf16 |N(0,.02)|, biases
 bf16 N(0,.01)), f32 router N(0,.02), residual stream N(0,1). Between
 layers the next input is RMSNorm(residual) (unit bf16 weights). One step
-= one token through the 40 layers: one persistent launch (the default
-decode path), or one kernel per phase replayed from a HIP graph
-(--path kernels --graph).
+= one token through the 40 layers: three kernels per layer (router +
+shared gate/up; top-k + routed gate/up; down + combine) replayed from a
+HIP graph (default), one kernel per phase (--path kernels) or one
+persistent cooperative launch (--path persistent, eager).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2]
 
@@ -120,6 +121,62 @@ def trace_phases(kern, step, nl, nb=256):
     return out
 
 
+FA_TRACE_BLOCKS = 4096  # kFaTraceBlocks in streamoe_amd/csrc/kernels.h (8 points per block)
+
+
+def trace_fused(kern, step, nl):
+    """Per-block timestamps of the three-kernel decode from one graph replay,
+    summarised over layers 1..nl-1 in microseconds. Points per block: 0
+    start, 1 routing input landed (gate/up: logits; down: expert pointers),
+    2 top-k set known, 3 weights landed, 4 arithmetic done, 5 stores
+    acknowledged. Reported per kernel: span (first start to last
+    acknowledged store), spread of block starts, mean durations between
+    points, and the idle gap to the next kernel's first block."""
+    import numpy as np
+    import torch
+
+    import streamoe_amd as sa
+    from streamoe_amd import _abi
+
+    P = 8
+    per_layer = 3 * FA_TRACE_BLOCKS * P
+    buf = torch.zeros(nl * per_layer, dtype=torch.int64, device="cuda")
+    kern.set_option(_abi.SMOE_OPT_TRACE_BUFFER, buf.data_ptr())
+    try:
+        g = sa.capture_graph(kern, step)
+        buf.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+    finally:
+        kern.set_option(_abi.SMOE_OPT_TRACE_BUFFER, 0)
+    t = buf.cpu().numpy().reshape(nl, 3, FA_TRACE_BLOCKS, P).astype(np.float64) * 0.01
+    seg = {"route": [(0, 3, "to_weights"), (3, 4, "arith"), (4, 5, "store_ack")],
+           "gateup": [(0, 1, "to_logits"), (1, 2, "topk"), (2, 3, "to_weights"), (3, 4, "arith"),
+                      (4, 5, "store_ack")],
+           "down": [(0, 1, "to_pointers"), (1, 3, "to_weights"), (3, 4, "arith"), (4, 5, "combine_store")]}
+    out = {}
+    for q, name in enumerate(["route", "gateup", "down"]):
+        acc = {}
+        for l in range(1, nl):
+            b = t[l, q]
+            b = b[b[:, 0] > 0]
+            if not len(b):
+                continue
+            vals = {"span": b[:, 5].max() - b[:, 0].min(), "start_spread": b[:, 0].max() - b[:, 0].min()}
+            for i, j, lab in seg[name]:
+                ok = (b[:, i] > 0) & (b[:, j] > 0)
+                if ok.any():
+                    vals[lab] = (b[ok, j] - b[ok, i]).mean()
+            nxt = t[l, q + 1] if q < 2 else (t[l + 1, 0] if l + 1 < nl else None)
+            if nxt is not None:
+                nb = nxt[nxt[:, 0] > 0]
+                vals["gap_to_next"] = nb[:, 0].min() - b[:, 5].max()
+            for kk, v in vals.items():
+                acc.setdefault(kk, []).append(v)
+        out[name] = {kk: round(float(np.mean(v)), 3) for kk, v in acc.items()}
+    return out
+
+
 def run_decode(args, c):
     import numpy as np
     import torch
@@ -157,28 +214,16 @@ def run_decode(args, c):
     work = torch.empty(H, dtype=torch.float32, device=dev)
     torch.cuda.synchronize()
 
-    kern.set_decode_path({"auto": 0, "kernels": 1, "persistent": 2}[args.path])
+    path = {"auto": 0, "kernels": 1, "persistent": 2, "fused": 3}[args.path]
+    kern.set_decode_path(path)
 
     def step():
         sa.check(kern.moe_decode_layers(layers, norms, 1e-6, x0, resid, work), "smoe_moe_decode_layers")
 
     stream = torch.cuda.current_stream(dev)
     graph = None
-    if args.graph:
-        side = torch.cuda.Stream(dev)
-        side.wait_stream(stream)
-        with torch.cuda.stream(side):
-            sa.check(sa._lib.smoe_set_stream(kern.h, sa.C.c_void_p(side.cuda_stream)), "set_stream")
-            step()  # one eager step on the capture stream
-        stream.wait_stream(side)
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            sa.check(sa._lib.smoe_set_stream(kern.h, sa.C.c_void_p(torch.cuda.current_stream(dev).cuda_stream)),
-                     "set_stream")
-            step()
-        sa.check(sa._lib.smoe_set_stream(kern.h, sa.C.c_void_p(stream.cuda_stream)), "set_stream")
-        torch.cuda.synchronize()
+    if not args.eager and path != 2:  # a cooperative launch cannot be captured
+        graph = sa.capture_graph(kern, step)
 
     run = graph.replay if graph is not None else step
     for _ in range(args.warmup):
@@ -199,7 +244,7 @@ def run_decode(args, c):
     assert torch.isfinite(resid).all(), "residual stream is not finite"
     phases = None
     if args.trace:
-        phases = trace_phases(kern, step, nl)
+        phases = trace_phases(kern, step, nl) if path == 2 else trace_fused(kern, step, nl)
 
     nbytes = layer_bytes(c)
     achieved = nbytes / (us_layer * 1e-6) / 1e9
@@ -245,9 +290,11 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
-    ap.add_argument("--path", default="auto", choices=["auto", "kernels", "persistent"])
-    ap.add_argument("--graph", action="store_true", help="replay the step from a HIP graph (per-phase path)")
-    ap.add_argument("--trace", action="store_true", help="report per-phase times of the persistent decode")
+    ap.add_argument("--path", default="auto", choices=["auto", "kernels", "persistent", "fused"],
+                    help="decode path: auto (three-kernel where supported), kernels (one per phase), "
+                         "persistent (one cooperative launch), fused (three-kernel only)")
+    ap.add_argument("--eager", action="store_true", help="launch every step eagerly instead of replaying a HIP graph")
+    ap.add_argument("--trace", action="store_true", help="report per-phase times from in-kernel timestamps")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     args = ap.parse_args()

@@ -62,9 +62,14 @@ typedef enum {
 
 /* Handle options (smoe_set_option). */
 typedef enum {
-  SMOE_OPT_DECODE_PATH = 1,  /* 0 auto (default), 1 one kernel per phase, 2 persistent */
-  SMOE_OPT_TRACE_BUFFER = 2  /* device uint64 buffer for per-phase timestamps of the
-                                persistent decode (10 per layer), or 0 = off */
+  SMOE_OPT_DECODE_PATH = 1,  /* 0 auto (default: three-kernel where it has an
+                                instance, else one kernel per phase), 1 one
+                                kernel per phase, 2 persistent cooperative,
+                                3 three-kernel only */
+  SMOE_OPT_TRACE_BUFFER = 2  /* device uint64 buffer for in-kernel timestamps, or 0 =
+                                off. Persistent decode: per layer and block 8 words;
+                                three-kernel decode: per layer 3 * 4096 * 8 words
+                                (kernel, block, point). Diagnostics only. */
 } smoe_option;
 
 typedef struct smoe_handle smoe_handle;
@@ -230,10 +235,11 @@ typedef struct {
 } smoe_layer;
 
 /* Decode one token through one layer with routing on the device:
- * router -> top-k -> routed + shared expert FFN -> combine. For the shapes
- * it has an instance for (hidden 2048; inter 512 with <= 256 experts, or
- * inter 1024 with <= 64; k <= 8) this is one persistent launch, else one
- * kernel per phase.
+ * router -> top-k -> routed + shared expert FFN -> combine. For hidden
+ * 2048, inter 512 or 1024, <= 256 experts this is three kernels (router +
+ * shared gate/up; top-k + routed gate/up; down + combine) that allocate
+ * nothing and set no memory, so a caller can capture them in a HIP graph;
+ * other shapes take one kernel per phase. See SMOE_OPT_DECODE_PATH.
  * input: device f32[hidden] (the post-attention-norm hidden);
  * h_mid: device f32[hidden] (residual); hidden_out: device f32[hidden];
  * idx_out / w_out: device int32[k] / f32[k], or NULL.

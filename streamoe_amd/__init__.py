@@ -137,11 +137,15 @@ class Kernels:
     def sync(self):
         check(_lib.smoe_sync(self.h), "smoe_sync")
 
+    def set_stream(self, stream):
+        """Launch on `stream` (a torch.cuda.Stream) from now on (smoe_set_stream)."""
+        check(_lib.smoe_set_stream(self.h, C.c_void_p(stream.cuda_stream)), "smoe_set_stream")
+
     def set_option(self, option, value):
         check(_lib.smoe_set_option(self.h, option, value), "smoe_set_option")
 
     def set_decode_path(self, path):
-        """0 auto, 1 one kernel per phase, 2 persistent (SMOE_OPT_DECODE_PATH)."""
+        """0 auto, 1 one kernel per phase, 2 persistent, 3 three-kernel (SMOE_OPT_DECODE_PATH)."""
         self.set_option(_abi.SMOE_OPT_DECODE_PATH, path)
 
     def reserve(self, max_hidden, max_inter, max_experts):
@@ -231,6 +235,34 @@ class Kernels:
 
     def synth_normal_bf16(self, out, seed, sigma=1.0):
         return _lib.smoe_synth_normal_bf16(self.h, _ptr(out), out.numel(), seed, C.c_float(sigma))
+
+
+def capture_graph(kernels: Kernels, fn):
+    """Record the launches `fn()` makes on `kernels` into a HIP graph (torch's
+    CUDAGraph over hipGraph) and return it; fn runs once eagerly on the
+    capture stream first. The handle launches on torch's current stream
+    again afterwards. Only launch sequences that allocate nothing and set no
+    memory (the per-phase and three-kernel decode) can be captured."""
+    import torch
+
+    dev = torch.device("cuda", kernels.device)
+    stream = torch.cuda.current_stream(dev)
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(stream)
+    try:
+        with torch.cuda.stream(side):
+            kernels.set_stream(side)
+            fn()
+        stream.wait_stream(side)
+        torch.cuda.synchronize(dev)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            kernels.set_stream(torch.cuda.current_stream(dev))
+            fn()
+    finally:
+        kernels.set_stream(stream)
+    torch.cuda.synchronize(dev)
+    return graph
 
 
 def gpu_batched_experts_forward(kernels: Kernels, layout: ExpertLayout, actual_k, expert_data,

@@ -17,7 +17,7 @@ struct smoe_handle {
   // Decode scratch (MoeBuffers' flat buffers, expert_forward.rs:379-528).
   void* mem = nullptr;
   float* act = nullptr;       // [kMaxSlots, max_inter]
-  float* logits = nullptr;    // [max_experts]
+  float* logits = nullptr;    // [max_experts + 1]
   float* gate = nullptr;      // [1] shared-expert gate score
   FfnTable* table = nullptr;  // routing table of the current token
   // Persistent decode: tagged handoff buffers (epoch << 32 | value).
@@ -29,7 +29,7 @@ struct smoe_handle {
   uint32_t epoch = 1;             // next unused epoch (0 is never used)
   uint32_t max_hidden = 0, max_inter = 0, max_experts = 0;
   // Options.
-  int decode_path = 0;  // 0 auto, 1 per-phase kernels, 2 persistent
+  int decode_path = 0;  // 0 auto, 1 per-phase kernels, 2 persistent, 3 three-kernel
   uint64_t* trace = nullptr;
 };
 
@@ -69,7 +69,7 @@ int reserve(smoe_handle* h, uint32_t H, uint32_t I, uint32_t E) {
   E = E > h->max_experts ? E : h->max_experts;
   auto al = [](size_t n) { return (n + 255) & ~(size_t)255; };
   const size_t act_b = al((size_t)kMaxSlotsHost * I * sizeof(float));
-  const size_t log_b = al((size_t)E * sizeof(float));
+  const size_t log_b = al(((size_t)E + 1) * sizeof(float));
   const size_t tab_b = al(sizeof(FfnTable));
   const size_t tr_b = al((size_t)H * 8), tl_b = al(((size_t)E + 1) * 8);
   const size_t ta_b = al((size_t)kMaxSlotsHost * I * 8), tro_b = al(32 * 8);
@@ -195,7 +195,7 @@ int smoe_set_option(smoe_handle* h, int option, int64_t value) {
   if (!h) return SMOE_ERR_INVALID_ARG;
   switch (option) {
     case SMOE_OPT_DECODE_PATH:
-      if (value < 0 || value > 2) return SMOE_ERR_INVALID_ARG;
+      if (value < 0 || value > 3) return SMOE_ERR_INVALID_ARG;
       h->decode_path = (int)value;
       return SMOE_OK;
     case SMOE_OPT_TRACE_BUFFER:
@@ -392,6 +392,45 @@ static int decode_layer(smoe_handle* h, const smoe_layer* L, const float* input,
   return hip_status(e);
 }
 
+// The three-kernel layer (fused.hip). Returns SMOE_ERR_UNSUPPORTED_SHAPE
+// when it has no instance for the layer.
+static bool fused_ok(const smoe_layer* L) {
+  const smoe_expert_shape& s = L->shape;
+  return fused_supported(s.hidden, s.inter, s.group, s.bits, L->n_experts, L->k);
+}
+
+static int decode_fused(smoe_handle* h, const smoe_layer* L, const float* x_in, const float* resid,
+                        const uint16_t* norm, float eps, float* x_out, const float* h_mid,
+                        float* out, int32_t* idx_out, float* w_out, uint32_t layer_index) {
+  if (!fused_ok(L)) return SMOE_ERR_UNSUPPORTED_SHAPE;
+  const smoe_expert_shape& s = L->shape;
+  FusedLayer a{};
+  a.x_in = x_in;
+  a.resid = resid;
+  a.norm = norm;
+  a.eps = eps;
+  a.x_out = x_out;
+  a.router = L->router_w;
+  a.shared = (const uint8_t*)L->shared_expert;
+  a.gate = L->shared_expert ? L->shared_gate : nullptr;
+  a.experts = (const uint8_t*)L->experts;
+  a.stride = L->stride;
+  a.routed = blob_geom(s.hidden, s.inter, s.group, s.bits);
+  a.sgeom = blob_geom(s.hidden, s.inter, s.group, 4);
+  a.E = L->n_experts;
+  a.k = L->k;
+  a.normalize = L->normalize != 0;
+  a.logits = h->logits;
+  a.act = h->act;
+  a.table = h->table;
+  a.h_mid = h_mid;
+  a.out = out;
+  a.idx_out = idx_out;
+  a.w_out = w_out;
+  a.trace = h->trace ? h->trace + (uint64_t)layer_index * kFaTraceLayer : nullptr;
+  return hip_status(launch_fused_layer(a, h->stream));
+}
+
 // One persistent launch over layers[0..n) (n <= kMaxPLayers). Returns
 // SMOE_ERR_UNSUPPORTED_SHAPE when no instance covers the shapes.
 static int decode_persistent(smoe_handle* h, const smoe_layer* layers, uint32_t n,
@@ -460,9 +499,13 @@ int smoe_moe_decode_layer(smoe_handle* h, const smoe_layer* layer, const float* 
   if (int rc = check_layer(h, layer)) return rc;
   if (!aligned(input, 0, 16)) return SMOE_ERR_MISALIGNED;
   if (int rc = use_device(h)) return rc;
+  if (h->decode_path == 2) {
+    return decode_persistent(h, layer, 1, nullptr, 0.f, input, h_mid, hidden_out, idx_out, w_out);
+  }
   if (h->decode_path != 1) {
-    const int rc = decode_persistent(h, layer, 1, nullptr, 0.f, input, h_mid, hidden_out, idx_out, w_out);
-    if (rc != SMOE_ERR_UNSUPPORTED_SHAPE || h->decode_path == 2) return rc;
+    const int rc = decode_fused(h, layer, input, nullptr, nullptr, 0.f, nullptr, h_mid, hidden_out,
+                                idx_out, w_out, 0);
+    if (rc != SMOE_ERR_UNSUPPORTED_SHAPE || h->decode_path == 3) return rc;
   }
   return decode_layer(h, layer, input, h_mid, hidden_out, idx_out, w_out);
 }
@@ -480,7 +523,21 @@ int smoe_moe_decode_layers(smoe_handle* h, const smoe_layer* layers, uint32_t n_
     return SMOE_ERR_MISALIGNED;
   if (int rc = use_device(h)) return rc;
   const uint32_t H = layers[0].shape.hidden;
-  if (h->decode_path != 1) {
+  if (h->decode_path == 0 || h->decode_path == 3) {
+    bool all = true;
+    for (uint32_t l = 0; l < n_layers; ++l) all = all && fused_ok(&layers[l]);
+    if (all) {
+      for (uint32_t l = 0; l < n_layers; ++l) {
+        const uint16_t* nw = (norm_w && l > 0) ? (const uint16_t*)norm_w[l] : nullptr;
+        if (int rc = decode_fused(h, &layers[l], l == 0 ? input : nullptr, residual_io, nw, eps,
+                                  work, residual_io, residual_io, nullptr, nullptr, l))
+          return rc;
+      }
+      return SMOE_OK;
+    }
+    if (h->decode_path == 3) return SMOE_ERR_UNSUPPORTED_SHAPE;
+  }
+  if (h->decode_path == 2) {
     // Persistent launches of up to kMaxPLayers layers; between chunks the
     // next chunk's input is RMSNorm(residual).
     int rc = SMOE_OK;
@@ -498,7 +555,7 @@ int smoe_moe_decode_layers(smoe_handle* h, const smoe_layer* layers, uint32_t n_
       rc = decode_persistent(h, layers + l0, n, norm_w ? norm_w + l0 : nullptr, eps, x, residual_io,
                              residual_io, nullptr, nullptr);
     }
-    if (rc != SMOE_ERR_UNSUPPORTED_SHAPE || h->decode_path == 2) return rc;
+    return rc;
   }
   for (uint32_t l = 0; l < n_layers; ++l) {
     const float* x = input;

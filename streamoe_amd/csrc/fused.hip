@@ -1,0 +1,460 @@
+// fused.hip — one decode token through one MoE layer as three kernels
+// (gfx950), meant to be replayed from a HIP graph.
+//
+// A decode layer has three all-to-all dependencies: the hidden state feeds
+// every router row, the router's top-k feeds every expert row, and every
+// activation feeds every down row. On MI355X the cheapest grid-wide
+// synchronisation is a kernel boundary inside a graph (~1.6 us, and it
+// makes the producer's stores visible through every XCD's L2); in-kernel
+// broadcasts through agent-scope atomics cost 2.7-9 us at 256 consumer
+// blocks and a cooperative grid.sync() ~33 us. So each dependency is one
+// kernel boundary, and everything a kernel can compute redundantly instead
+// of waiting for (RMSNorm's sum of squares, softmax and the top-k set) it
+// computes in every wave.
+//
+//   K_A  k_fa_route    one wave per router row / per SR shared-expert rows:
+//                      x = RMSNorm(r) * w (or the given input), then
+//                      logits[e] = W_e . x (row E: shared gate), or
+//                      act[k, i] = silu(gate_i . x) * (up_i . x) for the
+//                      shared expert.  Wave 0 stores x for K_B.
+//   K_B  k_fa_gateup   one wave per RW rows of one routed slot: softmax and
+//                      the top-k set of the logits (every wave), then
+//                      act[s, i] = silu(gate_i . x) * (up_i . x) for expert
+//                      set[s]. Block 0 also publishes the route table
+//                      (expert blobs and renormalised weights, the shared
+//                      gate score) and, when asked, the reference's exact
+//                      slot order.
+//   K_C  k_fa_down     one block per kFaR hidden rows, one lane per (slot,
+//                      chunk of 32 activations): every slot's down rows,
+//                      combined in table order moe = fma(out_s, w_s, moe)
+//                      (deferred.rs:458-466) plus the shared term and the
+//                      residual.
+//
+// Weights are read exactly once per token with 128-bit (4-bit) or 96-bit
+// (3-bit) non-temporal loads; activations (x, act, logits: <= 40 KB) are
+// re-read from L2 by every wave that needs them.
+#include "common.h"
+#include "kernels.h"
+#include "topk.h"
+
+namespace smoe {
+
+constexpr uint32_t kFaH = 2048;              // hidden size of this path (64 lanes x 32)
+constexpr int kFaSR = 2;                     // shared-expert rows per K_A wave
+constexpr int kFaRW = 4;                     // routed rows per K_B wave
+
+// Optional timestamps (100 MHz s_memrealtime) for latency analysis; with
+// `drain` the wave first waits for all its outstanding memory operations.
+__device__ __forceinline__ void fa_trace(const FusedLayer& a, int q, int point, bool drain) {
+  if (!a.trace) return;
+  if (drain) __builtin_amdgcn_s_waitcnt(0);
+  if (threadIdx.x == 0)
+    a.trace[((size_t)q * kFaTraceBlocks + blockIdx.x) * kFaTracePoints + point] =
+        __builtin_amdgcn_s_memrealtime();
+}
+
+// Raw bf16 scale and bias of chunk c of `row` in one [rows, in_dim] block.
+// They are widened only where used, so the loads stay in flight together
+// with the codes.
+__device__ __forceinline__ void load_sb(const uint8_t* blob, uint64_t s_off, uint64_t b_off,
+                                        uint32_t row, uint32_t gpr, uint32_t cpg_shift, uint32_t c,
+                                        uint16_t& s, uint16_t& b) {
+  const size_t gi = ((size_t)row * gpr + (c >> cpg_shift)) * 2;
+  s = *reinterpret_cast<const uint16_t*>(blob + s_off + gi);
+  b = *reinterpret_cast<const uint16_t*>(blob + b_off + gi);
+}
+
+// x chunk of this lane: the given input, or RMSNorm(r) * w (bf16 weights)
+// with the sum of squares reduced over the wave (rms_norm_bf16_n_tokens_cpu,
+// backend/cpu/mod.rs:406-430: inv = 1 / sqrt(sum_sq / dim + eps),
+// x = r * inv * w), or r itself when w is null. The vector and the norm
+// weights are loaded together (one memory round trip): a missing operand
+// reads a harmless stand-in and is then ignored.
+struct FaX {
+  float x[kChunk];
+  u32x4 w[4];
+};
+
+__device__ __forceinline__ void fa_x_load(const FusedLayer& a, int lane, FaX& f) {
+  const float* src = a.x_in ? a.x_in : a.resid;
+  const uint16_t* nw = a.norm ? a.norm : reinterpret_cast<const uint16_t*>(src);
+  const u32x4* wp = reinterpret_cast<const u32x4*>(nw + (size_t)lane * kChunk);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) f.w[i] = wp[i];
+  load_x32(src + (size_t)lane * kChunk, f.x);
+}
+
+__device__ __forceinline__ void fa_x_finish(const FusedLayer& a, FaX& f) {
+  if (a.x_in || !a.norm) return;
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < kChunk; ++j) ss += f.x[j] * f.x[j];
+  ss = readlane_f(group_sum_last<64>(ss), 63);
+  const float inv = 1.0f / sqrtf(ss / (float)kFaH + a.eps);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t w4[4] = {f.w[i].x, f.w[i].y, f.w[i].z, f.w[i].w};
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const int j = 8 * i + 2 * h;
+      f.x[j] = f.x[j] * inv * bf16f((uint16_t)(w4[h] & 0xFFFFu));
+      f.x[j + 1] = f.x[j + 1] * inv * bf16f((uint16_t)(w4[h] >> 16));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// K_A: router logits (+ shared gate) and the shared expert's gate/up.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void k_fa_route(FusedLayer a) {
+  fa_trace(a, 0, 0, false);
+  const int lane = threadIdx.x;
+  const uint32_t w = blockIdx.x;
+  const uint32_t nrouter = a.E + (a.gate ? 1u : 0u);
+  const uint32_t c = lane;  // this lane's chunk of the hidden vector
+
+  if (w < nrouter) {
+    const float* row = w < a.E ? a.router + (size_t)w * kFaH : a.gate;
+    f32x4 wr[kChunk / 4];
+    const f32x4* rp = reinterpret_cast<const f32x4*>(row + (size_t)c * kChunk);
+#pragma unroll
+    for (int i = 0; i < kChunk / 4; ++i) wr[i] = __builtin_nontemporal_load(rp + i);
+    FaX f;
+    fa_x_load(a, lane, f);
+    __builtin_amdgcn_sched_barrier(0);
+    fa_trace(a, 0, 3, true);
+    fa_x_finish(a, f);
+    const float(&x)[kChunk] = f.x;
+    if (w == 0 && !a.x_in) {
+      float4* xo = reinterpret_cast<float4*>(a.x_out + (size_t)c * kChunk);
+#pragma unroll
+      for (int i = 0; i < kChunk / 4; ++i) xo[i] = make_float4(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
+    }
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+    for (int i = 0; i < kChunk / 4; ++i) {
+      a0 = __builtin_fmaf(wr[i].x, x[4 * i + 0], a0);
+      a1 = __builtin_fmaf(wr[i].y, x[4 * i + 1], a1);
+      a2 = __builtin_fmaf(wr[i].z, x[4 * i + 2], a2);
+      a3 = __builtin_fmaf(wr[i].w, x[4 * i + 3], a3);
+    }
+    const float s = group_sum_last<64>((a0 + a1) + (a2 + a3));
+    fa_trace(a, 0, 4, false);
+    if (lane == 63) a.logits[w] = s;
+    fa_trace(a, 0, 5, true);
+    return;
+  }
+
+  // Shared expert rows [r0, r0 + kFaSR) of gate and up (4-bit).
+  const BlobGeom& g = a.sgeom;
+  const uint32_t r0 = (w - nrouter) * kFaSR;
+  const uint32_t gpr = kFaH / g.group;
+  const uint32_t cps = __builtin_ctz(g.group / kChunk);
+  constexpr uint32_t RB = kFaH / 2;  // 4-bit row bytes
+  Raw<4> rg[kFaSR], ru[kFaSR];
+  uint16_t sg[kFaSR], bg[kFaSR], su[kFaSR], bu[kFaSR];
+#pragma unroll
+  for (int p = 0; p < kFaSR; ++p) {
+    const uint32_t row = r0 + p;
+    rg[p] = load_raw4(a.shared + g.w[0] + (size_t)row * RB + c * 16);
+    ru[p] = load_raw4(a.shared + g.w[1] + (size_t)row * RB + c * 16);
+    load_sb(a.shared, g.s[0], g.b[0], row, gpr, cps, c, sg[p], bg[p]);
+    load_sb(a.shared, g.s[1], g.b[1], row, gpr, cps, c, su[p], bu[p]);
+  }
+  FaX f;
+  fa_x_load(a, lane, f);
+  __builtin_amdgcn_sched_barrier(0);
+  fa_trace(a, 0, 3, true);
+  fa_x_finish(a, f);
+  const float(&x)[kChunk] = f.x;
+  const float xs = xsum(x);
+  float* act = a.act + (size_t)a.k * g.inter;
+#pragma unroll
+  for (int p = 0; p < kFaSR; ++p) {
+    const float gs = group_sum_last<64>(chunk_dot<4>(rg[p], x, xs, bf16f(sg[p]), bf16f(bg[p])));
+    const float us = group_sum_last<64>(chunk_dot<4>(ru[p], x, xs, bf16f(su[p]), bf16f(bu[p])));
+    if (lane == 63) act[r0 + p] = silu_mul(gs, us);
+  }
+  fa_trace(a, 0, 5, true);
+}
+
+// ---------------------------------------------------------------------------
+// K_B: top-k set in every wave, routed gate/up; block 0 publishes the table.
+// ---------------------------------------------------------------------------
+template <int BITS, int P>
+__global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a) {
+  constexpr int CB = chunk_bytes<BITS>();
+  constexpr uint32_t RB = kFaH / kChunk * CB;  // row bytes
+  __shared__ int32_t sid[kMaxK];
+  __shared__ float sval[kMaxK];
+  __shared__ float sprob[64 * P];
+  fa_trace(a, 1, 0, false);
+  const int lane = threadIdx.x;
+  const BlobGeom& g = a.routed;
+  const uint32_t I = g.inter, E = a.E, k = a.k;
+  const uint32_t tiles = I / kFaRW;
+  const uint32_t slot = blockIdx.x / tiles;
+  const uint32_t r0 = (blockIdx.x % tiles) * kFaRW;
+  const uint32_t c = lane;
+  const float* xsrc = a.x_in ? a.x_in : a.x_out;
+
+  float v[P];
+#pragma unroll
+  for (int e = 0; e < P; ++e) {
+    const uint32_t j = lane * P + e;
+    v[e] = j < E ? a.logits[j] : -INFINITY;
+  }
+  fa_trace(a, 1, 1, true);
+  float x[kChunk];
+  load_x32(xsrc + (size_t)c * kChunk, x);
+
+  // moe_router.rs:52-72 softmax, then the top-k set (moe_router.rs:83-124
+  // keeps exactly the k largest when the k-th and (k+1)-th differ; ties,
+  // NaN and degenerate scores take the exact running-minimum scan).
+  wave_softmax<P>(v, E, lane);
+  const bool is_set = topk_set<P>(v, E, k, lane, sid);
+  __syncthreads();
+  if (!is_set) {
+    exact_topk<P>(v, k, lane, sid, sval);
+    __syncthreads();
+  }
+  const int32_t id = sid[slot];
+  const uint8_t* blob = a.experts + (uint64_t)id * a.stride;
+  fa_trace(a, 1, 2, false);
+
+  const uint32_t gpr = kFaH / g.group;
+  const uint32_t cps = __builtin_ctz(g.group / kChunk);
+  Raw<BITS> rg[kFaRW], ru[kFaRW];
+  uint16_t sg[kFaRW], bg[kFaRW], su[kFaRW], bu[kFaRW];
+#pragma unroll
+  for (int p = 0; p < kFaRW; ++p) {
+    const uint32_t row = r0 + p;
+    rg[p] = load_raw<BITS>(blob + g.w[0] + (size_t)row * RB + c * CB);
+    ru[p] = load_raw<BITS>(blob + g.w[1] + (size_t)row * RB + c * CB);
+    load_sb(blob, g.s[0], g.b[0], row, gpr, cps, c, sg[p], bg[p]);
+    load_sb(blob, g.s[1], g.b[1], row, gpr, cps, c, su[p], bu[p]);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  fa_trace(a, 1, 3, true);
+
+  if (blockIdx.x == 0) {
+    // Route table in the order the act slots use, weights renormalised in
+    // that order (normalize_weights, moe_router.rs:130-141).
+#pragma unroll
+    for (int e = 0; e < P; ++e) sprob[lane * P + e] = v[e];
+    __syncthreads();
+    if (is_set && lane < (int)k) sval[lane] = sprob[sid[lane]];
+    __syncthreads();
+    if (lane < (int)k) {
+      float wt = sval[lane];
+      if (a.normalize) {
+        float sum = 0.f;
+        for (uint32_t i = 0; i < k; ++i) sum += sval[i];
+        if (sum > 0.f) wt = sval[lane] * (1.0f / sum);
+      }
+      a.table->blob[lane] = a.experts + (uint64_t)sid[lane] * a.stride;
+      a.table->weight[lane] = wt;
+    }
+    if (lane == 0) {
+      a.table->k = k;
+      a.table->has_shared = a.shared != nullptr;
+      if (a.shared) {
+        a.table->blob[k] = a.shared;
+        a.table->weight[k] = 1.0f;
+      }
+      a.table->shared_gate = a.gate ? a.logits[E] : __builtin_nanf("");
+    }
+    if (a.idx_out || a.w_out) {
+      // The reference's exact slot order for the caller.
+      __shared__ int32_t eid[kMaxK];
+      __shared__ float evl[kMaxK];
+      if (is_set) {
+        exact_topk<P>(v, k, lane, eid, evl);
+      } else if (lane < (int)k) {
+        eid[lane] = sid[lane];
+        evl[lane] = sval[lane];
+      }
+      __syncthreads();
+      if (lane < (int)k) {
+        float wt = evl[lane];
+        if (a.normalize) {
+          float sum = 0.f;
+          for (uint32_t i = 0; i < k; ++i) sum += evl[i];
+          if (sum > 0.f) wt = evl[lane] * (1.0f / sum);
+        }
+        if (a.idx_out) a.idx_out[lane] = eid[lane];
+        if (a.w_out) a.w_out[lane] = wt;
+      }
+    }
+  }
+
+  const float xs = xsum(x);
+  float* act = a.act + (size_t)slot * I;
+#pragma unroll
+  for (int p = 0; p < kFaRW; ++p) {
+    const float gs = group_sum_last<64>(chunk_dot<BITS>(rg[p], x, xs, bf16f(sg[p]), bf16f(bg[p])));
+    const float us = group_sum_last<64>(chunk_dot<BITS>(ru[p], x, xs, bf16f(su[p]), bf16f(bu[p])));
+    if (lane == 63) act[r0 + p] = silu_mul(gs, us);
+  }
+  fa_trace(a, 1, 4, false);
+  fa_trace(a, 1, 5, true);
+}
+
+// ---------------------------------------------------------------------------
+// K_C: down rows of every slot + combine + residual.
+//
+// Lanes are slot-major: lane (s, c) owns chunk c (LI = inter / 32 chunks
+// per row) of slot s, so its 32 activations stay in registers for all kFaR
+// rows of the block. Routed slots fill waves 0 .. ceil(k / SPW) - 1 (SPW =
+// 64 / LI slots per wave); the shared expert (4-bit) has the last wave to
+// itself. Every load is issued up front: the activation chunk, the expert
+// pointer (route table) and then all kFaR rows' codes, scales and biases.
+// Per-(row, slot) sums go through LDS to kFaR combine threads, which apply
+// the reference's order: moe = fma(out_s, w_s, moe) over the routed slots,
+// then the shared term and the residual (deferred.rs:441-490).
+// ---------------------------------------------------------------------------
+constexpr int kFaR = 8;  // hidden rows per K_C block
+
+template <int BITS, int LI>
+__device__ __forceinline__ void down_rows(const FusedLayer& a, const uint8_t* blob, const BlobGeom& g,
+                                          uint32_t row0, uint32_t c, const float* act_chunk,
+                                          float (&o)[kFaR]) {
+  constexpr int CB = chunk_bytes<BITS>();
+  constexpr uint32_t RB = LI * CB;
+  const uint32_t gpr = g.inter / g.group;
+  const uint32_t cps = __builtin_ctz(g.group / kChunk);
+  Raw<BITS> raw[kFaR];
+  uint16_t sr[kFaR], br[kFaR];
+#pragma unroll
+  for (int r = 0; r < kFaR; ++r) {
+    const uint32_t row = row0 + r;
+    raw[r] = load_raw<BITS>(blob + g.w[2] + (size_t)row * RB + c * CB);
+    const size_t gi = ((size_t)row * gpr + (c >> cps)) * 2;
+    sr[r] = *reinterpret_cast<const uint16_t*>(blob + g.s[2] + gi);
+    br[r] = *reinterpret_cast<const uint16_t*>(blob + g.b[2] + gi);
+  }
+  float act[kChunk];
+  load_x32(act_chunk, act);
+  // Keep every load above in flight before any arithmetic.
+  __builtin_amdgcn_sched_barrier(0);
+  fa_trace(a, 2, 3, true);
+  const float xs = xsum(act);
+#pragma unroll
+  for (int r = 0; r < kFaR; ++r)
+    o[r] = group_sum_last<LI>(chunk_dot<BITS>(raw[r], act, xs, bf16f(sr[r]), bf16f(br[r])));
+}
+
+// Waves per K_C block: ceil(k / SPW) routed + 1 shared, k <= 16.
+template <int LI>
+constexpr int fa_down_threads() {
+  return ((kMaxK + kWave / LI - 1) / (kWave / LI) + 1) * kWave;
+}
+
+template <int BITS, int LI>
+__global__ __launch_bounds__(fa_down_threads<LI>()) void k_fa_down(FusedLayer a) {
+  constexpr int SPW = kWave / LI;
+  __shared__ float so[kFaR][kMaxSlots];
+  __shared__ float sw[kMaxSlots];
+  fa_trace(a, 2, 0, false);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t k = a.k;
+  const uint32_t rwaves = (k + SPW - 1) / SPW;
+  const uint32_t row0 = blockIdx.x * kFaR;
+  const uint32_t c = lane % LI;
+  const uint32_t I = a.routed.inter;
+
+  // Combine threads: residual and routing weights, loaded early.
+  float hm = 0.f, wk = 0.f;
+  if (threadIdx.x < (unsigned)kFaR) hm = a.h_mid[row0 + threadIdx.x];
+  if (threadIdx.x < k) wk = a.table->weight[threadIdx.x];
+
+  float o[kFaR];
+  uint32_t slot;
+  bool valid;
+  if ((uint32_t)wave < rwaves) {
+    slot = wave * SPW + lane / LI;
+    valid = slot < k;
+    const uint32_t sl = valid ? slot : 0;  // idle lanes read slot 0
+    const uint8_t* blob = a.table->blob[sl];
+    if (a.trace) {
+      __builtin_amdgcn_s_waitcnt(0);
+      if (lane == 0 && wave == 0)
+        a.trace[((size_t)2 * kFaTraceBlocks + blockIdx.x) * kFaTracePoints + 1] = __builtin_amdgcn_s_memrealtime();
+    }
+    down_rows<BITS, LI>(a, blob, a.routed, row0, c, a.act + (size_t)sl * I + c * kChunk, o);
+  } else {
+    slot = k;
+    valid = lane < LI;
+    down_rows<4, LI>(a, a.shared, a.sgeom, row0, c, a.act + (size_t)k * I + c * kChunk, o);
+  }
+  if (c == LI - 1 && valid) {
+#pragma unroll
+    for (int r = 0; r < kFaR; ++r) so[r][slot] = o[r];
+  }
+  if (threadIdx.x < k) sw[threadIdx.x] = wk;
+  fa_trace(a, 2, 4, false);
+  __syncthreads();
+  if (threadIdx.x < (unsigned)kFaR) {
+    const uint32_t r = threadIdx.x;
+    float moe = 0.f;
+    for (uint32_t s = 0; s < k; ++s) moe = __builtin_fmaf(so[r][s], sw[s], moe);
+    float sum = moe;
+    if (a.shared) {
+      const float sh = so[r][k];
+      const float gate = a.table->shared_gate;
+      sum = __builtin_isnan(gate) ? moe + sh : __builtin_fmaf(sh, sigmoidf_ref(gate), moe);
+    }
+    a.out[row0 + r] = hm + sum;
+  }
+  fa_trace(a, 2, 5, true);
+}
+
+// ---------------------------------------------------------------------------
+// Host side.
+// ---------------------------------------------------------------------------
+bool fused_supported(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t bits,
+                     uint32_t n_experts, uint32_t k) {
+  if (hidden != kFaH) return false;
+  if (inter != 512 && inter != 1024) return false;
+  if (group % kChunk != 0 || (group & (group - 1)) != 0 || inter % group != 0) return false;
+  if (bits != 4 && bits != 3) return false;
+  if (n_experts < 1 || n_experts > 256 || k < 1 || k > (uint32_t)kMaxK || k > n_experts) return false;
+  return true;
+}
+
+template <int BITS>
+static void launch_gateup_fa(const FusedLayer& a, uint32_t blocks, hipStream_t st) {
+  const uint32_t p = (a.E + 63) / 64;
+  if (p <= 1)
+    hipLaunchKernelGGL((k_fa_gateup<BITS, 1>), dim3(blocks), dim3(64), 0, st, a);
+  else if (p <= 2)
+    hipLaunchKernelGGL((k_fa_gateup<BITS, 2>), dim3(blocks), dim3(64), 0, st, a);
+  else
+    hipLaunchKernelGGL((k_fa_gateup<BITS, 4>), dim3(blocks), dim3(64), 0, st, a);
+}
+
+template <int BITS, int LI>
+static void launch_down_fa(const FusedLayer& a, hipStream_t st) {
+  constexpr uint32_t SPW = kWave / LI;
+  const uint32_t waves = (a.k + SPW - 1) / SPW + (a.shared ? 1u : 0u);
+  hipLaunchKernelGGL((k_fa_down<BITS, LI>), dim3(kFaH / kFaR), dim3(waves * kWave), 0, st, a);
+}
+
+hipError_t launch_fused_layer(const FusedLayer& a, hipStream_t st) {
+  const uint32_t I = a.routed.inter;
+  const uint32_t ka = a.E + (a.gate ? 1u : 0u) + (a.shared ? I / kFaSR : 0u);
+  hipLaunchKernelGGL(k_fa_route, dim3(ka), dim3(64), 0, st, a);
+  const uint32_t kb = a.k * (I / kFaRW);
+  if (a.routed.bits == 4)
+    launch_gateup_fa<4>(a, kb, st);
+  else
+    launch_gateup_fa<3>(a, kb, st);
+  if (a.routed.bits == 4) {
+    if (I == 512) launch_down_fa<4, 16>(a, st); else launch_down_fa<4, 32>(a, st);
+  } else {
+    if (I == 512) launch_down_fa<3, 16>(a, st); else launch_down_fa<3, 32>(a, st);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace smoe

@@ -51,6 +51,45 @@ struct RouteOut {
 
 BlobGeom blob_geom(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t bits);
 
+// One decode layer for the three-kernel path (fused.hip).
+struct FusedLayer {
+  const float* x_in;       // x given as is, or null: x = RMSNorm(resid) * norm
+  const float* resid;      // residual r (when x_in is null)
+  const uint16_t* norm;    // bf16 RMSNorm weights, or null: x = r
+  float eps;
+  float* x_out;            // x staged for the expert kernel (when x_in is null)
+  const float* router;     // f32 [E, hidden]
+  const float* gate;       // f32 [hidden] shared-expert gate, or null (unscaled)
+  const uint8_t* experts;  // expert e at experts + e * stride
+  uint64_t stride;
+  const uint8_t* shared;   // 4-bit shared expert blob, or null
+  BlobGeom routed, sgeom;  // routed / shared (4-bit) geometry
+  uint32_t E, k, normalize;
+  float* logits;           // [E + 1]: router logits, shared gate score at E
+  float* act;              // [(k + 1) * inter]: routed slots, shared at slot k
+  FfnTable* table;         // route table of this token
+  const float* h_mid;      // residual added by the combine
+  float* out;              // hidden out (may alias h_mid / resid)
+  int32_t* idx_out;        // [k] exact slot order, or null
+  float* w_out;            // [k], or null
+  uint64_t* trace;         // per-block timestamps of this layer, or null
+};
+
+// Trace layout of the three-kernel path: per layer kFaTraceLayer words;
+// kernel q (0 route, 1 gate/up, 2 down), block b at
+// [(q * kFaTraceBlocks + b) * 8 + point]. Points: 0 start, 1 routing input
+// landed (gate/up: logits; down: expert pointers), 2 top-k set known
+// (gate/up), 3 weights landed, 4 arithmetic done, 5 stores acknowledged.
+constexpr uint32_t kFaTraceBlocks = 4096;
+constexpr uint32_t kFaTracePoints = 8;
+constexpr uint64_t kFaTraceLayer = 3ull * kFaTraceBlocks * kFaTracePoints;
+
+bool fused_supported(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t bits,
+                     uint32_t n_experts, uint32_t k);
+// K_A (router + shared gate/up), K_B (top-k + routed gate/up), K_C (down +
+// combine) on `st`; no allocation, no memset (graph-capturable).
+hipError_t launch_fused_layer(const FusedLayer& a, hipStream_t st);
+
 // All launchers return hipSuccess or the launch error; `*unsupported`
 // is set when no kernel instance exists for the shape.
 hipError_t launch_qmv(const QView& w, const float* x, float* y, uint32_t out_dim, uint32_t in_dim,

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import oracle
-from helpers import expert_pair, gen_expert_blob, gen_quant_matrix, rel_err
+from helpers import bf16, expert_pair, gen_expert_blob, gen_quant_matrix, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -328,8 +328,9 @@ def _layer_case(kernels, H, I, E, k, bits, normalize, shared, seed):
         slay = sa.ExpertLayout(H, I, 4, 64)
         sh_blob = torch.empty(slay.expert_size, dtype=torch.uint8, device="cuda")
         assert kernels.synth_experts(sh_blob, 1, slay.expert_size, slay, seed + 4) == 0
-        sh_gate = torch.empty(H, dtype=torch.float32, device="cuda")
-        assert kernels.synth_normal_f32(sh_gate, seed + 5, 0.02) == 0
+        if shared != "ungated":
+            sh_gate = torch.empty(H, dtype=torch.float32, device="cuda")
+            assert kernels.synth_normal_f32(sh_gate, seed + 5, 0.02) == 0
     L = kernels.layer(lay, arena, stride, E, k, normalize, router_w, sh_blob, sh_gate)
     out = torch.empty(H, dtype=torch.float32, device="cuda")
     idx = torch.empty(k, dtype=torch.int32, device="cuda")
@@ -349,11 +350,16 @@ LAYER_CASES = [
     ("a3b-3bit", 2048, 512, 256, 8, 3, True, True),  # config 3
     ("a3b-noshared", 2048, 512, 256, 8, 4, True, False),
     ("k4-e128", 2048, 512, 128, 4, 4, False, True),
-    ("k16", 2048, 512, 128, 16, 4, True, True),      # beyond the persistent kernel: per-phase path
+    ("k16", 2048, 512, 128, 16, 4, True, True),      # beyond the persistent kernel
+    ("a3b-ungated", 2048, 512, 256, 8, 4, True, "ungated"),  # shared expert added unscaled
+    ("olmoe-3bit-e32", 2048, 1024, 32, 2, 3, True, False),
 ]
 
+PATHS = [1, 2, 3]
+PATH_IDS = ["per-phase", "persistent", "three-kernel"]
 
-@pytest.mark.parametrize("path", [1, 2], ids=["per-phase", "persistent"])
+
+@pytest.mark.parametrize("path", PATHS, ids=PATH_IDS)
 @pytest.mark.parametrize("name,H,I,E,k,bits,normalize,shared", LAYER_CASES)
 def test_moe_decode_layer_matches_oracle(kernels, path, name, H, I, E, k, bits, normalize, shared):
     from streamoe_amd import _abi
@@ -416,61 +422,138 @@ def test_persistent_repeated_launches_are_identical(kernels):
         kernels.set_decode_path(0)
 
 
-@pytest.mark.parametrize("path", [1, 2], ids=["per-phase", "persistent"])
-def test_decode_40_layers_matches_oracle_chain(kernels, path):
-    """Config 2 at full size: 40 resident layers (256 experts each, 18 GB),
-    one token; between layers x = RMSNorm(residual) with unit bf16 weights.
-    The CPU chain fetches only the experts its router picks. Routing must
-    agree at every layer (the k-th/(k+1)-th probability gap is reported)
-    and the final residual within 1e-3."""
+def _chain(kernels, NL, E, k, bits, seed, norm_sigma=0.0, I=512, H=2048):
+    """NL resident config-2-style layers (routed `bits`, 4-bit shared expert
+    with gate) and per-layer bf16 RMSNorm weights 1 + N(0, norm_sigma)."""
     import streamoe_amd as sa
 
     torch = _torch()
-    H, I, E, k, NL = 2048, 512, 256, 8, 40
-    lay = sa.ExpertLayout(H, I, 4, 64)
+    lay = sa.ExpertLayout(H, I, bits, 64)
+    slay = sa.ExpertLayout(H, I, 4, 64)
     stride = lay.expert_size
-    arenas, routers, shareds, gates, layers = [], [], [], [], []
+    rng = np.random.default_rng(seed)
+    c = dict(H=H, I=I, E=E, k=k, bits=bits, stride=stride, sstride=slay.expert_size, arenas=[], routers=[],
+             shareds=[], gates=[], norms=[], layers=[])
     for l in range(NL):
         a = torch.empty(E * stride, dtype=torch.uint8, device="cuda")
-        assert kernels.synth_experts(a, E, stride, lay, 5000 + l) == 0
+        assert kernels.synth_experts(a, E, stride, lay, seed + 100 * l + 1) == 0
         r = torch.empty((E, H), dtype=torch.float32, device="cuda")
-        assert kernels.synth_normal_f32(r, 6000 + l, 0.02) == 0
-        s = torch.empty(stride, dtype=torch.uint8, device="cuda")
-        assert kernels.synth_experts(s, 1, stride, lay, 7000 + l) == 0
+        assert kernels.synth_normal_f32(r, seed + 100 * l + 2, 0.02) == 0
+        s_ = torch.empty(slay.expert_size, dtype=torch.uint8, device="cuda")
+        assert kernels.synth_experts(s_, 1, slay.expert_size, slay, seed + 100 * l + 3) == 0
         g = torch.empty(H, dtype=torch.float32, device="cuda")
-        assert kernels.synth_normal_f32(g, 8000 + l, 0.02) == 0
-        arenas.append(a), routers.append(r), shareds.append(s), gates.append(g)
-        layers.append(kernels.layer(lay, a, stride, E, k, True, r, s, g))
-    ones = torch.full((H,), 0x3F80, dtype=torch.int16, device="cuda")
+        assert kernels.synth_normal_f32(g, seed + 100 * l + 4, 0.02) == 0
+        nw = bf16(1.0 + norm_sigma * rng.standard_normal(H)).view(np.int16)
+        c["arenas"].append(a), c["routers"].append(r), c["shareds"].append(s_), c["gates"].append(g)
+        c["norms"].append(torch.from_numpy(nw.copy()).cuda())
+        c["layers"].append(kernels.layer(lay, a, stride, E, k, True, r, s_, g))
     x0 = torch.empty(H, dtype=torch.float32, device="cuda")
-    assert kernels.synth_normal_f32(x0, 9000, 1.0) == 0
-    resid = x0.clone()
-    work = torch.empty(H, dtype=torch.float32, device="cuda")
+    assert kernels.synth_normal_f32(x0, seed + 99, 1.0) == 0
+    c["x0"] = x0
+    return c
+
+
+def _chain_oracle(c, eps):
+    """The CPU chain: the oracle router, only the chosen experts' FFNs, the
+    combine; x_{l+1} = RMSNorm(r_{l+1}) * w_{l+1}. Returns (residual, min
+    k-th/(k+1)-th probability gap)."""
+    H, I, k, stride, bits = c["H"], c["I"], c["k"], c["stride"], c["bits"]
+    r = host(c["x0"]).copy()
+    x = r.copy()
+    min_gap = 1.0
+    for l in range(len(c["layers"])):
+        if l > 0:
+            x = oracle.rms_norm_bf16(r, host(c["norms"][l]).view(np.uint16), eps)
+        logits = oracle.f32_matvec(host(c["routers"][l]), x)
+        p = np.sort(oracle.softmax(logits))[::-1]
+        min_gap = min(min_gap, float(p[k - 1] - p[k]))
+        _, idx, w = oracle.router(logits, k, True)
+        arena = c["arenas"][l]
+        outs = np.stack([oracle.expert_swiglu(host(arena[int(e) * stride:(int(e) + 1) * stride]), bits, H, I, 64, x)
+                         for e in idx])
+        sh = oracle.expert_swiglu(host(c["shareds"][l]), 4, H, I, 64, x)
+        score = oracle.f32_matvec(host(c["gates"][l])[None, :], x)[0]
+        r = oracle.combine(outs, w, r, sh, score)
+    return r, min_gap
+
+
+@pytest.mark.parametrize("bits", [4, 3])
+@pytest.mark.parametrize("path", PATHS, ids=PATH_IDS)
+def test_decode_chain_with_norm_weights(kernels, path, bits):
+    """Four layers with non-unit RMSNorm weights between them (the norm is
+    computed inside the router kernel on the three-kernel path)."""
+    torch = _torch()
+    c = _chain(kernels, 4, 256, 8, bits, seed=4242 + bits, norm_sigma=0.1)
+    resid = c["x0"].clone()
+    work = torch.empty(c["H"], dtype=torch.float32, device="cuda")
     kernels.set_decode_path(path)
     try:
-        assert kernels.moe_decode_layers(layers, [ones] * NL, 1e-6, x0, resid, work) == 0
+        assert kernels.moe_decode_layers(c["layers"], c["norms"], 1e-6, c["x0"], resid, work) == 0
+        kernels.sync()
+    finally:
+        kernels.set_decode_path(0)
+    want, gap = _chain_oracle(c, 1e-6)
+    err = rel_err(host(resid), want)
+    print(f"norm chain path={path} bits={bits}: rel_err={err:.3e} min gap={gap:.3e}")
+    assert err <= TOL
+
+
+def test_three_kernel_decode_graph_replays_match_eager(kernels):
+    """The three-kernel decode allocates nothing and sets no memory, so it
+    can live in a HIP graph. Every replay, with eager work (the residual
+    reset) and a synchronisation between replays, gives the eager result
+    bit for bit."""
+    import streamoe_amd as sa
+
+    torch = _torch()
+    c = _chain(kernels, 4, 256, 8, 4, seed=777, norm_sigma=0.1)
+    resid = torch.empty_like(c["x0"])
+    work = torch.empty(c["H"], dtype=torch.float32, device="cuda")
+
+    def step():
+        assert kernels.moe_decode_layers(c["layers"], c["norms"], 1e-6, c["x0"], resid, work) == 0
+
+    kernels.set_decode_path(3)
+    try:
+        resid.copy_(c["x0"])
+        step()
+        kernels.sync()
+        ref = host(resid).view(np.uint32).copy()
+        resid.copy_(c["x0"])
+        graph = sa.capture_graph(kernels, step)
+        for i in range(4):
+            resid.copy_(c["x0"])
+            graph.replay()
+            torch.cuda.synchronize()
+            got = host(resid).view(np.uint32)
+            assert np.array_equal(got, ref), f"replay {i} differs from the eager result"
+        kernels.sync()
+    finally:
+        kernels.set_decode_path(0)
+
+
+@pytest.mark.parametrize("path", PATHS, ids=PATH_IDS)
+def test_decode_40_layers_matches_oracle_chain(kernels, path):
+    """Config 2 at full size: 40 resident layers (256 experts each, 18 GB),
+    one token; between layers x = RMSNorm(residual) with unit bf16 weights.
+    The CPU chain fetches only the experts its router picks. The final
+    residual must agree within 1e-3 (the smallest k-th/(k+1)-th
+    probability gap over the layers is reported)."""
+    torch = _torch()
+    c = _chain(kernels, 40, 256, 8, 4, seed=5000)
+    resid = c["x0"].clone()
+    work = torch.empty(c["H"], dtype=torch.float32, device="cuda")
+    kernels.set_decode_path(path)
+    try:
+        assert kernels.moe_decode_layers(c["layers"], c["norms"], 1e-6, c["x0"], resid, work) == 0
         kernels.sync()
     finally:
         kernels.set_decode_path(0)
     got = host(resid)
-    # CPU chain.
-    r = host(x0).copy()
-    x = r.copy()
-    w1 = np.full(H, 0x3F80, np.uint16)
-    min_gap = 1.0
-    for l in range(NL):
-        if l > 0:
-            x = oracle.rms_norm_bf16(r, w1, 1e-6)
-        logits = oracle.f32_matvec(host(routers[l]), x)
-        p = np.sort(oracle.softmax(logits))[::-1]
-        min_gap = min(min_gap, float(p[k - 1] - p[k]))
-        _, idx, w = oracle.router(logits, k, True)
-        outs = np.stack([oracle.expert_swiglu(host(arenas[l][int(e) * stride:(int(e) + 1) * stride]), 4, H, I, 64, x)
-                         for e in idx])
-        sh = oracle.expert_swiglu(host(shareds[l]), 4, H, I, 64, x)
-        score = oracle.f32_matvec(host(gates[l])[None, :], x)[0]
-        r = oracle.combine(outs, w, r, sh, score)
-    err = rel_err(got, r)
+    want, min_gap = _chain_oracle(c, 1e-6)
+    err = rel_err(got, want)
     print(f"40-layer chain path={path}: rel_err={err:.3e} min top-k gap={min_gap:.3e}")
     assert np.all(np.isfinite(got))
     assert err <= TOL
+    del c
+    torch.cuda.empty_cache()
