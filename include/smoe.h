@@ -135,8 +135,9 @@ typedef struct {
 int smoe_qmv(smoe_handle* h, const smoe_qweights* w, const float* x, float* y, uint32_t out_dim,
              uint32_t in_dim);
 
-/* Greedy argmax of a device f32[n] (first index wins on ties) into a
- * device int32. The LM head's token pick. */
+/* Greedy argmax of a device f32[n] (16-byte aligned; first index wins on
+ * ties, as a sequential scan) into a device int32. The LM head's token
+ * pick. Two launches: 256 slice blocks, then one block over the partials. */
 int smoe_argmax(smoe_handle* h, const float* v, uint32_t n, int32_t* out_index);
 
 /* Dequantize rows [row0, row0 + n_rows) of `w` into device

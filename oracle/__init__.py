@@ -78,6 +78,15 @@ def _c(a, dt):
     return np.ascontiguousarray(a, dtype=dt)
 
 
+def _words(a):
+    """Packed 4-bit codes as little-endian u32 words; a byte array is
+    reinterpreted (not converted element by element)."""
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint8:
+        return a.view(np.uint32)
+    return _c(a, np.uint32)
+
+
 class OrcLayer(C.Structure):
     _fields_ = [
         ("hidden", _U32), ("inter", _U32), ("n_experts", _U32), ("k", _U32), ("group", _U32),
@@ -110,14 +119,14 @@ def expert_offsets(hidden, inter, bits, group, block):
 
 # ---- dequant / matvec ------------------------------------------------------
 def dequant_4bit(packed, scales, biases, in_dim, out_dim, group):
-    packed, scales, biases = _c(packed, np.uint32), _c(scales, np.uint16), _c(biases, np.uint16)
+    packed, scales, biases = _words(packed), _c(scales, np.uint16), _c(biases, np.uint16)
     out = np.empty((out_dim, in_dim), np.float32)
     lib().orc_dequant_4bit(_p(packed), _p(scales), _p(biases), in_dim, out_dim, group, _p(out))
     return out
 
 
 def dequant_matvec_4bit_gs(packed, scales, biases, in_dim, out_dim, group, x, nthreads=0):
-    packed, scales, biases = _c(packed, np.uint32), _c(scales, np.uint16), _c(biases, np.uint16)
+    packed, scales, biases = _words(packed), _c(scales, np.uint16), _c(biases, np.uint16)
     x = _c(x, np.float32)
     out = np.empty(out_dim, np.float32)
     rc = lib().orc_dequant_matvec_4bit_gs(_p(packed), _p(scales), _p(biases), in_dim, out_dim,
@@ -126,7 +135,7 @@ def dequant_matvec_4bit_gs(packed, scales, biases, in_dim, out_dim, group, x, nt
 
 
 def lm_head(packed, scales, biases, hidden, vocab, group, x):
-    packed, scales, biases = _c(packed, np.uint32), _c(scales, np.uint16), _c(biases, np.uint16)
+    packed, scales, biases = _words(packed), _c(scales, np.uint16), _c(biases, np.uint16)
     x = _c(x, np.float32)
     out = np.empty(vocab, np.float32)
     rc = lib().orc_lm_head(_p(packed), _p(scales), _p(biases), hidden, vocab, group, _p(x), _p(out))
@@ -148,7 +157,7 @@ def argmax(v):
 
 # ---- 3-bit ------------------------------------------------------------------
 def pack_3bit(words4):
-    words4 = _c(words4, np.uint32).ravel()
+    words4 = _words(words4).ravel()
     out = np.empty(words4.size * 3, np.uint8)
     lib().orc_pack_3bit(_p(words4), words4.size, _p(out))
     return out

@@ -7,7 +7,9 @@ import ctypes as C
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libsmoe.so")
+# SMOE_LIB names another build of the same library (e.g. one compiled with
+# different kernel tunables); the default is the in-tree build.
+LIB_PATH = os.environ.get("SMOE_LIB") or os.path.join(HERE, "libsmoe.so")
 
 SMOE_MAX_K = 16
 

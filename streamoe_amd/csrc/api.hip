@@ -20,6 +20,9 @@ struct smoe_handle {
   float* logits = nullptr;    // [max_experts + 1]
   float* gate = nullptr;      // [1] shared-expert gate score
   FfnTable* table = nullptr;  // routing table of the current token
+  uint32_t* xl = nullptr;     // [max_hidden / 32 * kXLimbWords] x as integer limbs
+  float* arg_v = nullptr;     // [256] argmax partial values
+  uint32_t* arg_i = nullptr;  // [256] argmax partial indices
   // Persistent decode: tagged handoff buffers (epoch << 32 | value).
   uint64_t* tag_resid = nullptr;  // [max_hidden]
   uint64_t* tag_logit = nullptr;  // [max_experts + 1]
@@ -71,9 +74,11 @@ int reserve(smoe_handle* h, uint32_t H, uint32_t I, uint32_t E) {
   const size_t act_b = al((size_t)kMaxSlotsHost * I * sizeof(float));
   const size_t log_b = al(((size_t)E + 1) * sizeof(float));
   const size_t tab_b = al(sizeof(FfnTable));
+  const size_t xl_b = al((size_t)H / 32 * 32 * sizeof(uint32_t));
   const size_t tr_b = al((size_t)H * 8), tl_b = al(((size_t)E + 1) * 8);
   const size_t ta_b = al((size_t)kMaxSlotsHost * I * 8), tro_b = al(32 * 8);
-  const size_t total = act_b + log_b + 256 + tab_b + tr_b + tl_b + ta_b + tro_b + 256;
+  const size_t arg_b = 2 * 256 * sizeof(uint32_t);
+  const size_t total = act_b + log_b + 256 + tab_b + xl_b + arg_b + tr_b + tl_b + ta_b + tro_b + 256;
   void* mem = nullptr;
   if (hipSetDevice(h->device) != hipSuccess) return SMOE_ERR_HIP;
   if (hipMalloc(&mem, total) != hipSuccess) return SMOE_ERR_HIP;
@@ -92,6 +97,11 @@ int reserve(smoe_handle* h, uint32_t H, uint32_t I, uint32_t E) {
   h->gate = (float*)(p + act_b + log_b);
   h->table = (FfnTable*)(p + act_b + log_b + 256);
   char* q = p + act_b + log_b + 256 + tab_b;
+  h->xl = (uint32_t*)q;
+  q += xl_b;
+  h->arg_v = (float*)q;
+  h->arg_i = (uint32_t*)(q + 256 * sizeof(float));
+  q += arg_b;
   h->tag_resid = (uint64_t*)q;
   q += tr_b;
   h->tag_logit = (uint64_t*)q;
@@ -238,8 +248,9 @@ int smoe_qmv(smoe_handle* h, const smoe_qweights* w, const float* x, float* y, u
 
 int smoe_argmax(smoe_handle* h, const float* v, uint32_t n, int32_t* out_index) {
   if (!h || !v || !n || !out_index) return SMOE_ERR_INVALID_ARG;
+  if (!aligned(v, 0, 16)) return SMOE_ERR_MISALIGNED;
   if (int rc = use_device(h)) return rc;
-  return hip_status(launch_argmax(v, n, out_index, h->stream));
+  return hip_status(launch_argmax(v, n, out_index, h->arg_v, h->arg_i, h->stream));
 }
 
 int smoe_dequant(smoe_handle* h, const smoe_qweights* w, uint32_t in_dim, uint32_t row0,
@@ -409,7 +420,8 @@ static int decode_fused(smoe_handle* h, const smoe_layer* L, const float* x_in, 
   a.resid = resid;
   a.norm = norm;
   a.eps = eps;
-  a.x_out = x_out;
+  a.xl = h->xl;
+  (void)x_out;
   a.router = L->router_w;
   a.shared = (const uint8_t*)L->shared_expert;
   a.gate = L->shared_expert ? L->shared_gate : nullptr;

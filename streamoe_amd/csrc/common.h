@@ -44,12 +44,25 @@ constexpr int chunk_bytes() {
 }
 
 // Weights are streamed once per decode step: load them non-temporally so
-// they do not evict the activations and routing data from L2.
+// they do not evict the activations and routing data from L2
+// (SMOE_NT_LOADS=0 builds plain loads, for cache experiments).
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+#ifndef SMOE_NT_LOADS
+#define SMOE_NT_LOADS 1
+#endif
+template <typename T>
+__device__ __forceinline__ T ld_stream(const T* p) {
+#if SMOE_NT_LOADS
+  return __builtin_nontemporal_load(p);
+#else
+  return *p;
+#endif
+}
+
 __device__ __forceinline__ Raw<4> load_raw4(const uint8_t* p) {
-  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  const u32x4 v = ld_stream(reinterpret_cast<const u32x4*>(p));
   Raw<4> r;
   r.d[0] = v.x;
   r.d[1] = v.y;
@@ -60,9 +73,9 @@ __device__ __forceinline__ Raw<4> load_raw4(const uint8_t* p) {
 __device__ __forceinline__ Raw<3> load_raw3(const uint8_t* p) {
   const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
   Raw<3> r;
-  r.d[0] = __builtin_nontemporal_load(q + 0);
-  r.d[1] = __builtin_nontemporal_load(q + 1);
-  r.d[2] = __builtin_nontemporal_load(q + 2);
+  r.d[0] = ld_stream(q + 0);
+  r.d[1] = ld_stream(q + 1);
+  r.d[2] = ld_stream(q + 2);
   return r;
 }
 template <int BITS>
@@ -223,5 +236,142 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 }
 
 __device__ __forceinline__ float sigmoidf_ref(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// ---------------------------------------------------------------------------
+// Integer chunk dot product.
+//
+// A chunk of activations x[0..32) is written as 24-bit block floating
+// point, x_j ~= m_j * 2^-f with one exponent per chunk (|m_j| <= 2^22, i.e.
+// relative rounding 2^-23 of the chunk's largest |x|), and m_j is split
+// into three signed 8-bit limbs, m = d0 + 2^8 d1 + 2^16 d2. The codes are
+// unpacked to bytes, and v_dot4c_i32_i8 accumulates sum_j q_j d_Lj exactly
+// in int32 (|sum| <= 32 * 15 * 128). The dot product is then
+//     sum_j q_j x_j = 2^-f * (S0 + 2^8 S1 + 2^16 S2)
+// rounded once or twice at f32 precision: 1.1 VALU ops per 4-bit weight
+// instead of 2.4 for convert-and-FMA.
+//
+// Byte order: code word i (inputs 8i .. 8i+7) unpacks to lo = bytes
+// [q(8i), q(8i+2), q(8i+4), q(8i+6)] and hi = [q(8i+1), q(8i+3), q(8i+5),
+// q(8i+7)] (4-bit: nibble masks; 3-bit pack i: 6-bit fields spread to
+// bytes). Limb word 2i holds the lo order, word 2i+1 the hi order.
+// ---------------------------------------------------------------------------
+struct XLimbs {
+  uint32_t w[3][8];  // limb L, word 2i (lo order) / 2i+1 (hi order)
+  float scale;       // 2^-f
+  float xs;          // sum_j x_j (f32, for the bias term)
+};
+constexpr int kXLimbWords = 32;  // dwords per chunk in memory: 24 limbs, scale, xs, pad
+
+__device__ __forceinline__ uint32_t pack_bytes(int32_t a, int32_t b, int32_t c, int32_t d) {
+  return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) |
+         ((uint32_t)d << 24);
+}
+
+__device__ __forceinline__ void make_limbs(const float (&x)[kChunk], XLimbs& o) {
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < kChunk; ++j) amax = fmaxf(amax, fabsf(x[j]));
+  // |x| < 2^E with E the frexp exponent of amax; scale to |m| < 2^22.
+  const int f = amax > 0.f ? 22 - __builtin_amdgcn_frexp_expf(amax) : 0;
+  int32_t d[3][kChunk];
+#pragma unroll
+  for (int j = 0; j < kChunk; ++j) {
+    const int32_t m = (int32_t)__builtin_rintf(__builtin_ldexpf(x[j], f));
+    const int32_t d0 = (m << 24) >> 24;
+    const int32_t m1 = (m - d0) >> 8;
+    const int32_t d1 = (m1 << 24) >> 24;
+    d[0][j] = d0;
+    d[1][j] = d1;
+    d[2][j] = (m1 - d1) >> 8;
+  }
+#pragma unroll
+  for (int L = 0; L < 3; ++L)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o.w[L][2 * i] = pack_bytes(d[L][8 * i], d[L][8 * i + 2], d[L][8 * i + 4], d[L][8 * i + 6]);
+      o.w[L][2 * i + 1] = pack_bytes(d[L][8 * i + 1], d[L][8 * i + 3], d[L][8 * i + 5], d[L][8 * i + 7]);
+    }
+  o.scale = __builtin_ldexpf(1.0f, -f);
+  o.xs = xsum(x);
+}
+
+// Codes of a chunk as bytes in the order above.
+__device__ __forceinline__ void unpack_bytes(const Raw<4>& r, uint32_t (&b)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    b[2 * i] = r.d[i] & 0x0F0F0F0Fu;
+    b[2 * i + 1] = (r.d[i] >> 4) & 0x0F0F0F0Fu;
+  }
+}
+
+__device__ __forceinline__ void unpack_bytes(const Raw<3>& r, uint32_t (&b)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    // 24-bit pack i of the 96-bit chunk.
+    uint32_t p;
+    if (i == 0)
+      p = r.d[0];
+    else if (i == 1)
+      p = __builtin_amdgcn_alignbit(r.d[1], r.d[0], 24);
+    else if (i == 2)
+      p = __builtin_amdgcn_alignbit(r.d[2], r.d[1], 16);
+    else
+      p = r.d[2] >> 8;
+    // 6-bit field k (codes 2k, 2k+1) to byte k.
+    const uint32_t t = (p & 0x3Fu) | ((p & 0xFC0u) << 2) | ((p & 0x3F000u) << 4) | ((p & 0xFC0000u) << 6);
+    b[2 * i] = t & 0x07070707u;
+    b[2 * i + 1] = (t >> 3) & 0x07070707u;
+  }
+}
+
+// s * sum_j q_j x_j + b * sum_j x_j for one chunk.
+template <int BITS>
+__device__ __forceinline__ float chunk_dot_i(const Raw<BITS>& raw, const XLimbs& xl, float s, float b) {
+  uint32_t q[8];
+  unpack_bytes(raw, q);
+  int32_t S0 = 0, S1 = 0, S2 = 0;
+#pragma unroll
+  for (int w = 0; w < 8; ++w) {
+    S0 = __builtin_amdgcn_sdot4((int)q[w], (int)xl.w[0][w], S0, false);
+    S1 = __builtin_amdgcn_sdot4((int)q[w], (int)xl.w[1][w], S1, false);
+    S2 = __builtin_amdgcn_sdot4((int)q[w], (int)xl.w[2][w], S2, false);
+  }
+  const float t = __builtin_fmaf((float)S2, 65536.0f, __builtin_fmaf((float)S1, 256.0f, (float)S0));
+  return __builtin_fmaf(s, t * xl.scale, b * xl.xs);
+}
+
+__device__ __forceinline__ void load_limbs(const uint32_t* p, XLimbs& o) {
+  const u32x4* p4 = reinterpret_cast<const u32x4*>(p);
+  u32x4 v[7];
+#pragma unroll
+  for (int i = 0; i < 7; ++i) v[i] = p4[i];
+#pragma unroll
+  for (int i = 0; i < 6; ++i) {
+    const uint32_t e[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) o.w[(4 * i + c) / 8][(4 * i + c) % 8] = e[c];
+  }
+  o.scale = __uint_as_float(v[6].x);
+  o.xs = __uint_as_float(v[6].y);
+}
+
+__device__ __forceinline__ void store_limbs(uint32_t* p, const XLimbs& o) {
+  u32x4* p4 = reinterpret_cast<u32x4*>(p);
+#pragma unroll
+  for (int i = 0; i < 6; ++i) {
+    u32x4 v;
+    v.x = o.w[(4 * i) / 8][(4 * i) % 8];
+    v.y = o.w[(4 * i + 1) / 8][(4 * i + 1) % 8];
+    v.z = o.w[(4 * i + 2) / 8][(4 * i + 2) % 8];
+    v.w = o.w[(4 * i + 3) / 8][(4 * i + 3) % 8];
+    p4[i] = v;
+  }
+  u32x4 t;
+  t.x = __float_as_uint(o.scale);
+  t.y = __float_as_uint(o.xs);
+  t.z = 0;
+  t.w = 0;
+  p4[6] = t;
+}
 
 }  // namespace smoe

@@ -58,12 +58,13 @@ __global__ __launch_bounds__(256) void k_qmv(const uint8_t* __restrict__ codes,
   const uint32_t gpr = CPR * kChunk / group;  // groups per row
   const uint32_t cpg_shift = __builtin_ctz(group / kChunk);
 
-  float xr[CPL][kChunk];
-  float xs[CPL];
+  // x in integer-limb form, built once per wave and reused for every row.
+  XLimbs xl[CPL];
 #pragma unroll
   for (int i = 0; i < CPL; ++i) {
-    load_x32(x + (size_t)(lch + L * i) * kChunk, xr[i]);
-    xs[i] = xsum(xr[i]);
+    float xr[kChunk];
+    load_x32(x + (size_t)(lch + L * i) * kChunk, xr);
+    make_limbs(xr, xl[i]);
   }
 
   constexpr uint32_t STEP_ROWS = RPP * U;
@@ -101,7 +102,7 @@ __global__ __launch_bounds__(256) void k_qmv(const uint8_t* __restrict__ codes,
     for (int u = 0; u < U; ++u) {
       float part = 0.f;
 #pragma unroll
-      for (int i = 0; i < CPL; ++i) part += chunk_dot<BITS>(cur[u][i], xr[i], xs[i], cs[u][i], cb[u][i]);
+      for (int i = 0; i < CPL; ++i) part += chunk_dot_i<BITS>(cur[u][i], xl[i], cs[u][i], cb[u][i]);
       const float sum = group_sum<L>(part);
       const uint32_t row = step * STEP_ROWS + u * RPP + lrow;
       if (lch == 0 && row < rows) y[row] = sum;
@@ -124,7 +125,9 @@ static hipError_t qmv_inst(const QView& w, const float* x, float* y, uint32_t ro
                            hipStream_t st) {
   constexpr int L = CPR < kWave ? CPR : kWave;
   constexpr int RPP = kWave / L;
-  constexpr int U = 4;
+  // Rows in flight per wave and step: HBM latency (~2 us under load) times
+  // the target bandwidth needs ~12 MB in flight over the 2048 waves.
+  constexpr int U = RPP == 1 ? 8 : 4;
   const uint32_t n_steps = (rows + RPP * U - 1) / (RPP * U);
   // Persistent grid: up to 8 waves per CU on 256 CUs.
   uint32_t n_waves = n_steps < 2048u ? n_steps : 2048u;
@@ -196,31 +199,29 @@ hipError_t launch_dequant(const QView& w, uint32_t in_dim, uint32_t row0, uint32
 }
 
 // ---------------------------------------------------------------------------
-// Argmax (first index on ties), one block.
+// Argmax (first index on ties) in two stages: kArgBlocks blocks each reduce
+// a contiguous slice with 128-bit loads to (value, index), then one block
+// reduces the partials. (value, index) pairs order by value, then by lower
+// index, so the result is the first maximal index, as a sequential scan.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ v, uint32_t n,
-                                                 int32_t* __restrict__ out) {
+constexpr uint32_t kArgBlocks = 256;
+
+__device__ __forceinline__ void argmax_merge(float& bv, uint32_t& bi, float v, uint32_t i) {
+  if (v > bv || (v == bv && i < bi)) {
+    bv = v;
+    bi = i;
+  }
+}
+
+// Block-wide (value, index) reduction; result valid in thread 0.
+__device__ __forceinline__ void argmax_block(float& best, uint32_t& bi) {
   __shared__ float sv[16];
   __shared__ uint32_t si[16];
-  float best = -INFINITY;
-  uint32_t bi = 0xFFFFFFFFu;
-  for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
-    const float x = v[i];
-    if (x > best || bi == 0xFFFFFFFFu) {
-      if (bi == 0xFFFFFFFFu || x > best) {
-        best = x;
-        bi = i;
-      }
-    }
-  }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     const float ob = __shfl_xor(best, o, 64);
     const uint32_t oi = __shfl_xor(bi, o, 64);
-    if (ob > best || (ob == best && oi < bi)) {
-      best = ob;
-      bi = oi;
-    }
+    argmax_merge(best, bi, ob, oi);
   }
   const int w = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) {
@@ -228,18 +229,47 @@ __global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ v, ui
     si[w] = bi;
   }
   __syncthreads();
+  if (threadIdx.x == 0)
+    for (int i = 1; i < (int)(blockDim.x >> 6); ++i) argmax_merge(best, bi, sv[i], si[i]);
+}
+
+__global__ __launch_bounds__(256) void k_argmax_part(const float* __restrict__ v, uint32_t n,
+                                                     float* __restrict__ pv, uint32_t* __restrict__ pi) {
+  const uint32_t per = ((n + kArgBlocks - 1) / kArgBlocks + 3) & ~3u;  // multiple of 4
+  const uint32_t lo = blockIdx.x * per, hi = min(n, lo + per);
+  float best = -INFINITY;
+  uint32_t bi = 0xFFFFFFFFu;
+  for (uint32_t i = lo + threadIdx.x * 4; i < hi; i += blockDim.x * 4) {
+    if (i + 3 < hi) {
+      const float4 q = *reinterpret_cast<const float4*>(v + i);
+      argmax_merge(best, bi, q.x, i);
+      argmax_merge(best, bi, q.y, i + 1);
+      argmax_merge(best, bi, q.z, i + 2);
+      argmax_merge(best, bi, q.w, i + 3);
+    } else {
+      for (uint32_t j = i; j < hi; ++j) argmax_merge(best, bi, v[j], j);
+    }
+  }
+  argmax_block(best, bi);
   if (threadIdx.x == 0) {
-    for (int i = 1; i < (int)(blockDim.x >> 6); ++i)
-      if (sv[i] > best || (sv[i] == best && si[i] < bi)) {
-        best = sv[i];
-        bi = si[i];
-      }
-    *out = (int32_t)bi;
+    pv[blockIdx.x] = best;
+    pi[blockIdx.x] = bi;
   }
 }
 
-hipError_t launch_argmax(const float* v, uint32_t n, int32_t* out, hipStream_t st) {
-  hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, st, v, n, out);
+__global__ __launch_bounds__(256) void k_argmax_final(const float* __restrict__ pv,
+                                                      const uint32_t* __restrict__ pi,
+                                                      int32_t* __restrict__ out) {
+  float best = pv[threadIdx.x];
+  uint32_t bi = pi[threadIdx.x];
+  argmax_block(best, bi);
+  if (threadIdx.x == 0) *out = (int32_t)bi;
+}
+
+hipError_t launch_argmax(const float* v, uint32_t n, int32_t* out, float* part_v, uint32_t* part_i,
+                         hipStream_t st) {
+  hipLaunchKernelGGL(k_argmax_part, dim3(kArgBlocks), dim3(256), 0, st, v, n, part_v, part_i);
+  hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(kArgBlocks), 0, st, part_v, part_i, out);
   return hipGetLastError();
 }
 

@@ -16,7 +16,8 @@
 //                      x = RMSNorm(r) * w (or the given input), then
 //                      logits[e] = W_e . x (row E: shared gate), or
 //                      act[k, i] = silu(gate_i . x) * (up_i . x) for the
-//                      shared expert.  Wave 0 stores x for K_B.
+//                      shared expert. Wave 0 stores x for K_B as integer
+//                      limbs (common.h, chunk_dot_i).
 //   K_B  k_fa_gateup   one wave per RW rows of one routed slot: softmax and
 //                      the top-k set of the logits (every wave), then
 //                      act[s, i] = silu(gate_i . x) * (up_i . x) for expert
@@ -40,17 +41,39 @@
 namespace smoe {
 
 constexpr uint32_t kFaH = 2048;              // hidden size of this path (64 lanes x 32)
-constexpr int kFaSR = 2;                     // shared-expert rows per K_A wave
-constexpr int kFaRW = 4;                     // routed rows per K_B wave
+// Work per wave / block (build-time tunables; the defaults are the measured
+// best on MI355X).
+#ifndef SMOE_FA_SR
+#define SMOE_FA_SR 2
+#endif
+#ifndef SMOE_FA_RW
+#define SMOE_FA_RW 4
+#endif
+#ifndef SMOE_FA_R
+#define SMOE_FA_R 4
+#endif
+constexpr int kFaSR = SMOE_FA_SR;            // shared-expert rows per K_A wave
+constexpr int kFaRW = SMOE_FA_RW;            // routed rows per K_B wave
 
-// Optional timestamps (100 MHz s_memrealtime) for latency analysis; with
-// `drain` the wave first waits for all its outstanding memory operations.
-__device__ __forceinline__ void fa_trace(const FusedLayer& a, int q, int point, bool drain) {
+// Optional timestamps (100 MHz s_memrealtime) for latency analysis. They
+// stay in registers until fa_flush at the end of the kernel, so tracing adds
+// no memory operation in between; with `drain` the wave first waits for all
+// its outstanding memory operations.
+struct FaClock {
+  uint64_t t[6] = {0, 0, 0, 0, 0, 0};
+};
+
+__device__ __forceinline__ void fa_stamp(const FusedLayer& a, FaClock& c, int point, bool drain) {
   if (!a.trace) return;
   if (drain) __builtin_amdgcn_s_waitcnt(0);
-  if (threadIdx.x == 0)
-    a.trace[((size_t)q * kFaTraceBlocks + blockIdx.x) * kFaTracePoints + point] =
-        __builtin_amdgcn_s_memrealtime();
+  c.t[point] = __builtin_amdgcn_s_memrealtime();
+}
+
+__device__ __forceinline__ void fa_flush(const FusedLayer& a, const FaClock& c, int q) {
+  if (!a.trace || threadIdx.x != 0) return;
+  uint64_t* d = a.trace + ((size_t)q * kFaTraceBlocks + blockIdx.x) * kFaTracePoints;
+#pragma unroll
+  for (int p = 0; p < 6; ++p) d[p] = c.t[p];
 }
 
 // Raw bf16 scale and bias of chunk c of `row` in one [rows, in_dim] block.
@@ -107,7 +130,8 @@ __device__ __forceinline__ void fa_x_finish(const FusedLayer& a, FaX& f) {
 // K_A: router logits (+ shared gate) and the shared expert's gate/up.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(64) void k_fa_route(FusedLayer a) {
-  fa_trace(a, 0, 0, false);
+  FaClock clk;
+  fa_stamp(a, clk, 0, false);
   const int lane = threadIdx.x;
   const uint32_t w = blockIdx.x;
   const uint32_t nrouter = a.E + (a.gate ? 1u : 0u);
@@ -118,17 +142,17 @@ __global__ __launch_bounds__(64) void k_fa_route(FusedLayer a) {
     f32x4 wr[kChunk / 4];
     const f32x4* rp = reinterpret_cast<const f32x4*>(row + (size_t)c * kChunk);
 #pragma unroll
-    for (int i = 0; i < kChunk / 4; ++i) wr[i] = __builtin_nontemporal_load(rp + i);
+    for (int i = 0; i < kChunk / 4; ++i) wr[i] = ld_stream(rp + i);
     FaX f;
     fa_x_load(a, lane, f);
     __builtin_amdgcn_sched_barrier(0);
-    fa_trace(a, 0, 3, true);
+    fa_stamp(a, clk, 3, true);
     fa_x_finish(a, f);
     const float(&x)[kChunk] = f.x;
-    if (w == 0 && !a.x_in) {
-      float4* xo = reinterpret_cast<float4*>(a.x_out + (size_t)c * kChunk);
-#pragma unroll
-      for (int i = 0; i < kChunk / 4; ++i) xo[i] = make_float4(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
+    if (w == 0) {
+      XLimbs xl;
+      make_limbs(x, xl);
+      store_limbs(a.xl + (size_t)c * kXLimbWords, xl);
     }
     float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
 #pragma unroll
@@ -139,9 +163,10 @@ __global__ __launch_bounds__(64) void k_fa_route(FusedLayer a) {
       a3 = __builtin_fmaf(wr[i].w, x[4 * i + 3], a3);
     }
     const float s = group_sum_last<64>((a0 + a1) + (a2 + a3));
-    fa_trace(a, 0, 4, false);
+    fa_stamp(a, clk, 4, false);
     if (lane == 63) a.logits[w] = s;
-    fa_trace(a, 0, 5, true);
+    fa_stamp(a, clk, 5, true);
+    fa_flush(a, clk, 0);
     return;
   }
 
@@ -164,7 +189,7 @@ __global__ __launch_bounds__(64) void k_fa_route(FusedLayer a) {
   FaX f;
   fa_x_load(a, lane, f);
   __builtin_amdgcn_sched_barrier(0);
-  fa_trace(a, 0, 3, true);
+  fa_stamp(a, clk, 3, true);
   fa_x_finish(a, f);
   const float(&x)[kChunk] = f.x;
   const float xs = xsum(x);
@@ -175,7 +200,8 @@ __global__ __launch_bounds__(64) void k_fa_route(FusedLayer a) {
     const float us = group_sum_last<64>(chunk_dot<4>(ru[p], x, xs, bf16f(su[p]), bf16f(bu[p])));
     if (lane == 63) act[r0 + p] = silu_mul(gs, us);
   }
-  fa_trace(a, 0, 5, true);
+  fa_stamp(a, clk, 5, true);
+  fa_flush(a, clk, 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -188,7 +214,8 @@ __global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a) {
   __shared__ int32_t sid[kMaxK];
   __shared__ float sval[kMaxK];
   __shared__ float sprob[64 * P];
-  fa_trace(a, 1, 0, false);
+  FaClock clk;
+  fa_stamp(a, clk, 0, false);
   const int lane = threadIdx.x;
   const BlobGeom& g = a.routed;
   const uint32_t I = g.inter, E = a.E, k = a.k;
@@ -196,7 +223,6 @@ __global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a) {
   const uint32_t slot = blockIdx.x / tiles;
   const uint32_t r0 = (blockIdx.x % tiles) * kFaRW;
   const uint32_t c = lane;
-  const float* xsrc = a.x_in ? a.x_in : a.x_out;
 
   float v[P];
 #pragma unroll
@@ -204,23 +230,23 @@ __global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a) {
     const uint32_t j = lane * P + e;
     v[e] = j < E ? a.logits[j] : -INFINITY;
   }
-  fa_trace(a, 1, 1, true);
-  float x[kChunk];
-  load_x32(xsrc + (size_t)c * kChunk, x);
+  fa_stamp(a, clk, 1, true);
+  XLimbs xl;
+  load_limbs(a.xl + (size_t)c * kXLimbWords, xl);
 
-  // moe_router.rs:52-72 softmax, then the top-k set (moe_router.rs:83-124
-  // keeps exactly the k largest when the k-th and (k+1)-th differ; ties,
-  // NaN and degenerate scores take the exact running-minimum scan).
-  wave_softmax<P>(v, E, lane);
-  const bool is_set = topk_set<P>(v, E, k, lane, sid);
-  __syncthreads();
+  // The top-k set from the logits (topk_set_logits: equal to the k largest
+  // softmax probabilities whenever the reference's running-minimum scan,
+  // moe_router.rs:83-124, sees no tie at the boundary). Otherwise the
+  // softmax (moe_router.rs:52-72) and the exact scan.
+  const bool is_set = topk_set_logits<P>(v, E, k, lane, sid);
   if (!is_set) {
+    wave_softmax<P>(v, E, lane);
     exact_topk<P>(v, k, lane, sid, sval);
-    __syncthreads();
   }
+  __syncthreads();
   const int32_t id = sid[slot];
   const uint8_t* blob = a.experts + (uint64_t)id * a.stride;
-  fa_trace(a, 1, 2, false);
+  fa_stamp(a, clk, 2, false);
 
   const uint32_t gpr = kFaH / g.group;
   const uint32_t cps = __builtin_ctz(g.group / kChunk);
@@ -235,11 +261,12 @@ __global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a) {
     load_sb(blob, g.s[1], g.b[1], row, gpr, cps, c, su[p], bu[p]);
   }
   __builtin_amdgcn_sched_barrier(0);
-  fa_trace(a, 1, 3, true);
+  fa_stamp(a, clk, 3, true);
 
   if (blockIdx.x == 0) {
     // Route table in the order the act slots use, weights renormalised in
     // that order (normalize_weights, moe_router.rs:130-141).
+    if (is_set) wave_softmax<P>(v, E, lane);
 #pragma unroll
     for (int e = 0; e < P; ++e) sprob[lane * P + e] = v[e];
     __syncthreads();
@@ -288,16 +315,16 @@ __global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a) {
     }
   }
 
-  const float xs = xsum(x);
   float* act = a.act + (size_t)slot * I;
 #pragma unroll
   for (int p = 0; p < kFaRW; ++p) {
-    const float gs = group_sum_last<64>(chunk_dot<BITS>(rg[p], x, xs, bf16f(sg[p]), bf16f(bg[p])));
-    const float us = group_sum_last<64>(chunk_dot<BITS>(ru[p], x, xs, bf16f(su[p]), bf16f(bu[p])));
+    const float gs = group_sum_last<64>(chunk_dot_i<BITS>(rg[p], xl, bf16f(sg[p]), bf16f(bg[p])));
+    const float us = group_sum_last<64>(chunk_dot_i<BITS>(ru[p], xl, bf16f(su[p]), bf16f(bu[p])));
     if (lane == 63) act[r0 + p] = silu_mul(gs, us);
   }
-  fa_trace(a, 1, 4, false);
-  fa_trace(a, 1, 5, true);
+  fa_stamp(a, clk, 4, false);
+  fa_stamp(a, clk, 5, true);
+  fa_flush(a, clk, 1);
 }
 
 // ---------------------------------------------------------------------------
@@ -313,10 +340,11 @@ __global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a) {
 // the reference's order: moe = fma(out_s, w_s, moe) over the routed slots,
 // then the shared term and the residual (deferred.rs:441-490).
 // ---------------------------------------------------------------------------
-constexpr int kFaR = 8;  // hidden rows per K_C block
+constexpr int kFaR = SMOE_FA_R;  // hidden rows per K_C block
 
 template <int BITS, int LI>
-__device__ __forceinline__ void down_rows(const FusedLayer& a, const uint8_t* blob, const BlobGeom& g,
+__device__ __forceinline__ void down_rows(const FusedLayer& a, FaClock& clk, const uint8_t* blob,
+                                          const BlobGeom& g,
                                           uint32_t row0, uint32_t c, const float* act_chunk,
                                           float (&o)[kFaR]) {
   constexpr int CB = chunk_bytes<BITS>();
@@ -337,7 +365,7 @@ __device__ __forceinline__ void down_rows(const FusedLayer& a, const uint8_t* bl
   load_x32(act_chunk, act);
   // Keep every load above in flight before any arithmetic.
   __builtin_amdgcn_sched_barrier(0);
-  fa_trace(a, 2, 3, true);
+  fa_stamp(a, clk, 3, true);
   const float xs = xsum(act);
 #pragma unroll
   for (int r = 0; r < kFaR; ++r)
@@ -355,7 +383,8 @@ __global__ __launch_bounds__(fa_down_threads<LI>()) void k_fa_down(FusedLayer a)
   constexpr int SPW = kWave / LI;
   __shared__ float so[kFaR][kMaxSlots];
   __shared__ float sw[kMaxSlots];
-  fa_trace(a, 2, 0, false);
+  FaClock clk;
+  fa_stamp(a, clk, 0, false);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t k = a.k;
   const uint32_t rwaves = (k + SPW - 1) / SPW;
@@ -376,23 +405,19 @@ __global__ __launch_bounds__(fa_down_threads<LI>()) void k_fa_down(FusedLayer a)
     valid = slot < k;
     const uint32_t sl = valid ? slot : 0;  // idle lanes read slot 0
     const uint8_t* blob = a.table->blob[sl];
-    if (a.trace) {
-      __builtin_amdgcn_s_waitcnt(0);
-      if (lane == 0 && wave == 0)
-        a.trace[((size_t)2 * kFaTraceBlocks + blockIdx.x) * kFaTracePoints + 1] = __builtin_amdgcn_s_memrealtime();
-    }
-    down_rows<BITS, LI>(a, blob, a.routed, row0, c, a.act + (size_t)sl * I + c * kChunk, o);
+    fa_stamp(a, clk, 1, true);
+    down_rows<BITS, LI>(a, clk, blob, a.routed, row0, c, a.act + (size_t)sl * I + c * kChunk, o);
   } else {
     slot = k;
     valid = lane < LI;
-    down_rows<4, LI>(a, a.shared, a.sgeom, row0, c, a.act + (size_t)k * I + c * kChunk, o);
+    down_rows<4, LI>(a, clk, a.shared, a.sgeom, row0, c, a.act + (size_t)k * I + c * kChunk, o);
   }
   if (c == LI - 1 && valid) {
 #pragma unroll
     for (int r = 0; r < kFaR; ++r) so[r][slot] = o[r];
   }
   if (threadIdx.x < k) sw[threadIdx.x] = wk;
-  fa_trace(a, 2, 4, false);
+  fa_stamp(a, clk, 4, false);
   __syncthreads();
   if (threadIdx.x < (unsigned)kFaR) {
     const uint32_t r = threadIdx.x;
@@ -406,7 +431,8 @@ __global__ __launch_bounds__(fa_down_threads<LI>()) void k_fa_down(FusedLayer a)
     }
     a.out[row0 + r] = hm + sum;
   }
-  fa_trace(a, 2, 5, true);
+  fa_stamp(a, clk, 5, true);
+  fa_flush(a, clk, 2);
 }
 
 // ---------------------------------------------------------------------------

@@ -57,7 +57,8 @@ struct FusedLayer {
   const float* resid;      // residual r (when x_in is null)
   const uint16_t* norm;    // bf16 RMSNorm weights, or null: x = r
   float eps;
-  float* x_out;            // x staged for the expert kernel (when x_in is null)
+  uint32_t* xl;            // x as integer limbs for the expert kernel, hidden / 32 chunks
+                           // of kXLimbWords dwords (written by the router kernel)
   const float* router;     // f32 [E, hidden]
   const float* gate;       // f32 [hidden] shared-expert gate, or null (unscaled)
   const uint8_t* experts;  // expert e at experts + e * stride
@@ -96,7 +97,9 @@ hipError_t launch_qmv(const QView& w, const float* x, float* y, uint32_t out_dim
                       hipStream_t st, bool* unsupported);
 hipError_t launch_dequant(const QView& w, uint32_t in_dim, uint32_t row0, uint32_t n_rows,
                           float* out, hipStream_t st);
-hipError_t launch_argmax(const float* v, uint32_t n, int32_t* out, hipStream_t st);
+// Argmax (first index on ties); part_v / part_i: 256-entry scratch.
+hipError_t launch_argmax(const float* v, uint32_t n, int32_t* out, float* part_v, uint32_t* part_i,
+                         hipStream_t st);
 
 // logits[t, e] = W[e] . x[t] for e < n_experts; gate_scores[t] =
 // gate_w . x[t] when gate_w is not null.

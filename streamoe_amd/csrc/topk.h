@@ -174,4 +174,93 @@ __device__ bool topk_set(const float (&v)[P], uint32_t n, uint32_t k, int lane,
 }
 
 
+// ---------------------------------------------------------------------------
+// Top-k SET straight from the logits, for the routed expert kernels.
+//
+// Softmax is monotone, so the k largest probabilities are the k largest
+// logits whenever the reference's running-minimum scan cannot see a tie
+// at the boundary. The scan keeps exactly the k largest probabilities when
+// the k-th is strictly above the (k+1)-th (moe_router.rs:83-124). With
+// e = exp(l - max), every probability is e * (1 / sum) rounded once, and a
+// positive common factor with one rounding preserves a strict order when
+// the two e values are more than 2^-20 apart relatively. So the set is
+// taken from the logits' orderable integer keys with k + 1 rounds of a
+// wave-wide unsigned max (one DPP op per level), and accepted only when
+// exp(l_k - max) > exp(l_{k+1} - max) * (1 + 2^-20); ties, NaN or an
+// infinite max return false and the caller takes the exact scan. Returns
+// the set in ascending index order in set_ids[0..k).
+// ---------------------------------------------------------------------------
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint32_t dpp_umax_src(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xF, true);
+}
+
+// Unsigned max over the wave, valid in lane 63.
+__device__ __forceinline__ uint32_t wave_umax_last(uint32_t v) {
+  v = max(v, dpp_umax_src<0x111>(v));
+  v = max(v, dpp_umax_src<0x112>(v));
+  v = max(v, dpp_umax_src<0x114>(v));
+  v = max(v, dpp_umax_src<0x118>(v));
+  v = max(v, dpp_umax_src<0x142, 0xA>(v));
+  v = max(v, dpp_umax_src<0x143, 0xC>(v));
+  return v;
+}
+
+__device__ __forceinline__ float from_orderable(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+template <int P>
+__device__ bool topk_set_logits(const float (&l)[P], uint32_t n, uint32_t k, int lane,
+                                int32_t* set_ids) {
+  uint32_t key[P];
+  bool bad = false;
+#pragma unroll
+  for (int e = 0; e < P; ++e) {
+    const uint32_t j = lane * P + e;
+    bad |= (l[e] != l[e]);
+    key[e] = j < n ? orderable(l[e]) : 0u;
+  }
+  if (__ballot(bad)) return false;
+  uint32_t sk[P];
+#pragma unroll
+  for (int e = 0; e < P; ++e) sk[e] = key[e];
+#pragma unroll
+  for (int a = 0; a < P; ++a)
+#pragma unroll
+    for (int b = P - 1; b > a; --b) {
+      const uint32_t hi = max(sk[b - 1], sk[b]), lo = min(sk[b - 1], sk[b]);
+      sk[b - 1] = hi;
+      sk[b] = lo;
+    }
+  uint32_t top = 0, kth = 0, next = 0;
+  for (uint32_t r = 0; r <= k; ++r) {
+    const uint32_t m = (uint32_t)__builtin_amdgcn_readlane((int)wave_umax_last(sk[0]), 63);
+    if (r == 0) top = m;
+    if (r == k) {
+      next = m;
+      break;
+    }
+    kth = m;
+    const uint64_t ball = __ballot(sk[0] == m);
+    const int first = __builtin_amdgcn_readfirstlane(__ffsll((unsigned long long)ball) - 1);
+    if (lane == first) {
+#pragma unroll
+      for (int e = 0; e < P - 1; ++e) sk[e] = sk[e + 1];
+      sk[P - 1] = 0;
+    }
+  }
+  const float fm = from_orderable(top), fk = from_orderable(kth), fn = from_orderable(next);
+  if (!(fm < INFINITY) || !(fk > fn)) return false;
+  if (!(expf(fk - fm) > expf(fn - fm) * (1.0f + 0x1p-20f))) return false;
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  uint32_t at = 0;
+#pragma unroll
+  for (int e = 0; e < P; ++e) at += __popcll(__ballot(key[e] >= kth) & below);
+#pragma unroll
+  for (int e = 0; e < P; ++e)
+    if (key[e] >= kth) set_ids[at++] = (int32_t)(lane * P + e);
+  return true;
+}
+
 }  // namespace smoe

@@ -116,6 +116,21 @@ def test_lm_head_qwen3_shape_and_argmax(kernels):
     assert int(host(am)[0]) == oracle.argmax(want)
 
 
+@pytest.mark.parametrize("n", [1, 3, 4, 255, 1023, 4097, 151936, 151939])
+def test_argmax_first_index_on_ties(kernels, n):
+    """Argmax equals numpy's (first maximal index) with the maximum planted
+    several times, including in the ragged tail and across slice borders."""
+    torch = _torch()
+    rng = np.random.default_rng(n)
+    v = rng.standard_normal(n).astype(np.float32)
+    peak = np.float32(10.0)
+    for pos in sorted({n - 1, n // 2, (n * 3) // 4, min(n - 1, 600)}, reverse=True):
+        v[pos] = peak
+    out = torch.empty(1, dtype=torch.int32, device="cuda")
+    assert kernels.argmax(dev(v), n, out) == 0
+    assert int(host(out)[0]) == int(np.argmax(v)) == oracle.argmax(v)
+
+
 # --- dequant (bit-exact) --------------------------------------------------------------
 
 @pytest.mark.parametrize("bits,group", [(4, 64), (3, 64), (4, 32), (3, 128)])
