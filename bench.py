@@ -41,24 +41,38 @@ CONFIGS = {
 }
 
 
-def stream_read_peak(dev, gib=2):
-    """Measured streaming-read bandwidth of this GPU: torch's sum over a
-    `gib` GiB tensor (a plain HBM read), best of 5, GB/s."""
+# HBM bytes actually moved per unit of work, from rocprofv3 FETCH_SIZE and
+# WRITE_SIZE passes scaled by a 256 MiB copy calibration (FETCH x 2.0,
+# WRITE x 1.0): profiles/decode_c2_a3b_4bit.md (one layer = the three
+# k_fa_* launches) and profiles/lm_head_c1_qmv_argmax.md (k_qmv + argmax).
+# None where no counter pass was taken.
+MEASURED_TRAFFIC = {"c2": 19_522_595, "c1": 176_528_574}
+
+
+def stream_read_peak(dev, gib=4):
+    """Measured streaming-read bandwidth of this GPU: libsmoe's read kernel
+    (128-bit non-temporal loads over the whole chip) over a `gib` GiB
+    buffer, best of 5, GB/s."""
     import torch
 
-    n = gib * (1 << 30) // 4
-    t = torch.ones(n, dtype=torch.float32, device=dev)
-    t.sum()
+    import streamoe_amd as sa
+
+    kern = sa.Kernels(dev.index or 0)
+    n = gib * (1 << 30)
+    buf = torch.ones(n // 4, dtype=torch.float32, device=dev)
+    sink = torch.empty(2048, dtype=torch.int32, device=dev)
+    sa.check(kern.stream_read(buf, n, sink), "smoe_stream_read")
     torch.cuda.synchronize()
     best = 0.0
     for _ in range(5):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
-        t.sum()
+        sa.check(kern.stream_read(buf, n, sink), "smoe_stream_read")
         e1.record()
         torch.cuda.synchronize()
-        best = max(best, n * 4 / (e0.elapsed_time(e1) * 1e-3) / 1e9)
-    del t
+        best = max(best, n / (e0.elapsed_time(e1) * 1e-3) / 1e9)
+    kern.close()
+    del buf
     torch.cuda.empty_cache()
     return round(best, 1)
 
@@ -291,8 +305,10 @@ def run_decode(args, c):
         "gbps": round(achieved, 1),
         "pct_of_hbm_peak": round(100 * achieved / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "unit_of_work": f"one layer: {nbytes} algorithmic bytes", "kernel": "decode layer (all launches)"},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": MEASURED_TRAFFIC.get(c.get("key")) if path in (0, 3) else None,
+                     "unit_of_work": f"one layer: {nbytes} algorithmic bytes",
+                     "kernel": "decode layer: k_fa_route + k_fa_gateup + k_fa_down (one HIP graph)"
+                               if path in (0, 3) else "decode layer (all launches)"},
         "wall_s": round(wall, 3),
     }
     if phases:
@@ -367,7 +383,7 @@ def run_lm_head(args, c):
                    "mode": "hipgraph" if graph is not None else "eager"},
         "gbps": round(achieved, 1), "pct_of_hbm_peak": round(100 * achieved / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": MEASURED_TRAFFIC.get("c1"),
                      "unit_of_work": f"one token: {nbytes} algorithmic bytes (codes + bf16 scales/biases)",
                      "kernel": "k_qmv + k_argmax"},
     }
@@ -410,7 +426,7 @@ def main():
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the multi-GPU "
               "sharding of this path is a design note, not a measured configuration.", file=sys.stderr)
         sys.exit(2)
-    c = CONFIGS[args.config]
+    c = dict(CONFIGS[args.config], key=args.config)
     out = run_lm_head(args, c) if args.config == "c1" else run_decode(args, c)
     if not args.no_stream_peak:
         import torch

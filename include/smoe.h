@@ -295,6 +295,12 @@ int smoe_moe_prefill(smoe_handle* h, const smoe_expert_shape* shape, const void*
  * memory from a counter-based generator, so a given (seed, size) gives
  * the same bytes on any run. */
 
+/* Diagnostic (no reference counterpart): read every byte of the device
+ * buffer `buf` once with 128-bit loads across the whole GPU, the measured
+ * HBM read peak the decode is compared against. bytes: multiple of 16;
+ * sink: device uint32[2048] (per-block XOR of the data read). */
+int smoe_stream_read(smoe_handle* h, const void* buf, uint64_t bytes, uint32_t* sink);
+
 /* n_experts blobs at base + e * stride: codes uniform (4-bit: random
  * u32 words; 3-bit: random 24-bit packs), scales bf16(|N(0, scale_sigma)|),
  * biases bf16(N(0, bias_sigma)). */

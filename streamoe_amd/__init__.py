@@ -223,6 +223,11 @@ class Kernels:
                                      _ptr(out_sum), _ptr(workspace),
                                      0 if workspace is None else workspace.numel() * workspace.element_size())
 
+    # -- diagnostics --------------------------------------------------------------
+    def stream_read(self, buf, nbytes, sink):
+        """Read nbytes of the device tensor `buf` once (HBM read-peak probe)."""
+        return _lib.smoe_stream_read(self.h, _ptr(buf), nbytes, _ptr(sink))
+
     # -- synthetic data ---------------------------------------------------------
     def synth_experts(self, base, n_experts, stride, layout, seed, scale_sigma=0.02,
                       bias_sigma=0.01):

@@ -109,6 +109,7 @@ PROTOTYPES = {
     "smoe_moe_prefill_workspace_size": (_U64, [C.POINTER(ExpertShape), _U32, _U32, _U32]),
     "smoe_moe_prefill": (_I, [_P, C.POINTER(ExpertShape), _P, _U64, _U32, _P, _P, _P, _I, _U32, _U32, _P, _P,
                               _U64]),
+    "smoe_stream_read": (_I, [_P, _P, C.c_uint64, _P]),
     "smoe_synth_experts": (_I, [_P, _P, _U32, _U64, C.POINTER(ExpertShape), _U64, C.c_float, C.c_float]),
     "smoe_synth_normal_f32": (_I, [_P, _P, _U64, _U64, C.c_float]),
     "smoe_synth_normal_bf16": (_I, [_P, _P, _U64, _U64, C.c_float]),

@@ -601,6 +601,13 @@ int smoe_synth_experts(smoe_handle* h, void* base, uint32_t n_experts, uint64_t 
                                          bias_sigma, h->stream));
 }
 
+int smoe_stream_read(smoe_handle* h, const void* buf, uint64_t bytes, uint32_t* sink) {
+  if (!h || !buf || !bytes || !sink) return SMOE_ERR_INVALID_ARG;
+  if (bytes % 16 || !aligned(buf, 0, 16)) return SMOE_ERR_MISALIGNED;
+  if (int rc = use_device(h)) return rc;
+  return hip_status(launch_stream_read(buf, bytes, sink, h->stream));
+}
+
 int smoe_synth_normal_f32(smoe_handle* h, float* out, uint64_t n, uint64_t seed, float sigma) {
   if (!h || !out || !n) return SMOE_ERR_INVALID_ARG;
   if (int rc = use_device(h)) return rc;

@@ -124,6 +124,11 @@ hipError_t launch_down_combine(const BlobGeom& routed, const BlobGeom& shared,
 hipError_t launch_rmsnorm(const float* r, const uint16_t* w, float eps, uint32_t dim, float* x_out,
                           hipStream_t st);
 
+// Streaming-read diagnostic over `bytes` (multiple of 16) with
+// kStreamBlocks blocks; sink: kStreamBlocks u32.
+constexpr uint32_t kStreamBlocks = 2048;
+hipError_t launch_stream_read(const void* buf, uint64_t bytes, uint32_t* sink, hipStream_t st);
+
 // Synthetic data.
 hipError_t launch_synth_experts(uint8_t* base, uint32_t n_experts, uint64_t stride,
                                 const BlobGeom& g, uint64_t seed, float ssig, float bsig,

@@ -108,3 +108,42 @@ hipError_t launch_synth_normal_bf16(uint16_t* out, uint64_t n, uint64_t seed, fl
 }
 
 }  // namespace smoe
+
+namespace smoe {
+
+// ---------------------------------------------------------------------------
+// Streaming-read diagnostic: every byte of `buf` is read once with 128-bit
+// loads (grid-stride, 4 loads in flight per thread); each block writes the
+// XOR of what it read to sink[block] so the loads cannot be dropped.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_stream_read(const u32x4* __restrict__ p, uint64_t n16,
+                                                     uint32_t* __restrict__ sink) {
+  __shared__ uint32_t red[4];
+  uint32_t acc = 0;
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    const u32x4 a = __builtin_nontemporal_load(p + i);
+    const u32x4 b = __builtin_nontemporal_load(p + i + stride);
+    const u32x4 c = __builtin_nontemporal_load(p + i + 2 * stride);
+    const u32x4 d = __builtin_nontemporal_load(p + i + 3 * stride);
+    acc ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w ^ c.x ^ c.y ^ c.z ^ c.w ^ d.x ^ d.y ^ d.z ^ d.w;
+  }
+  for (; i < n16; i += stride) {
+    const u32x4 a = __builtin_nontemporal_load(p + i);
+    acc ^= a.x ^ a.y ^ a.z ^ a.w;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) acc ^= __shfl_xor(acc, o, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) sink[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
+}
+
+hipError_t launch_stream_read(const void* buf, uint64_t bytes, uint32_t* sink, hipStream_t st) {
+  hipLaunchKernelGGL(k_stream_read, dim3(kStreamBlocks), dim3(256), 0, st,
+                     reinterpret_cast<const u32x4*>(buf), bytes / 16, sink);
+  return hipGetLastError();
+}
+
+}  // namespace smoe
