@@ -242,6 +242,25 @@ class Kernels:
         return _lib.smoe_synth_normal_bf16(self.h, _ptr(out), out.numel(), seed, C.c_float(sigma))
 
 
+def zipf_routing(n_tokens, n_experts, k, s=1.1, seed=0):
+    """Synthetic prefill routing (the skewed config-4 workload): per token,
+    k distinct experts drawn by Gumbel-top-k with p_e proportional to
+    rank_e^-s over a seeded permutation of the experts; weights = softmax of
+    k seeded N(0, 1) logits. Returns (idx int32 [n, k], w float32 [n, k])."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    ranks = np.empty(n_experts)
+    ranks[rng.permutation(n_experts)] = np.arange(1, n_experts + 1)
+    logp = -s * np.log(ranks)
+    keys = logp[None, :] + rng.gumbel(size=(n_tokens, n_experts))
+    idx = np.argsort(-keys, axis=1, kind="stable")[:, :k].astype(np.int32)
+    lg = rng.standard_normal((n_tokens, k))
+    w = np.exp(lg - lg.max(axis=1, keepdims=True))
+    w /= w.sum(axis=1, keepdims=True)
+    return idx, w.astype(np.float32)
+
+
 def capture_graph(kernels: Kernels, fn):
     """Record the launches `fn()` makes on `kernels` into a HIP graph (torch's
     CUDAGraph over hipGraph) and return it; fn runs once eagerly on the

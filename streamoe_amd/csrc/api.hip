@@ -196,7 +196,7 @@ int smoe_sync(smoe_handle* h) {
   if (hipMemcpy(&e, h->err, sizeof(e), hipMemcpyDeviceToHost) != hipSuccess) return SMOE_ERR_HIP;
   if (e) {
     if (hipMemset(h->err, 0, sizeof(e)) != hipSuccess) return SMOE_ERR_HIP;
-    return SMOE_ERR_DEVICE_TIMEOUT;
+    return e == 2u ? SMOE_ERR_INVALID_ARG : SMOE_ERR_DEVICE_TIMEOUT;
   }
   return SMOE_OK;
 }
@@ -585,6 +585,47 @@ int smoe_moe_decode_layers(smoe_handle* h, const smoe_layer* layers, uint32_t n_
       return rc;
   }
   return SMOE_OK;
+}
+
+uint64_t smoe_moe_prefill_workspace_size(const smoe_expert_shape* shape, uint32_t n_tokens,
+                                         uint32_t n_experts, uint32_t k) {
+  if (!shape || !shape->group || !n_tokens || !n_experts || !k) return 0;
+  return prefill_workspace(shape->hidden, shape->inter, shape->group, n_tokens, n_experts, k, nullptr,
+                           nullptr);
+}
+
+int smoe_moe_prefill(smoe_handle* h, const smoe_expert_shape* shape, const void* experts,
+                     uint64_t stride, uint32_t n_experts, const int32_t* idx,
+                     const float* weights, const void* x, int x_is_bf16, uint32_t n_tokens,
+                     uint32_t k, float* out_sum, void* workspace, uint64_t workspace_bytes) {
+  if (!h || !experts || !idx || !weights || !x || !out_sum || !workspace || !n_tokens || !n_experts)
+    return SMOE_ERR_INVALID_ARG;
+  if (int rc = check_shape(shape)) return rc;
+  if (k < 1 || k > SMOE_MAX_K || k > n_experts) return SMOE_ERR_BAD_K;
+  if (stride < smoe_expert_bytes(shape)) return SMOE_ERR_INVALID_ARG;
+  if (!prefill_supported(shape->hidden, shape->inter, shape->group, shape->bits, n_tokens, n_experts, k))
+    return SMOE_ERR_UNSUPPORTED_SHAPE;
+  if (!blob_aligned(experts, shape->bits) || stride % 16 || !aligned(x, 0, 16) ||
+      !aligned(out_sum, 0, 16) || !aligned(workspace, 0, 256))
+    return SMOE_ERR_MISALIGNED;
+  PfArgs a{};
+  const uint64_t need = prefill_workspace(shape->hidden, shape->inter, shape->group, n_tokens,
+                                          n_experts, k, &a, (uint8_t*)workspace);
+  if (workspace_bytes < need) return SMOE_ERR_WORKSPACE_TOO_SMALL;
+  if (int rc = use_device(h)) return rc;
+  a.g = blob_geom(shape->hidden, shape->inter, shape->group, shape->bits);
+  a.experts = (const uint8_t*)experts;
+  a.stride = stride;
+  a.E = n_experts;
+  a.k = k;
+  a.n_tokens = n_tokens;
+  a.idx = idx;
+  a.w = weights;
+  a.x = x;
+  a.x_bf16 = x_is_bf16 != 0;
+  a.out = out_sum;
+  a.err = h->err;
+  return hip_status(launch_prefill(a, h->stream));
 }
 
 int smoe_synth_experts(smoe_handle* h, void* base, uint32_t n_experts, uint64_t stride,

@@ -91,6 +91,43 @@ bool fused_supported(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t b
 // combine) on `st`; no allocation, no memset (graph-capturable).
 hipError_t launch_fused_layer(const FusedLayer& a, hipStream_t st);
 
+// Prefill (prefill.hip): limits, arguments and workspace.
+constexpr uint32_t kPfMaxTokens = 1024;
+constexpr uint32_t kPfMaxExperts = 256;
+constexpr uint32_t kPfMaxK = 16;
+constexpr uint32_t kPfMaxGroupsK = 128;  // K / group of either GEMM (e.g. 4096 / 32)
+
+struct PfArgs {
+  BlobGeom g;              // routed expert geometry
+  const uint8_t* experts;  // expert e at experts + e * stride
+  uint64_t stride;
+  uint32_t E, k, n_tokens, max_items;
+  const int32_t* idx;      // [n_tokens, k]
+  const float* w;          // [n_tokens, k]
+  const void* x;           // [n_tokens, hidden], bf16 or f32
+  int x_bf16;
+  float* out;              // [n_tokens, hidden]
+  uint32_t* err;           // device error word (2: invalid routing input)
+  // Workspace (prefill_workspace).
+  uint32_t* items;         // [max_items, 2]: expert, start | count << 16
+  uint32_t* n_items;
+  int32_t* ent_token;      // [n*k] token of each entry (entries sorted by expert, then token)
+  float* ent_weight;       // [n*k]
+  int32_t* tok_pos;        // [n, k] entry positions of each token in ascending expert order
+  float* xsum;             // [n, hidden / group]
+  float* asum;             // [n*k, inter / group]
+  float* act;              // [n*k, inter]
+  float* down;             // [n*k, hidden]
+};
+
+// Workspace bytes for these sizes; with `a` and `base`, also points a's
+// workspace fields into base.
+uint64_t prefill_workspace(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t n_tokens,
+                           uint32_t n_experts, uint32_t k, PfArgs* a, uint8_t* base);
+bool prefill_supported(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t bits,
+                       uint32_t n_tokens, uint32_t n_experts, uint32_t k);
+hipError_t launch_prefill(const PfArgs& a, hipStream_t st);
+
 // All launchers return hipSuccess or the launch error; `*unsupported`
 // is set when no kernel instance exists for the shape.
 hipError_t launch_qmv(const QView& w, const float* x, float* y, uint32_t out_dim, uint32_t in_dim,

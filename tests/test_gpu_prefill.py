@@ -1,0 +1,130 @@
+"""Prefill (many tokens through one layer's routed experts) on the GPU vs the
+oracle's build_expert_buckets + moe_permute_fuse (moe_router.rs:374-436,
+moe_cpu.rs:282-339). Bar: max|d| / max|ref| <= 1e-3."""
+import numpy as np
+import pytest
+
+import oracle
+from helpers import rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+def _torch():
+    import torch
+
+    return torch
+
+
+def host(t):
+    return t.detach().cpu().numpy()
+
+
+def _case(kernels, n_tokens, H, I, E, k, bits, group, x_bf16, seed, routing="zipf"):
+    import streamoe_amd as sa
+
+    torch = _torch()
+    lay = sa.ExpertLayout(H, I, bits, group)
+    stride = lay.expert_size
+    arena = torch.empty(E * stride, dtype=torch.uint8, device="cuda")
+    assert kernels.synth_experts(arena, E, stride, lay, seed) == 0
+    if routing == "zipf":
+        idx, w = sa.zipf_routing(n_tokens, E, k, 1.1, seed=seed)
+    elif routing == "hot":  # every token picks expert 0 plus k-1 others
+        rng = np.random.default_rng(seed)
+        idx = np.stack([np.concatenate([[0], rng.choice(np.arange(1, E), k - 1, replace=False)])
+                        for _ in range(n_tokens)]).astype(np.int32)
+        w = rng.random((n_tokens, k)).astype(np.float32)
+    else:
+        raise ValueError(routing)
+    if x_bf16:
+        xb = torch.empty((n_tokens, H), dtype=torch.int16, device="cuda")
+        assert kernels.synth_normal_bf16(xb, seed + 1, 1.0) == 0
+        x_host = oracle.bf16_to_f32(host(xb).view(np.uint16)).reshape(n_tokens, H)
+        x_dev = xb
+    else:
+        x_dev = torch.empty((n_tokens, H), dtype=torch.float32, device="cuda")
+        assert kernels.synth_normal_f32(x_dev, seed + 1, 1.0) == 0
+        x_host = host(x_dev)
+    idx_d = torch.from_numpy(idx).cuda()
+    w_d = torch.from_numpy(w).cuda()
+    out = torch.empty((n_tokens, H), dtype=torch.float32, device="cuda")
+    need = kernels.moe_prefill_workspace_size(lay, n_tokens, E, k)
+    assert need > 0
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    rc = kernels.moe_prefill(lay, arena, stride, E, idx_d, w_d, x_dev, x_bf16, n_tokens, k, out, ws)
+    assert rc == 0, rc
+    kernels.sync()
+    buckets = oracle.build_expert_buckets(idx, w, n_tokens, k, E)
+    assert buckets[0] == 0
+    want = oracle.moe_permute_fuse(host(arena), stride, bits, H, I, group, x_host, buckets, n_tokens)
+    return host(out), want, (arena, idx_d, w_d, x_dev, out, ws, lay, stride)
+
+
+@pytest.mark.parametrize("name,n,H,I,E,k,bits,group,x_bf16,routing", [
+    ("c4-a3b", 512, 2048, 512, 256, 8, 4, 64, True, "zipf"),          # config 4
+    ("c4-a3b-3bit", 512, 2048, 512, 256, 8, 3, 64, True, "zipf"),
+    ("f32-x", 96, 2048, 512, 64, 8, 4, 64, False, "zipf"),
+    ("olmoe-shape", 64, 2048, 1024, 64, 8, 4, 64, True, "zipf"),
+    ("g32", 40, 1024, 512, 32, 4, 4, 32, True, "zipf"),
+    ("g128-3bit", 40, 1024, 512, 32, 4, 3, 128, False, "zipf"),
+    ("hot-expert", 200, 2048, 512, 64, 8, 4, 64, True, "hot"),
+    ("one-token", 1, 2048, 512, 256, 8, 4, 64, True, "zipf"),
+    ("k1", 33, 1024, 256 * 2, 16, 1, 4, 64, True, "zipf"),
+])
+def test_prefill_matches_oracle(kernels, name, n, H, I, E, k, bits, group, x_bf16, routing):
+    got, want, _ = _case(kernels, n, H, I, E, k, bits, group, x_bf16, seed=sum(map(ord, name)), routing=routing)
+    err = rel_err(got, want)
+    print(f"prefill {name}: rel_err={err:.3e} max|ref|={np.max(np.abs(want)):.3e}")
+    assert np.all(np.isfinite(got))
+    assert err <= TOL
+
+
+def test_prefill_is_deterministic(kernels):
+    """Fixed-order reductions and no atomics in the arithmetic: two runs give
+    the same bits."""
+    import streamoe_amd as sa
+
+    torch = _torch()
+    got, _, st = _case(kernels, 128, 2048, 512, 64, 8, 4, 64, True, seed=11)
+    arena, idx_d, w_d, x_dev, out, ws, lay, stride = st
+    out2 = torch.empty_like(out)
+    assert kernels.moe_prefill(lay, arena, stride, 64, idx_d, w_d, x_dev, True, 128, 8, out2, ws) == 0
+    kernels.sync()
+    assert np.array_equal(host(out2).view(np.uint32), got.view(np.uint32))
+
+
+def test_prefill_argument_errors(kernels):
+    import streamoe_amd as sa
+    from streamoe_amd import _abi
+
+    torch = _torch()
+    lay = sa.ExpertLayout(2048, 512, 4, 64)
+    arena = torch.zeros(4 * lay.expert_size, dtype=torch.uint8, device="cuda")
+    idx = torch.zeros((4, 2), dtype=torch.int32, device="cuda")
+    w = torch.zeros((4, 2), dtype=torch.float32, device="cuda")
+    x = torch.zeros((4, 2048), dtype=torch.int16, device="cuda")
+    out = torch.zeros((4, 2048), dtype=torch.float32, device="cuda")
+    need = kernels.moe_prefill_workspace_size(lay, 4, 4, 2)
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    small = torch.empty(need // 2, dtype=torch.uint8, device="cuda")
+    c = _abi.CODES
+    assert kernels.moe_prefill(lay, arena, lay.expert_size, 4, idx, w, x, True, 4, 2, out, small) == \
+        c["SMOE_ERR_WORKSPACE_TOO_SMALL"]
+    assert kernels.moe_prefill(lay, arena, lay.expert_size, 4, idx, w, x, True, 4, 5, out, ws) == c["SMOE_ERR_BAD_K"]
+    assert kernels.moe_prefill(lay, arena, lay.expert_size, 4, idx, w, x, True, 4, 0, out, ws) == c["SMOE_ERR_BAD_K"]
+    assert kernels.moe_prefill(lay, arena, lay.expert_size, 4, idx, w, x, True, 2000, 2, out, ws) == \
+        c["SMOE_ERR_UNSUPPORTED_SHAPE"]
+    # Invalid routing is caught on the device and reported by smoe_sync.
+    bad = torch.tensor([[0, 1], [2, 9], [3, 0], [1, 2]], dtype=torch.int32, device="cuda")
+    assert kernels.moe_prefill(lay, arena, lay.expert_size, 4, bad, w, x, True, 4, 2, out, ws) == 0
+    with pytest.raises(sa.SmoeError) as ei:
+        kernels.sync()
+    assert ei.value.status == c["SMOE_ERR_INVALID_ARG"]
+    dup = torch.tensor([[0, 1], [2, 2], [3, 0], [1, 2]], dtype=torch.int32, device="cuda")
+    assert kernels.moe_prefill(lay, arena, lay.expert_size, 4, dup, w, x, True, 4, 2, out, ws) == 0
+    with pytest.raises(sa.SmoeError):
+        kernels.sync()
+    kernels.sync()  # the error word was cleared
