@@ -625,7 +625,10 @@ int smoe_moe_prefill(smoe_handle* h, const smoe_expert_shape* shape, const void*
   a.x_bf16 = x_is_bf16 != 0;
   a.out = out_sum;
   a.err = h->err;
-  return hip_status(launch_prefill(a, h->stream));
+  int n_cu = 0;
+  if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, h->device) != hipSuccess || n_cu <= 0)
+    return SMOE_ERR_HIP;
+  return hip_status(launch_prefill(a, (uint32_t)n_cu, h->stream));
 }
 
 int smoe_synth_experts(smoe_handle* h, void* base, uint32_t n_experts, uint64_t stride,

@@ -114,9 +114,12 @@ struct PfArgs {
   int32_t* ent_token;      // [n*k] token of each entry (entries sorted by expert, then token)
   float* ent_weight;       // [n*k]
   int32_t* tok_pos;        // [n, k] entry positions of each token in ascending expert order
-  float* xsum;             // [n, hidden / group]
-  float* asum;             // [n*k, inter / group]
-  float* act;              // [n*k, inter]
+  float* xsum;             // [n*k, hidden / group] group sums of each entry's x row
+  float* asum;             // [n*k, inter / group] group sums of the activations
+  uint16_t* x_hi;          // [n*k, hidden] x rows in entry order, bf16, MFMA order
+  uint16_t* x_lo;          // [n*k, hidden] low halves (fp32 input only)
+  uint16_t* act_hi;        // [n*k, inter] SwiGLU output, bf16 hi, MFMA order
+  uint16_t* act_lo;        // [n*k, inter] bf16 lo
   float* down;             // [n*k, hidden]
 };
 
@@ -126,7 +129,7 @@ uint64_t prefill_workspace(uint32_t hidden, uint32_t inter, uint32_t group, uint
                            uint32_t n_experts, uint32_t k, PfArgs* a, uint8_t* base);
 bool prefill_supported(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t bits,
                        uint32_t n_tokens, uint32_t n_experts, uint32_t k);
-hipError_t launch_prefill(const PfArgs& a, hipStream_t st);
+hipError_t launch_prefill(const PfArgs& a, uint32_t n_cu, hipStream_t st);
 
 // All launchers return hipSuccess or the launch error; `*unsupported`
 // is set when no kernel instance exists for the shape.

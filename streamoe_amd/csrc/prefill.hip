@@ -41,17 +41,12 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
-constexpr uint32_t kPfMC = 32;  // entries per work item (two 16-row MFMA tiles)
+constexpr uint32_t kPfMC = 32;   // entries per work item (two 16-row MFMA tiles)
+constexpr uint32_t kPfKC = 256;  // inputs per pipelined K chunk
 
 // ---------------------------------------------------------------------------
 // Bucketing (one block of 1024 threads).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t popc_below(const uint32_t* row, uint32_t e) {
-  uint32_t c = 0;
-  for (uint32_t w = 0; w < (e >> 5); ++w) c += __popc(row[w]);
-  return c + __popc(row[e >> 5] & ((1u << (e & 31)) - 1u));
-}
-
 // Exclusive scan of v over threads [0, n) (n <= 1024) through LDS.
 __device__ uint32_t block_exscan(uint32_t v, uint32_t n, uint32_t* tmp, uint32_t* total) {
   const uint32_t t = threadIdx.x;
@@ -71,12 +66,13 @@ __device__ uint32_t block_exscan(uint32_t v, uint32_t n, uint32_t* tmp, uint32_t
 }
 
 __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
-  __shared__ uint32_t bits[kPfMaxTokens * (kPfMaxExperts / 32)];
-  __shared__ uint8_t slot_of[kPfMaxTokens * kPfMaxK];
+  // col[e][c]: bit (t & 31) set when token 32c + (t & 31) chose expert e.
+  __shared__ uint32_t col[kPfMaxExperts * (kPfMaxTokens / 32)];
   __shared__ uint32_t tmp[1024];
+  __shared__ uint32_t offs[kPfMaxExperts];
   const uint32_t tid = threadIdx.x, n = a.n_tokens, k = a.k, E = a.E;
-  const uint32_t words = (E + 31) / 32, total = n * k;
-  for (uint32_t i = tid; i < n * words; i += blockDim.x) bits[i] = 0;
+  const uint32_t cw = (n + 31) / 32, total = n * k;
+  for (uint32_t i = tid; i < E * cw; i += blockDim.x) col[i] = 0;
   __syncthreads();
   for (uint32_t i = tid; i < total; i += blockDim.x) {
     const int32_t e = a.idx[i];
@@ -84,20 +80,14 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
       *a.err = 2u;
       continue;
     }
-    const uint32_t old = atomicOr(&bits[(i / k) * words + (e >> 5)], 1u << (e & 31));
-    if (old & (1u << (e & 31))) *a.err = 2u;  // an expert twice in one token
+    const uint32_t t = i / k;
+    const uint32_t old = atomicOr(&col[e * cw + (t >> 5)], 1u << (t & 31));
+    if (old & (1u << (t & 31))) *a.err = 2u;  // an expert twice in one token
   }
   __syncthreads();
-  // Entry rank of (t, s) among t's experts in ascending order -> slot s.
-  for (uint32_t i = tid; i < total; i += blockDim.x) {
-    const int32_t e = a.idx[i];
-    if (e < 0 || (uint32_t)e >= E) continue;
-    const uint32_t t = i / k;
-    slot_of[t * k + popc_below(&bits[t * words], (uint32_t)e)] = (uint8_t)(i - t * k);
-  }
   uint32_t cnt = 0;
   if (tid < E)
-    for (uint32_t t = 0; t < n; ++t) cnt += (bits[t * words + (tid >> 5)] >> (tid & 31)) & 1u;
+    for (uint32_t c = 0; c < cw; ++c) cnt += __popc(col[tid * cw + c]);
   uint32_t n_entries;
   const uint32_t off = block_exscan(cnt, E, tmp, &n_entries);
   const uint32_t nch = (cnt + kPfMC - 1) / kPfMC;
@@ -105,46 +95,29 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
   const uint32_t ibase = block_exscan(nch, E, tmp, &n_items);
   if (tid == 0) *a.n_items = n_items;
   if (tid < E) {
+    offs[tid] = off;
     for (uint32_t c = 0; c < nch; ++c) {
-      const uint32_t start = off + c * kPfMC;
-      const uint32_t m = min(kPfMC, cnt - c * kPfMC);
       a.items[2 * (ibase + c)] = tid;
-      a.items[2 * (ibase + c) + 1] = start | (m << 16);
-    }
-    uint32_t pos = off;
-    for (uint32_t t = 0; t < n && pos < off + cnt; ++t) {
-      const uint32_t* row = &bits[t * words];
-      if (!((row[tid >> 5] >> (tid & 31)) & 1u)) continue;
-      const uint32_t r = popc_below(row, tid);
-      const uint32_t s = slot_of[t * k + r];
-      a.ent_token[pos] = (int32_t)t;
-      a.ent_weight[pos] = a.w[t * k + s];
-      a.tok_pos[t * k + r] = (int32_t)pos;
-      ++pos;
+      a.items[2 * (ibase + c) + 1] = (off + c * kPfMC) | (min(kPfMC, cnt - c * kPfMC) << 16);
     }
   }
-}
-
-// ---------------------------------------------------------------------------
-// Group sums: out[r, g] = sum of src[r, G*g .. G*g + G) (bf16 or f32 rows).
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_pf_rowsum(const void* src, int is_bf16, uint32_t cols,
-                                                   uint32_t G, const uint32_t* n_rows_dev,
-                                                   uint32_t n_rows, float* out) {
-  const uint32_t r = blockIdx.x;
-  if (n_rows_dev && r >= *n_rows_dev) return;
-  if (r >= n_rows) return;
-  const uint32_t ng = cols / G;
-  for (uint32_t g = threadIdx.x; g < ng; g += blockDim.x) {
-    float s = 0.f;
-    if (is_bf16) {
-      const uint16_t* p = reinterpret_cast<const uint16_t*>(src) + (size_t)r * cols + (size_t)g * G;
-      for (uint32_t j = 0; j < G; ++j) s += bf16f(p[j]);
-    } else {
-      const float* p = reinterpret_cast<const float*>(src) + (size_t)r * cols + (size_t)g * G;
-      for (uint32_t j = 0; j < G; ++j) s += p[j];
-    }
-    out[(size_t)r * ng + g] = s;
+  __syncthreads();
+  // Every entry places itself: position = the expert's offset + the tokens
+  // before t that chose the same expert; rank among t's experts in
+  // ascending expert order = how many of t's experts are smaller.
+  for (uint32_t i = tid; i < total; i += blockDim.x) {
+    const int32_t e = a.idx[i];
+    if (e < 0 || (uint32_t)e >= E) continue;
+    const uint32_t t = i / k;
+    const uint32_t* c = &col[e * cw];
+    uint32_t before = __popc(c[t >> 5] & ((1u << (t & 31)) - 1u));
+    for (uint32_t w = 0; w < (t >> 5); ++w) before += __popc(c[w]);
+    uint32_t r = 0;
+    for (uint32_t s = 0; s < k; ++s) r += (a.idx[t * k + s] < e) ? 1u : 0u;
+    const uint32_t pos = offs[e] + before;
+    a.ent_token[pos] = (int32_t)t;
+    a.ent_weight[pos] = a.w[i];
+    a.tok_pos[t * k + min(r, k - 1)] = (int32_t)pos;
   }
 }
 
@@ -213,234 +186,428 @@ __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
-// Codes of `row` for lane block q of group g: NU u32 words of 8 codes each
-// (4-bit), or NU 24-bit packs (3-bit), for inputs G*g + 8*NU*q + [0, 8*NU).
-template <int BITS, int NU>
-__device__ __forceinline__ void load_codes(const uint8_t* base, uint32_t row_bytes, uint32_t row,
-                                           uint32_t g, uint32_t q, uint32_t (&w)[NU]) {
-  const uint8_t* r = base + (size_t)row * row_bytes;
-  if (BITS == 4) {
-    // byte offset (32*NU*g + 8*NU*q) / 2
-    const uint32_t* p = reinterpret_cast<const uint32_t*>(r + (size_t)(4 * g + q) * NU * 4);
-#pragma unroll
-    for (int u = 0; u < NU; ++u) w[u] = ld_stream(p + u);
-  } else {
-    // 3*NU bytes at byte offset 3*(32*NU*g + 8*NU*q)/8 = 3*NU*(4g + q); load
-    // the dword-aligned window around them (within the blob: the scales
-    // follow the codes of every block).
-    const uint32_t o = (4 * g + q) * NU * 3;
-    const uint32_t* p = reinterpret_cast<const uint32_t*>(r + (o & ~3u));
-    constexpr int ND = (3 * NU + 6) / 4;
-    uint32_t d[ND];
-#pragma unroll
-    for (int i = 0; i < ND; ++i) d[i] = ld_stream(p + i);
-    const uint32_t sh = (o & 3u) * 8;
-#pragma unroll
-    for (int u = 0; u < NU; ++u) {
-      const uint32_t bit = sh + 24 * u;
-      uint32_t lo = 0, hi = 0;
-#pragma unroll
-      for (int i = 0; i < ND; ++i) {
-        if ((uint32_t)i == (bit >> 5)) lo = d[i];
-        if ((uint32_t)i == (bit >> 5) + 1) hi = d[i];
-      }
-      w[u] = __builtin_amdgcn_alignbit(hi, lo, bit & 31) & 0xFFFFFFu;
-    }
-  }
-}
-
 template <int BITS>
 __device__ __forceinline__ u32x4 codes_bf16(uint32_t w) {
   return BITS == 4 ? codes_bf16_4(w) : codes_bf16_3(w);
 }
 
 // ---------------------------------------------------------------------------
-// Grouped GEMM over the work list. One block (16 waves) per (item, 256
-// output columns); wave w owns columns 16w .. 16w + 15 of the block, lane
-// (n = l % 16, q = l / 16) column n and k-block q. The item's <= 32 entry
-// rows are staged in LDS chunk by chunk (kPfKC inputs, permuted to the code
-// order, split into bf16 hi + lo when they are fp32); the next chunk's codes
-// and scales are loaded into registers while the current chunk computes.
-// MODE 0: gate and up (K = hidden, A = x rows of the entries' tokens),
-// act = silu(gate) * up. MODE 1: down (K = inter, A = act rows).
+// Persistent pipelined GEMM (k_pf_mm). One block of 8 waves per CU loops
+// over work units (item, NCOL output columns); a unit is K / 256 chunks,
+// and the block's chunk sequence streams through an S-stage LDS ring:
+// global_load_lds copies each chunk's weight codes, bf16 scales/biases,
+// A rows (MFMA-ready bf16, already permuted) and A group sums straight
+// into LDS (no registers), S - 1 chunks ahead of the MFMAs. Each wave
+// waits only for its own copies of the chunk it is about to use
+// (s_waitcnt vmcnt), then one barrier makes all waves' copies visible.
+// Waves 0-3 and 4-7 take the lower and upper K half of each chunk for the
+// same columns (two waves per SIMD, so one's VALU work overlaps the other's
+// MFMAs) and add their sums through LDS when a unit ends. Swizzles: weight rows XOR (4-bit) or rotate (3-bit) their 16-byte parts
+// by the row, A rows XOR their parts by the row, so the 16 lanes of an
+// MFMA operand read different banks.
 // ---------------------------------------------------------------------------
-// Inputs per LDS chunk: 128 for gate/up (two weight matrices in flight per
-// lane), 256 for down; both dimensions of the layer are multiples of 256.
-template <int MODE>
-constexpr int pf_kc() {
-  return MODE == 0 ? 128 : 256;
-}
-constexpr int kPfKC = 256;
+#define PF_GPTR(p) ((const __attribute__((address_space(1))) void*)(p))
+#define PF_LPTR(p) ((__attribute__((address_space(3))) void*)(p))
 
-template <int BITS, int G, int NMAT, int KC>
-struct PfChunk {
-  static constexpr int NU = G / 32, CG = KC / G;
-  uint32_t w[NMAT][CG][NU];
-  uint32_t sb[NMAT][CG];  // bf16 scale | bf16 bias << 16
+__device__ __forceinline__ void dma16(const void* g, void* l) {
+  __builtin_amdgcn_global_load_lds(PF_GPTR(g), PF_LPTR(l), 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void* g, void* l) {
+  __builtin_amdgcn_global_load_lds(PF_GPTR(g), PF_LPTR(l), 4, 0, 0);
+}
+
+// Position of natural index i (0..7) of an 8-block in the MFMA order
+// [v0, v4, v1, v5, v2, v6, v3, v7].
+__device__ __forceinline__ uint32_t perm8_pos(uint32_t i) { return i < 4 ? 2 * i : 2 * (i - 4) + 1; }
+
+template <int BITS, int G, int MODE, bool SPLIT>
+struct PfMM {
+  static constexpr int NW = 8;                        // waves per block: 4 column waves x 2 K halves
+  static constexpr int KC = kPfKC;                    // inputs per chunk
+  static constexpr int CG = KC / G;                   // groups per chunk
+  static constexpr int CGW = CG / 2;                  // groups per wave (its K half of the chunk)
+  static constexpr int NU = G / 32;                   // MFMA steps per group
+  static constexpr int NMAT = MODE == 0 ? 2 : 1;      // weight matrices per column
+  static constexpr int CT = MODE == 0 ? 1 : 4;        // 16-column tiles per wave
+  static constexpr int NCOL = 64 * CT;                // output columns per unit
+  static constexpr int ROWS = NMAT * NCOL;            // weight rows per unit
+  static constexpr int RB = KC * BITS / 8;            // code bytes per row and chunk
+  static constexpr int PPR = RB / 16;                 // 16-byte parts per row
+  static constexpr int SB_BYTES = 2 * CG;             // scale (or bias) bytes per row and chunk
+  static constexpr int SB_SZ = SB_BYTES >= 16 ? 16 : 4;
+  static constexpr int SB_PIECES = SB_BYTES / SB_SZ;  // per row and array
+  static constexpr int S = MODE == 0 ? (SPLIT ? 3 : 4) : 2;
+  // Copy pieces per chunk and category; every wave copies an equal,
+  // contiguous share (so every wave issues the same number of copies).
+  static constexpr int P_BQ = ROWS * PPR;             // 16-byte code parts
+  static constexpr int P_BS = ROWS * 2 * SB_PIECES;   // scale / bias pieces
+  static constexpr int P_A = kPfMC * KC * 2 / 16;     // 16-byte A parts (per half)
+  static constexpr int P_XS = kPfMC * CG;             // group sums
+  static constexpr int N_BQ = (P_BQ / NW + 63) / 64;  // copy instructions per wave
+  static constexpr int N_BS = (P_BS / NW + 63) / 64;
+  static constexpr int N_A = (P_A / NW + 63) / 64;
+  static constexpr int N_XS = (P_XS / NW + 63) / 64;
+  static constexpr int D = N_BQ + N_BS + N_A * (SPLIT ? 2 : 1) + N_XS;
+  // LDS layout of one stage (bytes).
+  static constexpr int OFF_BQ = 0;
+  static constexpr int OFF_BS = OFF_BQ + P_BQ * 16;
+  static constexpr int OFF_AH = OFF_BS + P_BS * SB_SZ;
+  static constexpr int OFF_AL = OFF_AH + P_A * 16;
+  static constexpr int OFF_XS = OFF_AL + (SPLIT ? P_A * 16 : 0);
+  static constexpr int STAGE = OFF_XS + P_XS * 4;
+  // Accumulators per lane, exchanged between the K halves through LDS.
+  static constexpr int NT = NMAT * CT * 2 * 4;
+  static_assert(CG % 2 == 0, "K halves");
+  static_assert(P_BQ % NW == 0 && P_BS % NW == 0 && P_A % NW == 0 && P_XS % NW == 0, "equal shares");
+  static_assert((S - 2) * D <= 63, "vmcnt range");
+  static_assert(S * STAGE <= 160 * 1024, "LDS per CU");
+  static_assert(4 * NT * 64 * 4 <= STAGE, "accumulator exchange fits a stage");
 };
 
 template <int BITS, int G, int MODE, bool SPLIT>
-__global__ __launch_bounds__(1024) void k_pf_gemm(PfArgs a) {
-  constexpr int KC = pf_kc<MODE>();
-  constexpr int AROW = KC + 8;  // LDS row stride in bf16 (16-byte pad)
-  constexpr int NU = G / 32, CG = KC / G, NMAT = MODE == 0 ? 2 : 1;
-  static_assert(CG >= 1, "chunk must hold a whole group");
-  __shared__ __attribute__((aligned(16))) uint16_t ahi[kPfMC * AROW];
-  __shared__ __attribute__((aligned(16))) uint16_t alo[(SPLIT ? kPfMC : 1) * AROW];
-  __shared__ float sxs[kPfMC * kPfMaxGroupsK];
-  const uint32_t item = blockIdx.x;
-  if (item >= *a.n_items) return;
-  const uint32_t e = a.items[2 * item];
-  const uint32_t start = a.items[2 * item + 1] & 0xFFFFu, cnt = a.items[2 * item + 1] >> 16;
+__global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restrict__ items,
+                                               const uint32_t* __restrict__ n_items_p) {
+  using C = PfMM<BITS, G, MODE, SPLIT>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t cw = wave & 3, kh = wave >> 2;  // column wave, K half
   const uint32_t n = lane & 15, q = lane >> 4;
-  const BlobGeom& gm = a.g;
-  const uint32_t K = MODE == 0 ? gm.hidden : gm.inter;
-  const uint32_t N = MODE == 0 ? gm.inter : gm.hidden;
-  const uint32_t ng = K / G, nch = K / KC, rowb = K * BITS / 8;
-  const uint32_t col = blockIdx.y * 256 + wave * 16 + n;
-  const uint8_t* blob = a.experts + (size_t)e * a.stride;
-  const uint32_t ntiles = (cnt + 15) / 16;
+  // Every kernel argument used below is copied into a scalar local first,
+  // so that nothing takes the argument block's address (that would move it
+  // to scratch memory, and a wait on those loads would drain the copy
+  // pipeline).
+  const uint32_t K = MODE == 0 ? a.g.hidden : a.g.inter;
+  const uint32_t N = MODE == 0 ? a.g.inter : a.g.hidden;
+  const uint32_t ng = K / G, nch = K / C::KC, rowb = K * BITS / 8;
+  const uint32_t ncb = N / C::NCOL;
+  // XCD-aware schedule: block b runs on XCD b % 8, so items go round-robin
+  // over the 8 XCD groups and an item's ncb column blocks run side by side
+  // on one XCD, where its A rows are fetched into that XCD's L2 once.
+  const uint32_t nx = gridDim.x % 8 == 0 ? 8 : 1, per = gridDim.x / nx;
+  const uint32_t xg = blockIdx.x % nx, lb = blockIdx.x / nx;
+  const uint32_t n_items = *n_items_p;
+  const uint32_t group_units = (n_items > xg ? (n_items - xg + nx - 1) / nx : 0) * ncb;
+  const uint32_t my_units = group_units > lb ? (group_units - lb + per - 1) / per : 0;
+  const uint32_t total = my_units * nch;
+  if (total == 0) return;
+  // A rows are entries (x was gathered into entry order): no indirection.
+  const uint16_t* const ahi_src = MODE == 0 ? a.x_hi : a.act_hi;
+  const uint16_t* const alo_src = MODE == 0 ? a.x_lo : a.act_lo;
+  const float* const gsum = MODE == 0 ? a.xsum : a.asum;
+  const uint8_t* const experts = a.experts;
+  const uint64_t stride = a.stride;
+  uint16_t* const act_hi = a.act_hi;
+  uint16_t* const act_lo = a.act_lo;
+  float* const down = a.down;
+  const uint64_t wo0 = a.g.w[MODE == 0 ? 0 : 2], wo1 = a.g.w[MODE == 0 ? 1 : 2];
+  const uint64_t so0 = a.g.s[MODE == 0 ? 0 : 2], so1 = a.g.s[MODE == 0 ? 1 : 2];
+  const uint64_t bo0 = a.g.b[MODE == 0 ? 0 : 2];
 
-  // Group sums of the entries' A rows.
-  for (uint32_t i = tid; i < kPfMC * ng; i += blockDim.x) {
-    const uint32_t m = i / ng, g = i % ng, mm = min(m, cnt - 1);
-    sxs[i] = MODE == 0 ? a.xsum[(size_t)a.ent_token[start + mm] * ng + g]
-                       : a.asum[(size_t)(start + mm) * ng + g];
-  }
-
-  // A staging: thread -> (row m, 8 inputs at 8 * sp of the chunk); the first
-  // kPfMC * KC / 8 threads take part.
-  constexpr uint32_t SPR = KC / 8;  // staging threads per row
-  const bool stager = tid < kPfMC * SPR;
-  const uint32_t sm = stager ? tid / SPR : 0, sp = tid % SPR;
-  const uint32_t srow = MODE == 0 ? (uint32_t)a.ent_token[start + min(sm, cnt - 1)] : start + min(sm, cnt - 1);
-  float sf[8];
-  u32x4 sv;
-  auto a_load = [&](uint32_t c) {
-    if (!stager) return;
-    const size_t k0 = (size_t)c * KC + 8 * sp;
-    if (MODE == 0 && !SPLIT) {
-      sv = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)srow * K + k0);
-    } else {
-      const float* p = (MODE == 0 ? reinterpret_cast<const float*>(a.x) : a.act) + (size_t)srow * K + k0;
-      const float4 v0 = *reinterpret_cast<const float4*>(p);
-      const float4 v1 = *reinterpret_cast<const float4*>(p + 4);
-      sf[0] = v0.x; sf[1] = v0.y; sf[2] = v0.z; sf[3] = v0.w;
-      sf[4] = v1.x; sf[5] = v1.y; sf[6] = v1.z; sf[7] = v1.w;
-    }
-  };
-  auto a_store = [&]() {
-    if (!stager) return;
-    u32x4* dh = reinterpret_cast<u32x4*>(ahi + sm * AROW + 8 * sp);
-    if (MODE == 0 && !SPLIT) {
-      *dh = perm_bf16(sv);
-    } else {
-      u32x4 hi, lo;
-      split_f32(sf, hi, lo);
-      *dh = hi;
-      if (SPLIT) *reinterpret_cast<u32x4*>(alo + sm * AROW + 8 * sp) = lo;
-    }
-  };
-  auto b_load = [&](uint32_t c, PfChunk<BITS, G, NMAT, KC>& ch) {
+  // Issue every copy of flattened chunk j into stage j % S. Captures by
+  // value: a by-reference capture stores the locals' addresses, and the
+  // memory clobbers of the waits below would then keep them in scratch.
+  auto issue = [=](uint32_t j) {
+    const uint32_t v = lb + (j / nch) * per, c = j % nch;
+    const uint32_t item = xg + nx * (v / ncb), cb = v % ncb;
+    const uint32_t e = items[2 * item];
+    const uint32_t start = items[2 * item + 1] & 0xFFFFu, cnt = items[2 * item + 1] >> 16;
+    const uint8_t* blob = experts + (size_t)e * stride;
+    uint8_t* st = lds + (j % C::S) * C::STAGE;
+    // Weight codes: slot p = (row, slot part) holds the row's part
+    // (slot part ^ row & 7) [4-bit] or ((slot part + row) % 6) [3-bit].
 #pragma unroll
-    for (int mat = 0; mat < NMAT; ++mat) {
-      const int blk = MODE == 0 ? mat : 2;
+    for (int i = 0; i < C::N_BQ; ++i) {
+      const uint32_t o = i * 64 + lane;
+      const uint32_t p = wave * (C::P_BQ / C::NW) + o;
+      const uint32_t row = p / C::PPR, sp = p % C::PPR;
+      const uint32_t part = BITS == 4 ? (sp ^ (row & 7)) : (sp + row) % C::PPR;
+      const uint32_t mat = row / C::NCOL, wrow = cb * C::NCOL + row % C::NCOL;
+      const uint64_t wo = wo0 + mat * (wo1 - wo0);
+      if ((C::P_BQ / C::NW) % 64 == 0 || o < (uint32_t)(C::P_BQ / C::NW))
+        dma16(blob + wo + (size_t)wrow * rowb + (size_t)c * C::RB + part * 16,
+              st + C::OFF_BQ + (wave * (C::P_BQ / C::NW) + i * 64) * 16);
+    }
+    // Scales then biases of each row: [row][array][CG] bf16.
 #pragma unroll
-      for (int gl = 0; gl < CG; ++gl) {
-        const uint32_t g = c * CG + gl;
-        load_codes<BITS, NU>(blob + gm.w[blk], rowb, col, g, q, ch.w[mat][gl]);
-        const size_t gi = ((size_t)col * ng + g) * 2;
-        const uint32_t sv16 = *reinterpret_cast<const uint16_t*>(blob + gm.s[blk] + gi);
-        const uint32_t bv16 = *reinterpret_cast<const uint16_t*>(blob + gm.b[blk] + gi);
-        ch.sb[mat][gl] = sv16 | (bv16 << 16);
+    for (int i = 0; i < C::N_BS; ++i) {
+      const uint32_t o = i * 64 + lane;
+      const uint32_t p = wave * (C::P_BS / C::NW) + o;
+      const uint32_t row = p / (2 * C::SB_PIECES), arr = (p / C::SB_PIECES) % 2, pc = p % C::SB_PIECES;
+      const uint32_t mat = row / C::NCOL, wrow = cb * C::NCOL + row % C::NCOL;
+      // Arithmetic, not a select: a select between captured values becomes a
+      // load from a lane-varying address of the closure, in scratch memory.
+      // Biases follow scales at the same distance in both matrices.
+      const uint64_t so = so0 + mat * (so1 - so0) + arr * (bo0 - so0);
+      const uint8_t* src = blob + so + ((size_t)wrow * ng + (size_t)c * C::CG) * 2 + pc * C::SB_SZ;
+      uint8_t* dst = st + C::OFF_BS + (wave * (C::P_BS / C::NW) + i * 64) * C::SB_SZ;
+      if ((C::P_BS / C::NW) % 64 == 0 || o < (uint32_t)(C::P_BS / C::NW)) {
+        if (C::SB_SZ == 16) dma16(src, dst); else dma4(src, dst);
       }
     }
-  };
-  f32x4 tot[NMAT][2];
+    // A rows (bf16, MFMA order): slot part = part ^ (m & 15).
 #pragma unroll
-  for (int mat = 0; mat < NMAT; ++mat)
+    for (int hl = 0; hl < (SPLIT ? 2 : 1); ++hl) {
+      const uint16_t* src = hl ? alo_src : ahi_src;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) tot[mat][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  auto compute = [&](uint32_t c, const PfChunk<BITS, G, NMAT, KC>& ch) {
-#pragma unroll
-    for (int gl = 0; gl < CG; ++gl) {
-      const uint32_t g = c * CG + gl;
-      float s[NMAT], cb[NMAT];
-#pragma unroll
-      for (int mat = 0; mat < NMAT; ++mat) {
-        s[mat] = __uint_as_float(ch.sb[mat][gl] << 16);
-        cb[mat] = __builtin_fmaf(-128.0f, s[mat], __uint_as_float(ch.sb[mat][gl] & 0xFFFF0000u));
+      for (int i = 0; i < C::N_A; ++i) {
+        const uint32_t o = i * 64 + lane;
+        const uint32_t p = wave * (C::P_A / C::NW) + o;
+        const uint32_t m = p / 32, sp = p % 32, part = sp ^ (m & 15);
+        const size_t arow = start + min(m, cnt - 1);
+        if ((C::P_A / C::NW) % 64 == 0 || o < (uint32_t)(C::P_A / C::NW))
+          dma16(src + arow * K + (size_t)c * C::KC + part * 8,
+                st + (hl ? C::OFF_AL : C::OFF_AH) + (wave * (C::P_A / C::NW) + i * 64) * 16);
       }
+    }
+    // Group sums of the A rows, [group][row].
+#pragma unroll
+    for (int i = 0; i < C::N_XS; ++i) {
+      const uint32_t o = i * 64 + lane;
+      const uint32_t p = wave * (C::P_XS / C::NW) + o;
+      const uint32_t g = p / kPfMC, m = p % kPfMC;
+      const size_t arow = start + min(m, cnt - 1);
+      if ((C::P_XS / C::NW) % 64 == 0 || o < (uint32_t)(C::P_XS / C::NW))
+        dma4(gsum + arow * ng + (size_t)c * C::CG + g, st + C::OFF_XS + (wave * (C::P_XS / C::NW) + i * 64) * 4);
+    }
+  };
+
+  f32x4 tot[C::NMAT][C::CT][2];
+#pragma unroll
+  for (int mt = 0; mt < C::NMAT; ++mt)
+#pragma unroll
+    for (int ct = 0; ct < C::CT; ++ct)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) tot[mt][ct][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (uint32_t j = 0; j + 1 < (uint32_t)C::S && j < total; ++j) issue(j);
+  for (uint32_t j = 0; j < total; ++j) {
+    // Copies of chunks j + 1 .. j + S - 2 may stay in flight.
+    const uint32_t ahead = min((uint32_t)C::S - 2, total - 1 - j);
+    if (ahead == 0)
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    else if (ahead == 1)
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(C::D) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(2 * C::D) : "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (j + C::S - 1 < total) issue(j + C::S - 1);
+
+    const uint32_t v = lb + (j / nch) * per, c = j % nch;
+    const uint32_t item = xg + nx * (v / ncb), cb = v % ncb;
+    const uint32_t start = items[2 * item + 1] & 0xFFFFu, cnt = items[2 * item + 1] >> 16;
+    const uint32_t ntiles = (cnt + 15) / 16;
+    uint8_t* st = lds + (j % C::S) * C::STAGE;
+#pragma unroll
+    for (int gi = 0; gi < C::CGW; ++gi) {
+      const uint32_t gl = kh * C::CGW + gi;
+      uint32_t bw[C::NMAT][C::CT][C::NU];
+      float s[C::NMAT][C::CT], cbias[C::NMAT][C::CT];
+#pragma unroll
+      for (int mt = 0; mt < C::NMAT; ++mt)
+#pragma unroll
+        for (int ct = 0; ct < C::CT; ++ct) {
+          const uint32_t row = mt * C::NCOL + cw * 16 * C::CT + ct * 16 + n;
+          const uint8_t* rb = st + C::OFF_BQ + row * C::RB;
+          if (BITS == 4) {
+            const uint32_t off = gl * (G / 2) + 4 * C::NU * q;  // byte offset in the chunk row
+            const uint32_t slot = (off / 16) ^ (row & 7);
+            const uint32_t* w = reinterpret_cast<const uint32_t*>(rb + slot * 16 + off % 16);
+#pragma unroll
+            for (int uu = 0; uu < C::NU; ++uu) bw[mt][ct][uu] = w[uu];
+          } else {
+            const uint32_t off = (gl * G + 8 * C::NU * q) * 3 / 8;  // 3*NU bytes
+            constexpr int ND = (3 * C::NU + 6) / 4;
+            uint32_t d[ND];
+#pragma unroll
+            for (int i = 0; i < ND; ++i) {
+              const uint32_t dw = (off & ~3u) / 4 + i;  // dword index in the row (0 .. RB/4)
+              const uint32_t part = min(dw / 4, (uint32_t)C::PPR - 1);
+              const uint32_t slot = (part + C::PPR - row % C::PPR) % C::PPR;
+              d[i] = *reinterpret_cast<const uint32_t*>(rb + slot * 16 + (dw % 4) * 4);
+            }
+            const uint32_t sh = (off & 3u) * 8;
+#pragma unroll
+            for (int uu = 0; uu < C::NU; ++uu) {
+              const uint32_t bit = sh + 24 * uu;
+              uint32_t lo = 0, hi = 0;
+#pragma unroll
+              for (int i = 0; i < ND; ++i) {
+                if ((uint32_t)i == (bit >> 5)) lo = d[i];
+                if ((uint32_t)i == (bit >> 5) + 1) hi = d[i];
+              }
+              bw[mt][ct][uu] = __builtin_amdgcn_alignbit(hi, lo, bit & 31) & 0xFFFFFFu;
+            }
+          }
+          const uint16_t* sb = reinterpret_cast<const uint16_t*>(st + C::OFF_BS + row * 2 * C::SB_BYTES);
+          s[mt][ct] = bf16f(sb[gl]);
+          cbias[mt][ct] = __builtin_fmaf(-128.0f, s[mt][ct], bf16f(sb[C::CG + gl]));
+        }
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         if ((uint32_t)t >= ntiles) continue;
-        const uint32_t arow = (16 * t + n) * AROW + gl * G + 8 * NU * q;
-        f32x4 acc[NMAT];
+        const uint32_t m = 16 * t + n;
+        f32x4 acc[C::NMAT][C::CT];
 #pragma unroll
-        for (int mat = 0; mat < NMAT; ++mat) acc[mat] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int mt = 0; mt < C::NMAT; ++mt)
 #pragma unroll
-        for (int u = 0; u < NU; ++u) {
-          const u32x4 ah = *reinterpret_cast<const u32x4*>(ahi + arow + 8 * u);
+          for (int ct = 0; ct < C::CT; ++ct) acc[mt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int uu = 0; uu < C::NU; ++uu) {
+          const uint32_t part = (gl * G + 8 * C::NU * q + 8 * uu) / 8;
+          const uint32_t aoff = m * C::KC * 2 + ((part ^ (m & 15)) * 16);
+          const u32x4 ah = *reinterpret_cast<const u32x4*>(st + C::OFF_AH + aoff);
           u32x4 al;
-          if (SPLIT) al = *reinterpret_cast<const u32x4*>(alo + arow + 8 * u);
+          if (SPLIT) al = *reinterpret_cast<const u32x4*>(st + C::OFF_AL + aoff);
 #pragma unroll
-          for (int mat = 0; mat < NMAT; ++mat) {
-            const u32x4 bq = codes_bf16<BITS>(ch.w[mat][gl][u]);
-            acc[mat] = mfma(ah, bq, acc[mat]);
-            if (SPLIT) acc[mat] = mfma(al, bq, acc[mat]);
-          }
+          for (int mt = 0; mt < C::NMAT; ++mt)
+#pragma unroll
+            for (int ct = 0; ct < C::CT; ++ct) {
+              const u32x4 bq = codes_bf16<BITS>(bw[mt][ct][uu]);
+              acc[mt][ct] = mfma(ah, bq, acc[mt][ct]);
+              if (SPLIT) acc[mt][ct] = mfma(al, bq, acc[mt][ct]);
+            }
         }
+        // Group sums of rows 16t + 4q .. + 3 in one read ([group][row]).
+        const f32x4 xs = *reinterpret_cast<const f32x4*>(st + C::OFF_XS + (gl * kPfMC + 16 * t + 4 * q) * 4);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float xs = sxs[(16 * t + 4 * q + r) * ng + g];
+        for (int r = 0; r < 4; ++r)
 #pragma unroll
-          for (int mat = 0; mat < NMAT; ++mat)
-            tot[mat][t][r] = __builtin_fmaf(s[mat], acc[mat][r], __builtin_fmaf(cb[mat], xs, tot[mat][t][r]));
-        }
+          for (int mt = 0; mt < C::NMAT; ++mt)
+#pragma unroll
+            for (int ct = 0; ct < C::CT; ++ct)
+              tot[mt][ct][t][r] = __builtin_fmaf(s[mt][ct], acc[mt][ct][r],
+                                                 __builtin_fmaf(cbias[mt][ct], xs[r], tot[mt][ct][t][r]));
       }
     }
-  };
 
-  PfChunk<BITS, G, NMAT, KC> b0, b1;
-  a_load(0);
-  b_load(0, b0);
-  a_store();
-  __syncthreads();
-  for (uint32_t c = 0; c < nch; c += 2) {
-    if (c + 1 < nch) {
-      a_load(c + 1);
-      b_load(c + 1, b1);
+    if (c + 1 == nch) {  // unit complete: add the K halves, write it out
+      // Every wave is done reading this stage; the upper half parks its sums
+      // there ([column wave][accumulator][lane]) for the lower half.
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      float* ex = reinterpret_cast<float*>(st) + cw * C::NT * 64 + lane;
+      if (kh == 1) {
+#pragma unroll
+        for (int mt = 0; mt < C::NMAT; ++mt)
+#pragma unroll
+          for (int ct = 0; ct < C::CT; ++ct)
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) ex[(((mt * C::CT + ct) * 2 + t) * 4 + r) * 64] = tot[mt][ct][t][r];
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (kh == 0) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          if ((uint32_t)t >= ntiles) continue;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const uint32_t m = 16 * t + 4 * q + r;
+#pragma unroll
+            for (int ct = 0; ct < C::CT; ++ct) {
+              float o[C::NMAT];
+#pragma unroll
+              for (int mt = 0; mt < C::NMAT; ++mt)
+                o[mt] = tot[mt][ct][t][r] + ex[(((mt * C::CT + ct) * 2 + t) * 4 + r) * 64];
+              if (m >= cnt) continue;
+              const uint32_t colj = cb * C::NCOL + cw * 16 * C::CT + ct * 16 + n;
+              if constexpr (MODE == 0) {
+                // act as bf16 hi + lo in the MFMA order of the down GEMM.
+                const float v = silu_mul(o[0], o[1]);
+                const uint32_t hi = pk_bf16(v, 0.f) & 0xFFFFu;
+                const uint32_t lo = pk_bf16(v - __uint_as_float(hi << 16), 0.f) & 0xFFFFu;
+                const size_t at = (size_t)(start + m) * N + (colj & ~7u) + perm8_pos(colj & 7u);
+                act_hi[at] = (uint16_t)hi;
+                act_lo[at] = (uint16_t)lo;
+              } else {
+                down[(size_t)(start + m) * N + colj] = o[0];
+              }
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int mt = 0; mt < C::NMAT; ++mt)
+#pragma unroll
+        for (int ct = 0; ct < C::CT; ++ct)
+#pragma unroll
+          for (int t = 0; t < 2; ++t) tot[mt][ct][t] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    compute(c, b0);
-    if (c + 1 >= nch) break;
-    __syncthreads();
-    a_store();
-    __syncthreads();
-    if (c + 2 < nch) {
-      a_load(c + 2);
-      b_load(c + 2, b0);
-    }
-    compute(c + 1, b1);
-    if (c + 2 >= nch) break;
-    __syncthreads();
-    a_store();
-    __syncthreads();
   }
+}
 
+// Entry e's x row (token ent_token[e]) -> MFMA-ready bf16 hi (and lo for
+// fp32 input) in entry order, and its group sums over what the MFMA sees
+// (hi + lo). One block per entry.
+__global__ __launch_bounds__(256) void k_pf_prep_x(PfArgs a) {
+  __shared__ float part8[kPfMaxGroupsK * 128 / 8];
+  const uint32_t e = blockIdx.x, H = a.g.hidden, G = a.g.group;
+  // In range even when bucketing rejected the input (then *err is set).
+  const uint32_t t = min((uint32_t)a.ent_token[e], a.n_tokens - 1);
+  for (uint32_t k0 = threadIdx.x * 8; k0 < H; k0 += blockDim.x * 8) {
+    float f[8];
+    if (a.x_bf16) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)t * H + k0);
+      const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    if ((uint32_t)t >= ntiles) continue;
+      for (int i = 0; i < 4; ++i) {
+        f[2 * i] = __uint_as_float(w4[i] << 16);
+        f[2 * i + 1] = __uint_as_float(w4[i] & 0xFFFF0000u);
+      }
+    } else {
+      const float* p = reinterpret_cast<const float*>(a.x) + (size_t)t * H + k0;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const uint32_t m = 16 * t + 4 * q + r;
-      if (m >= cnt) continue;
-      if (MODE == 0)
-        a.act[(size_t)(start + m) * N + col] = silu_mul(tot[0][t][r], tot[1][t][r]);
-      else
-        a.down[(size_t)(start + m) * N + col] = tot[0][t][r];
+      for (int i = 0; i < 8; ++i) f[i] = p[i];
     }
+    u32x4 hi, lo;
+    split_f32(f, hi, lo);
+    *reinterpret_cast<u32x4*>(a.x_hi + (size_t)e * H + k0) = hi;
+    if (!a.x_bf16) *reinterpret_cast<u32x4*>(a.x_lo + (size_t)e * H + k0) = lo;
+    // Partial sum of these 8 inputs as the MFMA sees them.
+    const uint32_t hv[4] = {hi.x, hi.y, hi.z, hi.w}, lv[4] = {lo.x, lo.y, lo.z, lo.w};
+    float p = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p += __uint_as_float(hv[i] << 16) + __uint_as_float(hv[i] & 0xFFFF0000u);
+      if (!a.x_bf16) p += __uint_as_float(lv[i] << 16) + __uint_as_float(lv[i] & 0xFFFF0000u);
+    }
+    part8[k0 / 8] = p;
+  }
+  __syncthreads();
+  const uint32_t ng = H / G, per = G / 8;
+  for (uint32_t g = threadIdx.x; g < ng; g += blockDim.x) {
+    float s = 0.f;
+    for (uint32_t j = 0; j < per; ++j) s += part8[g * per + j];
+    a.xsum[(size_t)e * ng + g] = s;
+  }
+}
+
+// Group sums of the activations (hi + lo) per entry; one block per entry.
+__global__ __launch_bounds__(256) void k_pf_act_sum(PfArgs a) {
+  __shared__ float part8[kPfMaxGroupsK * 128 / 8];
+  const uint32_t r = blockIdx.x, I = a.g.inter, G = a.g.group;
+  for (uint32_t k0 = threadIdx.x * 8; k0 < I; k0 += blockDim.x * 8) {
+    const u32x4 h = *reinterpret_cast<const u32x4*>(a.act_hi + (size_t)r * I + k0);
+    const u32x4 l = *reinterpret_cast<const u32x4*>(a.act_lo + (size_t)r * I + k0);
+    const uint32_t hv[4] = {h.x, h.y, h.z, h.w}, lv[4] = {l.x, l.y, l.z, l.w};
+    float p = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      p += __uint_as_float(hv[i] << 16) + __uint_as_float(hv[i] & 0xFFFF0000u) + __uint_as_float(lv[i] << 16) +
+           __uint_as_float(lv[i] & 0xFFFF0000u);
+    part8[k0 / 8] = p;
+  }
+  __syncthreads();
+  const uint32_t ng = I / G, per = G / 8;
+  for (uint32_t g = threadIdx.x; g < ng; g += blockDim.x) {
+    float s = 0.f;
+    for (uint32_t j = 0; j < per; ++j) s += part8[g * per + j];
+    a.asum[(size_t)r * ng + g] = s;
   }
 }
 
@@ -491,9 +658,12 @@ uint64_t prefill_workspace(uint32_t hidden, uint32_t inter, uint32_t group, uint
   uint8_t* p_tok = take(nk * 4);
   uint8_t* p_w = take(nk * 4);
   uint8_t* p_pos = take(nk * 4);
-  uint8_t* p_xsum = take((uint64_t)n_tokens * (hidden / group) * 4);
+  uint8_t* p_xsum = take(nk * (hidden / group) * 4);
   uint8_t* p_asum = take(nk * (inter / group) * 4);
-  uint8_t* p_act = take(nk * inter * 4);
+  uint8_t* p_xhi = take(nk * hidden * 2);
+  uint8_t* p_xlo = take(nk * hidden * 2);
+  uint8_t* p_ahi = take(nk * inter * 2);
+  uint8_t* p_alo = take(nk * inter * 2);
   uint8_t* p_down = take(nk * hidden * 4);
   if (a) {
     a->items = reinterpret_cast<uint32_t*>(p_items);
@@ -503,7 +673,10 @@ uint64_t prefill_workspace(uint32_t hidden, uint32_t inter, uint32_t group, uint
     a->tok_pos = reinterpret_cast<int32_t*>(p_pos);
     a->xsum = reinterpret_cast<float*>(p_xsum);
     a->asum = reinterpret_cast<float*>(p_asum);
-    a->act = reinterpret_cast<float*>(p_act);
+    a->x_hi = reinterpret_cast<uint16_t*>(p_xhi);
+    a->x_lo = reinterpret_cast<uint16_t*>(p_xlo);
+    a->act_hi = reinterpret_cast<uint16_t*>(p_ahi);
+    a->act_lo = reinterpret_cast<uint16_t*>(p_alo);
     a->down = reinterpret_cast<float*>(p_down);
     a->max_items = (uint32_t)max_items;
   }
@@ -522,33 +695,45 @@ bool prefill_supported(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t
   return true;
 }
 
-template <int BITS, int G>
-static void launch_gemms(const PfArgs& a, hipStream_t st) {
-  const dim3 gu(a.max_items, a.g.inter / 256), dn(a.max_items, a.g.hidden / 256);
-  if (a.x_bf16)
-    hipLaunchKernelGGL((k_pf_gemm<BITS, G, 0, false>), gu, dim3(1024), 0, st, a);
-  else
-    hipLaunchKernelGGL((k_pf_gemm<BITS, G, 0, true>), gu, dim3(1024), 0, st, a);
-  const uint32_t nk = a.n_tokens * a.k;
-  hipLaunchKernelGGL(k_pf_rowsum, dim3(nk), dim3(64), 0, st, (const void*)a.act, 0, a.g.inter,
-                     (uint32_t)G, (const uint32_t*)nullptr, nk, a.asum);
-  hipLaunchKernelGGL((k_pf_gemm<BITS, G, 1, true>), dn, dim3(1024), 0, st, a);
+template <int BITS, int G, int MODE, bool SPLIT>
+static hipError_t launch_mm(const PfArgs& a, uint32_t n_units_max, uint32_t n_cu, hipStream_t st) {
+  using C = PfMM<BITS, G, MODE, SPLIT>;
+  const auto fn = reinterpret_cast<const void*>(&k_pf_mm<BITS, G, MODE, SPLIT>);
+  const size_t lds = (size_t)C::S * C::STAGE;
+  static bool attr_set = false;
+  if (!attr_set) {
+    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  const uint32_t grid = n_units_max < n_cu ? n_units_max : n_cu;
+  hipLaunchKernelGGL((k_pf_mm<BITS, G, MODE, SPLIT>), dim3(grid), dim3(64 * C::NW), lds, st, a,
+                     (const uint32_t*)a.items, (const uint32_t*)a.n_items);
+  return hipGetLastError();
 }
 
-hipError_t launch_prefill(const PfArgs& a, hipStream_t st) {
+template <int BITS, int G>
+static hipError_t launch_gemms(const PfArgs& a, uint32_t n_cu, hipStream_t st) {
+  hipError_t e = a.x_bf16 ? launch_mm<BITS, G, 0, false>(a, a.max_items * (a.g.inter / 64), n_cu, st)
+                          : launch_mm<BITS, G, 0, true>(a, a.max_items * (a.g.inter / 64), n_cu, st);
+  if (e != hipSuccess) return e;
+  const uint32_t nk = a.n_tokens * a.k;
+  hipLaunchKernelGGL(k_pf_act_sum, dim3(nk), dim3(256), 0, st, a);
+  return launch_mm<BITS, G, 1, true>(a, a.max_items * (a.g.hidden / 256), n_cu, st);
+}
+
+hipError_t launch_prefill(const PfArgs& a, uint32_t n_cu, hipStream_t st) {
   hipLaunchKernelGGL(k_pf_route, dim3(1), dim3(1024), 0, st, a);
-  hipLaunchKernelGGL(k_pf_rowsum, dim3(a.n_tokens), dim3(64), 0, st, a.x, a.x_bf16, a.g.hidden,
-                     a.g.group, (const uint32_t*)nullptr, a.n_tokens, a.xsum);
+  hipLaunchKernelGGL(k_pf_prep_x, dim3(a.n_tokens * a.k), dim3(256), 0, st, a);
   const uint32_t G = a.g.group;
-  if (a.g.bits == 4) {
-    if (G == 32) launch_gemms<4, 32>(a, st);
-    else if (G == 64) launch_gemms<4, 64>(a, st);
-    else launch_gemms<4, 128>(a, st);
-  } else {
-    if (G == 32) launch_gemms<3, 32>(a, st);
-    else if (G == 64) launch_gemms<3, 64>(a, st);
-    else launch_gemms<3, 128>(a, st);
-  }
+  hipError_t e;
+  if (a.g.bits == 4)
+    e = G == 32 ? launch_gemms<4, 32>(a, n_cu, st) : G == 64 ? launch_gemms<4, 64>(a, n_cu, st)
+                                                   : launch_gemms<4, 128>(a, n_cu, st);
+  else
+    e = G == 32 ? launch_gemms<3, 32>(a, n_cu, st) : G == 64 ? launch_gemms<3, 64>(a, n_cu, st)
+                                                   : launch_gemms<3, 128>(a, n_cu, st);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL(k_pf_combine, dim3(a.n_tokens), dim3(256), 0, st, a);
   return hipGetLastError();
 }
