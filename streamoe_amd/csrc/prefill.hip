@@ -245,10 +245,11 @@ struct PfMM {
   static constexpr int P_XS = kPfMC * CG;             // group sums
   static constexpr int N_BQ = (P_BQ / NW + 63) / 64;  // copy instructions per wave
   static constexpr int N_BS = (P_BS / NW + 63) / 64;
-  static constexpr int N_A = (P_A / NW + 63) / 64;
+  static constexpr int N_A = P_A / NW / 64;           // one row pair (m, m + 16) each
   static constexpr int N_XS = (P_XS / NW + 63) / 64;
   static constexpr int D = N_BQ + N_BS + N_A * (SPLIT ? 2 : 1) + N_XS;
-  // LDS layout of one stage (bytes).
+  // LDS layout of one stage (bytes). A rows sit in pairs: row m at slot
+  // 2 (m % 16) + m / 16, so one copy instruction moves rows m and m + 16.
   static constexpr int OFF_BQ = 0;
   static constexpr int OFF_BS = OFF_BQ + P_BQ * 16;
   static constexpr int OFF_AH = OFF_BS + P_BS * SB_SZ;
@@ -258,11 +259,127 @@ struct PfMM {
   // Accumulators per lane, exchanged between the K halves through LDS.
   static constexpr int NT = NMAT * CT * 2 * 4;
   static_assert(CG % 2 == 0, "K halves");
-  static_assert(P_BQ % NW == 0 && P_BS % NW == 0 && P_A % NW == 0 && P_XS % NW == 0, "equal shares");
+  static_assert(P_BQ % NW == 0 && P_BS % NW == 0 && P_XS % NW == 0, "equal shares");
+  static_assert(N_A * NW * 64 == P_A && P_A == 16 * 64, "one row pair per A copy");
   static_assert((S - 2) * D <= 63, "vmcnt range");
   static_assert(S * STAGE <= 160 * 1024, "LDS per CU");
   static_assert(4 * NT * 64 * 4 <= STAGE, "accumulator exchange fits a stage");
 };
+
+// (x & m) | c in one instruction (the compiler emits an AND and an OR).
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m), "v"(c));
+  return r;
+}
+
+// 8 codes of one 4-bit u32 as bf16 (128 + q), order [q0,q4,q1,q5,q2,q6,q3,q7];
+// m = 0x000F000F and c = 0x43004300 held in registers.
+__device__ __forceinline__ u32x4 codes_bf16_4r(uint32_t d, uint32_t m, uint32_t c) {
+  u32x4 r;
+  r.x = and_or(d, m, c);
+  r.y = and_or(d >> 4, m, c);
+  r.z = and_or(d >> 8, m, c);
+  r.w = and_or(d >> 12, m, c);
+  return r;
+}
+
+// The MFMA work of one chunk for one wave: groups gl0 .. gl0 + CGW - 1 of
+// the stage at st, NTL 16-row tiles, into tot. Straight-line code (no
+// branches), so the scheduler can overlap LDS reads with MFMAs.
+template <int BITS, int G, int MODE, bool SPLIT, int NTL>
+__device__ __forceinline__ void pf_chunk(const uint8_t* st, uint32_t gl0, uint32_t cw, uint32_t n, uint32_t q,
+                                         uint32_t mask4, uint32_t c43,
+                                         f32x4 (&tot)[PfMM<BITS, G, MODE, SPLIT>::NMAT][PfMM<BITS, G, MODE, SPLIT>::CT][2]) {
+  using C = PfMM<BITS, G, MODE, SPLIT>;
+#pragma unroll
+  for (int gi = 0; gi < C::CGW; ++gi) {
+    const uint32_t gl = gl0 + gi;
+    uint32_t bw[C::NMAT][C::CT][C::NU];
+    float s[C::NMAT][C::CT], cbias[C::NMAT][C::CT];
+#pragma unroll
+    for (int mt = 0; mt < C::NMAT; ++mt)
+#pragma unroll
+      for (int ct = 0; ct < C::CT; ++ct) {
+        const uint32_t row = mt * C::NCOL + cw * 16 * C::CT + ct * 16 + n;
+        const uint8_t* rb = st + C::OFF_BQ + row * C::RB;
+        if (BITS == 4) {
+          const uint32_t off = gl * (G / 2) + 4 * C::NU * q;  // byte offset in the chunk row
+          const uint32_t slot = (off / 16) ^ (row & 7);
+          const uint32_t* w = reinterpret_cast<const uint32_t*>(rb + slot * 16 + off % 16);
+#pragma unroll
+          for (int uu = 0; uu < C::NU; ++uu) bw[mt][ct][uu] = w[uu];
+        } else {
+          const uint32_t off = (gl * G + 8 * C::NU * q) * 3 / 8;  // 3*NU bytes
+          constexpr int ND = (3 * C::NU + 6) / 4;
+          uint32_t d[ND];
+#pragma unroll
+          for (int i = 0; i < ND; ++i) {
+            const uint32_t dw = (off & ~3u) / 4 + i;  // dword index in the row (0 .. RB/4)
+            const uint32_t part = min(dw / 4, (uint32_t)C::PPR - 1);
+            const uint32_t slot = (part + C::PPR - row % C::PPR) % C::PPR;
+            d[i] = *reinterpret_cast<const uint32_t*>(rb + slot * 16 + (dw % 4) * 4);
+          }
+          const uint32_t sh = (off & 3u) * 8;
+#pragma unroll
+          for (int uu = 0; uu < C::NU; ++uu) {
+            const uint32_t bit = sh + 24 * uu;
+            uint32_t lo = 0, hi = 0;
+#pragma unroll
+            for (int i = 0; i < ND; ++i) {
+              if ((uint32_t)i == (bit >> 5)) lo = d[i];
+              if ((uint32_t)i == (bit >> 5) + 1) hi = d[i];
+            }
+            bw[mt][ct][uu] = __builtin_amdgcn_alignbit(hi, lo, bit & 31) & 0xFFFFFFu;
+          }
+        }
+        const uint16_t* sb = reinterpret_cast<const uint16_t*>(st + C::OFF_BS + row * 2 * C::SB_BYTES);
+        s[mt][ct] = bf16f(sb[gl]);
+        cbias[mt][ct] = __builtin_fmaf(-128.0f, s[mt][ct], bf16f(sb[C::CG + gl]));
+      }
+    u32x4 bq[C::NMAT][C::CT][C::NU];
+#pragma unroll
+    for (int mt = 0; mt < C::NMAT; ++mt)
+#pragma unroll
+      for (int ct = 0; ct < C::CT; ++ct)
+#pragma unroll
+        for (int uu = 0; uu < C::NU; ++uu)
+          bq[mt][ct][uu] = BITS == 4 ? codes_bf16_4r(bw[mt][ct][uu], mask4, c43) : codes_bf16_3(bw[mt][ct][uu]);
+#pragma unroll
+    for (int t = 0; t < NTL; ++t) {
+      f32x4 acc[C::NMAT][C::CT];
+#pragma unroll
+      for (int mt = 0; mt < C::NMAT; ++mt)
+#pragma unroll
+        for (int ct = 0; ct < C::CT; ++ct) acc[mt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int uu = 0; uu < C::NU; ++uu) {
+        const uint32_t part = (gl * G + 8 * C::NU * q + 8 * uu) / 8;
+        const uint32_t aoff = (2 * n + t) * C::KC * 2 + ((part ^ n) * 16);
+        const u32x4 ah = *reinterpret_cast<const u32x4*>(st + C::OFF_AH + aoff);
+        u32x4 al;
+        if (SPLIT) al = *reinterpret_cast<const u32x4*>(st + C::OFF_AL + aoff);
+#pragma unroll
+        for (int mt = 0; mt < C::NMAT; ++mt)
+#pragma unroll
+          for (int ct = 0; ct < C::CT; ++ct) {
+            acc[mt][ct] = mfma(ah, bq[mt][ct][uu], acc[mt][ct]);
+            if (SPLIT) acc[mt][ct] = mfma(al, bq[mt][ct][uu], acc[mt][ct]);
+          }
+      }
+      // Group sums of rows 16t + 4q .. + 3 in one read ([group][row]).
+      const f32x4 xs = *reinterpret_cast<const f32x4*>(st + C::OFF_XS + (gl * kPfMC + 16 * t + 4 * q) * 4);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int mt = 0; mt < C::NMAT; ++mt)
+#pragma unroll
+          for (int ct = 0; ct < C::CT; ++ct)
+            tot[mt][ct][t][r] =
+                __builtin_fmaf(s[mt][ct], acc[mt][ct][r], __builtin_fmaf(cbias[mt][ct], xs[r], tot[mt][ct][t][r]));
+    }
+  }
+}
 
 template <int BITS, int G, int MODE, bool SPLIT>
 __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restrict__ items,
@@ -302,6 +419,28 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
   const uint64_t wo0 = a.g.w[MODE == 0 ? 0 : 2], wo1 = a.g.w[MODE == 0 ? 1 : 2];
   const uint64_t so0 = a.g.s[MODE == 0 ? 0 : 2], so1 = a.g.s[MODE == 0 ? 1 : 2];
   const uint64_t bo0 = a.g.b[MODE == 0 ? 0 : 2];
+  // Lane offsets of the weight copies (fixed for the whole kernel; the
+  // per-chunk part of the address is scalar).
+  uint32_t off_bq[C::N_BQ], off_bs[C::N_BS];
+#pragma unroll
+  for (int i = 0; i < C::N_BQ; ++i) {
+    const uint32_t p = wave * (C::P_BQ / C::NW) + i * 64 + lane;
+    const uint32_t row = p / C::PPR, sp = p % C::PPR;
+    const uint32_t part = BITS == 4 ? (sp ^ (row & 7)) : (sp + row) % C::PPR;
+    const uint32_t mat = row / C::NCOL;
+    off_bq[i] = (uint32_t)(mat * (wo1 - wo0)) + (row % C::NCOL) * rowb + part * 16;
+  }
+#pragma unroll
+  for (int i = 0; i < C::N_BS; ++i) {
+    const uint32_t p = wave * (C::P_BS / C::NW) + i * 64 + lane;
+    const uint32_t row = p / (2 * C::SB_PIECES), arr = (p / C::SB_PIECES) % 2, pc = p % C::SB_PIECES;
+    const uint32_t mat = row / C::NCOL;
+    // Biases follow scales at the same distance in both matrices.
+    off_bs[i] = (uint32_t)(mat * (so1 - so0) + arr * (bo0 - so0)) + (row % C::NCOL) * ng * 2 + pc * C::SB_SZ;
+  }
+  uint32_t mask4, c43;
+  asm("v_mov_b32 %0, 0x000f000f" : "=v"(mask4));
+  asm("v_mov_b32 %0, 0x43004300" : "=v"(c43));
 
   // Issue every copy of flattened chunk j into stage j % S. Captures by
   // value: a by-reference capture stores the locals' addresses, and the
@@ -315,59 +454,44 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
     uint8_t* st = lds + (j % C::S) * C::STAGE;
     // Weight codes: slot p = (row, slot part) holds the row's part
     // (slot part ^ row & 7) [4-bit] or ((slot part + row) % 6) [3-bit].
+    const uint8_t* bq_base = blob + wo0 + (size_t)cb * C::NCOL * rowb + (size_t)c * C::RB;
 #pragma unroll
-    for (int i = 0; i < C::N_BQ; ++i) {
-      const uint32_t o = i * 64 + lane;
-      const uint32_t p = wave * (C::P_BQ / C::NW) + o;
-      const uint32_t row = p / C::PPR, sp = p % C::PPR;
-      const uint32_t part = BITS == 4 ? (sp ^ (row & 7)) : (sp + row) % C::PPR;
-      const uint32_t mat = row / C::NCOL, wrow = cb * C::NCOL + row % C::NCOL;
-      const uint64_t wo = wo0 + mat * (wo1 - wo0);
-      if ((C::P_BQ / C::NW) % 64 == 0 || o < (uint32_t)(C::P_BQ / C::NW))
-        dma16(blob + wo + (size_t)wrow * rowb + (size_t)c * C::RB + part * 16,
-              st + C::OFF_BQ + (wave * (C::P_BQ / C::NW) + i * 64) * 16);
-    }
+    for (int i = 0; i < C::N_BQ; ++i)
+      if ((C::P_BQ / C::NW) % 64 == 0 || i * 64 + lane < (uint32_t)(C::P_BQ / C::NW))
+        dma16(bq_base + off_bq[i], st + C::OFF_BQ + (wave * (C::P_BQ / C::NW) + i * 64) * 16);
     // Scales then biases of each row: [row][array][CG] bf16.
+    const uint8_t* bs_base = blob + so0 + ((size_t)cb * C::NCOL * ng + (size_t)c * C::CG) * 2;
 #pragma unroll
     for (int i = 0; i < C::N_BS; ++i) {
-      const uint32_t o = i * 64 + lane;
-      const uint32_t p = wave * (C::P_BS / C::NW) + o;
-      const uint32_t row = p / (2 * C::SB_PIECES), arr = (p / C::SB_PIECES) % 2, pc = p % C::SB_PIECES;
-      const uint32_t mat = row / C::NCOL, wrow = cb * C::NCOL + row % C::NCOL;
-      // Arithmetic, not a select: a select between captured values becomes a
-      // load from a lane-varying address of the closure, in scratch memory.
-      // Biases follow scales at the same distance in both matrices.
-      const uint64_t so = so0 + mat * (so1 - so0) + arr * (bo0 - so0);
-      const uint8_t* src = blob + so + ((size_t)wrow * ng + (size_t)c * C::CG) * 2 + pc * C::SB_SZ;
       uint8_t* dst = st + C::OFF_BS + (wave * (C::P_BS / C::NW) + i * 64) * C::SB_SZ;
-      if ((C::P_BS / C::NW) % 64 == 0 || o < (uint32_t)(C::P_BS / C::NW)) {
-        if (C::SB_SZ == 16) dma16(src, dst); else dma4(src, dst);
+      if ((C::P_BS / C::NW) % 64 == 0 || i * 64 + lane < (uint32_t)(C::P_BS / C::NW)) {
+        if (C::SB_SZ == 16) dma16(bs_base + off_bs[i], dst); else dma4(bs_base + off_bs[i], dst);
       }
     }
-    // A rows (bf16, MFMA order): slot part = part ^ (m & 15).
+    // A rows (bf16, MFMA order), one row pair (m, m + 16) per copy; slot
+    // part = part ^ (m & 15). Rows 16.. are copied only for a second tile.
 #pragma unroll
     for (int hl = 0; hl < (SPLIT ? 2 : 1); ++hl) {
-      const uint16_t* src = hl ? alo_src : ahi_src;
+      const uint8_t* a_base = reinterpret_cast<const uint8_t*>((hl ? alo_src : ahi_src) + (size_t)start * K) +
+                              (size_t)c * C::KC * 2;
 #pragma unroll
       for (int i = 0; i < C::N_A; ++i) {
-        const uint32_t o = i * 64 + lane;
-        const uint32_t p = wave * (C::P_A / C::NW) + o;
-        const uint32_t m = p / 32, sp = p % 32, part = sp ^ (m & 15);
-        const size_t arow = start + min(m, cnt - 1);
-        if ((C::P_A / C::NW) % 64 == 0 || o < (uint32_t)(C::P_A / C::NW))
-          dma16(src + arow * K + (size_t)c * C::KC + part * 8,
-                st + (hl ? C::OFF_AL : C::OFF_AH) + (wave * (C::P_A / C::NW) + i * 64) * 16);
+        const uint32_t pair = wave * C::N_A + i, half = lane >> 5, sp = lane & 31;
+        const uint32_t m = pair + 16 * half;
+        const uint32_t off = min(m, cnt - 1) * K * 2 + (sp ^ pair) * 16;
+        if (half == 0 || cnt > 16)
+          dma16(a_base + off, st + (hl ? C::OFF_AL : C::OFF_AH) + pair * 64 * 16);
       }
     }
     // Group sums of the A rows, [group][row].
+    const uint8_t* xs_base = reinterpret_cast<const uint8_t*>(gsum + (size_t)start * ng + (size_t)c * C::CG);
 #pragma unroll
     for (int i = 0; i < C::N_XS; ++i) {
       const uint32_t o = i * 64 + lane;
       const uint32_t p = wave * (C::P_XS / C::NW) + o;
       const uint32_t g = p / kPfMC, m = p % kPfMC;
-      const size_t arow = start + min(m, cnt - 1);
       if ((C::P_XS / C::NW) % 64 == 0 || o < (uint32_t)(C::P_XS / C::NW))
-        dma4(gsum + arow * ng + (size_t)c * C::CG + g, st + C::OFF_XS + (wave * (C::P_XS / C::NW) + i * 64) * 4);
+        dma4(xs_base + (min(m, cnt - 1) * ng + g) * 4, st + C::OFF_XS + (wave * (C::P_XS / C::NW) + i * 64) * 4);
     }
   };
 
@@ -396,90 +520,11 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
     const uint32_t v = lb + (j / nch) * per, c = j % nch;
     const uint32_t item = xg + nx * (v / ncb), cb = v % ncb;
     const uint32_t start = items[2 * item + 1] & 0xFFFFu, cnt = items[2 * item + 1] >> 16;
-    const uint32_t ntiles = (cnt + 15) / 16;
     uint8_t* st = lds + (j % C::S) * C::STAGE;
-#pragma unroll
-    for (int gi = 0; gi < C::CGW; ++gi) {
-      const uint32_t gl = kh * C::CGW + gi;
-      uint32_t bw[C::NMAT][C::CT][C::NU];
-      float s[C::NMAT][C::CT], cbias[C::NMAT][C::CT];
-#pragma unroll
-      for (int mt = 0; mt < C::NMAT; ++mt)
-#pragma unroll
-        for (int ct = 0; ct < C::CT; ++ct) {
-          const uint32_t row = mt * C::NCOL + cw * 16 * C::CT + ct * 16 + n;
-          const uint8_t* rb = st + C::OFF_BQ + row * C::RB;
-          if (BITS == 4) {
-            const uint32_t off = gl * (G / 2) + 4 * C::NU * q;  // byte offset in the chunk row
-            const uint32_t slot = (off / 16) ^ (row & 7);
-            const uint32_t* w = reinterpret_cast<const uint32_t*>(rb + slot * 16 + off % 16);
-#pragma unroll
-            for (int uu = 0; uu < C::NU; ++uu) bw[mt][ct][uu] = w[uu];
-          } else {
-            const uint32_t off = (gl * G + 8 * C::NU * q) * 3 / 8;  // 3*NU bytes
-            constexpr int ND = (3 * C::NU + 6) / 4;
-            uint32_t d[ND];
-#pragma unroll
-            for (int i = 0; i < ND; ++i) {
-              const uint32_t dw = (off & ~3u) / 4 + i;  // dword index in the row (0 .. RB/4)
-              const uint32_t part = min(dw / 4, (uint32_t)C::PPR - 1);
-              const uint32_t slot = (part + C::PPR - row % C::PPR) % C::PPR;
-              d[i] = *reinterpret_cast<const uint32_t*>(rb + slot * 16 + (dw % 4) * 4);
-            }
-            const uint32_t sh = (off & 3u) * 8;
-#pragma unroll
-            for (int uu = 0; uu < C::NU; ++uu) {
-              const uint32_t bit = sh + 24 * uu;
-              uint32_t lo = 0, hi = 0;
-#pragma unroll
-              for (int i = 0; i < ND; ++i) {
-                if ((uint32_t)i == (bit >> 5)) lo = d[i];
-                if ((uint32_t)i == (bit >> 5) + 1) hi = d[i];
-              }
-              bw[mt][ct][uu] = __builtin_amdgcn_alignbit(hi, lo, bit & 31) & 0xFFFFFFu;
-            }
-          }
-          const uint16_t* sb = reinterpret_cast<const uint16_t*>(st + C::OFF_BS + row * 2 * C::SB_BYTES);
-          s[mt][ct] = bf16f(sb[gl]);
-          cbias[mt][ct] = __builtin_fmaf(-128.0f, s[mt][ct], bf16f(sb[C::CG + gl]));
-        }
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        if ((uint32_t)t >= ntiles) continue;
-        const uint32_t m = 16 * t + n;
-        f32x4 acc[C::NMAT][C::CT];
-#pragma unroll
-        for (int mt = 0; mt < C::NMAT; ++mt)
-#pragma unroll
-          for (int ct = 0; ct < C::CT; ++ct) acc[mt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int uu = 0; uu < C::NU; ++uu) {
-          const uint32_t part = (gl * G + 8 * C::NU * q + 8 * uu) / 8;
-          const uint32_t aoff = m * C::KC * 2 + ((part ^ (m & 15)) * 16);
-          const u32x4 ah = *reinterpret_cast<const u32x4*>(st + C::OFF_AH + aoff);
-          u32x4 al;
-          if (SPLIT) al = *reinterpret_cast<const u32x4*>(st + C::OFF_AL + aoff);
-#pragma unroll
-          for (int mt = 0; mt < C::NMAT; ++mt)
-#pragma unroll
-            for (int ct = 0; ct < C::CT; ++ct) {
-              const u32x4 bq = codes_bf16<BITS>(bw[mt][ct][uu]);
-              acc[mt][ct] = mfma(ah, bq, acc[mt][ct]);
-              if (SPLIT) acc[mt][ct] = mfma(al, bq, acc[mt][ct]);
-            }
-        }
-        // Group sums of rows 16t + 4q .. + 3 in one read ([group][row]).
-        const f32x4 xs = *reinterpret_cast<const f32x4*>(st + C::OFF_XS + (gl * kPfMC + 16 * t + 4 * q) * 4);
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-#pragma unroll
-          for (int mt = 0; mt < C::NMAT; ++mt)
-#pragma unroll
-            for (int ct = 0; ct < C::CT; ++ct)
-              tot[mt][ct][t][r] = __builtin_fmaf(s[mt][ct], acc[mt][ct][r],
-                                                 __builtin_fmaf(cbias[mt][ct], xs[r], tot[mt][ct][t][r]));
-      }
-    }
+    if (cnt > 16)
+      pf_chunk<BITS, G, MODE, SPLIT, 2>(st, kh * C::CGW, cw, n, q, mask4, c43, tot);
+    else
+      pf_chunk<BITS, G, MODE, SPLIT, 1>(st, kh * C::CGW, cw, n, q, mask4, c43, tot);
 
     if (c + 1 == nch) {  // unit complete: add the K halves, write it out
       // Every wave is done reading this stage; the upper half parks its sums
@@ -502,6 +547,7 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
       if (kh == 0) {
+        const uint32_t ntiles = cnt > 16 ? 2 : 1;
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
           if ((uint32_t)t >= ntiles) continue;
