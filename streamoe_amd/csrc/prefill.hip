@@ -266,21 +266,19 @@ struct PfMM {
   static_assert(4 * NT * 64 * 4 <= STAGE, "accumulator exchange fits a stage");
 };
 
-// (x & m) | c in one instruction (the compiler emits an AND and an OR).
-__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t c) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m), "v"(c));
-  return r;
-}
-
-// 8 codes of one 4-bit u32 as bf16 (128 + q), order [q0,q4,q1,q5,q2,q6,q3,q7];
-// m = 0x000F000F and c = 0x43004300 held in registers.
-__device__ __forceinline__ u32x4 codes_bf16_4r(uint32_t d, uint32_t m, uint32_t c) {
+// 8 codes of one 4-bit u32 as bf16 (128 + q), order [q0,q4,q1,q5,q2,q6,q3,q7],
+// in 7 instructions: the low and high nibbles of each byte, then one byte
+// permute per output word pairing them with 0x43 bytes (c43 = 0x43434343).
+// Builtins only: inline asm feeding an MFMA hides the VALU-to-MFMA
+// dependency from the compiler's hazard checks.
+__device__ __forceinline__ u32x4 codes_bf16_4p(uint32_t d, uint32_t c43) {
+  const uint32_t lo = d & 0x0F0F0F0Fu;         // q0, q2, q4, q6
+  const uint32_t hi = (d >> 4) & 0x0F0F0F0Fu;  // q1, q3, q5, q7
   u32x4 r;
-  r.x = and_or(d, m, c);
-  r.y = and_or(d >> 4, m, c);
-  r.z = and_or(d >> 8, m, c);
-  r.w = and_or(d >> 12, m, c);
+  r.x = __builtin_amdgcn_perm(c43, lo, 0x04020400u);  // (q0, q4)
+  r.y = __builtin_amdgcn_perm(c43, hi, 0x04020400u);  // (q1, q5)
+  r.z = __builtin_amdgcn_perm(c43, lo, 0x04030401u);  // (q2, q6)
+  r.w = __builtin_amdgcn_perm(c43, hi, 0x04030401u);  // (q3, q7)
   return r;
 }
 
@@ -289,7 +287,7 @@ __device__ __forceinline__ u32x4 codes_bf16_4r(uint32_t d, uint32_t m, uint32_t 
 // branches), so the scheduler can overlap LDS reads with MFMAs.
 template <int BITS, int G, int MODE, bool SPLIT, int NTL>
 __device__ __forceinline__ void pf_chunk(const uint8_t* st, uint32_t gl0, uint32_t cw, uint32_t n, uint32_t q,
-                                         uint32_t mask4, uint32_t c43,
+                                         uint32_t c43,
                                          f32x4 (&tot)[PfMM<BITS, G, MODE, SPLIT>::NMAT][PfMM<BITS, G, MODE, SPLIT>::CT][2]) {
   using C = PfMM<BITS, G, MODE, SPLIT>;
 #pragma unroll
@@ -344,7 +342,7 @@ __device__ __forceinline__ void pf_chunk(const uint8_t* st, uint32_t gl0, uint32
       for (int ct = 0; ct < C::CT; ++ct)
 #pragma unroll
         for (int uu = 0; uu < C::NU; ++uu)
-          bq[mt][ct][uu] = BITS == 4 ? codes_bf16_4r(bw[mt][ct][uu], mask4, c43) : codes_bf16_3(bw[mt][ct][uu]);
+          bq[mt][ct][uu] = BITS == 4 ? codes_bf16_4p(bw[mt][ct][uu], c43) : codes_bf16_3(bw[mt][ct][uu]);
 #pragma unroll
     for (int t = 0; t < NTL; ++t) {
       f32x4 acc[C::NMAT][C::CT];
@@ -397,13 +395,16 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
   const uint32_t N = MODE == 0 ? a.g.inter : a.g.hidden;
   const uint32_t ng = K / G, nch = K / C::KC, rowb = K * BITS / 8;
   const uint32_t ncb = N / C::NCOL;
-  // XCD-aware schedule: block b runs on XCD b % 8, so items go round-robin
-  // over the 8 XCD groups and an item's ncb column blocks run side by side
-  // on one XCD, where its A rows are fetched into that XCD's L2 once.
+  // XCD-aware schedule: block b runs on XCD b % 8. XCD group x takes the
+  // contiguous item range [n x / 8, n (x + 1) / 8): items are in expert
+  // order, so a hot expert's items (and an item's ncb column blocks) run
+  // side by side on one XCD, and its weights and A rows are fetched into
+  // that XCD's L2 once instead of once per item.
   const uint32_t nx = gridDim.x % 8 == 0 ? 8 : 1, per = gridDim.x / nx;
   const uint32_t xg = blockIdx.x % nx, lb = blockIdx.x / nx;
   const uint32_t n_items = *n_items_p;
-  const uint32_t group_units = (n_items > xg ? (n_items - xg + nx - 1) / nx : 0) * ncb;
+  const uint32_t item_lo = n_items * xg / nx, item_hi = n_items * (xg + 1) / nx;
+  const uint32_t group_units = (item_hi - item_lo) * ncb;
   const uint32_t my_units = group_units > lb ? (group_units - lb + per - 1) / per : 0;
   const uint32_t total = my_units * nch;
   if (total == 0) return;
@@ -438,16 +439,14 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
     // Biases follow scales at the same distance in both matrices.
     off_bs[i] = (uint32_t)(mat * (so1 - so0) + arr * (bo0 - so0)) + (row % C::NCOL) * ng * 2 + pc * C::SB_SZ;
   }
-  uint32_t mask4, c43;
-  asm("v_mov_b32 %0, 0x000f000f" : "=v"(mask4));
-  asm("v_mov_b32 %0, 0x43004300" : "=v"(c43));
+  const uint32_t c43 = 0x43434343u;
 
   // Issue every copy of flattened chunk j into stage j % S. Captures by
   // value: a by-reference capture stores the locals' addresses, and the
   // memory clobbers of the waits below would then keep them in scratch.
   auto issue = [=](uint32_t j) {
     const uint32_t v = lb + (j / nch) * per, c = j % nch;
-    const uint32_t item = xg + nx * (v / ncb), cb = v % ncb;
+    const uint32_t item = item_lo + v / ncb, cb = v % ncb;
     const uint32_t e = items[2 * item];
     const uint32_t start = items[2 * item + 1] & 0xFFFFu, cnt = items[2 * item + 1] >> 16;
     const uint8_t* blob = experts + (size_t)e * stride;
@@ -518,13 +517,13 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
     if (j + C::S - 1 < total) issue(j + C::S - 1);
 
     const uint32_t v = lb + (j / nch) * per, c = j % nch;
-    const uint32_t item = xg + nx * (v / ncb), cb = v % ncb;
+    const uint32_t item = item_lo + v / ncb, cb = v % ncb;
     const uint32_t start = items[2 * item + 1] & 0xFFFFu, cnt = items[2 * item + 1] >> 16;
     uint8_t* st = lds + (j % C::S) * C::STAGE;
     if (cnt > 16)
-      pf_chunk<BITS, G, MODE, SPLIT, 2>(st, kh * C::CGW, cw, n, q, mask4, c43, tot);
+      pf_chunk<BITS, G, MODE, SPLIT, 2>(st, kh * C::CGW, cw, n, q, c43, tot);
     else
-      pf_chunk<BITS, G, MODE, SPLIT, 1>(st, kh * C::CGW, cw, n, q, mask4, c43, tot);
+      pf_chunk<BITS, G, MODE, SPLIT, 1>(st, kh * C::CGW, cw, n, q, c43, tot);
 
     if (c + 1 == nch) {  // unit complete: add the K halves, write it out
       // Every wave is done reading this stage; the upper half parks its sums
