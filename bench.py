@@ -14,6 +14,9 @@ persistent cooperative launch (--path persistent, eager).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2]
 
+--config c0/c3 run the other decode shapes, c1 the LM head and c4 the
+512-token prefill layer, each with its own JSON line.
+
 Prints one JSON line. value = µs per layer (lower is better); the
 roofline object gives achieved HBM GB/s from the algorithmic bytes.
 """
@@ -38,15 +41,18 @@ CONFIGS = {
                E=256, k=8, bits=3, normalize=True, shared=True, layers=40),
     "c1": dict(name="Qwen3-shape LM head: dense 4-bit qmv 151936x2048 + greedy argmax (1 token)", V=151936,
                H=2048, bits=4),
+    "c4": dict(name="Qwen3.6-A3B-shape MoE layer prefill, 512 tokens (bf16 x, Zipf 1.1 routing)", H=2048, I=512,
+               E=256, k=8, bits=4, tokens=512),
 }
 
 
 # HBM bytes actually moved per unit of work, from rocprofv3 FETCH_SIZE and
 # WRITE_SIZE passes scaled by a 256 MiB copy calibration (FETCH x 2.0,
 # WRITE x 1.0): profiles/decode_c2_a3b_4bit.md (one layer = the three
-# k_fa_* launches) and profiles/lm_head_c1_qmv_argmax.md (k_qmv + argmax).
+# k_fa_* launches), profiles/lm_head_c1_qmv_argmax.md (k_qmv + argmax) and
+# profiles/prefill_c4_a3b_4bit.md (the six prefill launches of one layer).
 # None where no counter pass was taken.
-MEASURED_TRAFFIC = {"c2": 19_522_595, "c1": 176_528_574}
+MEASURED_TRAFFIC = {"c2": 19_522_595, "c1": 176_528_574, "c4": 596_394_906}
 
 
 def stream_read_peak(dev, gib=4):
@@ -407,6 +413,94 @@ def run_lm_head(args, c):
     return out
 
 
+def run_prefill(args, c):
+    """Config 4: one MoE layer's routed experts over 512 tokens (bucket by
+    expert, grouped gate/up GEMM, SwiGLU, down GEMM, weighted combine),
+    replayed from a HIP graph. value = µs per layer."""
+    import numpy as np
+    import torch
+
+    import oracle
+    import streamoe_amd as sa
+
+    dev = torch.device("cuda", 0)
+    kern = sa.Kernels(0)
+    H, I, E, k, n, bits = c["H"], c["I"], c["E"], c["k"], c["tokens"], c["bits"]
+    lay = sa.ExpertLayout(H, I, bits, 64)
+    stride = lay.expert_size
+    arena = torch.empty(E * stride, dtype=torch.uint8, device=dev)
+    sa.check(kern.synth_experts(arena, E, stride, lay, 0xC4), "synth")
+    idx, w = sa.zipf_routing(n, E, k, 1.1, seed=0xC4)
+    idx_d, w_d = torch.from_numpy(idx).to(dev), torch.from_numpy(w).to(dev)
+    x = torch.empty((n, H), dtype=torch.int16, device=dev)
+    sa.check(kern.synth_normal_bf16(x, 0xC41, 1.0), "synth")
+    out = torch.empty((n, H), dtype=torch.float32, device=dev)
+    ws = torch.empty(kern.moe_prefill_workspace_size(lay, n, E, k), dtype=torch.uint8, device=dev)
+
+    def step():
+        sa.check(kern.moe_prefill(lay, arena, stride, E, idx_d, w_d, x, True, n, k, out, ws), "smoe_moe_prefill")
+
+    graph = None if args.eager else sa.capture_graph(kern, step)
+    run = graph.replay if graph is not None else step
+    for _ in range(args.warmup):
+        run()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        run()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / args.steps
+    sa.check(_sync_status(kern), "smoe_sync")
+    hit = np.unique(idx)
+    nbytes = len(hit) * stride + n * H * 2 + n * H * 4  # weights of hit experts + bf16 X + f32 Y
+    flops = 2 * n * k * (2 * H * I + I * H)
+    achieved = nbytes / (us * 1e-6) / 1e9
+    tflops = flops / (us * 1e-6) / 1e12
+    out_d = {
+        "metric": "4-bit MoE expert decode µs/layer + achieved HBM GB/s (% of peak), 1 GPU",
+        "value": round(us, 2), "unit": "us/layer (512-token prefill)", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(us / 1e3, 5), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "u4 codes, bf16 MFMA, f32 accumulate",
+        "data": "synthetic (seeded, generated on the device)",
+        "config": {"workload": c["name"], "tokens": n, "hidden": H, "experts": E, "top_k": k, "inter": I,
+                   "bits": bits, "group": 64, "experts_hit": int(len(hit)),
+                   "mode": "hipgraph" if graph is not None else "eager"},
+        "gbps": round(achieved, 1), "pct_of_hbm_peak": round(100 * achieved / HBM_PEAK_GBS, 2),
+        "mfma_tflops": round(tflops, 2), "pct_of_bf16_mfma_peak": round(100 * tflops / 2500.0, 2),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": MEASURED_TRAFFIC.get("c4"),
+                     "unit_of_work": f"one layer: {nbytes} algorithmic bytes ({len(hit)} hit experts x {stride} "
+                                     f"+ X + Y), {flops} flops",
+                     "kernel": "prefill layer: k_pf_route + k_pf_prep_x + k_pf_mm (gate/up) + k_pf_act_sum + "
+                               "k_pf_mm (down) + k_pf_combine (one HIP graph)"},
+    }
+    if not args.no_cpu:
+        # The whole layer (a few seconds of CPU work), timed with all host
+        # threads; doubles as a parity check of every token.
+        ns = n
+        xs = oracle.bf16_to_f32(x[:ns].cpu().numpy().view(np.uint16)).reshape(ns, H)
+        ah = arena.cpu().numpy()
+        buckets = oracle.build_expert_buckets(idx[:ns], w[:ns], ns, k, E)
+        nt = cpu_threads()
+        t0 = time.perf_counter()
+        want = oracle.moe_permute_fuse(ah, stride, bits, H, I, 64, xs, buckets, ns, nthreads=nt)
+        dt = time.perf_counter() - t0
+        got = out[:ns].cpu().numpy()
+        cpu_us = dt * 1e6
+        out_d["cpu_baseline"] = {"value": round(cpu_us, 1), "unit": "us/layer (512 tokens)", "cores": nt,
+                                 "kind": "port",
+                                 "sample": f"all {ns} tokens through oracle moe_permute_fuse "
+                                           f"(moe_cpu.rs:282-339 order), {dt:.2f} s",
+                                 "gpu_speedup": round(cpu_us / us, 1)}
+        out_d["parity"] = {"rel_err": float(np.max(np.abs(got - want)) / np.max(np.abs(want))),
+                           "tokens_checked": ns, "tolerance": 1e-3}
+    kern.close()
+    return out_d
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -427,7 +521,8 @@ def main():
               "sharding of this path is a design note, not a measured configuration.", file=sys.stderr)
         sys.exit(2)
     c = dict(CONFIGS[args.config], key=args.config)
-    out = run_lm_head(args, c) if args.config == "c1" else run_decode(args, c)
+    runner = {"c1": run_lm_head, "c4": run_prefill}.get(args.config, run_decode)
+    out = runner(args, c)
     if not args.no_stream_peak:
         import torch
 
