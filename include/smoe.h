@@ -273,11 +273,19 @@ uint64_t smoe_moe_prefill_workspace_size(const smoe_expert_shape* shape, uint32_
 
 /* out_sum[t] = sum_s weights[t,s] * FFN_{idx[t,s]}(x[t]) for t < n_tokens:
  * tokens sorted by expert on the device, grouped gate/up GEMM with
- * in-kernel dequant on bf16/f16 MFMA (fp32 accumulate), SwiGLU, down
- * GEMM, then a fixed-order per-token combine (no atomics).
+ * exact in-kernel dequant on bf16 MFMA (fp32 accumulate), SwiGLU, down
+ * GEMM, then a fixed-order per-token combine (ascending expert, no
+ * atomics: bit-identical across runs).
  * x: device, bf16 [n_tokens, hidden] when x_is_bf16 else f32;
  * idx: device int32[n_tokens, k]; weights: device f32[n_tokens, k];
- * out_sum: device f32[n_tokens, hidden] (overwritten).
+ * out_sum: device f32[n_tokens, hidden] (overwritten); workspace:
+ * device, >= smoe_moe_prefill_workspace_size bytes, 256-byte aligned.
+ * Supported: bits 4 or 3, group 32/64/128, hidden and inter multiples of
+ * 256, 1..1024 tokens, <= 256 experts, 1 <= k <= min(16, n_experts);
+ * else SMOE_ERR_UNSUPPORTED_SHAPE / SMOE_ERR_BAD_K. An expert id out of
+ * range or repeated within a token is found on the device: the call
+ * returns SMOE_OK and the next smoe_sync returns SMOE_ERR_INVALID_ARG.
+ * Enqueue-only, allocates nothing, capturable in a HIP graph.
  * Replaces encode_moe_gather_id_fuse (expert_forward.rs:1874-2042) with
  * MoeIdMap0Call / MoeGatherIdCall / MoeCombineTopkCall (metal/lib.rs:
  * 932-1189), and its CPU oracle moe_permute_fuse_cpu
