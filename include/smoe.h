@@ -57,7 +57,8 @@ typedef enum {
   SMOE_ERR_WORKSPACE_TOO_SMALL = 9, /* caller workspace smaller than *_workspace_size */
   SMOE_ERR_HIP = 10,                /* a HIP runtime call failed (launch, memset, sync) */
   SMOE_ERR_NO_DEVICE = 11,          /* no gfx950 device at that ordinal */
-  SMOE_ERR_DEVICE_TIMEOUT = 12      /* a bounded device-side wait expired; outputs are invalid */
+  SMOE_ERR_DEVICE_TIMEOUT = 12,     /* a bounded device-side wait expired; outputs are invalid */
+  SMOE_ERR_IO = 13                  /* a file could not be opened or read, or is too short (ExpertIoError::Io) */
 } smoe_status;
 
 /* Handle options (smoe_set_option). */
@@ -294,6 +295,43 @@ int smoe_moe_prefill(smoe_handle* h, const smoe_expert_shape* shape, const void*
                      uint64_t stride, uint32_t n_experts, const int32_t* idx,
                      const float* weights, const void* x, int x_is_bf16, uint32_t n_tokens,
                      uint32_t k, float* out_sum, void* workspace, uint64_t workspace_bytes);
+
+/* ------------------------------------------------------------------ */
+/* Expert arena loader: packed_experts/layer_NN.bin -> device memory    */
+/* ------------------------------------------------------------------ */
+
+typedef struct {
+  uint32_t bits;        /* 4 or 3 */
+  uint32_t reserved;
+  uint64_t expert_size; /* bytes of one expert blob (smoe_expert_bytes) */
+  uint64_t stride;      /* bytes between experts in the file (>= expert_size) */
+} smoe_file_layout;
+
+/* Layout and expert stride of a layer file file_bytes long that holds
+ * n_experts experts of this hidden/inter/group (host only, no handle).
+ * declared_size / declared_stride: packed_experts/layout.json's
+ * expert_size / expert_stride, or 0 / 0 without one. The declared padded
+ * stride wins when it exceeds the size, the size is a known layout and the
+ * file is exactly n_experts strides long; else the layout whose n_experts
+ * blobs fill the file exactly (4-bit, then packed 3-bit); else 4-bit with
+ * stride = its size (the legacy assumption). Replaces layout_and_stride /
+ * layout_of_len / ExpertLayout::from_expert_size (io/expert_io.rs:229-267,
+ * variants.rs:442-450). */
+int smoe_layer_file_layout(uint64_t file_bytes, uint32_t n_experts, uint32_t hidden, uint32_t inter,
+                           uint32_t group, uint64_t declared_size, uint64_t declared_stride,
+                           smoe_file_layout* out);
+
+/* Copy bytes [offset, offset + bytes) of the file at path (bytes == 0:
+ * from offset to the end) into device memory dst of capacity dst_bytes,
+ * through two pinned staging buffers (kept by the handle) and async copies
+ * on the handle's stream; returns once the data is on the device.
+ * *bytes_read (nullable) = bytes copied. Replaces the resident-layer part
+ * of ExpertFiles::open + attach_to_device (io/expert_io.rs:300-420): a
+ * layer file becomes one device arena, expert e at dst + e * stride.
+ * SMOE_ERR_IO: cannot open or read, or the file ends before offset +
+ * bytes; SMOE_ERR_INVALID_ARG: null pointers or dst_bytes too small. */
+int smoe_load_file(smoe_handle* h, const char* path, uint64_t offset, uint64_t bytes, void* dst,
+                   uint64_t dst_bytes, uint64_t* bytes_read);
 
 /* ------------------------------------------------------------------ */
 /* Seeded synthetic data (bench and test inputs)                       */

@@ -10,6 +10,8 @@ follow the reference:
 * ``ExpertPayload``     crates/streammoe/src/riir/moe/expert_forward.rs:123-139
 * ``gpu_batched_experts_forward``  expert_forward.rs:718-746
 * ``moe_router``        crates/streammoe/src/riir/moe/moe_router.rs:151-181 (on the GPU)
+* ``ExpertFiles``, ``layout_and_stride``, ``declared_stride``
+                        crates/streammoe/src/riir/io/expert_io.rs:229-420 (resident layers)
 
 Device buffers are torch tensors on ``cuda`` (PyTorch is only the
 allocator and stream provider here). Every call goes through libsmoe;
@@ -17,6 +19,8 @@ nothing falls back to a CPU path: importing this package without the
 built library raises ImportError.
 """
 import ctypes as C
+import json
+import os
 from dataclasses import dataclass
 
 from . import _abi
@@ -223,6 +227,15 @@ class Kernels:
                                      _ptr(out_sum), _ptr(workspace),
                                      0 if workspace is None else workspace.numel() * workspace.element_size())
 
+    # -- expert files -------------------------------------------------------------
+    def load_file(self, path, dst, offset=0, nbytes=0):
+        """Copy bytes [offset, offset + nbytes) of the file (nbytes 0: to its
+        end) into the device tensor dst; returns the bytes copied."""
+        got = C.c_uint64(0)
+        check(_lib.smoe_load_file(self.h, os.fsencode(path), offset, nbytes, _ptr(dst),
+                                  dst.numel() * dst.element_size(), C.byref(got)), f"smoe_load_file({path})")
+        return got.value
+
     # -- diagnostics --------------------------------------------------------------
     def stream_read(self, buf, nbytes, sink):
         """Read nbytes of the device tensor `buf` once (HBM read-peak probe)."""
@@ -240,6 +253,78 @@ class Kernels:
 
     def synth_normal_bf16(self, out, seed, sigma=1.0):
         return _lib.smoe_synth_normal_bf16(self.h, _ptr(out), out.numel(), seed, C.c_float(sigma))
+
+
+class ExpertIoError(RuntimeError):
+    """ExpertIoError (io/expert_io.rs): Io, MixedLayouts."""
+
+
+def declared_stride(packed_dir):
+    """declared_stride (expert_io.rs:239-251): (expert_size, expert_stride)
+    from packed_dir/layout.json when it declares a stride above the size,
+    else None."""
+    try:
+        with open(os.path.join(packed_dir, "layout.json")) as f:
+            v = json.load(f)
+        size, stride = int(v["expert_size"]), int(v["expert_stride"])
+    except (OSError, ValueError, KeyError, TypeError):
+        return None
+    return (size, stride) if stride > size else None
+
+
+def layout_and_stride(file_bytes, n_experts, hidden, inter, group=64, declared=None):
+    """layout_and_stride (expert_io.rs:253-267) through libsmoe: the
+    (ExpertLayout, stride) of a layer file file_bytes long."""
+    out = _abi.FileLayout()
+    ds, dst = declared if declared else (0, 0)
+    check(_lib.smoe_layer_file_layout(file_bytes, n_experts, hidden, inter, group, ds, dst, C.byref(out)),
+          "smoe_layer_file_layout")
+    return ExpertLayout(hidden, inter, out.bits, group), out.stride
+
+
+class ExpertFiles:
+    """Resident expert arenas from experts_dir/packed_experts/layer_NN.bin
+    (ExpertFiles::open_range_tiered, expert_io.rs:332-420, with every layer
+    loaded into one device arena: expert e of layer l at arena(l) + e *
+    stride). Missing layer files stay None; layers whose layouts differ
+    raise ExpertIoError (MixedLayouts); a layout.json padded stride is
+    honoured as the reference does."""
+
+    def __init__(self, kernels: Kernels, experts_dir, n_layers, n_experts, hidden, inter, group=64,
+                 layers=None):
+        import torch
+
+        packed = os.path.join(experts_dir, "packed_experts")
+        declared = declared_stride(packed)
+        self.layout = None
+        self.stride = None
+        self.arenas = [None] * n_layers
+        first = None
+        for i in (range(n_layers) if layers is None else layers):
+            path = os.path.join(packed, f"layer_{i:02d}.bin")
+            try:
+                size = os.path.getsize(path)
+            except FileNotFoundError:
+                continue
+            lay, stride = layout_and_stride(size, n_experts, hidden, inter, group, declared)
+            if first is None:
+                first = i
+                self.layout, self.stride = lay, stride
+            elif lay.bits != self.layout.bits:
+                raise ExpertIoError(f"MixedLayouts: layer {i} is {lay.bits}-bit, layer {first} is "
+                                    f"{self.layout.bits}-bit")
+            arena = torch.empty(size, dtype=torch.uint8, device=f"cuda:{kernels.device}")
+            kernels.load_file(path, arena)
+            self.arenas[i] = arena
+        if self.layout is None:
+            self.layout, self.stride = ExpertLayout(hidden, inter, 4, group), None
+
+    def arena(self, layer):
+        return self.arenas[layer]
+
+    def binding(self, layer, expert):
+        """(arena, byte offset) of one expert: the reference's (&Buffer, u64)."""
+        return self.arenas[layer], expert * self.stride
 
 
 def zipf_routing(n_tokens, n_experts, k, s=1.1, seed=0):

@@ -27,6 +27,7 @@ STATUS = {
     10: "SMOE_ERR_HIP",
     11: "SMOE_ERR_NO_DEVICE",
     12: "SMOE_ERR_DEVICE_TIMEOUT",
+    13: "SMOE_ERR_IO",
 }
 SMOE_OPT_DECODE_PATH = 1
 SMOE_OPT_TRACE_BUFFER = 2
@@ -80,6 +81,15 @@ class Layer(C.Structure):
     ]
 
 
+class FileLayout(C.Structure):
+    _fields_ = [
+        ("bits", C.c_uint32),
+        ("reserved", C.c_uint32),
+        ("expert_size", C.c_uint64),
+        ("stride", C.c_uint64),
+    ]
+
+
 _P = C.c_void_p
 _U32 = C.c_uint32
 _U64 = C.c_uint64
@@ -109,6 +119,8 @@ PROTOTYPES = {
     "smoe_moe_prefill_workspace_size": (_U64, [C.POINTER(ExpertShape), _U32, _U32, _U32]),
     "smoe_moe_prefill": (_I, [_P, C.POINTER(ExpertShape), _P, _U64, _U32, _P, _P, _P, _I, _U32, _U32, _P, _P,
                               _U64]),
+    "smoe_layer_file_layout": (_I, [_U64, _U32, _U32, _U32, _U32, _U64, _U64, C.POINTER(FileLayout)]),
+    "smoe_load_file": (_I, [_P, C.c_char_p, _U64, _U64, _P, _U64, C.POINTER(_U64)]),
     "smoe_stream_read": (_I, [_P, _P, C.c_uint64, _P]),
     "smoe_synth_experts": (_I, [_P, _P, _U32, _U64, C.POINTER(ExpertShape), _U64, C.c_float, C.c_float]),
     "smoe_synth_normal_f32": (_I, [_P, _P, _U64, _U64, C.c_float]),

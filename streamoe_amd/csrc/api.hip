@@ -6,35 +6,12 @@
 #include <new>
 
 #include "../../include/smoe.h"
+#include "handle.h"
 #include "kernels.h"
 #include "persist.h"
 
 using namespace smoe;
 
-struct smoe_handle {
-  int device = 0;
-  hipStream_t stream = nullptr;
-  // Decode scratch (MoeBuffers' flat buffers, expert_forward.rs:379-528).
-  void* mem = nullptr;
-  float* act = nullptr;       // [kMaxSlots, max_inter]
-  float* logits = nullptr;    // [max_experts + 1]
-  float* gate = nullptr;      // [1] shared-expert gate score
-  FfnTable* table = nullptr;  // routing table of the current token
-  uint32_t* xl = nullptr;     // [max_hidden / 32 * kXLimbWords] x as integer limbs
-  float* arg_v = nullptr;     // [256] argmax partial values
-  uint32_t* arg_i = nullptr;  // [256] argmax partial indices
-  // Persistent decode: tagged handoff buffers (epoch << 32 | value).
-  uint64_t* tag_resid = nullptr;  // [max_hidden]
-  uint64_t* tag_logit = nullptr;  // [max_experts + 1]
-  uint64_t* tag_act = nullptr;    // [kMaxSlots * max_inter]
-  uint64_t* tag_route = nullptr;  // [32]
-  uint32_t* err = nullptr;        // device error word
-  uint32_t epoch = 1;             // next unused epoch (0 is never used)
-  uint32_t max_hidden = 0, max_inter = 0, max_experts = 0;
-  // Options.
-  int decode_path = 0;  // 0 auto, 1 per-phase kernels, 2 persistent, 3 three-kernel
-  uint64_t* trace = nullptr;
-};
 
 namespace {
 
@@ -139,6 +116,7 @@ const char* smoe_strerror(int status) {
     case SMOE_ERR_HIP: return "HIP runtime error";
     case SMOE_ERR_NO_DEVICE: return "no gfx950 device at that ordinal";
     case SMOE_ERR_DEVICE_TIMEOUT: return "a bounded device-side wait expired; outputs are invalid";
+    case SMOE_ERR_IO: return "file could not be opened or read, or is shorter than asked";
     default: return "unknown status";
   }
 }
@@ -173,6 +151,7 @@ int smoe_destroy(smoe_handle* h) {
     (void)hipStreamSynchronize(h->stream);
     (void)hipFree(h->mem);
   }
+  release_staging(h);
   delete h;
   return SMOE_OK;
 }

@@ -1,0 +1,44 @@
+// handle.h — the libsmoe handle (internal; the C ABI sees an opaque
+// pointer): device, stream, reserved decode scratch, options, and the file
+// loader's staging buffers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/smoe.h"
+#include "kernels.h"
+
+struct smoe_handle {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  // Decode scratch (MoeBuffers' flat buffers, expert_forward.rs:379-528).
+  void* mem = nullptr;
+  float* act = nullptr;       // [kMaxSlots, max_inter]
+  float* logits = nullptr;    // [max_experts + 1]
+  float* gate = nullptr;      // [1] shared-expert gate score
+  smoe::FfnTable* table = nullptr;  // routing table of the current token
+  uint32_t* xl = nullptr;     // [max_hidden / 32 * kXLimbWords] x as integer limbs
+  float* arg_v = nullptr;     // [256] argmax partial values
+  uint32_t* arg_i = nullptr;  // [256] argmax partial indices
+  // Persistent decode: tagged handoff buffers (epoch << 32 | value).
+  uint64_t* tag_resid = nullptr;  // [max_hidden]
+  uint64_t* tag_logit = nullptr;  // [max_experts + 1]
+  uint64_t* tag_act = nullptr;    // [kMaxSlots * max_inter]
+  uint64_t* tag_route = nullptr;  // [32]
+  uint32_t* err = nullptr;        // device error word
+  uint32_t epoch = 1;             // next unused epoch (0 is never used)
+  uint32_t max_hidden = 0, max_inter = 0, max_experts = 0;
+  // Options.
+  int decode_path = 0;  // 0 auto, 1 per-phase kernels, 2 persistent, 3 three-kernel
+  uint64_t* trace = nullptr;
+  // File loader: two pinned host staging buffers (allocated on first use,
+  // freed by smoe_destroy) and the events that say when a copy out of
+  // each has finished.
+  void* stage[2] = {nullptr, nullptr};
+  hipEvent_t stage_done[2] = {nullptr, nullptr};
+  uint64_t stage_bytes = 0;
+};
+
+// Frees the loader's staging buffers and events (loader.hip).
+void release_staging(smoe_handle* h);

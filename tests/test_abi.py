@@ -35,8 +35,8 @@ def test_strerror_and_version():
     from streamoe_amd import _abi
 
     lib = _abi.load()
-    texts = [lib.smoe_strerror(c).decode() for c in range(13)]
-    assert texts[0] == "ok" and len(set(texts)) == 13
+    texts = [lib.smoe_strerror(c).decode() for c in range(14)]
+    assert texts[0] == "ok" and len(set(texts)) == 14
     assert lib.smoe_strerror(99).decode() == "unknown status"
     assert lib.smoe_abi_version() >= 1
 
