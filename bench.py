@@ -83,12 +83,15 @@ def stream_read_peak(dev, gib=4):
     return round(best, 1)
 
 
-def layer_bytes(c):
+def layer_bytes(c, tokens=1):
+    """Algorithmic bytes of one layer for `tokens` tokens decoded together:
+    the router and the shared expert once, each token's k routed experts
+    (counted as distinct)."""
     import streamoe_amd as sa
 
     routed = sa.ExpertLayout(c["H"], c["I"], c["bits"], 64).expert_size
     shared = sa.ExpertLayout(c["H"], c["I"], 4, 64).expert_size if c["shared"] else 0
-    return c["k"] * routed + shared + c["E"] * c["H"] * 4
+    return tokens * c["k"] * routed + shared + c["E"] * c["H"] * 4
 
 
 def cpu_threads():
@@ -252,17 +255,21 @@ def run_decode(args, c):
         gates.append(g)
         norms.append(nw)
         layers.append(kern.layer(lay, a, stride, E, k, c["normalize"], r, s, g))
-    x0 = torch.empty(H, dtype=torch.float32, device=dev)
+    T = args.tokens
+    x0 = torch.empty((T, H) if T > 1 else (H,), dtype=torch.float32, device=dev)
     sa.check(kern.synth_normal_f32(x0, 5000, 1.0), "synth")
     resid = x0.clone()
-    work = torch.empty(H, dtype=torch.float32, device=dev)
+    work = torch.empty_like(x0)
     torch.cuda.synchronize()
 
     path = {"auto": 0, "kernels": 1, "persistent": 2, "fused": 3}[args.path]
     kern.set_decode_path(path)
 
     def step():
-        sa.check(kern.moe_decode_layers(layers, norms, 1e-6, x0, resid, work), "smoe_moe_decode_layers")
+        if T > 1:
+            sa.check(kern.moe_decode_tokens(layers, norms, 1e-6, T, x0, resid, work), "smoe_moe_decode_tokens")
+        else:
+            sa.check(kern.moe_decode_layers(layers, norms, 1e-6, x0, resid, work), "smoe_moe_decode_layers")
 
     stream = torch.cuda.current_stream(dev)
     graph = None
@@ -287,10 +294,10 @@ def run_decode(args, c):
     sa.check(_sync_status(kern), "smoe_sync")
     assert torch.isfinite(resid).all(), "residual stream is not finite"
     phases = None
-    if args.trace:
+    if args.trace and T == 1:
         phases = trace_phases(kern, step, nl) if path == 2 else trace_fused(kern, step, nl)
 
-    nbytes = layer_bytes(c)
+    nbytes = layer_bytes(c, T)
     achieved = nbytes / (us_layer * 1e-6) / 1e9
     out = {
         "metric": "4-bit MoE expert decode µs/layer + achieved HBM GB/s (% of peak), 1 GPU",
@@ -306,20 +313,23 @@ def run_decode(args, c):
         "dtype": "u4/u3 codes, f32 compute",
         "data": "synthetic (seeded, generated on the device)",
         "config": {"workload": c["name"], "hidden": H, "experts": E, "top_k": k, "inter": I, "bits": c["bits"],
-                   "group": 64, "layers": nl, "shared_expert": c["shared"], "tokens": 1,
+                   "group": 64, "layers": nl, "shared_expert": c["shared"], "tokens": T,
                    "mode": "hipgraph" if graph is not None else "eager"},
         "gbps": round(achieved, 1),
         "pct_of_hbm_peak": round(100 * achieved / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": MEASURED_TRAFFIC.get(c.get("key")) if path in (0, 3) else None,
-                     "unit_of_work": f"one layer: {nbytes} algorithmic bytes",
+                     "unit_of_work": f"one layer, {T} token(s): {nbytes} algorithmic bytes",
                      "kernel": "decode layer: k_fa_route + k_fa_gateup + k_fa_down (one HIP graph)"
                                if path in (0, 3) else "decode layer (all launches)"},
         "wall_s": round(wall, 3),
     }
+    if T > 1:
+        out["us_per_layer_per_token"] = round(us_layer / T, 4)
+        out["roofline"]["traffic"] = None
     if phases:
         out["phases_us"] = phases
-    if not args.no_cpu:
+    if not args.no_cpu and T == 1:
         a0 = arenas[0].cpu().numpy()
         r0 = routers[0].cpu().numpy()
         s0 = None if shareds[0] is None else shareds[0].cpu().numpy()
@@ -515,6 +525,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-stream-peak", action="store_true", help="skip the measured streaming-read peak")
+    ap.add_argument("--tokens", type=int, default=1, choices=[1, 2, 3, 4],
+                    help="decode configs: tokens decoded together through the layers (value = us per layer "
+                         "for all of them)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the multi-GPU "

@@ -214,6 +214,18 @@ class Kernels:
         return _lib.smoe_moe_decode_layers(self.h, arr, n, nw, C.c_float(eps), _ptr(input),
                                            _ptr(residual_io), _ptr(work))
 
+    def moe_decode_tokens(self, layers, norm_w, eps, n_tokens, input, residual_io, work, idx_out=None,
+                          w_out=None):
+        """T <= 4 tokens through the layers at once (decode_multi.rs
+        moe_dispatch_multi); rows of input / residual_io / work are tokens."""
+        n = len(layers)
+        arr = (_abi.Layer * n)(*layers)
+        nw = None
+        if norm_w is not None:
+            nw = (C.c_void_p * n)(*[None if t is None else t.data_ptr() for t in norm_w])
+        return _lib.smoe_moe_decode_tokens(self.h, arr, n, nw, C.c_float(eps), n_tokens, _ptr(input),
+                                           _ptr(residual_io), _ptr(work), _ptr(idx_out), _ptr(w_out))
+
     # -- prefill (encode_moe_gather_id_fuse) --------------------------------------
     def moe_prefill_workspace_size(self, layout, n_tokens, n_experts, k):
         shape = layout.shape()

@@ -48,10 +48,14 @@ int reserve(smoe_handle* h, uint32_t H, uint32_t I, uint32_t E) {
   I = I > h->max_inter ? I : h->max_inter;
   E = E > h->max_experts ? E : h->max_experts;
   auto al = [](size_t n) { return (n + 255) & ~(size_t)255; };
-  const size_t act_b = al((size_t)kMaxSlotsHost * I * sizeof(float));
-  const size_t log_b = al(((size_t)E + 1) * sizeof(float));
-  const size_t tab_b = al(sizeof(FfnTable));
-  const size_t xl_b = al((size_t)H / 32 * 32 * sizeof(uint32_t));
+  // act, logits, route table and limbs hold kMaxDecodeTokens tokens
+  // (multi-token decode); single-token paths use token 0's.
+  const size_t T = kMaxDecodeTokens;
+  const size_t lstride = al(((size_t)E + 1) * sizeof(float)) / sizeof(float);
+  const size_t act_b = al(T * kMaxSlotsHost * I * sizeof(float));
+  const size_t log_b = al(T * lstride * sizeof(float));
+  const size_t tab_b = al(T * sizeof(FfnTable));
+  const size_t xl_b = al(T * (size_t)H / 32 * 32 * sizeof(uint32_t));
   const size_t tr_b = al((size_t)H * 8), tl_b = al(((size_t)E + 1) * 8);
   const size_t ta_b = al((size_t)kMaxSlotsHost * I * 8), tro_b = al(32 * 8);
   const size_t arg_b = 2 * 256 * sizeof(uint32_t);
@@ -89,6 +93,9 @@ int reserve(smoe_handle* h, uint32_t H, uint32_t I, uint32_t E) {
   q += tro_b;
   h->err = (uint32_t*)q;
   h->epoch = 1;
+  h->lstride = (uint32_t)lstride;
+  h->astride = (uint32_t)(kMaxSlotsHost * I);
+  h->xstride = H / 32 * 32;
   h->max_hidden = H;
   h->max_inter = I;
   h->max_experts = E;
@@ -391,7 +398,8 @@ static bool fused_ok(const smoe_layer* L) {
 
 static int decode_fused(smoe_handle* h, const smoe_layer* L, const float* x_in, const float* resid,
                         const uint16_t* norm, float eps, float* x_out, const float* h_mid,
-                        float* out, int32_t* idx_out, float* w_out, uint32_t layer_index) {
+                        float* out, int32_t* idx_out, float* w_out, uint32_t layer_index,
+                        uint32_t n_tokens = 1) {
   if (!fused_ok(L)) return SMOE_ERR_UNSUPPORTED_SHAPE;
   const smoe_expert_shape& s = L->shape;
   FusedLayer a{};
@@ -418,7 +426,11 @@ static int decode_fused(smoe_handle* h, const smoe_layer* L, const float* x_in, 
   a.out = out;
   a.idx_out = idx_out;
   a.w_out = w_out;
-  a.trace = h->trace ? h->trace + (uint64_t)layer_index * kFaTraceLayer : nullptr;
+  a.trace = (h->trace && n_tokens == 1) ? h->trace + (uint64_t)layer_index * kFaTraceLayer : nullptr;
+  a.n_tokens = n_tokens;
+  a.lstride = h->lstride;
+  a.astride = h->astride;
+  a.xstride = h->xstride;
   return hip_status(launch_fused_layer(a, h->stream));
 }
 
@@ -561,6 +573,30 @@ int smoe_moe_decode_layers(smoe_handle* h, const smoe_layer* layers, uint32_t n_
       }
     }
     if (int rc = decode_layer(h, &layers[l], x, residual_io, residual_io, nullptr, nullptr))
+      return rc;
+  }
+  return SMOE_OK;
+}
+
+int smoe_moe_decode_tokens(smoe_handle* h, const smoe_layer* layers, uint32_t n_layers,
+                           const void* const* norm_w, float eps, uint32_t n_tokens, const float* input,
+                           float* residual_io, float* work, int32_t* idx_out, float* w_out) {
+  if (!h || !layers || !n_layers || !input || !residual_io || !work) return SMOE_ERR_INVALID_ARG;
+  if (n_tokens < 1 || n_tokens > kMaxDecodeTokens) return SMOE_ERR_INVALID_ARG;
+  for (uint32_t l = 0; l < n_layers; ++l) {
+    if (int rc = check_layer(h, &layers[l])) return rc;
+    if (layers[l].shape.hidden != layers[0].shape.hidden) return SMOE_ERR_INVALID_ARG;
+    if (norm_w && l > 0 && !norm_w[l]) return SMOE_ERR_INVALID_ARG;
+    if (!fused_ok(&layers[l])) return SMOE_ERR_UNSUPPORTED_SHAPE;
+  }
+  if (!aligned(input, 0, 16) || !aligned(residual_io, 0, 16) || !aligned(work, 0, 16))
+    return SMOE_ERR_MISALIGNED;
+  if (int rc = use_device(h)) return rc;
+  for (uint32_t l = 0; l < n_layers; ++l) {
+    const uint16_t* nw = (norm_w && l > 0) ? (const uint16_t*)norm_w[l] : nullptr;
+    const bool last = l + 1 == n_layers;
+    if (int rc = decode_fused(h, &layers[l], l == 0 ? input : nullptr, residual_io, nw, eps, work, residual_io,
+                              residual_io, last ? idx_out : nullptr, last ? w_out : nullptr, l, n_tokens))
       return rc;
   }
   return SMOE_OK;

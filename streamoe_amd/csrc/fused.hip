@@ -12,6 +12,10 @@
 // of waiting for (RMSNorm's sum of squares, softmax and the top-k set) it
 // computes in every wave.
 //
+// With T <= 4 tokens (multi-token decode), K_A reads each router and
+// shared-expert row once for all T tokens, and K_B / K_C run one grid
+// slice per token (grid dimension y).
+//
 //   K_A  k_fa_route    one wave per router row / per SR shared-expert rows:
 //                      x = RMSNorm(r) * w (or the given input), then
 //                      logits[e] = W_e . x (row E: shared gate), or
@@ -126,9 +130,31 @@ __device__ __forceinline__ void fa_x_finish(const FusedLayer& a, FaX& f) {
   }
 }
 
+// Token t's view of a multi-token layer: the same arguments with every
+// per-token pointer moved to token t's rows.
+__device__ __forceinline__ FusedLayer token_view(const FusedLayer& a, uint32_t t) {
+  FusedLayer b = a;
+  if (t == 0) return b;
+  const size_t hs = (size_t)t * kFaH;
+  if (b.x_in) b.x_in += hs;
+  if (b.resid) b.resid += hs;
+  b.h_mid += hs;
+  b.out += hs;
+  b.logits += (size_t)t * a.lstride;
+  b.act += (size_t)t * a.astride;
+  b.xl += (size_t)t * a.xstride;
+  b.table += t;
+  if (b.idx_out) b.idx_out += (size_t)t * a.k;
+  if (b.w_out) b.w_out += (size_t)t * a.k;
+  return b;
+}
+
 // ---------------------------------------------------------------------------
-// K_A: router logits (+ shared gate) and the shared expert's gate/up.
+// K_A: router logits (+ shared gate) and the shared expert's gate/up, for
+// T tokens: each wave reads its router / shared-expert rows once and
+// applies them to every token's x.
 // ---------------------------------------------------------------------------
+template <int T>
 __global__ __launch_bounds__(64) void k_fa_route(FusedLayer a) {
   FaClock clk;
   fa_stamp(a, clk, 0, false);
@@ -143,28 +169,33 @@ __global__ __launch_bounds__(64) void k_fa_route(FusedLayer a) {
     const f32x4* rp = reinterpret_cast<const f32x4*>(row + (size_t)c * kChunk);
 #pragma unroll
     for (int i = 0; i < kChunk / 4; ++i) wr[i] = ld_stream(rp + i);
-    FaX f;
-    fa_x_load(a, lane, f);
+    FaX f[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) fa_x_load(token_view(a, t), lane, f[t]);
     __builtin_amdgcn_sched_barrier(0);
     fa_stamp(a, clk, 3, true);
-    fa_x_finish(a, f);
-    const float(&x)[kChunk] = f.x;
-    if (w == 0) {
-      XLimbs xl;
-      make_limbs(x, xl);
-      store_limbs(a.xl + (size_t)c * kXLimbWords, xl);
-    }
-    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
 #pragma unroll
-    for (int i = 0; i < kChunk / 4; ++i) {
-      a0 = __builtin_fmaf(wr[i].x, x[4 * i + 0], a0);
-      a1 = __builtin_fmaf(wr[i].y, x[4 * i + 1], a1);
-      a2 = __builtin_fmaf(wr[i].z, x[4 * i + 2], a2);
-      a3 = __builtin_fmaf(wr[i].w, x[4 * i + 3], a3);
+    for (int t = 0; t < T; ++t) {
+      const FusedLayer at = token_view(a, t);
+      fa_x_finish(at, f[t]);
+      const float(&x)[kChunk] = f[t].x;
+      if (w == (uint32_t)t) {
+        XLimbs xl;
+        make_limbs(x, xl);
+        store_limbs(at.xl + (size_t)c * kXLimbWords, xl);
+      }
+      float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+      for (int i = 0; i < kChunk / 4; ++i) {
+        a0 = __builtin_fmaf(wr[i].x, x[4 * i + 0], a0);
+        a1 = __builtin_fmaf(wr[i].y, x[4 * i + 1], a1);
+        a2 = __builtin_fmaf(wr[i].z, x[4 * i + 2], a2);
+        a3 = __builtin_fmaf(wr[i].w, x[4 * i + 3], a3);
+      }
+      const float s = group_sum_last<64>((a0 + a1) + (a2 + a3));
+      if (lane == 63) at.logits[w] = s;
     }
-    const float s = group_sum_last<64>((a0 + a1) + (a2 + a3));
     fa_stamp(a, clk, 4, false);
-    if (lane == 63) a.logits[w] = s;
     fa_stamp(a, clk, 5, true);
     fa_flush(a, clk, 0);
     return;
@@ -186,19 +217,24 @@ __global__ __launch_bounds__(64) void k_fa_route(FusedLayer a) {
     load_sb(a.shared, g.s[0], g.b[0], row, gpr, cps, c, sg[p], bg[p]);
     load_sb(a.shared, g.s[1], g.b[1], row, gpr, cps, c, su[p], bu[p]);
   }
-  FaX f;
-  fa_x_load(a, lane, f);
+  FaX f[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) fa_x_load(token_view(a, t), lane, f[t]);
   __builtin_amdgcn_sched_barrier(0);
   fa_stamp(a, clk, 3, true);
-  fa_x_finish(a, f);
-  const float(&x)[kChunk] = f.x;
-  const float xs = xsum(x);
-  float* act = a.act + (size_t)a.k * g.inter;
 #pragma unroll
-  for (int p = 0; p < kFaSR; ++p) {
-    const float gs = group_sum_last<64>(chunk_dot<4>(rg[p], x, xs, bf16f(sg[p]), bf16f(bg[p])));
-    const float us = group_sum_last<64>(chunk_dot<4>(ru[p], x, xs, bf16f(su[p]), bf16f(bu[p])));
-    if (lane == 63) act[r0 + p] = silu_mul(gs, us);
+  for (int t = 0; t < T; ++t) {
+    const FusedLayer at = token_view(a, t);
+    fa_x_finish(at, f[t]);
+    const float(&x)[kChunk] = f[t].x;
+    const float xs = xsum(x);
+    float* act = at.act + (size_t)a.k * g.inter;
+#pragma unroll
+    for (int p = 0; p < kFaSR; ++p) {
+      const float gs = group_sum_last<64>(chunk_dot<4>(rg[p], x, xs, bf16f(sg[p]), bf16f(bg[p])));
+      const float us = group_sum_last<64>(chunk_dot<4>(ru[p], x, xs, bf16f(su[p]), bf16f(bu[p])));
+      if (lane == 63) act[r0 + p] = silu_mul(gs, us);
+    }
   }
   fa_stamp(a, clk, 5, true);
   fa_flush(a, clk, 0);
@@ -208,7 +244,8 @@ __global__ __launch_bounds__(64) void k_fa_route(FusedLayer a) {
 // K_B: top-k set in every wave, routed gate/up; block 0 publishes the table.
 // ---------------------------------------------------------------------------
 template <int BITS, int P>
-__global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a) {
+__global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a_all) {
+  const FusedLayer a = token_view(a_all, blockIdx.y);
   constexpr int CB = chunk_bytes<BITS>();
   constexpr uint32_t RB = kFaH / kChunk * CB;  // row bytes
   __shared__ int32_t sid[kMaxK];
@@ -379,7 +416,8 @@ constexpr int fa_down_threads() {
 }
 
 template <int BITS, int LI>
-__global__ __launch_bounds__(fa_down_threads<LI>()) void k_fa_down(FusedLayer a) {
+__global__ __launch_bounds__(fa_down_threads<LI>()) void k_fa_down(FusedLayer a_all) {
+  const FusedLayer a = token_view(a_all, blockIdx.y);
   constexpr int SPW = kWave / LI;
   __shared__ float so[kFaR][kMaxSlots];
   __shared__ float sw[kMaxSlots];
@@ -451,25 +489,32 @@ bool fused_supported(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t b
 template <int BITS>
 static void launch_gateup_fa(const FusedLayer& a, uint32_t blocks, hipStream_t st) {
   const uint32_t p = (a.E + 63) / 64;
+  const dim3 grid(blocks, a.n_tokens);
   if (p <= 1)
-    hipLaunchKernelGGL((k_fa_gateup<BITS, 1>), dim3(blocks), dim3(64), 0, st, a);
+    hipLaunchKernelGGL((k_fa_gateup<BITS, 1>), grid, dim3(64), 0, st, a);
   else if (p <= 2)
-    hipLaunchKernelGGL((k_fa_gateup<BITS, 2>), dim3(blocks), dim3(64), 0, st, a);
+    hipLaunchKernelGGL((k_fa_gateup<BITS, 2>), grid, dim3(64), 0, st, a);
   else
-    hipLaunchKernelGGL((k_fa_gateup<BITS, 4>), dim3(blocks), dim3(64), 0, st, a);
+    hipLaunchKernelGGL((k_fa_gateup<BITS, 4>), grid, dim3(64), 0, st, a);
 }
 
 template <int BITS, int LI>
 static void launch_down_fa(const FusedLayer& a, hipStream_t st) {
   constexpr uint32_t SPW = kWave / LI;
   const uint32_t waves = (a.k + SPW - 1) / SPW + (a.shared ? 1u : 0u);
-  hipLaunchKernelGGL((k_fa_down<BITS, LI>), dim3(kFaH / kFaR), dim3(waves * kWave), 0, st, a);
+  hipLaunchKernelGGL((k_fa_down<BITS, LI>), dim3(kFaH / kFaR, a.n_tokens), dim3(waves * kWave), 0, st, a);
 }
 
 hipError_t launch_fused_layer(const FusedLayer& a, hipStream_t st) {
+  if (a.n_tokens < 1 || a.n_tokens > kMaxDecodeTokens || (a.trace && a.n_tokens != 1)) return hipErrorInvalidValue;
   const uint32_t I = a.routed.inter;
   const uint32_t ka = a.E + (a.gate ? 1u : 0u) + (a.shared ? I / kFaSR : 0u);
-  hipLaunchKernelGGL(k_fa_route, dim3(ka), dim3(64), 0, st, a);
+  switch (a.n_tokens) {
+    case 1: hipLaunchKernelGGL(k_fa_route<1>, dim3(ka), dim3(64), 0, st, a); break;
+    case 2: hipLaunchKernelGGL(k_fa_route<2>, dim3(ka), dim3(64), 0, st, a); break;
+    case 3: hipLaunchKernelGGL(k_fa_route<3>, dim3(ka), dim3(64), 0, st, a); break;
+    default: hipLaunchKernelGGL(k_fa_route<4>, dim3(ka), dim3(64), 0, st, a); break;
+  }
   const uint32_t kb = a.k * (I / kFaRW);
   if (a.routed.bits == 4)
     launch_gateup_fa<4>(a, kb, st);

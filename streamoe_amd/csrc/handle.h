@@ -29,6 +29,8 @@ struct smoe_handle {
   uint32_t* err = nullptr;        // device error word
   uint32_t epoch = 1;             // next unused epoch (0 is never used)
   uint32_t max_hidden = 0, max_inter = 0, max_experts = 0;
+  // Per-token strides (elements) of logits, act and limbs in the scratch.
+  uint32_t lstride = 0, astride = 0, xstride = 0;
   // Options.
   int decode_path = 0;  // 0 auto, 1 per-phase kernels, 2 persistent, 3 three-kernel
   uint64_t* trace = nullptr;

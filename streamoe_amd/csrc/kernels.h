@@ -73,8 +73,17 @@ struct FusedLayer {
   float* out;              // hidden out (may alias h_mid / resid)
   int32_t* idx_out;        // [k] exact slot order, or null
   float* w_out;            // [k], or null
-  uint64_t* trace;         // per-block timestamps of this layer, or null
+  uint64_t* trace;         // per-block timestamps of this layer, or null (one token only)
+  // Several tokens at once (grid dimension y = token in K_B and K_C; K_A
+  // loops over the tokens so each router / shared-expert row is read once).
+  // Token t's x_in / resid / h_mid / out rows are at + t * hidden, its
+  // logits at + t * lstride, act at + t * astride, limbs at + t * xstride,
+  // route table at table + t, idx_out / w_out at + t * k.
+  uint32_t n_tokens;
+  uint32_t lstride, astride, xstride;
 };
+
+constexpr uint32_t kMaxDecodeTokens = 4;  // tokens per multi-token decode call
 
 // Trace layout of the three-kernel path: per layer kFaTraceLayer words;
 // kernel q (0 route, 1 gate/up, 2 down), block b at
