@@ -146,6 +146,21 @@ int smoe_argmax(smoe_handle* h, const float* v, uint32_t n, int32_t* out_index);
  * the reference CPU path forms (crates/streammoe/src/riir/backend/cpu/
  * cpu_matvec.rs:164-165). Verification entry point: the decode kernels
  * use the same code-unpacking routine and never materialise w. */
+/* Device workspace bytes smoe_qmm needs (0 for zero sizes). */
+uint64_t smoe_qmm_workspace_size(uint32_t in_dim, uint32_t group, uint32_t n_tokens);
+
+/* Dense quantized matmul y[n_tokens, out_dim] = x[n_tokens, in_dim] .
+ * dequant(W)[out_dim, in_dim]^T (f32 in and out, row-major), on bf16 MFMA
+ * with exact dequant and fp32 accumulation (x split into bf16 hi + lo):
+ * the QmmCall / encode_dense_matmul_n_tokens of metal/lib.rs:357-380,
+ * 684-734 and gpu_matvec.rs:256-302 (shared expert and projections at
+ * N > 1). Supported: bits 4 or 3, group 32/64/128, in_dim a multiple of
+ * 256 (<= 16384), out_dim a multiple of 256; weights, scales, biases, x, y
+ * 16-byte aligned, biases after the scales; workspace 256-byte aligned.
+ * Enqueue-only, allocates nothing. */
+int smoe_qmm(smoe_handle* h, const smoe_qweights* w, const float* x, float* y, uint32_t out_dim,
+             uint32_t in_dim, uint32_t n_tokens, void* workspace, uint64_t workspace_bytes);
+
 int smoe_dequant(smoe_handle* h, const smoe_qweights* w, uint32_t in_dim, uint32_t row0,
                  uint32_t n_rows, float* out);
 

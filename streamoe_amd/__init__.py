@@ -160,6 +160,15 @@ class Kernels:
         wc = w.c()
         return _lib.smoe_qmv(self.h, C.byref(wc), _ptr(x), _ptr(y), out_dim, in_dim)
 
+    def qmm_workspace_size(self, in_dim, group, n_tokens):
+        return _lib.smoe_qmm_workspace_size(in_dim, group, n_tokens)
+
+    def qmm(self, w: QuantWeights, x, y, out_dim, in_dim, n_tokens, workspace):
+        """QmmCall (metal/lib.rs:357-380): y[n, out] = x[n, in] . dequant(W)^T."""
+        wc = w.c()
+        return _lib.smoe_qmm(self.h, C.byref(wc), _ptr(x), _ptr(y), out_dim, in_dim, n_tokens,
+                             _ptr(workspace), workspace.numel() * workspace.element_size())
+
     def argmax(self, v, n, out):
         return _lib.smoe_argmax(self.h, _ptr(v), n, _ptr(out))
 

@@ -232,6 +232,48 @@ int smoe_qmv(smoe_handle* h, const smoe_qweights* w, const float* x, float* y, u
   return hip_status(e);
 }
 
+uint64_t smoe_qmm_workspace_size(uint32_t in_dim, uint32_t group, uint32_t n_tokens) {
+  if (!in_dim || !group || !n_tokens) return 0;
+  return qmm_workspace(in_dim, group, n_tokens, nullptr, nullptr);
+}
+
+int smoe_qmm(smoe_handle* h, const smoe_qweights* w, const float* x, float* y, uint32_t out_dim,
+             uint32_t in_dim, uint32_t n_tokens, void* workspace, uint64_t workspace_bytes) {
+  if (!h || !x || !y || !out_dim || !n_tokens || !workspace) return SMOE_ERR_INVALID_ARG;
+  QView v;
+  if (int rc = qview(w, in_dim, &v)) return rc;
+  if (!qmm_supported(in_dim, out_dim, w->group_size, w->bits, n_tokens)) return SMOE_ERR_UNSUPPORTED_SHAPE;
+  // The GEMM copies weights, scales and biases with 16-byte LDS DMA and
+  // addresses biases from the scales (biases after them).
+  if (!aligned(w->base, w->packed_offset, 16) || !aligned(w->base, w->scales_offset, 16) ||
+      !aligned(w->base, w->biases_offset, 16) || !aligned(x, 0, 16) || !aligned(y, 0, 16) ||
+      !aligned(workspace, 0, 256))
+    return SMOE_ERR_MISALIGNED;
+  if (w->biases_offset <= w->scales_offset || w->biases_offset - w->scales_offset >= (1ull << 31))
+    return SMOE_ERR_UNSUPPORTED_SHAPE;
+  if (workspace_bytes < qmm_workspace(in_dim, w->group_size, n_tokens, nullptr, nullptr))
+    return SMOE_ERR_WORKSPACE_TOO_SMALL;
+  if (int rc = use_device(h)) return rc;
+  PfArgs a{};
+  qmm_workspace(in_dim, w->group_size, n_tokens, &a, (uint8_t*)workspace);
+  a.g.bits = w->bits;
+  a.g.hidden = out_dim;
+  a.g.inter = in_dim;
+  a.g.group = w->group_size;
+  a.g.w[2] = w->packed_offset;
+  a.g.s[2] = w->scales_offset;
+  a.g.b[2] = w->biases_offset;
+  a.experts = (const uint8_t*)w->base;
+  a.stride = 0;
+  a.n_tokens = n_tokens;
+  a.k = 1;
+  a.down = y;
+  int n_cu = 0;
+  if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, h->device) != hipSuccess || n_cu <= 0)
+    return SMOE_ERR_HIP;
+  return hip_status(launch_qmm(a, x, (uint32_t)n_cu, h->stream));
+}
+
 int smoe_argmax(smoe_handle* h, const float* v, uint32_t n, int32_t* out_index) {
   if (!h || !v || !n || !out_index) return SMOE_ERR_INVALID_ARG;
   if (!aligned(v, 0, 16)) return SMOE_ERR_MISALIGNED;

@@ -140,6 +140,15 @@ bool prefill_supported(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t
                        uint32_t n_tokens, uint32_t n_experts, uint32_t k);
 hipError_t launch_prefill(const PfArgs& a, uint32_t n_cu, hipStream_t st);
 
+// Dense quantized GEMM on the prefill GEMM (prefill.hip): workspace, limits
+// (in_dim multiple of 256 and <= 16384 / 128 groups, out_dim multiple of
+// 256) and launch. PfArgs fields used: g (hidden = out_dim, inter = in_dim,
+// w/s/b[2] = the weight offsets from `experts`), experts, stride = 0,
+// n_tokens, the workspace fields of qmm_workspace, and down = y.
+uint64_t qmm_workspace(uint32_t in_dim, uint32_t group, uint32_t n_tokens, PfArgs* a, uint8_t* base);
+bool qmm_supported(uint32_t in_dim, uint32_t out_dim, uint32_t group, uint32_t bits, uint32_t n_tokens);
+hipError_t launch_qmm(const PfArgs& a, const float* x, uint32_t n_cu, hipStream_t st);
+
 // All launchers return hipSuccess or the launch error; `*unsupported`
 // is set when no kernel instance exists for the shape.
 hipError_t launch_qmv(const QView& w, const float* x, float* y, uint32_t out_dim, uint32_t in_dim,

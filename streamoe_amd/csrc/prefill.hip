@@ -783,4 +783,92 @@ hipError_t launch_prefill(const PfArgs& a, uint32_t n_cu, hipStream_t st) {
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Dense quantized GEMM (affine_qmm_t, metal/lib.rs:684-734 QmmCall):
+// y[n, N] = x[n, K] . dequant(W)[N, K]^T, run as the down-GEMM instance of
+// k_pf_mm over one weight matrix: the "items" are 32-token row blocks of
+// expert 0 at stride 0, A = x split into bf16 hi + lo in the MFMA order.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_qmm_prep(const float* x, uint32_t n, uint32_t K, uint32_t G,
+                                                  uint16_t* hi, uint16_t* lo, float* sums, uint32_t* items,
+                                                  uint32_t* n_items) {
+  __shared__ float part8[kPfMaxGroupsK * 128 / 8];
+  const uint32_t r = blockIdx.x;
+  for (uint32_t k0 = threadIdx.x * 8; k0 < K; k0 += blockDim.x * 8) {
+    float f[8];
+    const f32x4* p = reinterpret_cast<const f32x4*>(x + (size_t)r * K + k0);
+    const f32x4 u = p[0], v = p[1];
+    f[0] = u.x, f[1] = u.y, f[2] = u.z, f[3] = u.w, f[4] = v.x, f[5] = v.y, f[6] = v.z, f[7] = v.w;
+    u32x4 h, l;
+    split_f32(f, h, l);
+    *reinterpret_cast<u32x4*>(hi + (size_t)r * K + k0) = h;
+    *reinterpret_cast<u32x4*>(lo + (size_t)r * K + k0) = l;
+    const uint32_t hv[4] = {h.x, h.y, h.z, h.w}, lv[4] = {l.x, l.y, l.z, l.w};
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      s += __uint_as_float(hv[i] << 16) + __uint_as_float(hv[i] & 0xFFFF0000u) + __uint_as_float(lv[i] << 16) +
+           __uint_as_float(lv[i] & 0xFFFF0000u);
+    part8[k0 / 8] = s;
+  }
+  __syncthreads();
+  const uint32_t ng = K / G, per = G / 8;
+  for (uint32_t g = threadIdx.x; g < ng; g += blockDim.x) {
+    float s = 0.f;
+    for (uint32_t j = 0; j < per; ++j) s += part8[g * per + j];
+    sums[(size_t)r * ng + g] = s;
+  }
+  if (r == 0) {
+    const uint32_t nb = (n + kPfMC - 1) / kPfMC;
+    for (uint32_t i = threadIdx.x; i < nb; i += blockDim.x) {
+      items[2 * i] = 0;
+      items[2 * i + 1] = (i * kPfMC) | (min(kPfMC, n - i * kPfMC) << 16);
+    }
+    if (threadIdx.x == 0) *n_items = nb;
+  }
+}
+
+uint64_t qmm_workspace(uint32_t in_dim, uint32_t group, uint32_t n_tokens, PfArgs* a, uint8_t* base) {
+  const uint64_t n = n_tokens, nb = (n + kPfMC - 1) / kPfMC;
+  uint64_t off = 0;
+  auto take = [&](uint64_t bytes) {
+    const uint64_t o = off;
+    off += al256(bytes);
+    return base ? base + o : nullptr;
+  };
+  uint8_t* p_items = take(nb * 2 * 4);
+  uint8_t* p_nitems = take(4);
+  uint8_t* p_sums = take(n * (in_dim / group) * 4);
+  uint8_t* p_hi = take(n * in_dim * 2);
+  uint8_t* p_lo = take(n * in_dim * 2);
+  if (a) {
+    a->items = reinterpret_cast<uint32_t*>(p_items);
+    a->n_items = reinterpret_cast<uint32_t*>(p_nitems);
+    a->asum = reinterpret_cast<float*>(p_sums);
+    a->act_hi = reinterpret_cast<uint16_t*>(p_hi);
+    a->act_lo = reinterpret_cast<uint16_t*>(p_lo);
+    a->max_items = (uint32_t)nb;
+  }
+  return off;
+}
+
+bool qmm_supported(uint32_t in_dim, uint32_t out_dim, uint32_t group, uint32_t bits, uint32_t n_tokens) {
+  if (bits != 4 && bits != 3) return false;
+  if (group != 32 && group != 64 && group != 128) return false;
+  if (in_dim % kPfKC || out_dim % 256 || in_dim / group > kPfMaxGroupsK || in_dim / 8 > kPfMaxGroupsK * 128 / 8)
+    return false;
+  return n_tokens >= 1 && n_tokens <= 0xFFFFu - kPfMC;
+}
+
+hipError_t launch_qmm(const PfArgs& a, const float* x, uint32_t n_cu, hipStream_t st) {
+  hipLaunchKernelGGL(k_qmm_prep, dim3(a.n_tokens), dim3(256), 0, st, x, a.n_tokens, a.g.inter, a.g.group,
+                     a.act_hi, a.act_lo, a.asum, a.items, a.n_items);
+  const uint32_t units = a.max_items * (a.g.hidden / 256), G = a.g.group;
+  if (a.g.bits == 4)
+    return G == 32 ? launch_mm<4, 32, 1, true>(a, units, n_cu, st)
+                   : G == 64 ? launch_mm<4, 64, 1, true>(a, units, n_cu, st) : launch_mm<4, 128, 1, true>(a, units, n_cu, st);
+  return G == 32 ? launch_mm<3, 32, 1, true>(a, units, n_cu, st)
+                 : G == 64 ? launch_mm<3, 64, 1, true>(a, units, n_cu, st) : launch_mm<3, 128, 1, true>(a, units, n_cu, st);
+}
+
 }  // namespace smoe
