@@ -53,7 +53,9 @@ __global__ __launch_bounds__(256) void k_qmv(const uint8_t* __restrict__ codes,
   constexpr int CB = chunk_bytes<BITS>();
   constexpr uint32_t ROW_BYTES = CPR * CB;
   const int lane = threadIdx.x & 63;
-  const uint32_t wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  // Wave-uniform (the compiler cannot tell from threadIdx.x): keeps the step
+  // loop and the row bases scalar.
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
   const int lrow = lane / L, lch = lane % L;
   const uint32_t gpr = CPR * kChunk / group;  // groups per row
   const uint32_t cpg_shift = __builtin_ctz(group / kChunk);
@@ -70,10 +72,14 @@ __global__ __launch_bounds__(256) void k_qmv(const uint8_t* __restrict__ codes,
   constexpr uint32_t STEP_ROWS = RPP * U;
   const uint32_t n_steps = (rows + STEP_ROWS - 1) / STEP_ROWS;
   Raw<BITS> cur[U][CPL];
-  float cs[U][CPL], cb[U][CPL];
+  // bf16 scales and biases stay raw (one per 32-bit register, so the
+  // compiler does not pack pairs) until the step is computed: widening them
+  // where they are loaded would make the wave wait for the next step's
+  // loads before computing the current one.
+  uint32_t cs[U][CPL], cb[U][CPL];
 
-  auto issue = [&](uint32_t step, Raw<BITS>(&raw)[U][CPL], float(&sv)[U][CPL],
-                   float(&bv)[U][CPL]) {
+  auto issue = [&](uint32_t step, Raw<BITS>(&raw)[U][CPL], uint32_t(&sv)[U][CPL],
+                   uint32_t(&bv)[U][CPL]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       uint32_t row = step * STEP_ROWS + u * RPP + lrow;
@@ -83,40 +89,46 @@ __global__ __launch_bounds__(256) void k_qmv(const uint8_t* __restrict__ codes,
         const uint32_t c = lch + L * i;
         raw[u][i] = load_raw<BITS>(codes + (size_t)row * ROW_BYTES + c * CB);
         const size_t gi = (size_t)row * gpr + (c >> cpg_shift);
-        sv[u][i] = bf16f(scales[gi]);
-        bv[u][i] = bf16f(biases[gi]);
+        sv[u][i] = scales[gi];
+        bv[u][i] = biases[gi];
       }
     }
   };
 
-  uint32_t step = wave;
-  if (step >= n_steps) return;
-  issue(step, cur, cs, cb);
-  while (true) {
-    const uint32_t next = step + n_waves;
-    Raw<BITS> nxt[U][CPL];
-    float ns[U][CPL], nb[U][CPL];
-    const bool more = next < n_steps;
-    if (more) issue(next, nxt, ns, nb);
+  auto compute = [&](uint32_t step, const Raw<BITS>(&raw)[U][CPL], const uint32_t(&sv)[U][CPL],
+                     const uint32_t(&bv)[U][CPL]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       float part = 0.f;
 #pragma unroll
-      for (int i = 0; i < CPL; ++i) part += chunk_dot_i<BITS>(cur[u][i], xl[i], cs[u][i], cb[u][i]);
+      for (int i = 0; i < CPL; ++i)
+        part += chunk_dot_i<BITS>(raw[u][i], xl[i], __uint_as_float(sv[u][i] << 16),
+                                  __uint_as_float(bv[u][i] << 16));
       const float sum = group_sum<L>(part);
       const uint32_t row = step * STEP_ROWS + u * RPP + lrow;
       if (lch == 0 && row < rows) y[row] = sum;
     }
-    if (!more) break;
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int i = 0; i < CPL; ++i) {
-        cur[u][i] = nxt[u][i];
-        cs[u][i] = ns[u][i];
-        cb[u][i] = nb[u][i];
-      }
-    step = next;
+  };
+
+  // Ping-pong between two register sets (no copies between them, which
+  // would make the compiler wait for the loads at the copy): the loads of
+  // step s + n_waves are in flight while step s is computed. The loop runs
+  // an even number of steps with every issue unconditional: a step past the
+  // end loads the last row again (an L2 hit) and stores nothing, and a
+  // branch around the loads would merge the two paths' wait counts into a
+  // wait for the new loads before the computation.
+  const uint32_t step0 = wave;
+  if (step0 >= n_steps) return;
+  const uint32_t my_steps = (n_steps - step0 + n_waves - 1) / n_waves;
+  Raw<BITS> rb[U][CPL];
+  uint32_t sb[U][CPL], bb[U][CPL];
+  issue(step0, cur, cs, cb);
+  for (uint32_t i = 0; i < my_steps; i += 2) {
+    const uint32_t s0 = step0 + i * n_waves, s1 = s0 + n_waves, s2 = s1 + n_waves;
+    issue(s1, rb, sb, bb);
+    compute(s0, cur, cs, cb);
+    issue(s2, cur, cs, cb);
+    compute(s1, rb, sb, bb);
   }
 }
 
