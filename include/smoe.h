@@ -146,6 +146,14 @@ int smoe_argmax(smoe_handle* h, const float* v, uint32_t n, int32_t* out_index);
  * the reference CPU path forms (crates/streammoe/src/riir/backend/cpu/
  * cpu_matvec.rs:164-165). Verification entry point: the decode kernels
  * use the same code-unpacking routine and never materialise w. */
+/* smoe_qmv and smoe_argmax of its output in one pass (the LM head with
+ * the greedy pick, io/gpu_lm_head.rs:130-193): y as smoe_qmv computes it,
+ * *out_index = the first index of max(y) as smoe_argmax gives it, from
+ * per-wave partials of the matvec itself (y is not read back). Uses the
+ * handle's scratch (allocated by smoe_create). */
+int smoe_qmv_argmax(smoe_handle* h, const smoe_qweights* w, const float* x, float* y, uint32_t out_dim,
+                    uint32_t in_dim, int32_t* out_index);
+
 /* Device workspace bytes smoe_qmm needs (0 for zero sizes). */
 uint64_t smoe_qmm_workspace_size(uint32_t in_dim, uint32_t group, uint32_t n_tokens);
 

@@ -160,6 +160,11 @@ class Kernels:
         wc = w.c()
         return _lib.smoe_qmv(self.h, C.byref(wc), _ptr(x), _ptr(y), out_dim, in_dim)
 
+    def qmv_argmax(self, w: QuantWeights, x, y, out_dim, in_dim, out):
+        """qmv with the argmax of y fused (LM head + greedy pick)."""
+        wc = w.c()
+        return _lib.smoe_qmv_argmax(self.h, C.byref(wc), _ptr(x), _ptr(y), out_dim, in_dim, _ptr(out))
+
     def qmm_workspace_size(self, in_dim, group, n_tokens):
         return _lib.smoe_qmm_workspace_size(in_dim, group, n_tokens)
 

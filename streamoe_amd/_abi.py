@@ -106,6 +106,7 @@ PROTOTYPES = {
     "smoe_sync": (_I, [_P]),
     "smoe_set_option": (_I, [_P, _I, C.c_int64]),
     "smoe_qmv": (_I, [_P, C.POINTER(QWeights), _P, _P, _U32, _U32]),
+    "smoe_qmv_argmax": (_I, [_P, C.POINTER(QWeights), _P, _P, _U32, _U32, _P]),
     "smoe_qmm_workspace_size": (_U64, [_U32, _U32, _U32]),
     "smoe_qmm": (_I, [_P, C.POINTER(QWeights), _P, _P, _U32, _U32, _U32, _P, _U64]),
     "smoe_argmax": (_I, [_P, _P, _U32, _P]),

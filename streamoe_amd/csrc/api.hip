@@ -58,7 +58,7 @@ int reserve(smoe_handle* h, uint32_t H, uint32_t I, uint32_t E) {
   const size_t xl_b = al(T * (size_t)H / 32 * 32 * sizeof(uint32_t));
   const size_t tr_b = al((size_t)H * 8), tl_b = al(((size_t)E + 1) * 8);
   const size_t ta_b = al((size_t)kMaxSlotsHost * I * 8), tro_b = al(32 * 8);
-  const size_t arg_b = 2 * 256 * sizeof(uint32_t);
+  const size_t arg_b = 2 * (size_t)kQmvMaxWaves * sizeof(uint32_t);
   const size_t total = act_b + log_b + 256 + tab_b + xl_b + arg_b + tr_b + tl_b + ta_b + tro_b + 256;
   void* mem = nullptr;
   if (hipSetDevice(h->device) != hipSuccess) return SMOE_ERR_HIP;
@@ -81,7 +81,7 @@ int reserve(smoe_handle* h, uint32_t H, uint32_t I, uint32_t E) {
   h->xl = (uint32_t*)q;
   q += xl_b;
   h->arg_v = (float*)q;
-  h->arg_i = (uint32_t*)(q + 256 * sizeof(float));
+  h->arg_i = (uint32_t*)(q + kQmvMaxWaves * sizeof(float));
   q += arg_b;
   h->tag_resid = (uint64_t*)q;
   q += tr_b;
@@ -272,6 +272,20 @@ int smoe_qmm(smoe_handle* h, const smoe_qweights* w, const float* x, float* y, u
   if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, h->device) != hipSuccess || n_cu <= 0)
     return SMOE_ERR_HIP;
   return hip_status(launch_qmm(a, x, (uint32_t)n_cu, h->stream));
+}
+
+int smoe_qmv_argmax(smoe_handle* h, const smoe_qweights* w, const float* x, float* y, uint32_t out_dim,
+                    uint32_t in_dim, int32_t* out_index) {
+  if (!h || !x || !y || !out_dim || !out_index) return SMOE_ERR_INVALID_ARG;
+  QView v;
+  if (int rc = qview(w, in_dim, &v)) return rc;
+  if (!aligned(x, 0, 16)) return SMOE_ERR_MISALIGNED;
+  if (!h->arg_v) return SMOE_ERR_SCRATCH_TOO_SMALL;
+  if (int rc = use_device(h)) return rc;
+  bool unsupported = false;
+  const hipError_t e = launch_qmv(v, x, y, out_dim, in_dim, h->stream, &unsupported, h->arg_v, h->arg_i, out_index);
+  if (unsupported) return SMOE_ERR_UNSUPPORTED_SHAPE;
+  return hip_status(e);
 }
 
 int smoe_argmax(smoe_handle* h, const float* v, uint32_t n, int32_t* out_index) {

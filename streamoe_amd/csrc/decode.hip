@@ -41,12 +41,22 @@ BlobGeom blob_geom(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t bit
 // L = min(CPR, 64) lanes, each owning CPL = CPR / L chunks; a wave covers
 // RPP = 64 / L rows per pass and U passes per step.
 // ---------------------------------------------------------------------------
+// (value, index) merge that keeps the larger value and, on ties, the lower
+// index (the sequential scan's first maximum); NaN never wins.
+__device__ __forceinline__ void argmax_merge(float& bv, uint32_t& bi, float v, uint32_t i) {
+  if (v > bv || (v == bv && i < bi)) {
+    bv = v;
+    bi = i;
+  }
+}
+
 template <int BITS, int CPR, int U>
 __global__ __launch_bounds__(256) void k_qmv(const uint8_t* __restrict__ codes,
                                              const uint16_t* __restrict__ scales,
                                              const uint16_t* __restrict__ biases,
                                              const float* __restrict__ x, float* __restrict__ y,
-                                             uint32_t rows, uint32_t group, uint32_t n_waves) {
+                                             uint32_t rows, uint32_t group, uint32_t n_waves,
+                                             float* __restrict__ arg_v, uint32_t* __restrict__ arg_i) {
   constexpr int L = CPR < kWave ? CPR : kWave;
   constexpr int CPL = CPR / L;
   constexpr int RPP = kWave / L;
@@ -95,6 +105,8 @@ __global__ __launch_bounds__(256) void k_qmv(const uint8_t* __restrict__ codes,
     }
   };
 
+  float best = -INFINITY;
+  uint32_t best_i = 0xFFFFFFFFu;
   auto compute = [&](uint32_t step, const Raw<BITS>(&raw)[U][CPL], const uint32_t(&sv)[U][CPL],
                      const uint32_t(&bv)[U][CPL]) {
 #pragma unroll
@@ -106,7 +118,26 @@ __global__ __launch_bounds__(256) void k_qmv(const uint8_t* __restrict__ codes,
                                   __uint_as_float(bv[u][i] << 16));
       const float sum = group_sum<L>(part);
       const uint32_t row = step * STEP_ROWS + u * RPP + lrow;
-      if (lch == 0 && row < rows) y[row] = sum;
+      if (lch == 0 && row < rows) {
+        y[row] = sum;
+        argmax_merge(best, best_i, sum, row);
+      }
+    }
+  };
+  // Fused argmax: the wave's (max, first index) over its rows, written to
+  // arg_v / arg_i[wave] when they are given (lanes other than each row's
+  // lane 0 keep -inf).
+  auto publish = [&]() {
+    if (!arg_v) return;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ob = __shfl_xor(best, o, 64);
+      const uint32_t oi = __shfl_xor(best_i, o, 64);
+      argmax_merge(best, best_i, ob, oi);
+    }
+    if (lane == 0) {
+      arg_v[wave] = best;
+      arg_i[wave] = best_i;
     }
   };
 
@@ -118,7 +149,10 @@ __global__ __launch_bounds__(256) void k_qmv(const uint8_t* __restrict__ codes,
   // branch around the loads would merge the two paths' wait counts into a
   // wait for the new loads before the computation.
   const uint32_t step0 = wave;
-  if (step0 >= n_steps) return;
+  if (step0 >= n_steps) {
+    publish();
+    return;
+  }
   const uint32_t my_steps = (n_steps - step0 + n_waves - 1) / n_waves;
   Raw<BITS> rb[U][CPL];
   uint32_t sb[U][CPL], bb[U][CPL];
@@ -130,49 +164,58 @@ __global__ __launch_bounds__(256) void k_qmv(const uint8_t* __restrict__ codes,
     issue(s2, cur, cs, cb);
     compute(s1, rb, sb, bb);
   }
+  publish();
 }
+
+__global__ __launch_bounds__(256) void k_argmax_final(const float* __restrict__ pv,
+                                                      const uint32_t* __restrict__ pi, uint32_t n,
+                                                      int32_t* __restrict__ out);
 
 template <int BITS, int CPR>
 static hipError_t qmv_inst(const QView& w, const float* x, float* y, uint32_t rows,
-                           hipStream_t st) {
+                           hipStream_t st, float* arg_v, uint32_t* arg_i, int32_t* arg_out) {
   constexpr int L = CPR < kWave ? CPR : kWave;
   constexpr int RPP = kWave / L;
-  // Rows in flight per wave and step: HBM latency (~2 us under load) times
-  // the target bandwidth needs ~12 MB in flight over the 2048 waves.
-  constexpr int U = RPP == 1 ? 8 : 4;
+  // Rows per wave and step, and the persistent grid: 4 rows x 3072 waves
+  // (12 per CU on 256 CUs, the occupancy this instance's registers allow)
+  // measured best on MI355X for the 151,936 x 2048 LM head (45.6 us per
+  // token with the argmax, against 48-69 us for 8 or 16 rows and 1024-5120
+  // waves).
+  constexpr int U = 4;
   const uint32_t n_steps = (rows + RPP * U - 1) / (RPP * U);
-  // Persistent grid: up to 8 waves per CU on 256 CUs.
-  uint32_t n_waves = n_steps < 2048u ? n_steps : 2048u;
+  uint32_t n_waves = n_steps < kQmvMaxWaves ? n_steps : kQmvMaxWaves;
   const uint32_t wpb = 4;
   const uint32_t blocks = (n_waves + wpb - 1) / wpb;
   n_waves = blocks * wpb;
   hipLaunchKernelGGL((k_qmv<BITS, CPR, U>), dim3(blocks), dim3(wpb * 64), 0, st, w.codes, w.scales,
-                     w.biases, x, y, rows, w.group, n_waves);
+                     w.biases, x, y, rows, w.group, n_waves, arg_out ? arg_v : nullptr, arg_i);
+  if (arg_out) hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(256), 0, st, arg_v, arg_i, n_waves, arg_out);
   return hipGetLastError();
 }
 
 template <int BITS>
 static hipError_t qmv_bits(const QView& w, const float* x, float* y, uint32_t rows,
-                           uint32_t in_dim, hipStream_t st, bool* unsupported) {
+                           uint32_t in_dim, hipStream_t st, bool* unsupported, float* av, uint32_t* ai,
+                           int32_t* ao) {
   switch (in_dim / kChunk) {
-    case 16: return qmv_inst<BITS, 16>(w, x, y, rows, st);
-    case 32: return qmv_inst<BITS, 32>(w, x, y, rows, st);
-    case 64: return qmv_inst<BITS, 64>(w, x, y, rows, st);
-    case 128: return qmv_inst<BITS, 128>(w, x, y, rows, st);
-    case 256: return qmv_inst<BITS, 256>(w, x, y, rows, st);
+    case 16: return qmv_inst<BITS, 16>(w, x, y, rows, st, av, ai, ao);
+    case 32: return qmv_inst<BITS, 32>(w, x, y, rows, st, av, ai, ao);
+    case 64: return qmv_inst<BITS, 64>(w, x, y, rows, st, av, ai, ao);
+    case 128: return qmv_inst<BITS, 128>(w, x, y, rows, st, av, ai, ao);
+    case 256: return qmv_inst<BITS, 256>(w, x, y, rows, st, av, ai, ao);
     default: *unsupported = true; return hipSuccess;
   }
 }
 
 hipError_t launch_qmv(const QView& w, const float* x, float* y, uint32_t out_dim, uint32_t in_dim,
-                      hipStream_t st, bool* unsupported) {
+                      hipStream_t st, bool* unsupported, float* arg_v, uint32_t* arg_i, int32_t* arg_out) {
   *unsupported = false;
   if (in_dim % kChunk) {
     *unsupported = true;
     return hipSuccess;
   }
-  return w.bits == 4 ? qmv_bits<4>(w, x, y, out_dim, in_dim, st, unsupported)
-                     : qmv_bits<3>(w, x, y, out_dim, in_dim, st, unsupported);
+  return w.bits == 4 ? qmv_bits<4>(w, x, y, out_dim, in_dim, st, unsupported, arg_v, arg_i, arg_out)
+                     : qmv_bits<3>(w, x, y, out_dim, in_dim, st, unsupported, arg_v, arg_i, arg_out);
 }
 
 // ---------------------------------------------------------------------------
@@ -217,13 +260,6 @@ hipError_t launch_dequant(const QView& w, uint32_t in_dim, uint32_t row0, uint32
 // index, so the result is the first maximal index, as a sequential scan.
 // ---------------------------------------------------------------------------
 constexpr uint32_t kArgBlocks = 256;
-
-__device__ __forceinline__ void argmax_merge(float& bv, uint32_t& bi, float v, uint32_t i) {
-  if (v > bv || (v == bv && i < bi)) {
-    bv = v;
-    bi = i;
-  }
-}
 
 // Block-wide (value, index) reduction; result valid in thread 0.
 __device__ __forceinline__ void argmax_block(float& best, uint32_t& bi) {
@@ -270,10 +306,11 @@ __global__ __launch_bounds__(256) void k_argmax_part(const float* __restrict__ v
 }
 
 __global__ __launch_bounds__(256) void k_argmax_final(const float* __restrict__ pv,
-                                                      const uint32_t* __restrict__ pi,
+                                                      const uint32_t* __restrict__ pi, uint32_t n,
                                                       int32_t* __restrict__ out) {
-  float best = pv[threadIdx.x];
-  uint32_t bi = pi[threadIdx.x];
+  float best = -INFINITY;
+  uint32_t bi = 0xFFFFFFFFu;
+  for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) argmax_merge(best, bi, pv[i], pi[i]);
   argmax_block(best, bi);
   if (threadIdx.x == 0) *out = (int32_t)bi;
 }
@@ -281,7 +318,7 @@ __global__ __launch_bounds__(256) void k_argmax_final(const float* __restrict__ 
 hipError_t launch_argmax(const float* v, uint32_t n, int32_t* out, float* part_v, uint32_t* part_i,
                          hipStream_t st) {
   hipLaunchKernelGGL(k_argmax_part, dim3(kArgBlocks), dim3(256), 0, st, v, n, part_v, part_i);
-  hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(kArgBlocks), 0, st, part_v, part_i, out);
+  hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(256), 0, st, part_v, part_i, kArgBlocks, out);
   return hipGetLastError();
 }
 

@@ -151,8 +151,12 @@ hipError_t launch_qmm(const PfArgs& a, const float* x, uint32_t n_cu, hipStream_
 
 // All launchers return hipSuccess or the launch error; `*unsupported`
 // is set when no kernel instance exists for the shape.
+// With arg_out, also the argmax of y (first index on ties): per-wave
+// partials in arg_v / arg_i (kQmvMaxWaves entries) and one merge launch.
+constexpr uint32_t kQmvMaxWaves = 3072;
 hipError_t launch_qmv(const QView& w, const float* x, float* y, uint32_t out_dim, uint32_t in_dim,
-                      hipStream_t st, bool* unsupported);
+                      hipStream_t st, bool* unsupported, float* arg_v = nullptr, uint32_t* arg_i = nullptr,
+                      int32_t* arg_out = nullptr);
 hipError_t launch_dequant(const QView& w, uint32_t in_dim, uint32_t row0, uint32_t n_rows,
                           float* out, hipStream_t st);
 // Argmax (first index on ties); part_v / part_i: 256-entry scratch.

@@ -131,6 +131,36 @@ def test_argmax_first_index_on_ties(kernels, n):
     assert int(host(out)[0]) == int(np.argmax(v)) == oracle.argmax(v)
 
 
+@pytest.mark.parametrize("out_dim,in_dim,bits", [(151936, 2048, 4), (50000, 1024, 4), (9000, 2048, 3),
+                                                 (77, 512, 4)])
+def test_qmv_argmax_fused(kernels, out_dim, in_dim, bits):
+    """smoe_qmv_argmax: y identical to smoe_qmv, index = numpy's first
+    maximal index of y, with the maximum planted on several rows (identical
+    weight rows give bit-identical sums) across waves and steps."""
+    torch = _torch()
+    rng = np.random.default_rng(out_dim + bits)
+    codes, s, b = gen_quant_matrix(rng, out_dim, in_dim, 64, bits)
+    # Plant one large row and copy it over later rows: equal maxima.
+    s[:, :] = s // 2  # keep ordinary rows small
+    big = out_dim // 3
+    s[big] = (np.abs(s[big].view(np.int16)).astype(np.uint16) | 0x3F00).astype(np.uint16) & 0x7FFF
+    for r in sorted({big, out_dim - 1, (2 * out_dim) // 3, min(out_dim - 1, big + 5)}):
+        codes[r], s[r], b[r] = codes[big], s[big], b[big]
+    x = np.abs(rng.standard_normal(in_dim)).astype(np.float32)
+    w = qweights(codes, s, b, 64, bits)
+    y1 = torch.empty(out_dim, dtype=torch.float32, device="cuda")
+    y2 = torch.empty(out_dim, dtype=torch.float32, device="cuda")
+    i1 = torch.empty(1, dtype=torch.int32, device="cuda")
+    i2 = torch.empty(1, dtype=torch.int32, device="cuda")
+    assert kernels.qmv(w, dev(x), y1, out_dim, in_dim) == 0
+    assert kernels.argmax(y1, out_dim, i1) == 0
+    assert kernels.qmv_argmax(w, dev(x), y2, out_dim, in_dim, i2) == 0
+    got = host(y2)
+    assert np.array_equal(got.view(np.uint32), host(y1).view(np.uint32))
+    assert int(host(i2)[0]) == int(host(i1)[0]) == int(np.argmax(got))
+    assert int(np.argmax(got)) == min(big, out_dim - 1)
+
+
 # --- dequant (bit-exact) --------------------------------------------------------------
 
 @pytest.mark.parametrize("bits,group", [(4, 64), (3, 64), (4, 32), (3, 128)])
