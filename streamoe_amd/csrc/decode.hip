@@ -167,9 +167,9 @@ __global__ __launch_bounds__(256) void k_qmv(const uint8_t* __restrict__ codes,
   publish();
 }
 
-__global__ __launch_bounds__(256) void k_argmax_final(const float* __restrict__ pv,
-                                                      const uint32_t* __restrict__ pi, uint32_t n,
-                                                      int32_t* __restrict__ out);
+__global__ __launch_bounds__(1024) void k_argmax_final(const float* __restrict__ pv,
+                                                       const uint32_t* __restrict__ pi, uint32_t n,
+                                                       int32_t* __restrict__ out);
 
 template <int BITS, int CPR>
 static hipError_t qmv_inst(const QView& w, const float* x, float* y, uint32_t rows,
@@ -189,7 +189,7 @@ static hipError_t qmv_inst(const QView& w, const float* x, float* y, uint32_t ro
   n_waves = blocks * wpb;
   hipLaunchKernelGGL((k_qmv<BITS, CPR, U>), dim3(blocks), dim3(wpb * 64), 0, st, w.codes, w.scales,
                      w.biases, x, y, rows, w.group, n_waves, arg_out ? arg_v : nullptr, arg_i);
-  if (arg_out) hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(256), 0, st, arg_v, arg_i, n_waves, arg_out);
+  if (arg_out) hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(1024), 0, st, arg_v, arg_i, n_waves, arg_out);
   return hipGetLastError();
 }
 
@@ -305,12 +305,25 @@ __global__ __launch_bounds__(256) void k_argmax_part(const float* __restrict__ v
   }
 }
 
-__global__ __launch_bounds__(256) void k_argmax_final(const float* __restrict__ pv,
-                                                      const uint32_t* __restrict__ pi, uint32_t n,
-                                                      int32_t* __restrict__ out) {
+__global__ __launch_bounds__(1024) void k_argmax_final(const float* __restrict__ pv,
+                                                       const uint32_t* __restrict__ pi, uint32_t n,
+                                                       int32_t* __restrict__ out) {
   float best = -INFINITY;
   uint32_t bi = 0xFFFFFFFFu;
-  for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) argmax_merge(best, bi, pv[i], pi[i]);
+  // Four partials per thread per round, loaded before they are merged (the
+  // merges form a dependency chain; the loads must not).
+  for (uint32_t i0 = threadIdx.x; i0 < n; i0 += 4 * blockDim.x) {
+    float v[4];
+    uint32_t ix[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t i = min(i0 + j * blockDim.x, n - 1);
+      v[j] = pv[i];
+      ix[j] = pi[i];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) argmax_merge(best, bi, v[j], ix[j]);
+  }
   argmax_block(best, bi);
   if (threadIdx.x == 0) *out = (int32_t)bi;
 }
