@@ -51,7 +51,9 @@ int reserve(smoe_handle* h, uint32_t H, uint32_t I, uint32_t E) {
   // act, logits, route table and limbs hold kMaxDecodeTokens tokens
   // (multi-token decode); single-token paths use token 0's.
   const size_t T = kMaxDecodeTokens;
-  const size_t lstride = al(((size_t)E + 1) * sizeof(float)) / sizeof(float);
+  // Per token at least E + 1 logits and 256 (the decode kernels read the
+  // logits as 64 lanes x 4).
+  const size_t lstride = al(((size_t)(E + 1 > 256 ? E + 1 : 256)) * sizeof(float)) / sizeof(float);
   const size_t act_b = al(T * kMaxSlotsHost * I * sizeof(float));
   const size_t log_b = al(T * lstride * sizeof(float));
   const size_t tab_b = al(T * sizeof(FfnTable));

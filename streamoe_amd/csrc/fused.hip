@@ -12,23 +12,23 @@
 // of waiting for (RMSNorm's sum of squares, softmax and the top-k set) it
 // computes in every wave.
 //
-// With T <= 4 tokens (multi-token decode), K_A reads each router and
-// shared-expert row once for all T tokens, and K_B / K_C run one grid
-// slice per token (grid dimension y).
+// With T <= 4 tokens (multi-token decode), K_A reads each router row once
+// for all T tokens, and K_B / K_C run one grid slice per token (grid
+// dimension y).
 //
-//   K_A  k_fa_route    one wave per router row / per SR shared-expert rows:
-//                      x = RMSNorm(r) * w (or the given input), then
-//                      logits[e] = W_e . x (row E: shared gate), or
-//                      act[k, i] = silu(gate_i . x) * (up_i . x) for the
-//                      shared expert. Wave 0 stores x for K_B as integer
-//                      limbs (common.h, chunk_dot_i).
-//   K_B  k_fa_gateup   one wave per RW rows of one routed slot: softmax and
-//                      the top-k set of the logits (every wave), then
-//                      act[s, i] = silu(gate_i . x) * (up_i . x) for expert
-//                      set[s]. Block 0 also publishes the route table
-//                      (expert blobs and renormalised weights, the shared
-//                      gate score) and, when asked, the reference's exact
-//                      slot order.
+//   K_A  k_fa_route    one wave per router row: x = RMSNorm(r) * w (or the
+//                      given input), logits[e] = W_e . x (row E: shared
+//                      gate); one more wave per token stores x as integer
+//                      limbs for K_B (common.h, chunk_dot_i).
+//   K_B  k_fa_gateup   one wave per RW rows of one routed slot: the slot's
+//                      expert from the logits (every wave), then
+//                      act[s, i] = silu(gate_i . x) * (up_i . x); one wave
+//                      per RW rows of the shared expert (slot k), which
+//                      needs no routing and so streams its rows while the
+//                      routed waves select; one wave that publishes the
+//                      route table (expert blobs and renormalised weights,
+//                      the shared gate score) and, when asked, the
+//                      reference's exact slot order.
 //   K_C  k_fa_down     one block per kFaR hidden rows, one lane per (slot,
 //                      chunk of 32 activations): every slot's down rows,
 //                      combined in table order moe = fma(out_s, w_s, moe)
@@ -47,16 +47,12 @@ namespace smoe {
 constexpr uint32_t kFaH = 2048;              // hidden size of this path (64 lanes x 32)
 // Work per wave / block (build-time tunables; the defaults are the measured
 // best on MI355X).
-#ifndef SMOE_FA_SR
-#define SMOE_FA_SR 2
-#endif
 #ifndef SMOE_FA_RW
 #define SMOE_FA_RW 4
 #endif
 #ifndef SMOE_FA_R
 #define SMOE_FA_R 4
 #endif
-constexpr int kFaSR = SMOE_FA_SR;            // shared-expert rows per K_A wave
 constexpr int kFaRW = SMOE_FA_RW;            // routed rows per K_B wave
 
 // Optional timestamps (100 MHz s_memrealtime) for latency analysis. They
@@ -113,11 +109,13 @@ __device__ __forceinline__ void fa_x_load(const FusedLayer& a, int lane, FaX& f)
 
 __device__ __forceinline__ void fa_x_finish(const FusedLayer& a, FaX& f) {
   if (a.x_in || !a.norm) return;
+  // Every rounding is written out (no contraction left to the compiler), so
+  // all instantiations (T = 1..4 tokens) compute x bit for bit alike.
   float ss = 0.f;
 #pragma unroll
-  for (int j = 0; j < kChunk; ++j) ss += f.x[j] * f.x[j];
+  for (int j = 0; j < kChunk; ++j) ss = __builtin_fmaf(f.x[j], f.x[j], ss);
   ss = readlane_f(group_sum_last<64>(ss), 63);
-  const float inv = 1.0f / sqrtf(ss / (float)kFaH + a.eps);
+  const float inv = 1.0f / sqrtf(__builtin_fmaf(ss, 1.0f / (float)kFaH, a.eps));
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t w4[4] = {f.w[i].x, f.w[i].y, f.w[i].z, f.w[i].w};
@@ -150,9 +148,9 @@ __device__ __forceinline__ FusedLayer token_view(const FusedLayer& a, uint32_t t
 }
 
 // ---------------------------------------------------------------------------
-// K_A: router logits (+ shared gate) and the shared expert's gate/up, for
-// T tokens: each wave reads its router / shared-expert rows once and
-// applies them to every token's x.
+// K_A: router logits (+ shared gate) for T tokens: each wave reads its
+// router row once and applies it to every token's x. The last T waves
+// write x of token t as integer limbs for K_B.
 // ---------------------------------------------------------------------------
 template <int T>
 __global__ __launch_bounds__(64) void k_fa_route(FusedLayer a) {
@@ -163,60 +161,25 @@ __global__ __launch_bounds__(64) void k_fa_route(FusedLayer a) {
   const uint32_t nrouter = a.E + (a.gate ? 1u : 0u);
   const uint32_t c = lane;  // this lane's chunk of the hidden vector
 
-  if (w < nrouter) {
-    const float* row = w < a.E ? a.router + (size_t)w * kFaH : a.gate;
-    f32x4 wr[kChunk / 4];
-    const f32x4* rp = reinterpret_cast<const f32x4*>(row + (size_t)c * kChunk);
-#pragma unroll
-    for (int i = 0; i < kChunk / 4; ++i) wr[i] = ld_stream(rp + i);
-    FaX f[T];
-#pragma unroll
-    for (int t = 0; t < T; ++t) fa_x_load(token_view(a, t), lane, f[t]);
-    __builtin_amdgcn_sched_barrier(0);
+  if (w >= nrouter) {
+    // Limb wave of token t.
+    const FusedLayer at = token_view(a, w - nrouter);
+    FaX f;
+    fa_x_load(at, lane, f);
     fa_stamp(a, clk, 3, true);
-#pragma unroll
-    for (int t = 0; t < T; ++t) {
-      const FusedLayer at = token_view(a, t);
-      fa_x_finish(at, f[t]);
-      const float(&x)[kChunk] = f[t].x;
-      if (w == (uint32_t)t) {
-        XLimbs xl;
-        make_limbs(x, xl);
-        store_limbs(at.xl + (size_t)c * kXLimbWords, xl);
-      }
-      float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-#pragma unroll
-      for (int i = 0; i < kChunk / 4; ++i) {
-        a0 = __builtin_fmaf(wr[i].x, x[4 * i + 0], a0);
-        a1 = __builtin_fmaf(wr[i].y, x[4 * i + 1], a1);
-        a2 = __builtin_fmaf(wr[i].z, x[4 * i + 2], a2);
-        a3 = __builtin_fmaf(wr[i].w, x[4 * i + 3], a3);
-      }
-      const float s = group_sum_last<64>((a0 + a1) + (a2 + a3));
-      if (lane == 63) at.logits[w] = s;
-    }
-    fa_stamp(a, clk, 4, false);
+    fa_x_finish(at, f);
+    XLimbs xl;
+    make_limbs(f.x, xl);
+    store_limbs(at.xl + (size_t)c * kXLimbWords, xl);
     fa_stamp(a, clk, 5, true);
     fa_flush(a, clk, 0);
     return;
   }
-
-  // Shared expert rows [r0, r0 + kFaSR) of gate and up (4-bit).
-  const BlobGeom& g = a.sgeom;
-  const uint32_t r0 = (w - nrouter) * kFaSR;
-  const uint32_t gpr = kFaH / g.group;
-  const uint32_t cps = __builtin_ctz(g.group / kChunk);
-  constexpr uint32_t RB = kFaH / 2;  // 4-bit row bytes
-  Raw<4> rg[kFaSR], ru[kFaSR];
-  uint16_t sg[kFaSR], bg[kFaSR], su[kFaSR], bu[kFaSR];
+  const float* row = w < a.E ? a.router + (size_t)w * kFaH : a.gate;
+  f32x4 wr[kChunk / 4];
+  const f32x4* rp = reinterpret_cast<const f32x4*>(row + (size_t)c * kChunk);
 #pragma unroll
-  for (int p = 0; p < kFaSR; ++p) {
-    const uint32_t row = r0 + p;
-    rg[p] = load_raw4(a.shared + g.w[0] + (size_t)row * RB + c * 16);
-    ru[p] = load_raw4(a.shared + g.w[1] + (size_t)row * RB + c * 16);
-    load_sb(a.shared, g.s[0], g.b[0], row, gpr, cps, c, sg[p], bg[p]);
-    load_sb(a.shared, g.s[1], g.b[1], row, gpr, cps, c, su[p], bu[p]);
-  }
+  for (int i = 0; i < kChunk / 4; ++i) wr[i] = ld_stream(rp + i);
   FaX f[T];
 #pragma unroll
   for (int t = 0; t < T; ++t) fa_x_load(token_view(a, t), lane, f[t]);
@@ -227,64 +190,50 @@ __global__ __launch_bounds__(64) void k_fa_route(FusedLayer a) {
     const FusedLayer at = token_view(a, t);
     fa_x_finish(at, f[t]);
     const float(&x)[kChunk] = f[t].x;
-    const float xs = xsum(x);
-    float* act = at.act + (size_t)a.k * g.inter;
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
 #pragma unroll
-    for (int p = 0; p < kFaSR; ++p) {
-      const float gs = group_sum_last<64>(chunk_dot<4>(rg[p], x, xs, bf16f(sg[p]), bf16f(bg[p])));
-      const float us = group_sum_last<64>(chunk_dot<4>(ru[p], x, xs, bf16f(su[p]), bf16f(bu[p])));
-      if (lane == 63) act[r0 + p] = silu_mul(gs, us);
+    for (int i = 0; i < kChunk / 4; ++i) {
+      a0 = __builtin_fmaf(wr[i].x, x[4 * i + 0], a0);
+      a1 = __builtin_fmaf(wr[i].y, x[4 * i + 1], a1);
+      a2 = __builtin_fmaf(wr[i].z, x[4 * i + 2], a2);
+      a3 = __builtin_fmaf(wr[i].w, x[4 * i + 3], a3);
     }
+    const float s = group_sum_last<64>((a0 + a1) + (a2 + a3));
+    if (lane == 63) at.logits[w] = s;
   }
+  fa_stamp(a, clk, 4, false);
   fa_stamp(a, clk, 5, true);
   fa_flush(a, clk, 0);
 }
 
-// ---------------------------------------------------------------------------
-// K_B: top-k set in every wave, routed gate/up; block 0 publishes the table.
-// ---------------------------------------------------------------------------
-template <int BITS, int P>
-__global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a_all) {
-  const FusedLayer a = token_view(a_all, blockIdx.y);
+// The E logits, P per lane (lane l holds [l*P, l*P + P)); positions >= E
+// read as -inf. The logits buffer holds at least 64 * P floats per token.
+template <int P>
+__device__ __forceinline__ void load_logits(const float* logits, uint32_t E, int lane, float (&v)[P]) {
+  if constexpr (P == 4) {
+    const f32x4 q = *reinterpret_cast<const f32x4*>(logits + lane * 4);
+    v[0] = q.x;
+    v[1] = q.y;
+    v[2] = q.z;
+    v[3] = q.w;
+  } else {
+#pragma unroll
+    for (int e = 0; e < P; ++e) v[e] = logits[lane * P + e];
+  }
+#pragma unroll
+  for (int e = 0; e < P; ++e)
+    if ((uint32_t)(lane * P + e) >= E) v[e] = -INFINITY;
+}
+
+// gate and up rows [r0, r0 + kFaRW) of one expert blob against x (limbs),
+// SwiGLU, stored to act[r0 ..]. All loads are issued before any arithmetic.
+template <int BITS>
+__device__ __forceinline__ void gateup_rows(const FusedLayer& a, FaClock& clk, const uint8_t* blob,
+                                            const BlobGeom& g, uint32_t r0, int lane,
+                                            const XLimbs& xl, float* act) {
   constexpr int CB = chunk_bytes<BITS>();
   constexpr uint32_t RB = kFaH / kChunk * CB;  // row bytes
-  __shared__ int32_t sid[kMaxK];
-  __shared__ float sval[kMaxK];
-  __shared__ float sprob[64 * P];
-  FaClock clk;
-  fa_stamp(a, clk, 0, false);
-  const int lane = threadIdx.x;
-  const BlobGeom& g = a.routed;
-  const uint32_t I = g.inter, E = a.E, k = a.k;
-  const uint32_t tiles = I / kFaRW;
-  const uint32_t slot = blockIdx.x / tiles;
-  const uint32_t r0 = (blockIdx.x % tiles) * kFaRW;
   const uint32_t c = lane;
-
-  float v[P];
-#pragma unroll
-  for (int e = 0; e < P; ++e) {
-    const uint32_t j = lane * P + e;
-    v[e] = j < E ? a.logits[j] : -INFINITY;
-  }
-  fa_stamp(a, clk, 1, true);
-  XLimbs xl;
-  load_limbs(a.xl + (size_t)c * kXLimbWords, xl);
-
-  // The top-k set from the logits (topk_set_logits: equal to the k largest
-  // softmax probabilities whenever the reference's running-minimum scan,
-  // moe_router.rs:83-124, sees no tie at the boundary). Otherwise the
-  // softmax (moe_router.rs:52-72) and the exact scan.
-  const bool is_set = topk_set_logits<P>(v, E, k, lane, sid);
-  if (!is_set) {
-    wave_softmax<P>(v, E, lane);
-    exact_topk<P>(v, k, lane, sid, sval);
-  }
-  __syncthreads();
-  const int32_t id = sid[slot];
-  const uint8_t* blob = a.experts + (uint64_t)id * a.stride;
-  fa_stamp(a, clk, 2, false);
-
   const uint32_t gpr = kFaH / g.group;
   const uint32_t cps = __builtin_ctz(g.group / kChunk);
   Raw<BITS> rg[kFaRW], ru[kFaRW];
@@ -299,11 +248,72 @@ __global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a_all) {
   }
   __builtin_amdgcn_sched_barrier(0);
   fa_stamp(a, clk, 3, true);
+#pragma unroll
+  for (int p = 0; p < kFaRW; ++p) {
+    const float gs = group_sum_last<64>(chunk_dot_i<BITS>(rg[p], xl, bf16f(sg[p]), bf16f(bg[p])));
+    const float us = group_sum_last<64>(chunk_dot_i<BITS>(ru[p], xl, bf16f(su[p]), bf16f(bu[p])));
+    if (lane == 63) act[r0 + p] = silu_mul(gs, us);
+  }
+}
 
-  if (blockIdx.x == 0) {
-    // Route table in the order the act slots use, weights renormalised in
-    // that order (normalize_weights, moe_router.rs:130-141).
-    if (is_set) wave_softmax<P>(v, E, lane);
+// ---------------------------------------------------------------------------
+// K_B: routed gate/up, shared-expert gate/up and the route table.
+//
+// Blocks [0, k * tiles): one routed slot's kFaRW rows. The wave takes its
+// slot's expert from the logits (topk_slot_logits: ascending index order;
+// the exact scan when the set is ambiguous), then its rows.
+// Blocks [k * tiles, k * tiles + tiles): the shared expert's rows (slot k),
+// with no routing dependency, so their loads overlap the top-k of the
+// routed waves.
+// Last block: the route table (expert blobs, renormalised weights, shared
+// gate score) in the order the act slots use, and, when asked, the
+// reference's exact slot order.
+// ---------------------------------------------------------------------------
+template <int BITS, int P>
+__global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a_all) {
+  const FusedLayer a = token_view(a_all, blockIdx.y);
+  __shared__ int32_t sid[kMaxK];
+  __shared__ float sval[kMaxK];
+  FaClock clk;
+  fa_stamp(a, clk, 0, false);
+  const int lane = threadIdx.x;
+  const uint32_t I = a.routed.inter, E = a.E, k = a.k;
+  const uint32_t tiles = I / kFaRW;
+  const uint32_t nrouted = k * tiles;
+  const uint32_t nshared = a.shared ? tiles : 0u;
+
+  if (blockIdx.x < nrouted) {
+    const uint32_t slot = blockIdx.x / tiles;
+    const uint32_t r0 = (blockIdx.x % tiles) * kFaRW;
+    float v[P];
+    load_logits<P>(a.logits, E, lane, v);
+    XLimbs xl;
+    load_limbs(a.xl + (size_t)lane * kXLimbWords, xl);
+    fa_stamp(a, clk, 1, true);
+    int32_t id;
+    if (!topk_slot_logits<P>(v, E, k, slot, lane, id)) {
+      wave_softmax<P>(v, E, lane);
+      exact_topk<P>(v, k, lane, sid, sval);
+      __syncthreads();
+      id = sid[slot];
+    }
+    fa_stamp(a, clk, 2, false);
+    gateup_rows<BITS>(a, clk, a.experts + (uint64_t)id * a.stride, a.routed, r0, lane, xl,
+                      a.act + (size_t)slot * I);
+  } else if (blockIdx.x < nrouted + nshared) {
+    const uint32_t r0 = (blockIdx.x - nrouted) * kFaRW;
+    XLimbs xl;
+    load_limbs(a.xl + (size_t)lane * kXLimbWords, xl);
+    gateup_rows<4>(a, clk, a.shared, a.sgeom, r0, lane, xl, a.act + (size_t)k * I);
+  } else {
+    // Route table (normalize_weights, moe_router.rs:130-141).
+    __shared__ float sprob[64 * P];
+    float v[P];
+    load_logits<P>(a.logits, E, lane, v);
+    const float gate_score = a.gate ? a.logits[E] : __builtin_nanf("");
+    const bool is_set = topk_set_logits<P>(v, E, k, lane, sid);
+    wave_softmax<P>(v, E, lane);
+    if (!is_set) exact_topk<P>(v, k, lane, sid, sval);
 #pragma unroll
     for (int e = 0; e < P; ++e) sprob[lane * P + e] = v[e];
     __syncthreads();
@@ -326,7 +336,7 @@ __global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a_all) {
         a.table->blob[k] = a.shared;
         a.table->weight[k] = 1.0f;
       }
-      a.table->shared_gate = a.gate ? a.logits[E] : __builtin_nanf("");
+      a.table->shared_gate = gate_score;
     }
     if (a.idx_out || a.w_out) {
       // The reference's exact slot order for the caller.
@@ -350,14 +360,6 @@ __global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a_all) {
         if (a.w_out) a.w_out[lane] = wt;
       }
     }
-  }
-
-  float* act = a.act + (size_t)slot * I;
-#pragma unroll
-  for (int p = 0; p < kFaRW; ++p) {
-    const float gs = group_sum_last<64>(chunk_dot_i<BITS>(rg[p], xl, bf16f(sg[p]), bf16f(bg[p])));
-    const float us = group_sum_last<64>(chunk_dot_i<BITS>(ru[p], xl, bf16f(su[p]), bf16f(bu[p])));
-    if (lane == 63) act[r0 + p] = silu_mul(gs, us);
   }
   fa_stamp(a, clk, 4, false);
   fa_stamp(a, clk, 5, true);
@@ -508,14 +510,14 @@ static void launch_down_fa(const FusedLayer& a, hipStream_t st) {
 hipError_t launch_fused_layer(const FusedLayer& a, hipStream_t st) {
   if (a.n_tokens < 1 || a.n_tokens > kMaxDecodeTokens || (a.trace && a.n_tokens != 1)) return hipErrorInvalidValue;
   const uint32_t I = a.routed.inter;
-  const uint32_t ka = a.E + (a.gate ? 1u : 0u) + (a.shared ? I / kFaSR : 0u);
+  const uint32_t ka = a.E + (a.gate ? 1u : 0u) + a.n_tokens;
   switch (a.n_tokens) {
     case 1: hipLaunchKernelGGL(k_fa_route<1>, dim3(ka), dim3(64), 0, st, a); break;
     case 2: hipLaunchKernelGGL(k_fa_route<2>, dim3(ka), dim3(64), 0, st, a); break;
     case 3: hipLaunchKernelGGL(k_fa_route<3>, dim3(ka), dim3(64), 0, st, a); break;
     default: hipLaunchKernelGGL(k_fa_route<4>, dim3(ka), dim3(64), 0, st, a); break;
   }
-  const uint32_t kb = a.k * (I / kFaRW);
+  const uint32_t kb = (a.k + (a.shared ? 1u : 0u)) * (I / kFaRW) + 1u;
   if (a.routed.bits == 4)
     launch_gateup_fa<4>(a, kb, st);
   else

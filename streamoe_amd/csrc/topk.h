@@ -184,8 +184,9 @@ __device__ bool topk_set(const float (&v)[P], uint32_t n, uint32_t k, int lane,
 // e = exp(l - max), every probability is e * (1 / sum) rounded once, and a
 // positive common factor with one rounding preserves a strict order when
 // the two e values are more than 2^-20 apart relatively. So the set is
-// taken from the logits' orderable integer keys with k + 1 rounds of a
-// wave-wide unsigned max (one DPP op per level), and accepted only when
+// taken from the logits' orderable integer keys with at most k + 1 rounds
+// of a wave-wide unsigned max (one DPP op per level; every key equal to
+// the round's maximum leaves in that round), and accepted only when
 // exp(l_k - max) > exp(l_{k+1} - max) * (1 + 2^-20); ties, NaN or an
 // infinite max return false and the caller takes the exact scan. Returns
 // the set in ascending index order in set_ids[0..k).
@@ -210,10 +211,42 @@ __device__ __forceinline__ float from_orderable(uint32_t k) {
   return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
 }
 
+// Unsigned max over the whole wave, valid in every lane: a butterfly over
+// each 16-lane row (DPP row rotations by 8, 4, 2, 1), then across row
+// pairs and wave halves with the gfx950 permlane swaps. No scalar register
+// is involved, so a chain of these never waits on the scalar unit.
+__device__ __forceinline__ uint32_t wave_umax_all(uint32_t v) {
+  v = max(v, dpp_umax_src<0x128>(v));
+  v = max(v, dpp_umax_src<0x124>(v));
+  v = max(v, dpp_umax_src<0x122>(v));
+  v = max(v, dpp_umax_src<0x121>(v));
+  const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = max(r[0], r[1]);
+  const auto h = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return max(h[0], h[1]);
+}
+
+// The k-th largest key of the logits (key = orderable float, 0 for
+// positions >= n) when the top-k set is unambiguous, as described above.
+// Rounds take the wave maximum of the lanes' heads and pop every head equal
+// to it, so equal keys leave together; kth is the key at which the count of
+// taken keys first reaches k, next the key at which it first exceeds k
+// (equal exactly when a tie straddles the boundary). Returns false for
+// NaN, an infinite maximum, a tie at the boundary or a margin below
+// 2^-20; the caller then takes the exact scan.
+// Population count of a wave mask on the vector unit, so the round loop
+// below never waits for the scalar unit (v_bcnt_u32_b32: bits of the
+// scalar operand plus the vector addend).
+__device__ __forceinline__ uint32_t vbcnt64(uint64_t m, uint32_t add) {
+  uint32_t c;
+  asm volatile("v_bcnt_u32_b32 %0, %1, %2" : "=v"(c) : "s"((uint32_t)m), "v"(add));
+  asm volatile("v_bcnt_u32_b32 %0, %1, %2" : "=v"(c) : "s"((uint32_t)(m >> 32)), "v"(c));
+  return c;
+}
+
 template <int P>
-__device__ bool topk_set_logits(const float (&l)[P], uint32_t n, uint32_t k, int lane,
-                                int32_t* set_ids) {
-  uint32_t key[P];
+__device__ __forceinline__ bool topk_threshold(const float (&l)[P], uint32_t n, uint32_t k, int lane,
+                                               uint32_t (&key)[P], uint32_t& kth_out) {
   bool bad = false;
 #pragma unroll
   for (int e = 0; e < P; ++e) {
@@ -233,33 +266,80 @@ __device__ bool topk_set_logits(const float (&l)[P], uint32_t n, uint32_t k, int
       sk[b - 1] = hi;
       sk[b] = lo;
     }
-  uint32_t top = 0, kth = 0, next = 0;
+  // Round r: m = wave maximum of the heads; every head equal to m pops.
+  // Lane r records m and the running count of popped keys; the boundary
+  // rounds are found after the loop, so a round is vector work only.
+  uint32_t rec_m = 0, rec_c = 0, cnt = 0;
   for (uint32_t r = 0; r <= k; ++r) {
-    const uint32_t m = (uint32_t)__builtin_amdgcn_readlane((int)wave_umax_last(sk[0]), 63);
-    if (r == 0) top = m;
-    if (r == k) {
-      next = m;
-      break;
-    }
-    kth = m;
-    const uint64_t ball = __ballot(sk[0] == m);
-    const int first = __builtin_amdgcn_readfirstlane(__ffsll((unsigned long long)ball) - 1);
-    if (lane == first) {
+    const uint32_t m = wave_umax_all(sk[0]);
+    const bool pop = sk[0] == m;
+    const uint64_t pm = __ballot(pop);
 #pragma unroll
-      for (int e = 0; e < P - 1; ++e) sk[e] = sk[e + 1];
-      sk[P - 1] = 0;
+    for (int e = 0; e < P - 1; ++e) sk[e] = pop ? sk[e + 1] : sk[e];
+    sk[P - 1] = pop ? 0u : sk[P - 1];
+    cnt += (uint32_t)__popcll(pm);
+    if ((uint32_t)lane == r) {
+      rec_m = m;
+      rec_c = cnt;
     }
   }
+  // kth: the maximum of the round whose count first reaches k; next: of
+  // the round whose count first exceeds k (the same round when a tie
+  // straddles the boundary).
+  const bool live = (uint32_t)lane <= k;
+  const uint64_t reach = __ballot(live && rec_c >= k), over = __ballot(live && rec_c > k);
+  if (!reach || !over) return false;
+  const uint32_t top = (uint32_t)__builtin_amdgcn_readfirstlane((int)rec_m);
+  const uint32_t kth = (uint32_t)__builtin_amdgcn_readlane((int)rec_m, (int)__builtin_ctzll(reach));
+  const uint32_t next = (uint32_t)__builtin_amdgcn_readlane((int)rec_m, (int)__builtin_ctzll(over));
   const float fm = from_orderable(top), fk = from_orderable(kth), fn = from_orderable(next);
   if (!(fm < INFINITY) || !(fk > fn)) return false;
   if (!(expf(fk - fm) > expf(fn - fm) * (1.0f + 0x1p-20f))) return false;
-  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  kth_out = kth;
+  return true;
+}
+
+// The top-k set in ascending index order in set_ids[0..k) (LDS), or false
+// (see topk_threshold).
+template <int P>
+__device__ bool topk_set_logits(const float (&l)[P], uint32_t n, uint32_t k, int lane,
+                                int32_t* set_ids) {
+  uint32_t key[P], kth;
+  if (!topk_threshold<P>(l, n, k, lane, key, kth)) return false;
   uint32_t at = 0;
 #pragma unroll
-  for (int e = 0; e < P; ++e) at += __popcll(__ballot(key[e] >= kth) & below);
+  for (int e = 0; e < P; ++e) {
+    const uint64_t b = __ballot(key[e] >= kth);
+    at = __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, at));
+  }
 #pragma unroll
   for (int e = 0; e < P; ++e)
     if (key[e] >= kth) set_ids[at++] = (int32_t)(lane * P + e);
+  return true;
+}
+
+// Element `slot` (0 <= slot < k) of the top-k set in ascending index order,
+// in every lane, or false (see topk_threshold). No LDS, no barrier.
+template <int P>
+__device__ bool topk_slot_logits(const float (&l)[P], uint32_t n, uint32_t k, uint32_t slot,
+                                 int lane, int32_t& id) {
+  uint32_t key[P], kth;
+  if (!topk_threshold<P>(l, n, k, lane, key, kth)) return false;
+  uint32_t rank = 0;  // set members in lower lanes
+#pragma unroll
+  for (int e = 0; e < P; ++e) {
+    const uint64_t b = __ballot(key[e] >= kth);
+    rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, rank));
+  }
+  int32_t hit = -1;
+#pragma unroll
+  for (int e = 0; e < P; ++e) {
+    const bool in = key[e] >= kth;
+    if (in && rank == slot) hit = (int32_t)(lane * P + e);
+    rank += in ? 1u : 0u;
+  }
+  const uint64_t hb = __ballot(hit >= 0);
+  id = __builtin_amdgcn_readlane(hit, (int)__builtin_ctzll(hb));
   return true;
 }
 
