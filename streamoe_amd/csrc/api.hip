@@ -698,6 +698,7 @@ int smoe_moe_prefill(smoe_handle* h, const smoe_expert_shape* shape, const void*
   a.x_bf16 = x_is_bf16 != 0;
   a.out = out_sum;
   a.err = h->err;
+  a.trace = h->trace;
   int n_cu = 0;
   if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, h->device) != hipSuccess || n_cu <= 0)
     return SMOE_ERR_HIP;

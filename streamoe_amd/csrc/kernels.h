@@ -130,6 +130,7 @@ struct PfArgs {
   uint16_t* act_hi;        // [n*k, inter] SwiGLU output, bf16 hi, MFMA order
   uint16_t* act_lo;        // [n*k, inter] bf16 lo
   float* down;             // [n*k, hidden]
+  uint64_t* trace;         // k_pf_route timestamps (8 words), or null (diagnostics)
 };
 
 // Workspace bytes for these sizes; with `a` and `base`, also points a's

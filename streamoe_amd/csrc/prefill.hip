@@ -5,7 +5,8 @@
 // combine), whose CPU statement is build_expert_buckets (moe_router.rs:
 // 374-436) + moe_permute_fuse_cpu (moe_cpu.rs:282-339).
 //
-//   k_pf_route    one block: bucket the n*k assignments by expert (stable in
+//   k_pf_route    one block, one thread per token: bucket the n*k
+//                 assignments by expert (stable in
 //                 token order), per-token entry positions in ascending
 //                 expert order, and a work list of (expert, <= kPfMC
 //                 entries) items, so a hot expert is spread over many waves.
@@ -43,82 +44,184 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 constexpr uint32_t kPfMC = 32;   // entries per work item (two 16-row MFMA tiles)
 constexpr uint32_t kPfKC = 256;  // inputs per pipelined K chunk
+constexpr uint32_t kPfStage = 8192;  // entries k_pf_route stages in LDS
 
 // ---------------------------------------------------------------------------
 // Bucketing (one block of 1024 threads).
 // ---------------------------------------------------------------------------
-// Exclusive scan of v over threads [0, n) (n <= 1024) through LDS.
-__device__ uint32_t block_exscan(uint32_t v, uint32_t n, uint32_t* tmp, uint32_t* total) {
-  const uint32_t t = threadIdx.x;
-  if (t < n) tmp[t] = v;
-  __syncthreads();
-  for (uint32_t o = 1; o < n; o <<= 1) {
-    uint32_t add = 0;
-    if (t < n && t >= o) add = tmp[t - o];
-    __syncthreads();
-    if (t < n) tmp[t] += add;
-    __syncthreads();
-  }
-  const uint32_t incl = t < n ? tmp[t] : 0;
-  *total = tmp[n - 1];
-  __syncthreads();
-  return incl - (t < n ? v : 0);
-}
+#define PF_STAMP(i)                                                         \
+  do {                                                                      \
+    if (a.trace && threadIdx.x == 0) a.trace[i] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
 
 __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
-  // col[e][c]: bit (t & 31) set when token 32c + (t & 31) chose expert e.
+  PF_STAMP(0);
+  // col[e][c]: bit (t & 31) set when token 32c + (t & 31) chose expert e;
+  // pre[e][c]: tokens before 32c that chose e.
   __shared__ uint32_t col[kPfMaxExperts * (kPfMaxTokens / 32)];
-  __shared__ uint32_t tmp[1024];
+  __shared__ uint16_t pre[kPfMaxExperts * (kPfMaxTokens / 32)];
   __shared__ uint32_t offs[kPfMaxExperts];
+  __shared__ int32_t st_tok[kPfStage];
+  __shared__ float st_w[kPfStage];
   const uint32_t tid = threadIdx.x, n = a.n_tokens, k = a.k, E = a.E;
-  const uint32_t cw = (n + 31) / 32, total = n * k;
+  const uint32_t cw = (n + 31) / 32;
   for (uint32_t i = tid; i < E * cw; i += blockDim.x) col[i] = 0;
+  // Thread t owns token t: its k experts and weights stay in registers
+  // (one read of the routing input), validated here.
+  int32_t ex[kPfMaxK];
+  float wt[kPfMaxK];
+  const bool tok = tid < n;
+  bool bad = false;
+#pragma unroll
+  for (uint32_t s = 0; s < kPfMaxK; ++s) {
+    ex[s] = -1;
+    wt[s] = 0.f;
+  }
+  const bool vec = (k & 3) == 0 && ((reinterpret_cast<uintptr_t>(a.idx) | reinterpret_cast<uintptr_t>(a.w)) & 15) == 0;
+  if (tok && vec) {
+    // A token's k ids / weights are contiguous and 16-byte aligned: read
+    // them four at a time.
+    const int4* ip = reinterpret_cast<const int4*>(a.idx + tid * k);
+    const float4* wp = reinterpret_cast<const float4*>(a.w + tid * k);
+#pragma unroll
+    for (uint32_t q = 0; q < kPfMaxK / 4; ++q)
+      if (4 * q < k) {
+        const int4 iv = ip[q];
+        const float4 wv = wp[q];
+        ex[4 * q] = iv.x, ex[4 * q + 1] = iv.y, ex[4 * q + 2] = iv.z, ex[4 * q + 3] = iv.w;
+        wt[4 * q] = wv.x, wt[4 * q + 1] = wv.y, wt[4 * q + 2] = wv.z, wt[4 * q + 3] = wv.w;
+      }
+  } else if (tok) {
+#pragma unroll
+    for (uint32_t s = 0; s < kPfMaxK; ++s)
+      if (s < k) {
+        ex[s] = a.idx[tid * k + s];
+        wt[s] = a.w[tid * k + s];
+      }
+  }
+#pragma unroll
+  for (uint32_t s = 0; s < kPfMaxK; ++s)
+    if (tok && s < k) bad |= ex[s] < 0 || (uint32_t)ex[s] >= E;
   __syncthreads();
-  for (uint32_t i = tid; i < total; i += blockDim.x) {
-    const int32_t e = a.idx[i];
-    if (e < 0 || (uint32_t)e >= E) {
-      *a.err = 2u;
-      continue;
+  PF_STAMP(1);
+  if (tok) {
+#pragma unroll
+    for (uint32_t s = 0; s < kPfMaxK; ++s) {
+      if (s >= k || ex[s] < 0 || (uint32_t)ex[s] >= E) continue;
+      const uint32_t old = atomicOr(&col[ex[s] * cw + (tid >> 5)], 1u << (tid & 31));
+      bad |= (old >> (tid & 31)) & 1u;  // an expert twice in one token
     }
-    const uint32_t t = i / k;
-    const uint32_t old = atomicOr(&col[e * cw + (t >> 5)], 1u << (t & 31));
-    if (old & (1u << (t & 31))) *a.err = 2u;  // an expert twice in one token
+    if (bad) *a.err = 2u;
   }
   __syncthreads();
-  uint32_t cnt = 0;
-  if (tid < E)
-    for (uint32_t c = 0; c < cw; ++c) cnt += __popc(col[tid * cw + c]);
-  uint32_t n_entries;
-  const uint32_t off = block_exscan(cnt, E, tmp, &n_entries);
-  const uint32_t nch = (cnt + kPfMC - 1) / kPfMC;
-  uint32_t n_items;
-  const uint32_t ibase = block_exscan(nch, E, tmp, &n_items);
-  if (tid == 0) *a.n_items = n_items;
+  PF_STAMP(2);
+  __shared__ uint32_t scnt[kPfMaxExperts], snch[kPfMaxExperts], sibase[kPfMaxExperts];
   if (tid < E) {
-    offs[tid] = off;
+    uint32_t cnt = 0;
+    for (uint32_t c = 0; c < cw; ++c) {
+      pre[tid * cw + c] = (uint16_t)cnt;
+      cnt += __popc(col[tid * cw + c]);
+    }
+    scnt[tid] = cnt;
+    snch[tid] = (cnt + kPfMC - 1) / kPfMC;
+  }
+  __syncthreads();
+  PF_STAMP(3);
+  // Wave 0: exclusive scans of the counts (entry offsets) and of the items
+  // per expert (work-list bases), 4 experts per lane and a DPP scan.
+  if (tid < 64) {
+    uint32_t c4[4], n4[4], ca = 0, na = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t e = tid * 4 + q;
+      c4[q] = e < E ? scnt[e] : 0u;
+      n4[q] = e < E ? snch[e] : 0u;
+      ca += c4[q];
+      na += n4[q];
+    }
+    uint32_t ci = ca, ni = na;  // inclusive scans over lanes
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t tc = __shfl_up(ci, o, 64), tn = __shfl_up(ni, o, 64);
+      if (tid >= o) {
+        ci += tc;
+        ni += tn;
+      }
+    }
+    uint32_t co = ci - ca, no = ni - na;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t e = tid * 4 + q;
+      if (e < E) {
+        offs[e] = co;
+        sibase[e] = no;
+      }
+      co += c4[q];
+      no += n4[q];
+    }
+    if (tid == 63) *a.n_items = ni;
+  }
+  __syncthreads();
+  PF_STAMP(4);
+  if (tid < E) {
+    const uint32_t cnt = scnt[tid], nch = snch[tid], off = offs[tid], ibase = sibase[tid];
     for (uint32_t c = 0; c < nch; ++c) {
       a.items[2 * (ibase + c)] = tid;
       a.items[2 * (ibase + c) + 1] = (off + c * kPfMC) | (min(kPfMC, cnt - c * kPfMC) << 16);
     }
   }
-  __syncthreads();
   // Every entry places itself: position = the expert's offset + the tokens
   // before t that chose the same expert; rank among t's experts in
-  // ascending expert order = how many of t's experts are smaller.
-  for (uint32_t i = tid; i < total; i += blockDim.x) {
-    const int32_t e = a.idx[i];
-    if (e < 0 || (uint32_t)e >= E) continue;
-    const uint32_t t = i / k;
-    const uint32_t* c = &col[e * cw];
-    uint32_t before = __popc(c[t >> 5] & ((1u << (t & 31)) - 1u));
-    for (uint32_t w = 0; w < (t >> 5); ++w) before += __popc(c[w]);
-    uint32_t r = 0;
-    for (uint32_t s = 0; s < k; ++s) r += (a.idx[t * k + s] < e) ? 1u : 0u;
-    const uint32_t pos = offs[e] + before;
-    a.ent_token[pos] = (int32_t)t;
-    a.ent_weight[pos] = a.w[i];
-    a.tok_pos[t * k + min(r, k - 1)] = (int32_t)pos;
+  // ascending expert order = how many of t's experts are smaller. Entries
+  // go through LDS (when they fit) so the global writes are coalesced.
+  const uint32_t total = n * k;
+  const bool staged = total <= kPfStage;
+  int32_t row[kPfMaxK];
+#pragma unroll
+  for (uint32_t s = 0; s < kPfMaxK; ++s) row[s] = 0;
+  if (tok) {
+#pragma unroll
+    for (uint32_t s = 0; s < kPfMaxK; ++s) {
+      const int32_t e = ex[s];
+      if (s >= k || e < 0 || (uint32_t)e >= E) continue;
+      const uint32_t ci = e * cw + (tid >> 5);
+      const uint32_t pos = offs[e] + pre[ci] + __popc(col[ci] & ((1u << (tid & 31)) - 1u));
+      uint32_t r = 0;
+#pragma unroll
+      for (uint32_t q = 0; q < kPfMaxK; ++q) r += (q < k && ex[q] < e) ? 1u : 0u;
+      if (staged) {
+        st_tok[pos] = (int32_t)tid;
+        st_w[pos] = wt[s];
+      } else {
+        a.ent_token[pos] = (int32_t)tid;
+        a.ent_weight[pos] = wt[s];
+      }
+#pragma unroll
+      for (uint32_t q = 0; q < kPfMaxK; ++q)
+        if (q == min(r, k - 1)) row[q] = (int32_t)pos;
+    }
+    if ((k & 3) == 0) {
+      int4* tp = reinterpret_cast<int4*>(a.tok_pos + tid * k);
+#pragma unroll
+      for (uint32_t q = 0; q < kPfMaxK / 4; ++q)
+        if (4 * q < k) tp[q] = make_int4(row[4 * q], row[4 * q + 1], row[4 * q + 2], row[4 * q + 3]);
+    } else {
+#pragma unroll
+      for (uint32_t q = 0; q < kPfMaxK; ++q)
+        if (q < k) a.tok_pos[tid * k + q] = row[q];
+    }
   }
+  if (staged) {
+    __syncthreads();
+    for (uint32_t i = tid; i < total; i += blockDim.x) {
+      a.ent_token[i] = st_tok[i];
+      a.ent_weight[i] = st_w[i];
+    }
+  }
+  PF_STAMP(5);
+  __syncthreads();
+  __builtin_amdgcn_s_waitcnt(0);
+  PF_STAMP(6);
 }
 
 // ---------------------------------------------------------------------------
