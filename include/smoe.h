@@ -70,7 +70,8 @@ typedef enum {
   SMOE_OPT_TRACE_BUFFER = 2  /* device uint64 buffer for in-kernel timestamps, or 0 =
                                 off. Persistent decode: per layer and block 8 words;
                                 three-kernel decode: per layer 3 * 4096 * 8 words
-                                (kernel, block, point). Diagnostics only. */
+                                (kernel, block, point); prefill: 8 words (phase
+                                ends of the bucketing kernel). Diagnostics only. */
 } smoe_option;
 
 typedef struct smoe_handle smoe_handle;
