@@ -196,6 +196,34 @@ __device__ __forceinline__ float group_sum_last(float v) {
   return v;
 }
 
+// Transposed reductions: several per-lane partial sums reduced at once, each
+// exchange halving the values per lane while every lane stays busy.
+// swap32_add(a, b): lanes 0-31 hold a's partial over lanes {l, l + 32},
+// lanes 32-63 hold b's (v_permlane32_swap exchanges a's upper half with b's
+// lower half).
+__device__ __forceinline__ float swap32_add(float a, float b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// swap16_add(a, b): 16-lane rows 0..3 hold a (rows 0+1), b (rows 0+1),
+// a (rows 2+3), b (rows 2+3) (v_permlane16_swap exchanges a's odd rows with
+// b's even rows).
+__device__ __forceinline__ float swap16_add(float a, float b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Sum over each 16-lane row, in every lane of the row (row rotations by
+// 8, 4, 2, 1).
+__device__ __forceinline__ float row_sum16_all(float v) {
+  v += dpp_f<0x128>(v, 0.f);
+  v += dpp_f<0x124>(v, 0.f);
+  v += dpp_f<0x122>(v, 0.f);
+  v += dpp_f<0x121>(v, 0.f);
+  return v;
+}
+
 // Max over the wave, valid in lane 63.
 __device__ __forceinline__ float wave_max_last(float v) {
   v = fmaxf(v, dpp_f<0x111>(v, -INFINITY));

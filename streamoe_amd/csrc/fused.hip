@@ -45,15 +45,14 @@
 namespace smoe {
 
 constexpr uint32_t kFaH = 2048;              // hidden size of this path (64 lanes x 32)
-// Work per wave / block (build-time tunables; the defaults are the measured
-// best on MI355X).
-#ifndef SMOE_FA_RW
-#define SMOE_FA_RW 4
-#endif
+// Work per wave / block. K_B waves take 4 gate/up row pairs (their sums
+// are reduced together, gateup_rows); the K_C row count is a build-time
+// tunable. Both are the measured best on MI355X (2 or 8 rows per K_B wave,
+// 2 or 8 rows per K_C block: 0.4-1.4 us per layer slower).
 #ifndef SMOE_FA_R
 #define SMOE_FA_R 4
 #endif
-constexpr int kFaRW = SMOE_FA_RW;            // routed rows per K_B wave
+constexpr int kFaRW = 4;                     // routed rows per K_B wave
 
 // Optional timestamps (100 MHz s_memrealtime) for latency analysis. They
 // stay in registers until fa_flush at the end of the kernel, so tracing adds
@@ -129,23 +128,30 @@ __device__ __forceinline__ void fa_x_finish(const FusedLayer& a, FaX& f) {
 }
 
 // Token t's view of a multi-token layer: the same arguments with every
-// per-token pointer moved to token t's rows.
+// per-token pointer moved to token t's rows. Branch-free (selects), so it
+// adds no branch level in front of the first loads.
 __device__ __forceinline__ FusedLayer token_view(const FusedLayer& a, uint32_t t) {
   FusedLayer b = a;
-  if (t == 0) return b;
   const size_t hs = (size_t)t * kFaH;
-  if (b.x_in) b.x_in += hs;
-  if (b.resid) b.resid += hs;
+  b.x_in = a.x_in ? a.x_in + hs : nullptr;
+  b.resid = a.resid ? a.resid + hs : nullptr;
   b.h_mid += hs;
   b.out += hs;
   b.logits += (size_t)t * a.lstride;
   b.act += (size_t)t * a.astride;
   b.xl += (size_t)t * a.xstride;
   b.table += t;
-  if (b.idx_out) b.idx_out += (size_t)t * a.k;
-  if (b.w_out) b.w_out += (size_t)t * a.k;
+  b.idx_out = a.idx_out ? a.idx_out + (size_t)t * a.k : nullptr;
+  b.w_out = a.w_out ? a.w_out + (size_t)t * a.k : nullptr;
   return b;
 }
+
+// Pins the listed kernel arguments in SGPRs at this point, so that all their
+// scalar loads go out as one batch before the first branch. Left to itself
+// the compiler loads arguments lazily, one dependent batch per branch level,
+// and every batch is a memory round trip: a kernel's argument block is not in
+// L2 when the kernel starts.
+#define FA_ARGS_IN_SGPRS(...) asm volatile("" ::__VA_ARGS__)
 
 // ---------------------------------------------------------------------------
 // K_A: router logits (+ shared gate) for T tokens: each wave reads its
@@ -154,6 +160,8 @@ __device__ __forceinline__ FusedLayer token_view(const FusedLayer& a, uint32_t t
 // ---------------------------------------------------------------------------
 template <int T>
 __global__ __launch_bounds__(64) void k_fa_route(FusedLayer a) {
+  FA_ARGS_IN_SGPRS("s"(a.x_in), "s"(a.resid), "s"(a.norm), "s"(a.eps), "s"(a.router), "s"(a.gate),
+                   "s"(a.E), "s"(a.logits), "s"(a.xl), "s"(a.trace), "s"(a.lstride), "s"(a.xstride));
   FaClock clk;
   fa_stamp(a, clk, 0, false);
   const int lane = threadIdx.x;
@@ -248,12 +256,20 @@ __device__ __forceinline__ void gateup_rows(const FusedLayer& a, FaClock& clk, c
   }
   __builtin_amdgcn_sched_barrier(0);
   fa_stamp(a, clk, 3, true);
+  float gp[kFaRW], up[kFaRW];
 #pragma unroll
   for (int p = 0; p < kFaRW; ++p) {
-    const float gs = group_sum_last<64>(chunk_dot_i<BITS>(rg[p], xl, bf16f(sg[p]), bf16f(bg[p])));
-    const float us = group_sum_last<64>(chunk_dot_i<BITS>(ru[p], xl, bf16f(su[p]), bf16f(bu[p])));
-    if (lane == 63) act[r0 + p] = silu_mul(gs, us);
+    gp[p] = chunk_dot_i<BITS>(rg[p], xl, bf16f(sg[p]), bf16f(bg[p]));
+    up[p] = chunk_dot_i<BITS>(ru[p], xl, bf16f(su[p]), bf16f(bu[p]));
   }
+  // The eight rows' lane partials are summed together: after the two swaps
+  // the 16-lane rows hold gate/up rows 0, 2, 1, 3, and every lane of a row
+  // ends with its totals, so one SwiGLU serves all four outputs.
+  const float gs = row_sum16_all(swap16_add(swap32_add(gp[0], gp[1]), swap32_add(gp[2], gp[3])));
+  const float us = row_sum16_all(swap16_add(swap32_add(up[0], up[1]), swap32_add(up[2], up[3])));
+  const float v = silu_mul(gs, us);
+  const int row16 = lane >> 4;
+  if ((lane & 15) == 0) act[r0 + ((row16 >> 1) | ((row16 & 1) << 1))] = v;
 }
 
 // ---------------------------------------------------------------------------
@@ -269,8 +285,18 @@ __device__ __forceinline__ void gateup_rows(const FusedLayer& a, FaClock& clk, c
 // gate score) in the order the act slots use, and, when asked, the
 // reference's exact slot order.
 // ---------------------------------------------------------------------------
-template <int BITS, int P>
+template <int BITS, int P, int KC>
 __global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a_all) {
+  FA_ARGS_IN_SGPRS("s"(a_all.logits), "s"(a_all.xl), "s"(a_all.act), "s"(a_all.table), "s"(a_all.E),
+                   "s"(a_all.k), "s"(a_all.normalize), "s"(a_all.experts), "s"(a_all.stride),
+                   "s"(a_all.shared), "s"(a_all.gate), "s"(a_all.idx_out), "s"(a_all.w_out),
+                   "s"(a_all.trace), "s"(a_all.lstride), "s"(a_all.astride), "s"(a_all.xstride),
+                   "s"(a_all.routed.inter), "s"(a_all.routed.group), "s"(a_all.routed.w[0]),
+                   "s"(a_all.routed.w[1]), "s"(a_all.routed.s[0]), "s"(a_all.routed.s[1]),
+                   "s"(a_all.routed.b[0]), "s"(a_all.routed.b[1]));
+  FA_ARGS_IN_SGPRS("s"(a_all.sgeom.group), "s"(a_all.sgeom.w[0]), "s"(a_all.sgeom.w[1]),
+                   "s"(a_all.sgeom.s[0]), "s"(a_all.sgeom.s[1]), "s"(a_all.sgeom.b[0]),
+                   "s"(a_all.sgeom.b[1]));
   const FusedLayer a = token_view(a_all, blockIdx.y);
   __shared__ int32_t sid[kMaxK];
   __shared__ float sval[kMaxK];
@@ -291,7 +317,7 @@ __global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a_all) {
     load_limbs(a.xl + (size_t)lane * kXLimbWords, xl);
     fa_stamp(a, clk, 1, true);
     int32_t id;
-    if (!topk_slot_logits<P>(v, E, k, slot, lane, id)) {
+    if (!topk_slot_logits<P, KC>(v, E, k, slot, lane, id)) {
       wave_softmax<P>(v, E, lane);
       exact_topk<P>(v, k, lane, sid, sval);
       __syncthreads();
@@ -311,7 +337,7 @@ __global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a_all) {
     float v[P];
     load_logits<P>(a.logits, E, lane, v);
     const float gate_score = a.gate ? a.logits[E] : __builtin_nanf("");
-    const bool is_set = topk_set_logits<P>(v, E, k, lane, sid);
+    const bool is_set = topk_set_logits<P, KC>(v, E, k, lane, sid);
     wave_softmax<P>(v, E, lane);
     if (!is_set) exact_topk<P>(v, k, lane, sid, sval);
 #pragma unroll
@@ -419,6 +445,11 @@ constexpr int fa_down_threads() {
 
 template <int BITS, int LI>
 __global__ __launch_bounds__(fa_down_threads<LI>()) void k_fa_down(FusedLayer a_all) {
+  FA_ARGS_IN_SGPRS("s"(a_all.act), "s"(a_all.table), "s"(a_all.h_mid), "s"(a_all.out), "s"(a_all.trace),
+                   "s"(a_all.k), "s"(a_all.shared), "s"(a_all.astride), "s"(a_all.routed.inter),
+                   "s"(a_all.routed.group), "s"(a_all.routed.w[2]), "s"(a_all.routed.s[2]),
+                   "s"(a_all.routed.b[2]), "s"(a_all.sgeom.inter), "s"(a_all.sgeom.group),
+                   "s"(a_all.sgeom.w[2]), "s"(a_all.sgeom.s[2]), "s"(a_all.sgeom.b[2]));
   const FusedLayer a = token_view(a_all, blockIdx.y);
   constexpr int SPW = kWave / LI;
   __shared__ float so[kFaR][kMaxSlots];
@@ -488,16 +519,26 @@ bool fused_supported(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t b
   return true;
 }
 
-template <int BITS>
-static void launch_gateup_fa(const FusedLayer& a, uint32_t blocks, hipStream_t st) {
+// K_B instance: logits per lane P = ceil(E / 64); k = 8 (the A3B and OLMoE
+// shapes) has its own instance with unrolled top-k rounds.
+template <int BITS, int KC>
+static void launch_gateup_fa_k(const FusedLayer& a, uint32_t blocks, hipStream_t st) {
   const uint32_t p = (a.E + 63) / 64;
   const dim3 grid(blocks, a.n_tokens);
   if (p <= 1)
-    hipLaunchKernelGGL((k_fa_gateup<BITS, 1>), grid, dim3(64), 0, st, a);
+    hipLaunchKernelGGL((k_fa_gateup<BITS, 1, KC>), grid, dim3(64), 0, st, a);
   else if (p <= 2)
-    hipLaunchKernelGGL((k_fa_gateup<BITS, 2>), grid, dim3(64), 0, st, a);
+    hipLaunchKernelGGL((k_fa_gateup<BITS, 2, KC>), grid, dim3(64), 0, st, a);
   else
-    hipLaunchKernelGGL((k_fa_gateup<BITS, 4>), grid, dim3(64), 0, st, a);
+    hipLaunchKernelGGL((k_fa_gateup<BITS, 4, KC>), grid, dim3(64), 0, st, a);
+}
+
+template <int BITS>
+static void launch_gateup_fa(const FusedLayer& a, uint32_t blocks, hipStream_t st) {
+  if (a.k == 8)
+    launch_gateup_fa_k<BITS, 8>(a, blocks, st);
+  else
+    launch_gateup_fa_k<BITS, 0>(a, blocks, st);
 }
 
 template <int BITS, int LI>
