@@ -29,7 +29,7 @@
 //                      route table (expert blobs and renormalised weights,
 //                      the shared gate score) and, when asked, the
 //                      reference's exact slot order.
-//   K_C  k_fa_down     one block per kFaR hidden rows, one lane per (slot,
+//   K_C  k_fa_down     one block per kFaRB hidden rows, one lane per (slot,
 //                      chunk of 32 activations): every slot's down rows,
 //                      combined in table order moe = fma(out_s, w_s, moe)
 //                      (deferred.rs:458-466) plus the shared term and the
@@ -49,9 +49,6 @@ constexpr uint32_t kFaH = 2048;              // hidden size of this path (64 lan
 // are reduced together, gateup_rows); the K_C row count is a build-time
 // tunable. Both are the measured best on MI355X (2 or 8 rows per K_B wave,
 // 2 or 8 rows per K_C block: 0.4-1.4 us per layer slower).
-#ifndef SMOE_FA_R
-#define SMOE_FA_R 4
-#endif
 constexpr int kFaRW = 4;                     // routed rows per K_B wave
 
 // Optional timestamps (100 MHz s_memrealtime) for latency analysis. They
@@ -395,56 +392,78 @@ __global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a_all) {
 // ---------------------------------------------------------------------------
 // K_C: down rows of every slot + combine + residual.
 //
-// Lanes are slot-major: lane (s, c) owns chunk c (LI = inter / 32 chunks
-// per row) of slot s, so its 32 activations stay in registers for all kFaR
-// rows of the block. Routed slots fill waves 0 .. ceil(k / SPW) - 1 (SPW =
-// 64 / LI slots per wave); the shared expert (4-bit) has the last wave to
-// itself. Every load is issued up front: the activation chunk, the expert
-// pointer (route table) and then all kFaR rows' codes, scales and biases.
-// Per-(row, slot) sums go through LDS to kFaR combine threads, which apply
-// the reference's order: moe = fma(out_s, w_s, moe) over the routed slots,
-// then the shared term and the residual (deferred.rs:441-490).
+// One block per kFaRB = 8 hidden rows. Every block needs all (k + 1) * inter
+// activations, so a block stages them in LDS once (one cooperative load, a
+// quarter of what per-wave loads would move through the vector L1) and the
+// lanes read their chunk from there.
+//
+// Lanes are slot-major: lane (s, c) owns chunk c (LI = inter / 32 chunks per
+// row) of slot s. Routed waves: ceil(k / SPW) slot groups (SPW = 64 / LI
+// slots per wave) x H row parts, so a lane covers 8 / H rows (H = 2 while the
+// block stays within 16 waves, else 1); one shared-expert wave (4-bit) splits
+// its 64 lanes into 64 / LI row groups. Loads go out in dependency order:
+// the expert pointers (route table), the activation staging, then, once the
+// pointers land, every row's codes, scales and biases; the staging is
+// written to LDS while the weights are in flight.
+// Per-(row, slot) sums go through LDS to 8 combine threads, which apply the
+// reference's order: moe = fma(out_s, w_s, moe) over the routed slots, then
+// the shared term and the residual (deferred.rs:441-490).
 // ---------------------------------------------------------------------------
-constexpr int kFaR = SMOE_FA_R;  // hidden rows per K_C block
+constexpr int kFaRB = 8;         // hidden rows per K_C block
+constexpr int kFaStage = 8;      // staged float4 per thread, at most
+constexpr int kChunkPad = 36;    // LDS floats per 32-activation chunk (conflict-free reads)
 
-template <int BITS, int LI>
-__device__ __forceinline__ void down_rows(const FusedLayer& a, FaClock& clk, const uint8_t* blob,
-                                          const BlobGeom& g,
-                                          uint32_t row0, uint32_t c, const float* act_chunk,
-                                          float (&o)[kFaR]) {
+template <int BITS, int NR>
+struct DownLoads {
+  Raw<BITS> raw[NR];
+  uint16_t sr[NR], br[NR];
+};
+
+template <int BITS, int LI, int NR>
+__device__ __forceinline__ void down_load(const uint8_t* blob, const BlobGeom& g, uint32_t row0,
+                                          uint32_t c, DownLoads<BITS, NR>& d) {
   constexpr int CB = chunk_bytes<BITS>();
   constexpr uint32_t RB = LI * CB;
   const uint32_t gpr = g.inter / g.group;
   const uint32_t cps = __builtin_ctz(g.group / kChunk);
-  Raw<BITS> raw[kFaR];
-  uint16_t sr[kFaR], br[kFaR];
 #pragma unroll
-  for (int r = 0; r < kFaR; ++r) {
+  for (int r = 0; r < NR; ++r) {
     const uint32_t row = row0 + r;
-    raw[r] = load_raw<BITS>(blob + g.w[2] + (size_t)row * RB + c * CB);
+    d.raw[r] = load_raw<BITS>(blob + g.w[2] + (size_t)row * RB + c * CB);
     const size_t gi = ((size_t)row * gpr + (c >> cps)) * 2;
-    sr[r] = *reinterpret_cast<const uint16_t*>(blob + g.s[2] + gi);
-    br[r] = *reinterpret_cast<const uint16_t*>(blob + g.b[2] + gi);
+    d.sr[r] = *reinterpret_cast<const uint16_t*>(blob + g.s[2] + gi);
+    d.br[r] = *reinterpret_cast<const uint16_t*>(blob + g.b[2] + gi);
   }
+}
+
+template <int BITS, int LI, int NR>
+__device__ __forceinline__ void down_dot(const DownLoads<BITS, NR>& d, const float* sact_chunk,
+                                         float (&o)[NR]) {
   float act[kChunk];
-  load_x32(act_chunk, act);
-  // Keep every load above in flight before any arithmetic.
-  __builtin_amdgcn_sched_barrier(0);
-  fa_stamp(a, clk, 3, true);
+  const f32x4* p = reinterpret_cast<const f32x4*>(sact_chunk);
+#pragma unroll
+  for (int i = 0; i < kChunk / 4; ++i) {
+    const f32x4 v = p[i];
+    act[4 * i] = v.x;
+    act[4 * i + 1] = v.y;
+    act[4 * i + 2] = v.z;
+    act[4 * i + 3] = v.w;
+  }
   const float xs = xsum(act);
 #pragma unroll
-  for (int r = 0; r < kFaR; ++r)
-    o[r] = group_sum_last<LI>(chunk_dot<BITS>(raw[r], act, xs, bf16f(sr[r]), bf16f(br[r])));
+  for (int r = 0; r < NR; ++r)
+    o[r] = group_sum_last<LI>(chunk_dot<BITS>(d.raw[r], act, xs, bf16f(d.sr[r]), bf16f(d.br[r])));
 }
 
-// Waves per K_C block: ceil(k / SPW) routed + 1 shared, k <= 16.
+// Routed row parts per K_C block: 2 while 2 * ceil(k / SPW) + 1 waves fit in
+// 16, else 1.
 template <int LI>
-constexpr int fa_down_threads() {
-  return ((kMaxK + kWave / LI - 1) / (kWave / LI) + 1) * kWave;
+__host__ __device__ constexpr uint32_t fa_down_parts(uint32_t k) {
+  return 2u * ((k + kWave / LI - 1) / (kWave / LI)) + 1u <= 16u ? 2u : 1u;
 }
 
-template <int BITS, int LI>
-__global__ __launch_bounds__(fa_down_threads<LI>()) void k_fa_down(FusedLayer a_all) {
+template <int BITS, int LI, int H>
+__global__ __launch_bounds__(1024) void k_fa_down(FusedLayer a_all) {
   FA_ARGS_IN_SGPRS("s"(a_all.act), "s"(a_all.table), "s"(a_all.h_mid), "s"(a_all.out), "s"(a_all.trace),
                    "s"(a_all.k), "s"(a_all.shared), "s"(a_all.astride), "s"(a_all.routed.inter),
                    "s"(a_all.routed.group), "s"(a_all.routed.w[2]), "s"(a_all.routed.s[2]),
@@ -452,45 +471,83 @@ __global__ __launch_bounds__(fa_down_threads<LI>()) void k_fa_down(FusedLayer a_
                    "s"(a_all.sgeom.w[2]), "s"(a_all.sgeom.s[2]), "s"(a_all.sgeom.b[2]));
   const FusedLayer a = token_view(a_all, blockIdx.y);
   constexpr int SPW = kWave / LI;
-  __shared__ float so[kFaR][kMaxSlots];
+  constexpr int NR = kFaRB / H;             // rows per routed lane
+  constexpr int NRS = kFaRB / (kWave / LI); // rows per shared lane
+  extern __shared__ f32x4 sact4[];          // staged activations, kChunkPad floats per chunk
+  __shared__ float so[kFaRB][kMaxSlots];
   __shared__ float sw[kMaxSlots];
   FaClock clk;
   fa_stamp(a, clk, 0, false);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t k = a.k;
-  const uint32_t rwaves = (k + SPW - 1) / SPW;
-  const uint32_t row0 = blockIdx.x * kFaR;
+  const uint32_t rwaves = (k + SPW - 1) / SPW * H;
+  const uint32_t row0 = blockIdx.x * kFaRB;
   const uint32_t c = lane % LI;
   const uint32_t I = a.routed.inter;
+  const bool routed = (uint32_t)wave < rwaves;
 
-  // Combine threads: residual and routing weights, loaded early.
+  // Combine threads: residual and routing weights.
   float hm = 0.f, wk = 0.f;
-  if (threadIdx.x < (unsigned)kFaR) hm = a.h_mid[row0 + threadIdx.x];
+  if (threadIdx.x < (unsigned)kFaRB) hm = a.h_mid[row0 + threadIdx.x];
   if (threadIdx.x < k) wk = a.table->weight[threadIdx.x];
 
-  float o[kFaR];
-  uint32_t slot;
-  bool valid;
-  if ((uint32_t)wave < rwaves) {
-    slot = wave * SPW + lane / LI;
-    valid = slot < k;
-    const uint32_t sl = valid ? slot : 0;  // idle lanes read slot 0
-    const uint8_t* blob = a.table->blob[sl];
-    fa_stamp(a, clk, 1, true);
-    down_rows<BITS, LI>(a, clk, blob, a.routed, row0, c, a.act + (size_t)sl * I + c * kChunk, o);
-  } else {
-    slot = k;
-    valid = lane < LI;
-    down_rows<4, LI>(a, clk, a.shared, a.sgeom, row0, c, a.act + (size_t)k * I + c * kChunk, o);
-  }
-  if (c == LI - 1 && valid) {
+  // Lane roles. Routed: slot group wave / H, rows part wave % H; lanes of a
+  // slot >= k compute slot 0 and store nothing. Shared: row group lane / LI.
+  const uint32_t slot = routed ? (wave / H) * SPW + lane / LI : k;
+  const bool valid = routed ? slot < k : true;
+  const uint32_t sl = valid ? slot : 0u;
+  const uint32_t lrow0 = routed ? row0 + (wave % H) * NR : row0 + (lane / LI) * NRS;
+  const uint8_t* blob = routed ? a.table->blob[sl] : a.shared;
+
+  // Activation staging: float4 i of the (k + 1) * inter values goes to chunk
+  // i / 8, part i % 8 (out-of-range threads reload the last one).
+  const uint32_t n4 = (k + (a.shared ? 1u : 0u)) * I / 4;
+  const f32x4* act4 = reinterpret_cast<const f32x4*>(a.act);
+  f32x4 st[kFaStage];
 #pragma unroll
-    for (int r = 0; r < kFaR; ++r) so[r][slot] = o[r];
+  for (int i = 0; i < kFaStage; ++i) {
+    const uint32_t j = threadIdx.x + i * blockDim.x;
+    st[i] = act4[j < n4 ? j : n4 - 1];
+  }
+
+  fa_stamp(a, clk, 1, true);
+  // One barrier on either path: the staging is complete in LDS after it.
+  if (routed) {
+    DownLoads<BITS, NR> d;
+    down_load<BITS, LI, NR>(blob, a.routed, lrow0, c, d);
+#pragma unroll
+    for (int i = 0; i < kFaStage; ++i) {
+      const uint32_t j = threadIdx.x + i * blockDim.x;
+      if (j < n4) sact4[(j >> 3) * (kChunkPad / 4) + (j & 7)] = st[i];
+    }
+    __syncthreads();
+    fa_stamp(a, clk, 3, true);
+    float od[NR];
+    down_dot<BITS, LI, NR>(d, reinterpret_cast<const float*>(sact4) + (sl * (I / kChunk) + c) * kChunkPad, od);
+    if (c == LI - 1 && valid) {
+#pragma unroll
+      for (int r = 0; r < NR; ++r) so[lrow0 - row0 + r][slot] = od[r];
+    }
+  } else {
+    DownLoads<4, NRS> d;
+    down_load<4, LI, NRS>(blob, a.sgeom, lrow0, c, d);
+#pragma unroll
+    for (int i = 0; i < kFaStage; ++i) {
+      const uint32_t j = threadIdx.x + i * blockDim.x;
+      if (j < n4) sact4[(j >> 3) * (kChunkPad / 4) + (j & 7)] = st[i];
+    }
+    __syncthreads();
+    float od[NRS];
+    down_dot<4, LI, NRS>(d, reinterpret_cast<const float*>(sact4) + (k * (I / kChunk) + c) * kChunkPad, od);
+    if (c == LI - 1) {
+#pragma unroll
+      for (int r = 0; r < NRS; ++r) so[lrow0 - row0 + r][k] = od[r];
+    }
   }
   if (threadIdx.x < k) sw[threadIdx.x] = wk;
   fa_stamp(a, clk, 4, false);
   __syncthreads();
-  if (threadIdx.x < (unsigned)kFaR) {
+  if (threadIdx.x < (unsigned)kFaRB) {
     const uint32_t r = threadIdx.x;
     float moe = 0.f;
     for (uint32_t s = 0; s < k; ++s) moe = __builtin_fmaf(so[r][s], sw[s], moe);
@@ -541,11 +598,29 @@ static void launch_gateup_fa(const FusedLayer& a, uint32_t blocks, hipStream_t s
     launch_gateup_fa_k<BITS, 0>(a, blocks, st);
 }
 
-template <int BITS, int LI>
-static void launch_down_fa(const FusedLayer& a, hipStream_t st) {
+// K_C launch: 8 rows per block; LDS for the staged activations. Blocks of
+// more than 64 KB (k = 16 at inter 1024) need the attribute raised once.
+template <int BITS, int LI, int H>
+static hipError_t launch_down_fa_h(const FusedLayer& a, hipStream_t st) {
   constexpr uint32_t SPW = kWave / LI;
-  const uint32_t waves = (a.k + SPW - 1) / SPW + (a.shared ? 1u : 0u);
-  hipLaunchKernelGGL((k_fa_down<BITS, LI>), dim3(kFaH / kFaR, a.n_tokens), dim3(waves * kWave), 0, st, a);
+  const uint32_t waves = (a.k + SPW - 1) / SPW * H + (a.shared ? 1u : 0u);
+  const uint32_t chunks = (a.k + (a.shared ? 1u : 0u)) * (a.routed.inter / kChunk);
+  const size_t lds = (size_t)chunks * kChunkPad * sizeof(float);
+  // Every staged float4 has a thread (8 per thread at most); true for all
+  // k <= 16 and inter 512 / 1024, checked anyway.
+  if (chunks * (kChunk / 4) > (uint32_t)kFaStage * waves * kWave || waves > 16) return hipErrorInvalidValue;
+  static const bool raised = [] {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fa_down<BITS, LI, H>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024) == hipSuccess;
+  }();
+  (void)raised;
+  hipLaunchKernelGGL((k_fa_down<BITS, LI, H>), dim3(kFaH / kFaRB, a.n_tokens), dim3(waves * kWave), lds, st, a);
+  return hipSuccess;
+}
+
+template <int BITS, int LI>
+static hipError_t launch_down_fa(const FusedLayer& a, hipStream_t st) {
+  return fa_down_parts<LI>(a.k) == 2 ? launch_down_fa_h<BITS, LI, 2>(a, st) : launch_down_fa_h<BITS, LI, 1>(a, st);
 }
 
 hipError_t launch_fused_layer(const FusedLayer& a, hipStream_t st) {
@@ -563,11 +638,12 @@ hipError_t launch_fused_layer(const FusedLayer& a, hipStream_t st) {
     launch_gateup_fa<4>(a, kb, st);
   else
     launch_gateup_fa<3>(a, kb, st);
-  if (a.routed.bits == 4) {
-    if (I == 512) launch_down_fa<4, 16>(a, st); else launch_down_fa<4, 32>(a, st);
-  } else {
-    if (I == 512) launch_down_fa<3, 16>(a, st); else launch_down_fa<3, 32>(a, st);
-  }
+  hipError_t e;
+  if (a.routed.bits == 4)
+    e = I == 512 ? launch_down_fa<4, 16>(a, st) : launch_down_fa<4, 32>(a, st);
+  else
+    e = I == 512 ? launch_down_fa<3, 16>(a, st) : launch_down_fa<3, 32>(a, st);
+  if (e != hipSuccess) return e;
   return hipGetLastError();
 }
 

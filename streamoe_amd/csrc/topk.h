@@ -263,7 +263,8 @@ __device__ __forceinline__ bool topk_threshold(const float (&l)[P], uint32_t n, 
   // Lane r records m and the running count of popped keys; the boundary
   // rounds are found after the loop, so a round is vector work only.
   uint32_t rec_m = 0, rec_c = 0, cnt = 0;
-#pragma unroll (KC > 0 ? KC + 1 : 1)
+  constexpr int kRounds = KC > 0 ? KC + 1 : 1;  // unroll factor
+#pragma unroll kRounds
   for (uint32_t r = 0; r <= k; ++r) {
     const uint32_t m = wave_umax_all(sk[0]);
     const bool pop = sk[0] == m;
