@@ -18,7 +18,7 @@
 //
 //   K_A  k_fa_route    one wave per router row: x = RMSNorm(r) * w (or the
 //                      given input), logits[e] = W_e . x (row E: shared
-//                      gate); one more wave per token stores x as integer
+//                      gate); four more waves per token store x as integer
 //                      limbs for K_B (common.h, chunk_dot_i).
 //   K_B  k_fa_gateup   one wave per RW rows of one routed slot: the slot's
 //                      expert from the logits (every wave), then
@@ -103,24 +103,71 @@ __device__ __forceinline__ void fa_x_load(const FusedLayer& a, int lane, FaX& f)
   load_x32(src + (size_t)lane * kChunk, f.x);
 }
 
-__device__ __forceinline__ void fa_x_finish(const FusedLayer& a, FaX& f) {
-  if (a.x_in || !a.norm) return;
-  // Every rounding is written out (no contraction left to the compiler), so
-  // all instantiations (T = 1..4 tokens) compute x bit for bit alike.
+// 1 / rms of the hidden vector whose chunk `lane` every lane holds in f.x.
+// Every rounding is written out (no contraction left to the compiler), so
+// all instantiations (T = 1..4 tokens) compute x bit for bit alike.
+__device__ __forceinline__ float fa_inv_rms(const FusedLayer& a, const FaX& f) {
   float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < kChunk; ++j) ss = __builtin_fmaf(f.x[j], f.x[j], ss);
   ss = readlane_f(group_sum_last<64>(ss), 63);
-  const float inv = 1.0f / sqrtf(__builtin_fmaf(ss, 1.0f / (float)kFaH, a.eps));
+  return 1.0f / sqrtf(__builtin_fmaf(ss, 1.0f / (float)kFaH, a.eps));
+}
+
+// x[j] = r[j] * inv * w[j] for eight consecutive values (w: 8 bf16).
+__device__ __forceinline__ void fa_norm8(float* x, float inv, const u32x4& w) {
+  const uint32_t w4[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t w4[4] = {f.w[i].x, f.w[i].y, f.w[i].z, f.w[i].w};
+  for (int h = 0; h < 4; ++h) {
+    x[2 * h] = x[2 * h] * inv * bf16f((uint16_t)(w4[h] & 0xFFFFu));
+    x[2 * h + 1] = x[2 * h + 1] * inv * bf16f((uint16_t)(w4[h] >> 16));
+  }
+}
+
+__device__ __forceinline__ void fa_x_finish(const FusedLayer& a, FaX& f) {
+  if (a.x_in || !a.norm) return;
+  const float inv = fa_inv_rms(a, f);
 #pragma unroll
-    for (int h = 0; h < 4; ++h) {
-      const int j = 8 * i + 2 * h;
-      f.x[j] = f.x[j] * inv * bf16f((uint16_t)(w4[h] & 0xFFFFu));
-      f.x[j + 1] = f.x[j + 1] * inv * bf16f((uint16_t)(w4[h] >> 16));
-    }
+  for (int i = 0; i < 4; ++i) fa_norm8(f.x + 8 * i, inv, f.w[i]);
+}
+
+// x as integer limbs (common.h, make_limbs) with four lanes per 32-value
+// chunk: lane q of the quad holds values 8q .. 8q + 7 and writes limb words
+// 2q and 2q + 1 of every limb; the chunk's exponent and sum come from the
+// quad (DPP).
+__device__ __forceinline__ void store_limbs_quad(uint32_t* dst, const float (&x)[8], int q) {
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(x[j]));
+  amax = fmaxf(amax, dpp_f<0xB1>(amax, 0.f));  // quad lanes ^ 1
+  amax = fmaxf(amax, dpp_f<0x4E>(amax, 0.f));  // quad lanes ^ 2
+  const int f = amax > 0.f ? 22 - __builtin_amdgcn_frexp_expf(amax) : 0;
+  int32_t d[3][8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int32_t m = (int32_t)__builtin_rintf(__builtin_ldexpf(x[j], f));
+    const int32_t d0 = (m << 24) >> 24;
+    const int32_t m1 = (m - d0) >> 8;
+    const int32_t d1 = (m1 << 24) >> 24;
+    d[0][j] = d0;
+    d[1][j] = d1;
+    d[2][j] = (m1 - d1) >> 8;
+  }
+#pragma unroll
+  for (int L = 0; L < 3; ++L) {
+    uint2 v;
+    v.x = pack_bytes(d[L][0], d[L][2], d[L][4], d[L][6]);
+    v.y = pack_bytes(d[L][1], d[L][3], d[L][5], d[L][7]);
+    *reinterpret_cast<uint2*>(dst + 8 * L + 2 * q) = v;
+  }
+  float xs = ((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]));
+  xs += dpp_f<0xB1>(xs, 0.f);
+  xs += dpp_f<0x4E>(xs, 0.f);
+  if (q == 0) {
+    uint2 v;
+    v.x = __float_as_uint(__builtin_ldexpf(1.0f, -f));
+    v.y = __float_as_uint(xs);
+    *reinterpret_cast<uint2*>(dst + 24) = v;
   }
 }
 
@@ -152,8 +199,8 @@ __device__ __forceinline__ FusedLayer token_view(const FusedLayer& a, uint32_t t
 
 // ---------------------------------------------------------------------------
 // K_A: router logits (+ shared gate) for T tokens: each wave reads its
-// router row once and applies it to every token's x. The last T waves
-// write x of token t as integer limbs for K_B.
+// router row once and applies it to every token's x. The last 4T waves
+// write x of the tokens as integer limbs for K_B.
 // ---------------------------------------------------------------------------
 template <int T>
 __global__ __launch_bounds__(64) void k_fa_route(FusedLayer a) {
@@ -167,15 +214,26 @@ __global__ __launch_bounds__(64) void k_fa_route(FusedLayer a) {
   const uint32_t c = lane;  // this lane's chunk of the hidden vector
 
   if (w >= nrouter) {
-    // Limb wave of token t.
-    const FusedLayer at = token_view(a, w - nrouter);
+    // Limb waves, four per token: wave p of token t converts chunks
+    // [16p, 16p + 16), four lanes per chunk (8 values each). Every lane also
+    // loads chunk `lane` for the sum of squares.
+    const uint32_t lw = w - nrouter;
+    const FusedLayer at = token_view(a, lw >> 2);
+    const uint32_t ch = (lw & 3) * 16 + (uint32_t)(lane >> 2);
+    const int q = lane & 3;
     FaX f;
     fa_x_load(at, lane, f);
+    const float* src = at.x_in ? at.x_in : at.resid;
+    const uint16_t* nw = at.norm ? at.norm : reinterpret_cast<const uint16_t*>(src);
+    const uint32_t e0 = ch * kChunk + q * 8;
+    const f32x4 v0 = *reinterpret_cast<const f32x4*>(src + e0);
+    const f32x4 v1 = *reinterpret_cast<const f32x4*>(src + e0 + 4);
+    const u32x4 w8 = *reinterpret_cast<const u32x4*>(nw + e0);
+    __builtin_amdgcn_sched_barrier(0);
     fa_stamp(a, clk, 3, true);
-    fa_x_finish(at, f);
-    XLimbs xl;
-    make_limbs(f.x, xl);
-    store_limbs(at.xl + (size_t)c * kXLimbWords, xl);
+    float x[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    if (!at.x_in && at.norm) fa_norm8(x, fa_inv_rms(at, f), w8);
+    store_limbs_quad(at.xl + (size_t)ch * kXLimbWords, x, q);
     fa_stamp(a, clk, 5, true);
     fa_flush(a, clk, 0);
     return;
@@ -626,7 +684,7 @@ static hipError_t launch_down_fa(const FusedLayer& a, hipStream_t st) {
 hipError_t launch_fused_layer(const FusedLayer& a, hipStream_t st) {
   if (a.n_tokens < 1 || a.n_tokens > kMaxDecodeTokens || (a.trace && a.n_tokens != 1)) return hipErrorInvalidValue;
   const uint32_t I = a.routed.inter;
-  const uint32_t ka = a.E + (a.gate ? 1u : 0u) + a.n_tokens;
+  const uint32_t ka = a.E + (a.gate ? 1u : 0u) + 4u * a.n_tokens;
   switch (a.n_tokens) {
     case 1: hipLaunchKernelGGL(k_fa_route<1>, dim3(ka), dim3(64), 0, st, a); break;
     case 2: hipLaunchKernelGGL(k_fa_route<2>, dim3(ka), dim3(64), 0, st, a); break;
