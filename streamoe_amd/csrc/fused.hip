@@ -544,9 +544,12 @@ __global__ __launch_bounds__(1024) void k_fa_down(FusedLayer a_all) {
   const uint32_t I = a.routed.inter;
   const bool routed = (uint32_t)wave < rwaves;
 
-  // Combine threads: residual and routing weights.
-  float hm = 0.f, wk = 0.f;
-  if (threadIdx.x < (unsigned)kFaRB) hm = a.h_mid[row0 + threadIdx.x];
+  // Combine threads: residual, routing weights and the shared-expert gate.
+  float hm = 0.f, wk = 0.f, gate = 0.f;
+  if (threadIdx.x < (unsigned)kFaRB) {
+    hm = a.h_mid[row0 + threadIdx.x];
+    gate = a.table->shared_gate;
+  }
   if (threadIdx.x < k) wk = a.table->weight[threadIdx.x];
 
   // Lane roles. Routed: slot group wave / H, rows part wave % H; lanes of a
@@ -603,6 +606,8 @@ __global__ __launch_bounds__(1024) void k_fa_down(FusedLayer a_all) {
     }
   }
   if (threadIdx.x < k) sw[threadIdx.x] = wk;
+  // The gate's sigmoid is ready before the partial sums are.
+  const float sig = sigmoidf_ref(gate);
   fa_stamp(a, clk, 4, false);
   __syncthreads();
   if (threadIdx.x < (unsigned)kFaRB) {
@@ -612,8 +617,7 @@ __global__ __launch_bounds__(1024) void k_fa_down(FusedLayer a_all) {
     float sum = moe;
     if (a.shared) {
       const float sh = so[r][k];
-      const float gate = a.table->shared_gate;
-      sum = __builtin_isnan(gate) ? moe + sh : __builtin_fmaf(sh, sigmoidf_ref(gate), moe);
+      sum = __builtin_isnan(gate) ? moe + sh : __builtin_fmaf(sh, sig, moe);
     }
     a.out[row0 + r] = hm + sum;
   }
