@@ -36,8 +36,9 @@
 //                      residual.
 //
 // Weights are read exactly once per token with 128-bit (4-bit) or 96-bit
-// (3-bit) non-temporal loads; activations (x, act, logits: <= 40 KB) are
-// re-read from L2 by every wave that needs them.
+// (3-bit) non-temporal loads; x limbs and logits (<= 10 KB) are re-read
+// from L2 by every wave that needs them, and each K_C block stages the
+// activations (<= 68 KB) in LDS once.
 #include "common.h"
 #include "kernels.h"
 #include "topk.h"
