@@ -544,25 +544,46 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
   }
   const uint32_t c43 = 0x43434343u;
 
-  // Issue every copy of flattened chunk j into stage j % S. Captures by
-  // value: a by-reference capture stores the locals' addresses, and the
-  // memory clobbers of the waits below would then keep them in scratch.
-  auto issue = [=](uint32_t j) {
-    const uint32_t v = lb + (j / nch) * per, c = j % nch;
+  // Copy sources of one unit at its chunk 0 (the chunk offsets are added
+  // per chunk). Computed once per unit; the unit's item is decoded with one
+  // division.
+  struct UnitSrc {
+    const uint8_t* bq;
+    const uint8_t* bs;
+    const uint8_t* ah;
+    const uint8_t* al;
+    const uint8_t* xs;
+    uint32_t cnt;
+  };
+  auto unit_src = [=](uint32_t v) {
     const uint32_t item = item_lo + v / ncb, cb = v % ncb;
     const uint32_t e = items[2 * item];
     const uint32_t start = items[2 * item + 1] & 0xFFFFu, cnt = items[2 * item + 1] >> 16;
     const uint8_t* blob = experts + (size_t)e * stride;
-    uint8_t* st = lds + (j % C::S) * C::STAGE;
+    UnitSrc u;
+    u.bq = blob + wo0 + (size_t)cb * C::NCOL * rowb;
+    u.bs = blob + so0 + (size_t)cb * C::NCOL * ng * 2;
+    u.ah = reinterpret_cast<const uint8_t*>(ahi_src + (size_t)start * K);
+    u.al = reinterpret_cast<const uint8_t*>(alo_src + (size_t)start * K);
+    u.xs = reinterpret_cast<const uint8_t*>(gsum + (size_t)start * ng);
+    u.cnt = cnt;
+    return u;
+  };
+  // Issue every copy of chunk c of unit u into stage `slot`. Captures by
+  // value: a by-reference capture stores the locals' addresses, and the
+  // memory clobbers of the waits below would then keep them in scratch.
+  auto issue = [=](const UnitSrc& u, uint32_t c, uint32_t slot) {
+    const uint32_t cnt = u.cnt;
+    uint8_t* st = lds + slot * C::STAGE;
     // Weight codes: slot p = (row, slot part) holds the row's part
     // (slot part ^ row & 7) [4-bit] or ((slot part + row) % 6) [3-bit].
-    const uint8_t* bq_base = blob + wo0 + (size_t)cb * C::NCOL * rowb + (size_t)c * C::RB;
+    const uint8_t* bq_base = u.bq + (size_t)c * C::RB;
 #pragma unroll
     for (int i = 0; i < C::N_BQ; ++i)
       if ((C::P_BQ / C::NW) % 64 == 0 || i * 64 + lane < (uint32_t)(C::P_BQ / C::NW))
         dma16(bq_base + off_bq[i], st + C::OFF_BQ + (wave * (C::P_BQ / C::NW) + i * 64) * 16);
     // Scales then biases of each row: [row][array][CG] bf16.
-    const uint8_t* bs_base = blob + so0 + ((size_t)cb * C::NCOL * ng + (size_t)c * C::CG) * 2;
+    const uint8_t* bs_base = u.bs + (size_t)c * C::CG * 2;
 #pragma unroll
     for (int i = 0; i < C::N_BS; ++i) {
       uint8_t* dst = st + C::OFF_BS + (wave * (C::P_BS / C::NW) + i * 64) * C::SB_SZ;
@@ -574,8 +595,7 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
     // part = part ^ (m & 15). Rows 16.. are copied only for a second tile.
 #pragma unroll
     for (int hl = 0; hl < (SPLIT ? 2 : 1); ++hl) {
-      const uint8_t* a_base = reinterpret_cast<const uint8_t*>((hl ? alo_src : ahi_src) + (size_t)start * K) +
-                              (size_t)c * C::KC * 2;
+      const uint8_t* a_base = (hl ? u.al : u.ah) + (size_t)c * C::KC * 2;
 #pragma unroll
       for (int i = 0; i < C::N_A; ++i) {
         const uint32_t pair = wave * C::N_A + i, half = lane >> 5, sp = lane & 31;
@@ -586,7 +606,7 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
       }
     }
     // Group sums of the A rows, [group][row].
-    const uint8_t* xs_base = reinterpret_cast<const uint8_t*>(gsum + (size_t)start * ng + (size_t)c * C::CG);
+    const uint8_t* xs_base = u.xs + (size_t)c * C::CG * 4;
 #pragma unroll
     for (int i = 0; i < C::N_XS; ++i) {
       const uint32_t o = i * 64 + lane;
@@ -605,7 +625,22 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
 #pragma unroll
       for (int t = 0; t < 2; ++t) tot[mt][ct][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (uint32_t j = 0; j + 1 < (uint32_t)C::S && j < total; ++j) issue(j);
+  // Issue position (unit iv, chunk ic, stage islot) runs S - 1 chunks ahead
+  // of the compute position (unit cv, chunk cc, stage cslot).
+  uint32_t iv = lb, ic = 0, islot = 0, issued = 0;
+  UnitSrc isrc = unit_src(iv);
+  for (; issued + 1 < (uint32_t)C::S && issued < total; ++issued) {
+    issue(isrc, ic, islot);
+    islot = islot + 1 == (uint32_t)C::S ? 0u : islot + 1;
+    if (++ic == nch) {
+      ic = 0;
+      iv += per;
+      if (iv < group_units) isrc = unit_src(iv);
+    }
+  }
+  uint32_t cv = lb, cc = 0, cslot = 0;
+  uint32_t c_item = item_lo + cv / ncb, c_cb = cv % ncb;
+  uint32_t c_start = items[2 * c_item + 1] & 0xFFFFu, c_cnt = items[2 * c_item + 1] >> 16;
   for (uint32_t j = 0; j < total; ++j) {
     // Copies of chunks j + 1 .. j + S - 2 may stay in flight.
     const uint32_t ahead = min((uint32_t)C::S - 2, total - 1 - j);
@@ -617,18 +652,34 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
       asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(2 * C::D) : "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (j + C::S - 1 < total) issue(j + C::S - 1);
+    if (issued < total) {
+      issue(isrc, ic, islot);
+      ++issued;
+      islot = islot + 1 == (uint32_t)C::S ? 0u : islot + 1;
+      if (++ic == nch) {
+        ic = 0;
+        iv += per;
+        if (iv < group_units) isrc = unit_src(iv);
+      }
+    }
 
-    const uint32_t v = lb + (j / nch) * per, c = j % nch;
-    const uint32_t item = item_lo + v / ncb, cb = v % ncb;
-    const uint32_t start = items[2 * item + 1] & 0xFFFFu, cnt = items[2 * item + 1] >> 16;
-    uint8_t* st = lds + (j % C::S) * C::STAGE;
+    const uint32_t start = c_start, cnt = c_cnt, cb = c_cb;
+    uint8_t* st = lds + cslot * C::STAGE;
+    cslot = cslot + 1 == (uint32_t)C::S ? 0u : cslot + 1;
     if (cnt > 16)
       pf_chunk<BITS, G, MODE, SPLIT, 2>(st, kh * C::CGW, cw, n, q, c43, tot);
     else
       pf_chunk<BITS, G, MODE, SPLIT, 1>(st, kh * C::CGW, cw, n, q, c43, tot);
 
-    if (c + 1 == nch) {  // unit complete: add the K halves, write it out
+    if (++cc == nch) {  // unit complete: add the K halves, write it out
+      cc = 0;
+      cv += per;
+      if (cv < group_units) {
+        c_item = item_lo + cv / ncb;
+        c_cb = cv % ncb;
+        c_start = items[2 * c_item + 1] & 0xFFFFu;
+        c_cnt = items[2 * c_item + 1] >> 16;
+      }
       // Every wave is done reading this stage; the upper half parks its sums
       // there ([column wave][accumulator][lane]) for the lower half.
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
