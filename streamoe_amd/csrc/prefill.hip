@@ -323,7 +323,7 @@ __device__ __forceinline__ void dma4(const void* g, void* l) {
 // [v0, v4, v1, v5, v2, v6, v3, v7].
 __device__ __forceinline__ uint32_t perm8_pos(uint32_t i) { return i < 4 ? 2 * i : 2 * (i - 4) + 1; }
 
-template <int BITS, int G, int MODE, bool SPLIT>
+template <int BITS, int G, int MODE, bool SPLIT, int KU = 0>
 struct PfMM {
   static constexpr int NW = 8;                        // waves per block: 4 column waves x 2 K halves
   static constexpr int KC = kPfKC;                    // inputs per chunk
@@ -336,21 +336,31 @@ struct PfMM {
   static constexpr int ROWS = NMAT * NCOL;            // weight rows per unit
   static constexpr int RB = KC * BITS / 8;            // code bytes per row and chunk
   static constexpr int PPR = RB / 16;                 // 16-byte parts per row
+  // Scales and biases: per chunk in each stage ([row][array][CG] bf16), or,
+  // with KU = K > 0, for a whole unit in one of two unit buffers ([row][array]
+  // [K / G], rows padded by 16 bytes against bank conflicts), copied once per
+  // unit in 16-byte pieces instead of 8 small pieces per chunk.
+  static constexpr bool USB = KU > 0;
+  static constexpr int NGU = USB ? KU / G : CG;       // groups per scale row in LDS
   static constexpr int SB_BYTES = 2 * CG;             // scale (or bias) bytes per row and chunk
   static constexpr int SB_SZ = SB_BYTES >= 16 ? 16 : 4;
   static constexpr int SB_PIECES = SB_BYTES / SB_SZ;  // per row and array
-  static constexpr int S = MODE == 0 ? (SPLIT ? 3 : 4) : 2;
+  static constexpr int SB_ROW = USB ? 4 * NGU + 16 : 2 * SB_BYTES;  // LDS bytes per scale row
+  static constexpr int S = MODE == 0 ? (SPLIT || USB ? 3 : 4) : 2;
   // Copy pieces per chunk and category; every wave copies an equal,
   // contiguous share (so every wave issues the same number of copies).
   static constexpr int P_BQ = ROWS * PPR;             // 16-byte code parts
-  static constexpr int P_BS = ROWS * 2 * SB_PIECES;   // scale / bias pieces
+  static constexpr int P_BS = USB ? 0 : ROWS * 2 * SB_PIECES;  // scale / bias pieces
   static constexpr int P_A = kPfMC * KC * 2 / 16;     // 16-byte A parts (per half)
   static constexpr int P_XS = kPfMC * CG;             // group sums
+  static constexpr int P_US = USB ? ROWS * (2 * (2 * NGU / 16) + 1) : 0;  // unit scale slots (16 B, one pad per row)
   static constexpr int N_BQ = (P_BQ / NW + 63) / 64;  // copy instructions per wave
   static constexpr int N_BS = (P_BS / NW + 63) / 64;
   static constexpr int N_A = P_A / NW / 64;           // one row pair (m, m + 16) each
   static constexpr int N_XS = (P_XS / NW + 63) / 64;
-  static constexpr int D = N_BQ + N_BS + N_A * (SPLIT ? 2 : 1) + N_XS;
+  static constexpr int N_US = (P_US / NW + 63) / 64;
+  static constexpr int D = N_BQ + N_BS + N_A * (SPLIT ? 2 : 1) + N_XS;  // per chunk
+  static constexpr int DU = N_US;                                         // per unit
   // LDS layout of one stage (bytes). A rows sit in pairs: row m at slot
   // 2 (m % 16) + m / 16, so one copy instruction moves rows m and m + 16.
   static constexpr int OFF_BQ = 0;
@@ -359,14 +369,17 @@ struct PfMM {
   static constexpr int OFF_AL = OFF_AH + P_A * 16;
   static constexpr int OFF_XS = OFF_AL + (SPLIT ? P_A * 16 : 0);
   static constexpr int STAGE = OFF_XS + P_XS * 4;
+  static constexpr int UBUF = USB ? ROWS * SB_ROW : 0;  // one unit buffer, after the stages
+  static constexpr int LDS = S * STAGE + 2 * UBUF;
   // Accumulators per lane, exchanged between the K halves through LDS.
   static constexpr int NT = NMAT * CT * 2 * 4;
   static_assert(CG % 2 == 0, "K halves");
-  static_assert(P_BQ % NW == 0 && P_BS % NW == 0 && P_XS % NW == 0, "equal shares");
+  static_assert(P_BQ % NW == 0 && P_BS % NW == 0 && P_XS % NW == 0 && P_US % NW == 0, "equal shares");
   static_assert(N_A * NW * 64 == P_A && P_A == 16 * 64, "one row pair per A copy");
-  static_assert((S - 2) * D <= 63, "vmcnt range");
-  static_assert(S * STAGE <= 160 * 1024, "LDS per CU");
+  static_assert((S - 2) * D + DU <= 63, "vmcnt range");
+  static_assert(LDS <= 160 * 1024, "LDS per CU");
   static_assert(4 * NT * 64 * 4 <= STAGE, "accumulator exchange fits a stage");
+  static_assert(!USB || (2 * NGU) % 16 == 0, "unit scale rows in 16-byte pieces");
 };
 
 // 8 codes of one 4-bit u32 as bf16 (128 + q), order [q0,q4,q1,q5,q2,q6,q3,q7],
@@ -388,11 +401,11 @@ __device__ __forceinline__ u32x4 codes_bf16_4p(uint32_t d, uint32_t c43) {
 // The MFMA work of one chunk for one wave: groups gl0 .. gl0 + CGW - 1 of
 // the stage at st, NTL 16-row tiles, into tot. Straight-line code (no
 // branches), so the scheduler can overlap LDS reads with MFMAs.
-template <int BITS, int G, int MODE, bool SPLIT, int NTL>
-__device__ __forceinline__ void pf_chunk(const uint8_t* st, uint32_t gl0, uint32_t cw, uint32_t n, uint32_t q,
-                                         uint32_t c43,
-                                         f32x4 (&tot)[PfMM<BITS, G, MODE, SPLIT>::NMAT][PfMM<BITS, G, MODE, SPLIT>::CT][2]) {
-  using C = PfMM<BITS, G, MODE, SPLIT>;
+template <int BITS, int G, int MODE, bool SPLIT, int KU, int NTL>
+__device__ __forceinline__ void pf_chunk(const uint8_t* st, const uint8_t* sbb, uint32_t gofs, uint32_t gl0,
+                                         uint32_t cw, uint32_t n, uint32_t q, uint32_t c43,
+                                         f32x4 (&tot)[PfMM<BITS, G, MODE, SPLIT, KU>::NMAT][PfMM<BITS, G, MODE, SPLIT, KU>::CT][2]) {
+  using C = PfMM<BITS, G, MODE, SPLIT, KU>;
 #pragma unroll
   for (int gi = 0; gi < C::CGW; ++gi) {
     const uint32_t gl = gl0 + gi;
@@ -434,9 +447,11 @@ __device__ __forceinline__ void pf_chunk(const uint8_t* st, uint32_t gl0, uint32
             bw[mt][ct][uu] = __builtin_amdgcn_alignbit(hi, lo, bit & 31) & 0xFFFFFFu;
           }
         }
-        const uint16_t* sb = reinterpret_cast<const uint16_t*>(st + C::OFF_BS + row * 2 * C::SB_BYTES);
+        // Scales of the row, then biases: [row][array][NGU] at sbb; this chunk's
+        // groups start at gofs.
+        const uint16_t* sb = reinterpret_cast<const uint16_t*>(sbb + row * C::SB_ROW) + gofs;
         s[mt][ct] = bf16f(sb[gl]);
-        cbias[mt][ct] = __builtin_fmaf(-128.0f, s[mt][ct], bf16f(sb[C::CG + gl]));
+        cbias[mt][ct] = __builtin_fmaf(-128.0f, s[mt][ct], bf16f(sb[C::NGU + gl]));
       }
     u32x4 bq[C::NMAT][C::CT][C::NU];
 #pragma unroll
@@ -482,10 +497,10 @@ __device__ __forceinline__ void pf_chunk(const uint8_t* st, uint32_t gl0, uint32
   }
 }
 
-template <int BITS, int G, int MODE, bool SPLIT>
+template <int BITS, int G, int MODE, bool SPLIT, int KU>
 __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restrict__ items,
                                                const uint32_t* __restrict__ n_items_p) {
-  using C = PfMM<BITS, G, MODE, SPLIT>;
+  using C = PfMM<BITS, G, MODE, SPLIT, KU>;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t cw = wave & 3, kh = wave >> 2;  // column wave, K half
@@ -525,7 +540,7 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
   const uint64_t bo0 = a.g.b[MODE == 0 ? 0 : 2];
   // Lane offsets of the weight copies (fixed for the whole kernel; the
   // per-chunk part of the address is scalar).
-  uint32_t off_bq[C::N_BQ], off_bs[C::N_BS];
+  uint32_t off_bq[C::N_BQ], off_bs[C::N_BS > 0 ? C::N_BS : 1], off_us[C::N_US > 0 ? C::N_US : 1];
 #pragma unroll
   for (int i = 0; i < C::N_BQ; ++i) {
     const uint32_t p = wave * (C::P_BQ / C::NW) + i * 64 + lane;
@@ -541,6 +556,19 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
     const uint32_t mat = row / C::NCOL;
     // Biases follow scales at the same distance in both matrices.
     off_bs[i] = (uint32_t)(mat * (so1 - so0) + arr * (bo0 - so0)) + (row % C::NCOL) * ng * 2 + pc * C::SB_SZ;
+  }
+  // Unit scale slots: LDS slot p = (row, slot r of 2 UPC + 1) holds piece
+  // r % UPC of the row's scales (r < UPC) or biases (r < 2 UPC); the last
+  // slot pads the row and repeats piece 0. off_us = global offset from the
+  // unit's scale base.
+  constexpr uint32_t UPC = 2 * C::NGU / 16;  // pieces per row and array
+#pragma unroll
+  for (int i = 0; i < C::N_US; ++i) {
+    const uint32_t p = wave * (C::P_US / C::NW) + i * 64 + lane;
+    const uint32_t row = p / (2 * UPC + 1), r = p % (2 * UPC + 1);
+    const uint32_t arr = r < 2 * UPC ? r / UPC : 0u, pc = r < 2 * UPC ? r % UPC : 0u;
+    const uint32_t mat = row / C::NCOL;
+    off_us[i] = (uint32_t)(mat * (so1 - so0) + arr * (bo0 - so0)) + (row % C::NCOL) * ng * 2 + pc * 16;
   }
   const uint32_t c43 = 0x43434343u;
 
@@ -572,6 +600,14 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
   // Issue every copy of chunk c of unit u into stage `slot`. Captures by
   // value: a by-reference capture stores the locals' addresses, and the
   // memory clobbers of the waits below would then keep them in scratch.
+  // Unit scale copies into unit buffer ub (before the unit's first chunk).
+  auto issue_unit = [=](const UnitSrc& u, uint32_t ub) {
+    uint8_t* ubuf = lds + C::S * C::STAGE + ub * C::UBUF;
+#pragma unroll
+    for (int i = 0; i < C::N_US; ++i)
+      if ((C::P_US / C::NW) % 64 == 0 || i * 64 + lane < (uint32_t)(C::P_US / C::NW))
+        dma16(u.bs + off_us[i], ubuf + (wave * (C::P_US / C::NW) + i * 64) * 16);
+  };
   auto issue = [=](const UnitSrc& u, uint32_t c, uint32_t slot) {
     const uint32_t cnt = u.cnt;
     uint8_t* st = lds + slot * C::STAGE;
@@ -627,37 +663,48 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
 
   // Issue position (unit iv, chunk ic, stage islot) runs S - 1 chunks ahead
   // of the compute position (unit cv, chunk cc, stage cslot).
-  uint32_t iv = lb, ic = 0, islot = 0, issued = 0;
+  uint32_t iv = lb, ic = 0, islot = 0, issued = 0, iub = 0;
   UnitSrc isrc = unit_src(iv);
   for (; issued + 1 < (uint32_t)C::S && issued < total; ++issued) {
+    if (C::USB && ic == 0) issue_unit(isrc, iub);
     issue(isrc, ic, islot);
     islot = islot + 1 == (uint32_t)C::S ? 0u : islot + 1;
     if (++ic == nch) {
       ic = 0;
+      iub ^= 1u;
       iv += per;
       if (iv < group_units) isrc = unit_src(iv);
     }
   }
-  uint32_t cv = lb, cc = 0, cslot = 0;
+  uint32_t cv = lb, cc = 0, cslot = 0, cub = 0;
   uint32_t c_item = item_lo + cv / ncb, c_cb = cv % ncb;
   uint32_t c_start = items[2 * c_item + 1] & 0xFFFFu, c_cnt = items[2 * c_item + 1] >> 16;
   for (uint32_t j = 0; j < total; ++j) {
-    // Copies of chunks j + 1 .. j + S - 2 may stay in flight.
+    // Copies of chunks j + 1 .. j + S - 2 may stay in flight: D each, plus
+    // DU unit scale copies for a chunk that starts a unit (nch >= 2, so at
+    // most one of the next two does).
     const uint32_t ahead = min((uint32_t)C::S - 2, total - 1 - j);
+    const bool ustart = C::USB && ((ahead >= 1 && cc + 1 == nch) || (ahead >= 2 && cc + 2 == nch));
     if (ahead == 0)
       asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-    else if (ahead == 1)
+    else if (ahead == 1 && !ustart)
       asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(C::D) : "memory");
-    else
+    else if (ahead == 1)
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(C::D + C::DU) : "memory");
+    else if (!ustart)
       asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(2 * C::D) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(2 * C::D + C::DU) : "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     if (issued < total) {
+      if (C::USB && ic == 0) issue_unit(isrc, iub);
       issue(isrc, ic, islot);
       ++issued;
       islot = islot + 1 == (uint32_t)C::S ? 0u : islot + 1;
       if (++ic == nch) {
         ic = 0;
+        iub ^= 1u;
         iv += per;
         if (iv < group_units) isrc = unit_src(iv);
       }
@@ -666,13 +713,16 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
     const uint32_t start = c_start, cnt = c_cnt, cb = c_cb;
     uint8_t* st = lds + cslot * C::STAGE;
     cslot = cslot + 1 == (uint32_t)C::S ? 0u : cslot + 1;
+    const uint8_t* sbb = C::USB ? lds + C::S * C::STAGE + cub * C::UBUF : st + C::OFF_BS;
+    const uint32_t gofs = C::USB ? cc * C::CG : 0u;
     if (cnt > 16)
-      pf_chunk<BITS, G, MODE, SPLIT, 2>(st, kh * C::CGW, cw, n, q, c43, tot);
+      pf_chunk<BITS, G, MODE, SPLIT, KU, 2>(st, sbb, gofs, kh * C::CGW, cw, n, q, c43, tot);
     else
-      pf_chunk<BITS, G, MODE, SPLIT, 1>(st, kh * C::CGW, cw, n, q, c43, tot);
+      pf_chunk<BITS, G, MODE, SPLIT, KU, 1>(st, sbb, gofs, kh * C::CGW, cw, n, q, c43, tot);
 
     if (++cc == nch) {  // unit complete: add the K halves, write it out
       cc = 0;
+      cub ^= 1u;
       cv += per;
       if (cv < group_units) {
         c_item = item_lo + cv / ncb;
@@ -894,11 +944,11 @@ bool prefill_supported(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t
   return true;
 }
 
-template <int BITS, int G, int MODE, bool SPLIT>
+template <int BITS, int G, int MODE, bool SPLIT, int KU>
 static hipError_t launch_mm(const PfArgs& a, uint32_t n_units_max, uint32_t n_cu, hipStream_t st) {
-  using C = PfMM<BITS, G, MODE, SPLIT>;
-  const auto fn = reinterpret_cast<const void*>(&k_pf_mm<BITS, G, MODE, SPLIT>);
-  const size_t lds = (size_t)C::S * C::STAGE;
+  using C = PfMM<BITS, G, MODE, SPLIT, KU>;
+  const auto fn = reinterpret_cast<const void*>(&k_pf_mm<BITS, G, MODE, SPLIT, KU>);
+  const size_t lds = (size_t)C::LDS;
   static bool attr_set = false;
   if (!attr_set) {
     const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -906,19 +956,30 @@ static hipError_t launch_mm(const PfArgs& a, uint32_t n_units_max, uint32_t n_cu
     attr_set = true;
   }
   const uint32_t grid = n_units_max < n_cu ? n_units_max : n_cu;
-  hipLaunchKernelGGL((k_pf_mm<BITS, G, MODE, SPLIT>), dim3(grid), dim3(64 * C::NW), lds, st, a,
+  hipLaunchKernelGGL((k_pf_mm<BITS, G, MODE, SPLIT, KU>), dim3(grid), dim3(64 * C::NW), lds, st, a,
                      (const uint32_t*)a.items, (const uint32_t*)a.n_items);
   return hipGetLastError();
 }
 
+// Per-unit scale staging (KU = K) where it fits in LDS: the A3B-shape gate/up
+// GEMM (bf16 x, hidden 2048, group 64 or 128) and down GEMM (inter 512,
+// group 64); other shapes copy scales per chunk.
 template <int BITS, int G>
 static hipError_t launch_gemms(const PfArgs& a, uint32_t n_cu, hipStream_t st) {
-  hipError_t e = a.x_bf16 ? launch_mm<BITS, G, 0, false>(a, a.max_items * (a.g.inter / 64), n_cu, st)
-                          : launch_mm<BITS, G, 0, true>(a, a.max_items * (a.g.inter / 64), n_cu, st);
+  const uint32_t gu_units = a.max_items * (a.g.inter / 64);
+  hipError_t e;
+  if (!a.x_bf16)
+    e = launch_mm<BITS, G, 0, true, 0>(a, gu_units, n_cu, st);
+  else if ((G == 64 || G == 128) && a.g.hidden == 2048)
+    e = launch_mm<BITS, G, 0, false, (G == 64 || G == 128) ? 2048 : 0>(a, gu_units, n_cu, st);
+  else
+    e = launch_mm<BITS, G, 0, false, 0>(a, gu_units, n_cu, st);
   if (e != hipSuccess) return e;
   const uint32_t nk = a.n_tokens * a.k;
   hipLaunchKernelGGL(k_pf_act_sum, dim3(nk), dim3(256), 0, st, a);
-  return launch_mm<BITS, G, 1, true>(a, a.max_items * (a.g.hidden / 256), n_cu, st);
+  const uint32_t dn_units = a.max_items * (a.g.hidden / 256);
+  if (G == 64 && a.g.inter == 512) return launch_mm<BITS, G, 1, true, G == 64 ? 512 : 0>(a, dn_units, n_cu, st);
+  return launch_mm<BITS, G, 1, true, 0>(a, dn_units, n_cu, st);
 }
 
 hipError_t launch_prefill(const PfArgs& a, uint32_t n_cu, hipStream_t st) {
@@ -1019,10 +1080,12 @@ hipError_t launch_qmm(const PfArgs& a, const float* x, uint32_t n_cu, hipStream_
                      a.act_hi, a.act_lo, a.asum, a.items, a.n_items);
   const uint32_t units = a.max_items * (a.g.hidden / 256), G = a.g.group;
   if (a.g.bits == 4)
-    return G == 32 ? launch_mm<4, 32, 1, true>(a, units, n_cu, st)
-                   : G == 64 ? launch_mm<4, 64, 1, true>(a, units, n_cu, st) : launch_mm<4, 128, 1, true>(a, units, n_cu, st);
-  return G == 32 ? launch_mm<3, 32, 1, true>(a, units, n_cu, st)
-                 : G == 64 ? launch_mm<3, 64, 1, true>(a, units, n_cu, st) : launch_mm<3, 128, 1, true>(a, units, n_cu, st);
+    return G == 32 ? launch_mm<4, 32, 1, true, 0>(a, units, n_cu, st)
+                   : G == 64 ? launch_mm<4, 64, 1, true, 0>(a, units, n_cu, st)
+                             : launch_mm<4, 128, 1, true, 0>(a, units, n_cu, st);
+  return G == 32 ? launch_mm<3, 32, 1, true, 0>(a, units, n_cu, st)
+                 : G == 64 ? launch_mm<3, 64, 1, true, 0>(a, units, n_cu, st)
+                           : launch_mm<3, 128, 1, true, 0>(a, units, n_cu, st);
 }
 
 }  // namespace smoe
