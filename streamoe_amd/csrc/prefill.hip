@@ -352,15 +352,18 @@ struct PfMM {
   static constexpr int P_BQ = ROWS * PPR;             // 16-byte code parts
   static constexpr int P_BS = USB ? 0 : ROWS * 2 * SB_PIECES;  // scale / bias pieces
   static constexpr int P_A = kPfMC * KC * 2 / 16;     // 16-byte A parts (per half)
-  static constexpr int P_XS = kPfMC * CG;             // group sums
+  static constexpr int P_XS = USB ? 0 : kPfMC * CG;  // group sums ([group][row] per chunk)
   static constexpr int P_US = USB ? ROWS * (2 * (2 * NGU / 16) + 1) : 0;  // unit scale slots (16 B, one pad per row)
   static constexpr int N_BQ = (P_BQ / NW + 63) / 64;  // copy instructions per wave
   static constexpr int N_BS = (P_BS / NW + 63) / 64;
   static constexpr int N_A = P_A / NW / 64;           // one row pair (m, m + 16) each
   static constexpr int N_XS = (P_XS / NW + 63) / 64;
   static constexpr int N_US = (P_US / NW + 63) / 64;
+  // With USB the A group sums also come once per unit: [row][NGU] f32.
+  static constexpr int P_UXS = USB ? kPfMC * NGU / 4 : 0;  // 16-byte pieces
+  static constexpr int N_UXS = (P_UXS / NW + 63) / 64;
   static constexpr int D = N_BQ + N_BS + N_A * (SPLIT ? 2 : 1) + N_XS;  // per chunk
-  static constexpr int DU = N_US;                                         // per unit
+  static constexpr int DU = N_US + N_UXS;                                 // per unit
   // LDS layout of one stage (bytes). A rows sit in pairs: row m at slot
   // 2 (m % 16) + m / 16, so one copy instruction moves rows m and m + 16.
   static constexpr int OFF_BQ = 0;
@@ -369,12 +372,15 @@ struct PfMM {
   static constexpr int OFF_AL = OFF_AH + P_A * 16;
   static constexpr int OFF_XS = OFF_AL + (SPLIT ? P_A * 16 : 0);
   static constexpr int STAGE = OFF_XS + P_XS * 4;
-  static constexpr int UBUF = USB ? ROWS * SB_ROW : 0;  // one unit buffer, after the stages
+  static constexpr int OFF_UXS = ROWS * SB_ROW;           // group sums in a unit buffer
+  static constexpr int UBUF = USB ? OFF_UXS + P_UXS * 16 : 0;  // one unit buffer, after the stages
   static constexpr int LDS = S * STAGE + 2 * UBUF;
   // Accumulators per lane, exchanged between the K halves through LDS.
   static constexpr int NT = NMAT * CT * 2 * 4;
   static_assert(CG % 2 == 0, "K halves");
-  static_assert(P_BQ % NW == 0 && P_BS % NW == 0 && P_XS % NW == 0 && P_US % NW == 0, "equal shares");
+  static_assert(P_BQ % NW == 0 && P_BS % NW == 0 && P_XS % NW == 0 && P_US % NW == 0 && P_UXS % NW == 0,
+                "equal shares");
+  static_assert(!USB || NGU % 4 == 0, "unit group sums in 16-byte pieces");
   static_assert(N_A * NW * 64 == P_A && P_A == 16 * 64, "one row pair per A copy");
   static_assert((S - 2) * D + DU <= 63, "vmcnt range");
   static_assert(LDS <= 160 * 1024, "LDS per CU");
@@ -402,7 +408,7 @@ __device__ __forceinline__ u32x4 codes_bf16_4p(uint32_t d, uint32_t c43) {
 // the stage at st, NTL 16-row tiles, into tot. Straight-line code (no
 // branches), so the scheduler can overlap LDS reads with MFMAs.
 template <int BITS, int G, int MODE, bool SPLIT, int KU, int NTL>
-__device__ __forceinline__ void pf_chunk(const uint8_t* st, const uint8_t* sbb, uint32_t gofs, uint32_t gl0,
+__device__ __forceinline__ void pf_chunk(const uint8_t* st, const uint8_t* sbb, const float* uxs, uint32_t gofs, uint32_t gl0,
                                          uint32_t cw, uint32_t n, uint32_t q, uint32_t c43,
                                          f32x4 (&tot)[PfMM<BITS, G, MODE, SPLIT, KU>::NMAT][PfMM<BITS, G, MODE, SPLIT, KU>::CT][2]) {
   using C = PfMM<BITS, G, MODE, SPLIT, KU>;
@@ -483,8 +489,15 @@ __device__ __forceinline__ void pf_chunk(const uint8_t* st, const uint8_t* sbb, 
             if (SPLIT) acc[mt][ct] = mfma(al, bq[mt][ct][uu], acc[mt][ct]);
           }
       }
-      // Group sums of rows 16t + 4q .. + 3 in one read ([group][row]).
-      const f32x4 xs = *reinterpret_cast<const f32x4*>(st + C::OFF_XS + (gl * kPfMC + 16 * t + 4 * q) * 4);
+      // Group sums of rows 16t + 4q .. + 3: one read from the stage
+      // ([group][row]), or four from the unit buffer ([row][NGU]).
+      f32x4 xs;
+      if constexpr (C::USB) {
+        const float* xr = uxs + (16 * t + 4 * q) * C::NGU + gofs + gl;
+        xs = f32x4{xr[0], xr[C::NGU], xr[2 * C::NGU], xr[3 * C::NGU]};
+      } else {
+        xs = *reinterpret_cast<const f32x4*>(st + C::OFF_XS + (gl * kPfMC + 16 * t + 4 * q) * 4);
+      }
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -607,6 +620,17 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
     for (int i = 0; i < C::N_US; ++i)
       if ((C::P_US / C::NW) % 64 == 0 || i * 64 + lane < (uint32_t)(C::P_US / C::NW))
         dma16(u.bs + off_us[i], ubuf + (wave * (C::P_US / C::NW) + i * 64) * 16);
+    // Group sums: piece p = (row m, piece in row); rows >= cnt repeat row
+    // cnt - 1.
+    constexpr uint32_t XPR = C::NGU / 4;  // pieces per row
+#pragma unroll
+    for (int i = 0; i < C::N_UXS; ++i) {
+      const uint32_t p = wave * (C::P_UXS / C::NW) + i * 64 + lane;
+      const uint32_t m = p / XPR, pc = p % XPR;
+      if ((C::P_UXS / C::NW) % 64 == 0 || i * 64 + lane < (uint32_t)(C::P_UXS / C::NW))
+        dma16(u.xs + (size_t)min(m, u.cnt - 1) * ng * 4 + pc * 16,
+              ubuf + C::OFF_UXS + (wave * (C::P_UXS / C::NW) + i * 64) * 16);
+    }
   };
   auto issue = [=](const UnitSrc& u, uint32_t c, uint32_t slot) {
     const uint32_t cnt = u.cnt;
@@ -713,12 +737,14 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
     const uint32_t start = c_start, cnt = c_cnt, cb = c_cb;
     uint8_t* st = lds + cslot * C::STAGE;
     cslot = cslot + 1 == (uint32_t)C::S ? 0u : cslot + 1;
-    const uint8_t* sbb = C::USB ? lds + C::S * C::STAGE + cub * C::UBUF : st + C::OFF_BS;
+    const uint8_t* ub = lds + C::S * C::STAGE + cub * C::UBUF;
+    const uint8_t* sbb = C::USB ? ub : st + C::OFF_BS;
+    const float* uxs = reinterpret_cast<const float*>(ub + C::OFF_UXS);
     const uint32_t gofs = C::USB ? cc * C::CG : 0u;
     if (cnt > 16)
-      pf_chunk<BITS, G, MODE, SPLIT, KU, 2>(st, sbb, gofs, kh * C::CGW, cw, n, q, c43, tot);
+      pf_chunk<BITS, G, MODE, SPLIT, KU, 2>(st, sbb, uxs, gofs, kh * C::CGW, cw, n, q, c43, tot);
     else
-      pf_chunk<BITS, G, MODE, SPLIT, KU, 1>(st, sbb, gofs, kh * C::CGW, cw, n, q, c43, tot);
+      pf_chunk<BITS, G, MODE, SPLIT, KU, 1>(st, sbb, uxs, gofs, kh * C::CGW, cw, n, q, c43, tot);
 
     if (++cc == nch) {  // unit complete: add the K halves, write it out
       cc = 0;
