@@ -323,9 +323,14 @@ __device__ __forceinline__ void dma4(const void* g, void* l) {
 // [v0, v4, v1, v5, v2, v6, v3, v7].
 __device__ __forceinline__ uint32_t perm8_pos(uint32_t i) { return i < 4 ? 2 * i : 2 * (i - 4) + 1; }
 
-template <int BITS, int G, int MODE, bool SPLIT, int KU = 0>
+template <int BITS, int G, int MODE, bool SPLIT, int KU = 0, int NWD = 0>
 struct PfMM {
-  static constexpr int NW = 8;                        // waves per block: 4 column waves x 2 K halves
+  // Compute waves: 4 column waves x 2 K halves. With NWD > 0, NWD more
+  // waves only copy (their issue stalls on the memory pipeline never delay
+  // the MFMA work); else the compute waves copy too.
+  static constexpr int NWC = 8;
+  static constexpr int NWT = NWC + NWD;               // waves per block
+  static constexpr int NW = NWD > 0 ? NWD : NWC;      // copying waves
   static constexpr int KC = kPfKC;                    // inputs per chunk
   static constexpr int CG = KC / G;                   // groups per chunk
   static constexpr int CGW = CG / 2;                  // groups per wave (its K half of the chunk)
@@ -383,6 +388,7 @@ struct PfMM {
   static_assert(!USB || NGU % 4 == 0, "unit group sums in 16-byte pieces");
   static_assert(N_A * NW * 64 == P_A && P_A == 16 * 64, "one row pair per A copy");
   static_assert((S - 2) * D + DU <= 63, "vmcnt range");
+  static_assert(NWD == 0 || (MODE == 0 && USB), "copy waves: unit-staged gate/up only");
   static_assert(LDS <= 160 * 1024, "LDS per CU");
   static_assert(4 * NT * 64 * 4 <= STAGE, "accumulator exchange fits a stage");
   static_assert(!USB || (2 * NGU) % 16 == 0, "unit scale rows in 16-byte pieces");
@@ -510,13 +516,16 @@ __device__ __forceinline__ void pf_chunk(const uint8_t* st, const uint8_t* sbb, 
   }
 }
 
-template <int BITS, int G, int MODE, bool SPLIT, int KU>
-__global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restrict__ items,
-                                               const uint32_t* __restrict__ n_items_p) {
-  using C = PfMM<BITS, G, MODE, SPLIT, KU>;
+template <int BITS, int G, int MODE, bool SPLIT, int KU, int NWD>
+__global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32_t* __restrict__ items,
+                                                          const uint32_t* __restrict__ n_items_p) {
+  using C = PfMM<BITS, G, MODE, SPLIT, KU, NWD>;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t cw = wave & 3, kh = wave >> 2;  // column wave, K half
+  const uint32_t cw = wave & 3, kh = (wave >> 2) & 1;  // column wave, K half (compute waves)
+  const bool copier = NWD == 0 || wave >= (uint32_t)C::NWC;   // issues copies
+  const bool computer = NWD == 0 || wave < (uint32_t)C::NWC;  // runs MFMAs
+  const uint32_t dw = NWD > 0 ? wave - C::NWC : wave;          // copy share index
   const uint32_t n = lane & 15, q = lane >> 4;
   // Every kernel argument used below is copied into a scalar local first,
   // so that nothing takes the argument block's address (that would move it
@@ -556,7 +565,7 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
   uint32_t off_bq[C::N_BQ], off_bs[C::N_BS > 0 ? C::N_BS : 1], off_us[C::N_US > 0 ? C::N_US : 1];
 #pragma unroll
   for (int i = 0; i < C::N_BQ; ++i) {
-    const uint32_t p = wave * (C::P_BQ / C::NW) + i * 64 + lane;
+    const uint32_t p = dw * (C::P_BQ / C::NW) + i * 64 + lane;
     const uint32_t row = p / C::PPR, sp = p % C::PPR;
     const uint32_t part = BITS == 4 ? (sp ^ (row & 7)) : (sp + row) % C::PPR;
     const uint32_t mat = row / C::NCOL;
@@ -564,7 +573,7 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
   }
 #pragma unroll
   for (int i = 0; i < C::N_BS; ++i) {
-    const uint32_t p = wave * (C::P_BS / C::NW) + i * 64 + lane;
+    const uint32_t p = dw * (C::P_BS / C::NW) + i * 64 + lane;
     const uint32_t row = p / (2 * C::SB_PIECES), arr = (p / C::SB_PIECES) % 2, pc = p % C::SB_PIECES;
     const uint32_t mat = row / C::NCOL;
     // Biases follow scales at the same distance in both matrices.
@@ -577,7 +586,7 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
   constexpr uint32_t UPC = 2 * C::NGU / 16;  // pieces per row and array
 #pragma unroll
   for (int i = 0; i < C::N_US; ++i) {
-    const uint32_t p = wave * (C::P_US / C::NW) + i * 64 + lane;
+    const uint32_t p = dw * (C::P_US / C::NW) + i * 64 + lane;
     const uint32_t row = p / (2 * UPC + 1), r = p % (2 * UPC + 1);
     const uint32_t arr = r < 2 * UPC ? r / UPC : 0u, pc = r < 2 * UPC ? r % UPC : 0u;
     const uint32_t mat = row / C::NCOL;
@@ -619,17 +628,17 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
 #pragma unroll
     for (int i = 0; i < C::N_US; ++i)
       if ((C::P_US / C::NW) % 64 == 0 || i * 64 + lane < (uint32_t)(C::P_US / C::NW))
-        dma16(u.bs + off_us[i], ubuf + (wave * (C::P_US / C::NW) + i * 64) * 16);
+        dma16(u.bs + off_us[i], ubuf + (dw * (C::P_US / C::NW) + i * 64) * 16);
     // Group sums: piece p = (row m, piece in row); rows >= cnt repeat row
     // cnt - 1.
     constexpr uint32_t XPR = C::NGU / 4;  // pieces per row
 #pragma unroll
     for (int i = 0; i < C::N_UXS; ++i) {
-      const uint32_t p = wave * (C::P_UXS / C::NW) + i * 64 + lane;
+      const uint32_t p = dw * (C::P_UXS / C::NW) + i * 64 + lane;
       const uint32_t m = p / XPR, pc = p % XPR;
       if ((C::P_UXS / C::NW) % 64 == 0 || i * 64 + lane < (uint32_t)(C::P_UXS / C::NW))
         dma16(u.xs + (size_t)min(m, u.cnt - 1) * ng * 4 + pc * 16,
-              ubuf + C::OFF_UXS + (wave * (C::P_UXS / C::NW) + i * 64) * 16);
+              ubuf + C::OFF_UXS + (dw * (C::P_UXS / C::NW) + i * 64) * 16);
     }
   };
   auto issue = [=](const UnitSrc& u, uint32_t c, uint32_t slot) {
@@ -641,12 +650,12 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
 #pragma unroll
     for (int i = 0; i < C::N_BQ; ++i)
       if ((C::P_BQ / C::NW) % 64 == 0 || i * 64 + lane < (uint32_t)(C::P_BQ / C::NW))
-        dma16(bq_base + off_bq[i], st + C::OFF_BQ + (wave * (C::P_BQ / C::NW) + i * 64) * 16);
+        dma16(bq_base + off_bq[i], st + C::OFF_BQ + (dw * (C::P_BQ / C::NW) + i * 64) * 16);
     // Scales then biases of each row: [row][array][CG] bf16.
     const uint8_t* bs_base = u.bs + (size_t)c * C::CG * 2;
 #pragma unroll
     for (int i = 0; i < C::N_BS; ++i) {
-      uint8_t* dst = st + C::OFF_BS + (wave * (C::P_BS / C::NW) + i * 64) * C::SB_SZ;
+      uint8_t* dst = st + C::OFF_BS + (dw * (C::P_BS / C::NW) + i * 64) * C::SB_SZ;
       if ((C::P_BS / C::NW) % 64 == 0 || i * 64 + lane < (uint32_t)(C::P_BS / C::NW)) {
         if (C::SB_SZ == 16) dma16(bs_base + off_bs[i], dst); else dma4(bs_base + off_bs[i], dst);
       }
@@ -658,7 +667,7 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
       const uint8_t* a_base = (hl ? u.al : u.ah) + (size_t)c * C::KC * 2;
 #pragma unroll
       for (int i = 0; i < C::N_A; ++i) {
-        const uint32_t pair = wave * C::N_A + i, half = lane >> 5, sp = lane & 31;
+        const uint32_t pair = dw * C::N_A + i, half = lane >> 5, sp = lane & 31;
         const uint32_t m = pair + 16 * half;
         const uint32_t off = min(m, cnt - 1) * K * 2 + (sp ^ pair) * 16;
         if (half == 0 || cnt > 16)
@@ -670,10 +679,10 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
 #pragma unroll
     for (int i = 0; i < C::N_XS; ++i) {
       const uint32_t o = i * 64 + lane;
-      const uint32_t p = wave * (C::P_XS / C::NW) + o;
+      const uint32_t p = dw * (C::P_XS / C::NW) + o;
       const uint32_t g = p / kPfMC, m = p % kPfMC;
       if ((C::P_XS / C::NW) % 64 == 0 || o < (uint32_t)(C::P_XS / C::NW))
-        dma4(xs_base + (min(m, cnt - 1) * ng + g) * 4, st + C::OFF_XS + (wave * (C::P_XS / C::NW) + i * 64) * 4);
+        dma4(xs_base + (min(m, cnt - 1) * ng + g) * 4, st + C::OFF_XS + (dw * (C::P_XS / C::NW) + i * 64) * 4);
     }
   };
 
@@ -690,8 +699,10 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
   uint32_t iv = lb, ic = 0, islot = 0, issued = 0, iub = 0;
   UnitSrc isrc = unit_src(iv);
   for (; issued + 1 < (uint32_t)C::S && issued < total; ++issued) {
-    if (C::USB && ic == 0) issue_unit(isrc, iub);
-    issue(isrc, ic, islot);
+    if (copier) {
+      if (C::USB && ic == 0) issue_unit(isrc, iub);
+      issue(isrc, ic, islot);
+    }
     islot = islot + 1 == (uint32_t)C::S ? 0u : islot + 1;
     if (++ic == nch) {
       ic = 0;
@@ -709,7 +720,9 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
     // most one of the next two does).
     const uint32_t ahead = min((uint32_t)C::S - 2, total - 1 - j);
     const bool ustart = C::USB && ((ahead >= 1 && cc + 1 == nch) || (ahead >= 2 && cc + 2 == nch));
-    if (ahead == 0)
+    if (!copier)
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    else if (ahead == 0)
       asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     else if (ahead == 1 && !ustart)
       asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(C::D) : "memory");
@@ -722,8 +735,10 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     if (issued < total) {
-      if (C::USB && ic == 0) issue_unit(isrc, iub);
-      issue(isrc, ic, islot);
+      if (copier) {
+        if (C::USB && ic == 0) issue_unit(isrc, iub);
+        issue(isrc, ic, islot);
+      }
       ++issued;
       islot = islot + 1 == (uint32_t)C::S ? 0u : islot + 1;
       if (++ic == nch) {
@@ -741,10 +756,12 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
     const uint8_t* sbb = C::USB ? ub : st + C::OFF_BS;
     const float* uxs = reinterpret_cast<const float*>(ub + C::OFF_UXS);
     const uint32_t gofs = C::USB ? cc * C::CG : 0u;
-    if (cnt > 16)
-      pf_chunk<BITS, G, MODE, SPLIT, KU, 2>(st, sbb, uxs, gofs, kh * C::CGW, cw, n, q, c43, tot);
-    else
-      pf_chunk<BITS, G, MODE, SPLIT, KU, 1>(st, sbb, uxs, gofs, kh * C::CGW, cw, n, q, c43, tot);
+    if (computer) {
+      if (cnt > 16)
+        pf_chunk<BITS, G, MODE, SPLIT, KU, 2>(st, sbb, uxs, gofs, kh * C::CGW, cw, n, q, c43, tot);
+      else
+        pf_chunk<BITS, G, MODE, SPLIT, KU, 1>(st, sbb, uxs, gofs, kh * C::CGW, cw, n, q, c43, tot);
+    }
 
     if (++cc == nch) {  // unit complete: add the K halves, write it out
       cc = 0;
@@ -762,7 +779,7 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
       float* ex = reinterpret_cast<float*>(st) + cw * C::NT * 64 + lane;
-      if (kh == 1) {
+      if (computer && kh == 1) {
 #pragma unroll
         for (int mt = 0; mt < C::NMAT; ++mt)
 #pragma unroll
@@ -775,7 +792,7 @@ __global__ __launch_bounds__(512) void k_pf_mm(PfArgs a, const uint32_t* __restr
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
-      if (kh == 0) {
+      if (computer && kh == 0) {
         const uint32_t ntiles = cnt > 16 ? 2 : 1;
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
@@ -970,10 +987,10 @@ bool prefill_supported(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t
   return true;
 }
 
-template <int BITS, int G, int MODE, bool SPLIT, int KU>
+template <int BITS, int G, int MODE, bool SPLIT, int KU, int NWD = 0>
 static hipError_t launch_mm(const PfArgs& a, uint32_t n_units_max, uint32_t n_cu, hipStream_t st) {
-  using C = PfMM<BITS, G, MODE, SPLIT, KU>;
-  const auto fn = reinterpret_cast<const void*>(&k_pf_mm<BITS, G, MODE, SPLIT, KU>);
+  using C = PfMM<BITS, G, MODE, SPLIT, KU, NWD>;
+  const auto fn = reinterpret_cast<const void*>(&k_pf_mm<BITS, G, MODE, SPLIT, KU, NWD>);
   const size_t lds = (size_t)C::LDS;
   static bool attr_set = false;
   if (!attr_set) {
@@ -982,7 +999,7 @@ static hipError_t launch_mm(const PfArgs& a, uint32_t n_units_max, uint32_t n_cu
     attr_set = true;
   }
   const uint32_t grid = n_units_max < n_cu ? n_units_max : n_cu;
-  hipLaunchKernelGGL((k_pf_mm<BITS, G, MODE, SPLIT, KU>), dim3(grid), dim3(64 * C::NW), lds, st, a,
+  hipLaunchKernelGGL((k_pf_mm<BITS, G, MODE, SPLIT, KU, NWD>), dim3(grid), dim3(64 * C::NWT), lds, st, a,
                      (const uint32_t*)a.items, (const uint32_t*)a.n_items);
   return hipGetLastError();
 }
@@ -997,7 +1014,7 @@ static hipError_t launch_gemms(const PfArgs& a, uint32_t n_cu, hipStream_t st) {
   if (!a.x_bf16)
     e = launch_mm<BITS, G, 0, true, 0>(a, gu_units, n_cu, st);
   else if ((G == 64 || G == 128) && a.g.hidden == 2048)
-    e = launch_mm<BITS, G, 0, false, (G == 64 || G == 128) ? 2048 : 0>(a, gu_units, n_cu, st);
+    e = launch_mm<BITS, G, 0, false, (G == 64 || G == 128) ? 2048 : 0, (G == 64 || G == 128) ? 4 : 0>(a, gu_units, n_cu, st);
   else
     e = launch_mm<BITS, G, 0, false, 0>(a, gu_units, n_cu, st);
   if (e != hipSuccess) return e;
