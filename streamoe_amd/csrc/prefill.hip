@@ -414,7 +414,7 @@ __device__ __forceinline__ u32x4 codes_bf16_4p(uint32_t d, uint32_t c43) {
 // the stage at st, NTL 16-row tiles, into tot. Straight-line code (no
 // branches), so the scheduler can overlap LDS reads with MFMAs.
 template <int BITS, int G, int MODE, bool SPLIT, int KU, int NTL>
-__device__ __forceinline__ void pf_chunk(const uint8_t* st, const uint8_t* sbb, const float* uxs, uint32_t gofs, uint32_t gl0,
+__device__ __forceinline__ void pf_chunk_seq(const uint8_t* st, const uint8_t* sbb, const float* uxs, uint32_t gofs, uint32_t gl0,
                                          uint32_t cw, uint32_t n, uint32_t q, uint32_t c43,
                                          f32x4 (&tot)[PfMM<BITS, G, MODE, SPLIT, KU>::NMAT][PfMM<BITS, G, MODE, SPLIT, KU>::CT][2]) {
   using C = PfMM<BITS, G, MODE, SPLIT, KU>;
@@ -512,6 +512,177 @@ __device__ __forceinline__ void pf_chunk(const uint8_t* st, const uint8_t* sbb, 
           for (int ct = 0; ct < C::CT; ++ct)
             tot[mt][ct][t][r] =
                 __builtin_fmaf(s[mt][ct], acc[mt][ct][r], __builtin_fmaf(cbias[mt][ct], xs[r], tot[mt][ct][t][r]));
+    }
+  }
+}
+
+// Codes of group gl, matrix row `row`, lane block q (NU words) from a stage.
+template <int BITS, int G, int MODE, bool SPLIT, int KU>
+__device__ __forceinline__ void pf_codes(const uint8_t* st, uint32_t row, uint32_t gl, uint32_t q,
+                                         uint32_t (&bw)[PfMM<BITS, G, MODE, SPLIT, KU>::NU]) {
+  using C = PfMM<BITS, G, MODE, SPLIT, KU>;
+  const uint8_t* rb = st + C::OFF_BQ + row * C::RB;
+  if (BITS == 4) {
+    const uint32_t off = gl * (G / 2) + 4 * C::NU * q;  // byte offset in the chunk row
+    const uint32_t slot = (off / 16) ^ (row & 7);
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(rb + slot * 16 + off % 16);
+#pragma unroll
+    for (int uu = 0; uu < C::NU; ++uu) bw[uu] = w[uu];
+  } else {
+    const uint32_t off = (gl * G + 8 * C::NU * q) * 3 / 8;  // 3*NU bytes
+    constexpr int ND = (3 * C::NU + 6) / 4;
+    uint32_t d[ND];
+#pragma unroll
+    for (int i = 0; i < ND; ++i) {
+      const uint32_t dw = (off & ~3u) / 4 + i;  // dword index in the row (0 .. RB/4)
+      const uint32_t part = min(dw / 4, (uint32_t)C::PPR - 1);
+      const uint32_t slot = (part + C::PPR - row % C::PPR) % C::PPR;
+      d[i] = *reinterpret_cast<const uint32_t*>(rb + slot * 16 + (dw % 4) * 4);
+    }
+    const uint32_t sh = (off & 3u) * 8;
+#pragma unroll
+    for (int uu = 0; uu < C::NU; ++uu) {
+      const uint32_t bit = sh + 24 * uu;
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int i = 0; i < ND; ++i) {
+        if ((uint32_t)i == (bit >> 5)) lo = d[i];
+        if ((uint32_t)i == (bit >> 5) + 1) hi = d[i];
+      }
+      bw[uu] = __builtin_amdgcn_alignbit(hi, lo, bit & 31) & 0xFFFFFFu;
+    }
+  }
+}
+
+// The MFMA work of one chunk for one wave, in phases: every LDS read of the
+// chunk (codes, scales, A rows, group sums of all CGW groups and NTL tiles)
+// is issued first, so the wave waits for LDS once per chunk instead of once
+// per group; then the code conversions and MFMAs of all groups, then the
+// dequant epilogue. Straight-line code (no branches).
+template <int BITS, int G, int MODE, bool SPLIT, int KU, int NTL>
+__device__ __forceinline__ void pf_chunk(const uint8_t* st, const uint8_t* sbb, const float* uxs, uint32_t gofs,
+                                         uint32_t gl0, uint32_t cw, uint32_t n, uint32_t q, uint32_t c43,
+                                         f32x4 (&tot)[PfMM<BITS, G, MODE, SPLIT, KU>::NMAT][PfMM<BITS, G, MODE, SPLIT, KU>::CT][2]) {
+  using C = PfMM<BITS, G, MODE, SPLIT, KU>;
+  if constexpr (MODE != 0) {
+    pf_chunk_seq<BITS, G, MODE, SPLIT, KU, NTL>(st, sbb, uxs, gofs, gl0, cw, n, q, c43, tot);
+  } else {
+    constexpr int NG = C::CGW;
+    uint32_t bw[NG][C::NMAT][C::CT][C::NU];
+    uint16_t sr[NG][C::NMAT][C::CT], br[NG][C::NMAT][C::CT];
+    u32x4 ah[NG][NTL][C::NU], al[NG][NTL][C::NU];
+    f32x4 xs[NG][NTL];
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi) {
+      const uint32_t gl = gl0 + gi;
+#pragma unroll
+      for (int mt = 0; mt < C::NMAT; ++mt)
+#pragma unroll
+        for (int ct = 0; ct < C::CT; ++ct) {
+          const uint32_t row = mt * C::NCOL + cw * 16 * C::CT + ct * 16 + n;
+          pf_codes<BITS, G, MODE, SPLIT, KU>(st, row, gl, q, bw[gi][mt][ct]);
+          const uint16_t* sb = reinterpret_cast<const uint16_t*>(sbb + row * C::SB_ROW) + gofs;
+          sr[gi][mt][ct] = sb[gl];
+          br[gi][mt][ct] = sb[C::NGU + gl];
+        }
+#pragma unroll
+      for (int t = 0; t < NTL; ++t) {
+#pragma unroll
+        for (int uu = 0; uu < C::NU; ++uu) {
+          const uint32_t part = (gl * G + 8 * C::NU * q + 8 * uu) / 8;
+          const uint32_t aoff = (2 * n + t) * C::KC * 2 + ((part ^ n) * 16);
+          ah[gi][t][uu] = *reinterpret_cast<const u32x4*>(st + C::OFF_AH + aoff);
+          if (SPLIT) al[gi][t][uu] = *reinterpret_cast<const u32x4*>(st + C::OFF_AL + aoff);
+        }
+        if constexpr (C::USB) {
+          const float* xr = uxs + (16 * t + 4 * q) * C::NGU + gofs + gl;
+          xs[gi][t] = f32x4{xr[0], xr[C::NGU], xr[2 * C::NGU], xr[3 * C::NGU]};
+        } else {
+          xs[gi][t] = *reinterpret_cast<const f32x4*>(st + C::OFF_XS + (gl * kPfMC + 16 * t + 4 * q) * 4);
+        }
+      }
+    }
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi) {
+      float s[C::NMAT][C::CT], cbias[C::NMAT][C::CT];
+      u32x4 bq[C::NMAT][C::CT][C::NU];
+#pragma unroll
+      for (int mt = 0; mt < C::NMAT; ++mt)
+#pragma unroll
+        for (int ct = 0; ct < C::CT; ++ct) {
+          s[mt][ct] = bf16f(sr[gi][mt][ct]);
+          cbias[mt][ct] = __builtin_fmaf(-128.0f, s[mt][ct], bf16f(br[gi][mt][ct]));
+#pragma unroll
+          for (int uu = 0; uu < C::NU; ++uu)
+            bq[mt][ct][uu] = BITS == 4 ? codes_bf16_4p(bw[gi][mt][ct][uu], c43) : codes_bf16_3(bw[gi][mt][ct][uu]);
+        }
+#pragma unroll
+      for (int t = 0; t < NTL; ++t) {
+        f32x4 acc[C::NMAT][C::CT];
+#pragma unroll
+        for (int mt = 0; mt < C::NMAT; ++mt)
+#pragma unroll
+          for (int ct = 0; ct < C::CT; ++ct) acc[mt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int uu = 0; uu < C::NU; ++uu)
+#pragma unroll
+          for (int mt = 0; mt < C::NMAT; ++mt)
+#pragma unroll
+            for (int ct = 0; ct < C::CT; ++ct) {
+              acc[mt][ct] = mfma(ah[gi][t][uu], bq[mt][ct][uu], acc[mt][ct]);
+              if (SPLIT) acc[mt][ct] = mfma(al[gi][t][uu], bq[mt][ct][uu], acc[mt][ct]);
+            }
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int mt = 0; mt < C::NMAT; ++mt)
+#pragma unroll
+            for (int ct = 0; ct < C::CT; ++ct) {
+              // With unit buffers the bias term sum_g cbias_g * xs_g is added
+              // once per unit by fp32 MFMAs (pf_unit_bias).
+              if constexpr (C::USB)
+                tot[mt][ct][t][r] = __builtin_fmaf(s[mt][ct], acc[mt][ct][r], tot[mt][ct][t][r]);
+              else
+                tot[mt][ct][t][r] = __builtin_fmaf(s[mt][ct], acc[mt][ct][r],
+                                                   __builtin_fmaf(cbias[mt][ct], xs[gi][t][r], tot[mt][ct][t][r]));
+            }
+      }
+    }
+  }
+}
+
+// The bias part of the dequant epilogue for a whole unit (gate/up with unit
+// buffers): tot[m][c] += sum over this wave's groups g of (b - 128 s)[c][g] *
+// xs[m][g], as v_mfma_f32_16x16x4_f32 (A = group sums [16 rows x 4 groups],
+// B = column biases [4 groups x 16 columns]); the output layout is the
+// 16x16 layout of the bf16 MFMAs. Wave K half kh owns groups
+// c * CG + kh * CGW + gi of every chunk c.
+template <int BITS, int G, int MODE, bool SPLIT, int KU>
+__device__ __forceinline__ void pf_unit_bias(const uint8_t* ub, uint32_t nch, uint32_t kh, uint32_t cw,
+                                             uint32_t lane, uint32_t ntiles,
+                                             f32x4 (&tot)[PfMM<BITS, G, MODE, SPLIT, KU>::NMAT][PfMM<BITS, G, MODE, SPLIT, KU>::CT][2]) {
+  using C = PfMM<BITS, G, MODE, SPLIT, KU>;
+  static_assert(C::USB && C::CT == 1, "gate/up with unit buffers");
+  const float* uxs = reinterpret_cast<const float*>(ub + C::OFF_UXS);
+  const uint32_t r16 = lane & 15, kq = lane >> 4;
+  const uint32_t nk = nch * C::CGW;  // groups of this K half
+  for (uint32_t j = 0; j * 4 < nk; ++j) {
+    const uint32_t e = 4 * j + kq;  // this lane's group slot
+    const uint32_t g = (e / C::CGW) * C::CG + kh * C::CGW + e % C::CGW;
+    float bb[C::NMAT];
+#pragma unroll
+    for (int mt = 0; mt < C::NMAT; ++mt) {
+      const uint32_t row = mt * C::NCOL + cw * 16 + r16;
+      const uint16_t* sb = reinterpret_cast<const uint16_t*>(ub + row * C::SB_ROW);
+      bb[mt] = __builtin_fmaf(-128.0f, bf16f(sb[g]), bf16f(sb[C::NGU + g]));
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      if ((uint32_t)t >= ntiles) break;
+      const float xa = uxs[(16 * t + r16) * C::NGU + g];
+#pragma unroll
+      for (int mt = 0; mt < C::NMAT; ++mt)
+        tot[mt][0][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, bb[mt], tot[mt][0][t], 0, 0, 0);
     }
   }
 }
@@ -764,6 +935,8 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
     }
 
     if (++cc == nch) {  // unit complete: add the K halves, write it out
+      if constexpr (MODE == 0 && C::USB)
+        if (computer) pf_unit_bias<BITS, G, MODE, SPLIT, KU>(ub, nch, kh, cw, lane, cnt > 16 ? 2u : 1u, tot);
       cc = 0;
       cub ^= 1u;
       cv += per;
