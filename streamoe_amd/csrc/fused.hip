@@ -17,9 +17,9 @@
 // dimension y).
 //
 //   K_A  k_fa_route    one wave per router row: x = RMSNorm(r) * w (or the
-//                      given input), logits[e] = W_e . x (row E: shared
-//                      gate); four more waves per token store x as integer
-//                      limbs for K_B (common.h, chunk_dot_i).
+//                      given input), logits[e] = W_e . x; four more waves
+//                      per token store x as integer limbs for K_B
+//                      (common.h, chunk_dot_i).
 //   K_B  k_fa_gateup   one wave per RW rows of one routed slot: the slot's
 //                      expert from the logits (every wave), then
 //                      act[s, i] = silu(gate_i . x) * (up_i . x); one wave
@@ -27,8 +27,8 @@
 //                      needs no routing and so streams its rows while the
 //                      routed waves select; one wave that publishes the
 //                      route table (expert blobs and renormalised weights,
-//                      the shared gate score) and, when asked, the
-//                      reference's exact slot order.
+//                      the shared gate score gate . x) and, when asked,
+//                      the reference's exact slot order.
 //   K_C  k_fa_down     one block per kFaRB hidden rows, one lane per (slot,
 //                      chunk of 32 activations): every slot's down rows,
 //                      combined in table order moe = fma(out_s, w_s, moe)
@@ -198,20 +198,41 @@ __device__ __forceinline__ FusedLayer token_view(const FusedLayer& a, uint32_t t
 // L2 when the kernel starts.
 #define FA_ARGS_IN_SGPRS(...) asm volatile("" ::__VA_ARGS__)
 
+// A 2048-wide f32 row (router row or shared-expert gate), chunk c per lane.
+__device__ __forceinline__ void fa_row_load(const float* row, uint32_t c, f32x4 (&wr)[kChunk / 4]) {
+  const f32x4* rp = reinterpret_cast<const f32x4*>(row + (size_t)c * kChunk);
+#pragma unroll
+  for (int i = 0; i < kChunk / 4; ++i) wr[i] = ld_stream(rp + i);
+}
+
+// row . x over the wave (valid in lane 63): four FMA chains per lane, then
+// the wave sum.
+__device__ __forceinline__ float fa_row_dot(const f32x4 (&wr)[kChunk / 4], const float (&x)[kChunk]) {
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+  for (int i = 0; i < kChunk / 4; ++i) {
+    a0 = __builtin_fmaf(wr[i].x, x[4 * i + 0], a0);
+    a1 = __builtin_fmaf(wr[i].y, x[4 * i + 1], a1);
+    a2 = __builtin_fmaf(wr[i].z, x[4 * i + 2], a2);
+    a3 = __builtin_fmaf(wr[i].w, x[4 * i + 3], a3);
+  }
+  return group_sum_last<64>((a0 + a1) + (a2 + a3));
+}
+
 // ---------------------------------------------------------------------------
-// K_A: router logits (+ shared gate) for T tokens: each wave reads its
+// K_A: router logits for T tokens: each wave reads its
 // router row once and applies it to every token's x. The last 4T waves
 // write x of the tokens as integer limbs for K_B.
 // ---------------------------------------------------------------------------
 template <int T>
 __global__ __launch_bounds__(64) void k_fa_route(FusedLayer a) {
-  FA_ARGS_IN_SGPRS("s"(a.x_in), "s"(a.resid), "s"(a.norm), "s"(a.eps), "s"(a.router), "s"(a.gate),
-                   "s"(a.E), "s"(a.logits), "s"(a.xl), "s"(a.trace), "s"(a.lstride), "s"(a.xstride));
+  FA_ARGS_IN_SGPRS("s"(a.x_in), "s"(a.resid), "s"(a.norm), "s"(a.eps), "s"(a.router), "s"(a.E),
+                   "s"(a.logits), "s"(a.xl), "s"(a.trace), "s"(a.lstride), "s"(a.xstride));
   FaClock clk;
   fa_stamp(a, clk, 0, false);
   const int lane = threadIdx.x;
   const uint32_t w = blockIdx.x;
-  const uint32_t nrouter = a.E + (a.gate ? 1u : 0u);
+  const uint32_t nrouter = a.E;
   const uint32_t c = lane;  // this lane's chunk of the hidden vector
 
   if (w >= nrouter) {
@@ -239,11 +260,8 @@ __global__ __launch_bounds__(64) void k_fa_route(FusedLayer a) {
     fa_flush(a, clk, 0);
     return;
   }
-  const float* row = w < a.E ? a.router + (size_t)w * kFaH : a.gate;
   f32x4 wr[kChunk / 4];
-  const f32x4* rp = reinterpret_cast<const f32x4*>(row + (size_t)c * kChunk);
-#pragma unroll
-  for (int i = 0; i < kChunk / 4; ++i) wr[i] = ld_stream(rp + i);
+  fa_row_load(a.router + (size_t)w * kFaH, c, wr);
   FaX f[T];
 #pragma unroll
   for (int t = 0; t < T; ++t) fa_x_load(token_view(a, t), lane, f[t]);
@@ -253,16 +271,7 @@ __global__ __launch_bounds__(64) void k_fa_route(FusedLayer a) {
   for (int t = 0; t < T; ++t) {
     const FusedLayer at = token_view(a, t);
     fa_x_finish(at, f[t]);
-    const float(&x)[kChunk] = f[t].x;
-    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-#pragma unroll
-    for (int i = 0; i < kChunk / 4; ++i) {
-      a0 = __builtin_fmaf(wr[i].x, x[4 * i + 0], a0);
-      a1 = __builtin_fmaf(wr[i].y, x[4 * i + 1], a1);
-      a2 = __builtin_fmaf(wr[i].z, x[4 * i + 2], a2);
-      a3 = __builtin_fmaf(wr[i].w, x[4 * i + 3], a3);
-    }
-    const float s = group_sum_last<64>((a0 + a1) + (a2 + a3));
+    const float s = fa_row_dot(wr, f[t].x);
     if (lane == 63) at.logits[w] = s;
   }
   fa_stamp(a, clk, 4, false);
@@ -390,9 +399,16 @@ __global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a_all) {
   } else {
     // Route table (normalize_weights, moe_router.rs:130-141).
     __shared__ float sprob[64 * P];
+    // The shared-expert gate score gate . x is computed here, off the
+    // critical path (in the router kernel its extra wave ended last): its
+    // loads go out with the logits'.
+    const bool gated = a.gate != nullptr;
+    f32x4 gw[kChunk / 4];
+    FaX gx;
+    fa_row_load(gated ? a.gate : a.router, lane, gw);
+    fa_x_load(a, lane, gx);
     float v[P];
     load_logits<P>(a.logits, E, lane, v);
-    const float gate_score = a.gate ? a.logits[E] : __builtin_nanf("");
     const bool is_set = topk_set_logits<P, KC>(v, E, k, lane, sid);
     wave_softmax<P>(v, E, lane);
     if (!is_set) exact_topk<P>(v, k, lane, sid, sval);
@@ -411,6 +427,9 @@ __global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a_all) {
       a.table->blob[lane] = a.experts + (uint64_t)sid[lane] * a.stride;
       a.table->weight[lane] = wt;
     }
+    fa_x_finish(a, gx);
+    const float gate_dot = readlane_f(fa_row_dot(gw, gx.x), 63);
+    const float gate_score = gated ? gate_dot : __builtin_nanf("");
     if (lane == 0) {
       a.table->k = k;
       a.table->has_shared = a.shared != nullptr;
@@ -689,7 +708,7 @@ static hipError_t launch_down_fa(const FusedLayer& a, hipStream_t st) {
 hipError_t launch_fused_layer(const FusedLayer& a, hipStream_t st) {
   if (a.n_tokens < 1 || a.n_tokens > kMaxDecodeTokens || (a.trace && a.n_tokens != 1)) return hipErrorInvalidValue;
   const uint32_t I = a.routed.inter;
-  const uint32_t ka = a.E + (a.gate ? 1u : 0u) + 4u * a.n_tokens;
+  const uint32_t ka = a.E + 4u * a.n_tokens;
   switch (a.n_tokens) {
     case 1: hipLaunchKernelGGL(k_fa_route<1>, dim3(ka), dim3(64), 0, st, a); break;
     case 2: hipLaunchKernelGGL(k_fa_route<2>, dim3(ka), dim3(64), 0, st, a); break;

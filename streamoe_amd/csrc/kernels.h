@@ -66,7 +66,7 @@ struct FusedLayer {
   const uint8_t* shared;   // 4-bit shared expert blob, or null
   BlobGeom routed, sgeom;  // routed / shared (4-bit) geometry
   uint32_t E, k, normalize;
-  float* logits;           // [E + 1]: router logits, shared gate score at E
+  float* logits;           // [E]: router logits (the table wave computes the shared gate score)
   float* act;              // [(k + 1) * inter]: routed slots, shared at slot k
   FfnTable* table;         // route table of this token
   const float* h_mid;      // residual added by the combine
