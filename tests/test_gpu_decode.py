@@ -161,6 +161,28 @@ def test_qmv_argmax_fused(kernels, out_dim, in_dim, bits):
     assert int(np.argmax(got)) == min(big, out_dim - 1)
 
 
+def test_qmv_argmax_back_to_back(kernels):
+    """Calls of different grid sizes in a row (full LM-head grid, a
+    one-block grid, a mid-size 3-bit grid, the full grid again) each give
+    numpy's first maximal index of their own y: no partial left by a larger
+    earlier call enters a later call's merge."""
+    torch = _torch()
+    cases = [(151936, 2048, 4), (77, 512, 4), (9000, 2048, 3), (151936, 2048, 4), (300, 1024, 3)]
+    mats = {}
+    for n, (out_dim, in_dim, bits) in enumerate(cases):
+        rng = np.random.default_rng(0xA0 + n)
+        if (out_dim, in_dim, bits) not in mats:
+            codes, s, b = gen_quant_matrix(rng, out_dim, in_dim, 64, bits)
+            mats[(out_dim, in_dim, bits)] = qweights(codes, s, b, 64, bits)
+        w = mats[(out_dim, in_dim, bits)]
+        x = rng.standard_normal(in_dim).astype(np.float32)
+        y = torch.empty(out_dim, dtype=torch.float32, device="cuda")
+        i = torch.full((1,), -7, dtype=torch.int32, device="cuda")
+        assert kernels.qmv_argmax(w, dev(x), y, out_dim, in_dim, i) == 0
+        got = host(y)
+        assert int(host(i)[0]) == int(np.argmax(got)), (n, out_dim, in_dim, bits)
+
+
 # --- dequant (bit-exact) --------------------------------------------------------------
 
 @pytest.mark.parametrize("bits,group", [(4, 64), (3, 64), (4, 32), (3, 128)])
