@@ -10,12 +10,17 @@
 //                 token order), per-token entry positions in ascending
 //                 expert order, and a work list of (expert, <= kPfMC
 //                 entries) items, so a hot expert is spread over many waves.
-//   k_pf_rowsum   group sums of x rows (and later of the activations), the
+//   k_pf_prep_x   entry-ordered x rows in the MFMA k-order (bf16, or f32
+//                 split into bf16 hi + lo) and their group sums, the
 //                 per-group terms of the dequant epilogue.
-//   k_pf_gemm     one block per (item, 256 output columns), bf16 MFMA
-//                 (v_mfma_f32_16x16x32_bf16): mode 0 gate and up rows of the
-//                 item's expert -> act = silu(gate) * up; mode 1 down rows
-//                 over the activations split into bf16 hi + lo halves.
+//   k_pf_mm       persistent pipelined grouped GEMM, bf16 MFMA
+//                 (v_mfma_f32_16x16x32_bf16) over (item, column block)
+//                 units: mode 0 gate and up rows of the item's expert ->
+//                 act = silu(gate) * up as bf16 hi + lo, with the down
+//                 GEMM's activation group sums for G <= 64; mode 1 down rows
+//                 over the activations -> f32 per entry.
+//   k_pf_act_sum  activation group sums for G > 64 (a group spans more than
+//                 one gate/up unit).
 //   k_pf_combine  out[t] = sum over t's entries in ascending expert order of
 //                 fma(down[entry], w[entry], out) (moe_cpu.rs:330-337), no
 //                 atomics.
@@ -379,7 +384,11 @@ struct PfMM {
   static constexpr int STAGE = OFF_XS + P_XS * 4;
   static constexpr int OFF_UXS = ROWS * SB_ROW;           // group sums in a unit buffer
   static constexpr int UBUF = USB ? OFF_UXS + P_UXS * 16 : 0;  // one unit buffer, after the stages
-  static constexpr int LDS = S * STAGE + 2 * UBUF;
+  // Gate/up with G <= 64: the column waves' activation row sums of the
+  // last finished unit ([column wave][32 rows] f32), after the unit buffers.
+  static constexpr bool ASUM = MODE == 0 && G <= 64;
+  static constexpr int OFF_PS = S * STAGE + 2 * UBUF;
+  static constexpr int LDS = OFF_PS + (ASUM ? 4 * kPfMC * 4 : 0);
   // Accumulators per lane, exchanged between the K halves through LDS.
   static constexpr int NT = NMAT * CT * 2 * 4;
   static_assert(CG % 2 == 0, "K halves");
@@ -391,6 +400,7 @@ struct PfMM {
   static_assert(NWD == 0 || (MODE == 0 && USB), "copy waves: unit-staged gate/up only");
   static_assert(LDS <= 160 * 1024, "LDS per CU");
   static_assert(4 * NT * 64 * 4 <= STAGE, "accumulator exchange fits a stage");
+
   static_assert(!USB || (2 * NGU) % 16 == 0, "unit scale rows in 16-byte pieces");
 };
 
@@ -728,6 +738,7 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
   uint16_t* const act_hi = a.act_hi;
   uint16_t* const act_lo = a.act_lo;
   float* const down = a.down;
+  float* const asum_out = a.asum;
   const uint64_t wo0 = a.g.w[MODE == 0 ? 0 : 2], wo1 = a.g.w[MODE == 0 ? 1 : 2];
   const uint64_t so0 = a.g.s[MODE == 0 ? 0 : 2], so1 = a.g.s[MODE == 0 ? 1 : 2];
   const uint64_t bo0 = a.g.b[MODE == 0 ? 0 : 2];
@@ -885,6 +896,26 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
   uint32_t cv = lb, cc = 0, cslot = 0, cub = 0;
   uint32_t c_item = item_lo + cv / ncb, c_cb = cv % ncb;
   uint32_t c_start = items[2 * c_item + 1] & 0xFFFFu, c_cnt = items[2 * c_item + 1] >> 16;
+  // Activation group sums of the last finished unit, still to be written by
+  // wave 0 once a block barrier has ordered the column waves' row sums.
+  bool ps_pend = false;
+  uint32_t ps_start = 0, ps_cnt = 0, ps_cb = 0;
+  auto flush_asum = [&]() {
+    if (wave == 0) {
+      constexpr uint32_t GPU = 64 / G;  // groups per unit
+      const float* ps = reinterpret_cast<const float*>(lds + C::OFF_PS);
+      const uint32_t m = lane % kPfMC, gl = lane / kPfMC;
+      if (gl < GPU && m < ps_cnt) {
+        float sum;
+        if constexpr (GPU == 1)
+          sum = (ps[m] + ps[kPfMC + m]) + (ps[2 * kPfMC + m] + ps[3 * kPfMC + m]);
+        else
+          sum = ps[2 * gl * kPfMC + m] + ps[(2 * gl + 1) * kPfMC + m];
+        asum_out[(size_t)(ps_start + m) * (N / G) + ps_cb * GPU + gl] = sum;
+      }
+    }
+    ps_pend = false;
+  };
   for (uint32_t j = 0; j < total; ++j) {
     // Copies of chunks j + 1 .. j + S - 2 may stay in flight: D each, plus
     // DU unit scale copies for a chunk that starts a unit (nch >= 2, so at
@@ -919,6 +950,11 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
         if (iv < group_units) isrc = unit_src(iv);
       }
     }
+    // The row sums are read before the next unit end writes them again:
+    // that comes after one more block barrier, which wave 0 passes with its
+    // LDS reads complete.
+    if constexpr (C::ASUM)
+      if (ps_pend) flush_asum();
 
     const uint32_t start = c_start, cnt = c_cnt, cb = c_cb;
     uint8_t* st = lds + cslot * C::STAGE;
@@ -967,6 +1003,7 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
       asm volatile("" ::: "memory");
       if (computer && kh == 0) {
         const uint32_t ntiles = cnt > 16 ? 2 : 1;
+        float hl[2][4] = {};  // gate/up: hi + lo of this lane's activation, rows 16 t + 4 q + r
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
           if ((uint32_t)t >= ntiles) continue;
@@ -989,12 +1026,34 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
                 const size_t at = (size_t)(start + m) * N + (colj & ~7u) + perm8_pos(colj & 7u);
                 act_hi[at] = (uint16_t)hi;
                 act_lo[at] = (uint16_t)lo;
+                hl[t][r] = __uint_as_float(hi << 16) + __uint_as_float(lo << 16);
               } else {
                 down[(size_t)(start + m) * N + colj] = o[0];
               }
             }
           }
         }
+        // Gate/up with G <= 64: the down GEMM's activation group sums (over
+        // what its MFMAs see, hi + lo), for the 64 / G groups of this unit's
+        // 64 columns: each column wave sums its 16 columns per row (the
+        // lanes of a 16-lane row); wave 0 adds the column waves of a group
+        // after the next block barrier (flush_asum).
+        if constexpr (C::ASUM) {
+          float* ps = reinterpret_cast<float*>(lds + C::OFF_PS);
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float rs = row_sum16_all(hl[t][r]);
+              if (n == 0) ps[cw * kPfMC + 16 * t + 4 * q + r] = rs;
+            }
+        }
+      }
+      if constexpr (C::ASUM) {
+        ps_pend = true;
+        ps_start = start;
+        ps_cnt = cnt;
+        ps_cb = cb;
       }
 #pragma unroll
       for (int mt = 0; mt < C::NMAT; ++mt)
@@ -1003,6 +1062,13 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
 #pragma unroll
           for (int t = 0; t < 2; ++t) tot[mt][ct][t] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
+  }
+  if constexpr (C::ASUM) {
+    // The last unit's sums (every wave leaves the loop after the same chunk).
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (ps_pend) flush_asum();
   }
 }
 
@@ -1191,8 +1257,8 @@ static hipError_t launch_gemms(const PfArgs& a, uint32_t n_cu, hipStream_t st) {
   else
     e = launch_mm<BITS, G, 0, false, 0>(a, gu_units, n_cu, st);
   if (e != hipSuccess) return e;
-  const uint32_t nk = a.n_tokens * a.k;
-  hipLaunchKernelGGL(k_pf_act_sum, dim3(nk), dim3(256), 0, st, a);
+  // With G <= 64 the gate/up GEMM writes the activation group sums itself.
+  if (G > 64) hipLaunchKernelGGL(k_pf_act_sum, dim3(a.n_tokens * a.k), dim3(256), 0, st, a);
   const uint32_t dn_units = a.max_items * (a.g.hidden / 256);
   if (G == 64 && a.g.inter == 512) return launch_mm<BITS, G, 1, true, G == 64 ? 512 : 0>(a, dn_units, n_cu, st);
   return launch_mm<BITS, G, 1, true, 0>(a, dn_units, n_cu, st);
