@@ -18,6 +18,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace smoe {
 
 constexpr int kWave = 64;
@@ -400,6 +402,21 @@ __device__ __forceinline__ void store_limbs(uint32_t* p, const XLimbs& o) {
   t.z = 0;
   t.w = 0;
   p4[6] = t;
+}
+
+// Raises kernel fn's dynamic LDS limit to `bytes` on the current device,
+// once per device (`done` holds one bit per device index); function
+// attributes belong to a device, so a process that launches on several
+// devices sets them on each.
+inline hipError_t raise_lds_limit(const void* fn, int bytes, std::atomic<uint64_t>& done) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const uint64_t bit = 1ull << (dev & 63);
+  if (done.load(std::memory_order_acquire) & bit) return hipSuccess;
+  e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess) done.fetch_or(bit, std::memory_order_acq_rel);
+  return e;
 }
 
 }  // namespace smoe

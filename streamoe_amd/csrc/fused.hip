@@ -681,7 +681,8 @@ static void launch_gateup_fa(const FusedLayer& a, uint32_t blocks, hipStream_t s
 }
 
 // K_C launch: 8 rows per block; LDS for the staged activations. Blocks of
-// more than 64 KB (k = 16 at inter 1024) need the attribute raised once.
+// more than 64 KB (k = 16 at inter 1024) need the attribute raised (once
+// per device).
 template <int BITS, int LI, int H>
 static hipError_t launch_down_fa_h(const FusedLayer& a, hipStream_t st) {
   constexpr uint32_t SPW = kWave / LI;
@@ -690,12 +691,13 @@ static hipError_t launch_down_fa_h(const FusedLayer& a, hipStream_t st) {
   const size_t lds = (size_t)chunks * kChunkPad * sizeof(float);
   // Every staged float4 has a thread (8 per thread at most); true for all
   // k <= 16 and inter 512 / 1024, checked anyway.
-  if (chunks * (kChunk / 4) > (uint32_t)kFaStage * waves * kWave || waves > 16) return hipErrorInvalidValue;
-  static const bool raised = [] {
-    return hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fa_down<BITS, LI, H>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024) == hipSuccess;
-  }();
-  (void)raised;
+  if (chunks * (kChunk / 4) > (uint32_t)kFaStage * waves * kWave || waves > 16 || lds > 96 * 1024)
+    return hipErrorInvalidValue;
+  static std::atomic<uint64_t> raised{0};
+  if (lds > 64 * 1024) {
+    const hipError_t e = raise_lds_limit(reinterpret_cast<const void*>(&k_fa_down<BITS, LI, H>), 96 * 1024, raised);
+    if (e != hipSuccess) return e;
+  }
   hipLaunchKernelGGL((k_fa_down<BITS, LI, H>), dim3(kFaH / kFaRB, a.n_tokens), dim3(waves * kWave), lds, st, a);
   return hipSuccess;
 }

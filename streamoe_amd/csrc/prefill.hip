@@ -1231,12 +1231,9 @@ static hipError_t launch_mm(const PfArgs& a, uint32_t n_units_max, uint32_t n_cu
   using C = PfMM<BITS, G, MODE, SPLIT, KU, NWD>;
   const auto fn = reinterpret_cast<const void*>(&k_pf_mm<BITS, G, MODE, SPLIT, KU, NWD>);
   const size_t lds = (size_t)C::LDS;
-  static bool attr_set = false;
-  if (!attr_set) {
-    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> raised{0};
+  const hipError_t e = raise_lds_limit(fn, (int)lds, raised);
+  if (e != hipSuccess) return e;
   const uint32_t grid = n_units_max < n_cu ? n_units_max : n_cu;
   hipLaunchKernelGGL((k_pf_mm<BITS, G, MODE, SPLIT, KU, NWD>), dim3(grid), dim3(64 * C::NWT), lds, st, a,
                      (const uint32_t*)a.items, (const uint32_t*)a.n_items);

@@ -421,6 +421,7 @@ LAYER_CASES = [
     ("a3b-ungated", 2048, 512, 256, 8, 4, True, "ungated"),  # shared expert added unscaled
     ("olmoe-3bit-e32", 2048, 1024, 32, 2, 3, True, False),
     ("k16-i1024", 2048, 1024, 64, 16, 4, True, True),  # down kernel: 8 rows per lane, > 64 KB LDS
+    ("k10", 2048, 512, 128, 10, 4, True, True),      # the reference's other supported top-k
 ]
 
 PATHS = [1, 2, 3]
