@@ -1148,24 +1148,35 @@ __global__ __launch_bounds__(256) void k_pf_act_sum(PfArgs a) {
 __global__ __launch_bounds__(256) void k_pf_combine(PfArgs a) {
   const uint32_t t = blockIdx.x;
   const uint32_t H = a.g.hidden, k = a.k;
-  int32_t pos[kPfMaxK];
+  const float* const down = a.down;
+  float* const out = a.out;
+  // Loops over the k slots run to kPfMaxK with a guard, so that the arrays
+  // stay in registers and every load of a pass is issued before the first
+  // FMA waits for one.
+  uint32_t pos[kPfMaxK];
   float wt[kPfMaxK];
   const uint32_t nk = a.n_tokens * k;
-  for (uint32_t r = 0; r < k; ++r) {
+#pragma unroll
+  for (uint32_t r = 0; r < kPfMaxK; ++r)
     // In range even when bucketing rejected the input (then *err is set).
-    pos[r] = (int32_t)min((uint32_t)a.tok_pos[t * k + r], nk - 1);
-    wt[r] = a.ent_weight[pos[r]];
-  }
+    pos[r] = r < k ? min((uint32_t)a.tok_pos[t * k + r], nk - 1) : 0u;
+#pragma unroll
+  for (uint32_t r = 0; r < kPfMaxK; ++r) wt[r] = r < k ? a.ent_weight[pos[r]] : 0.f;
   for (uint32_t h = threadIdx.x * 4; h < H; h += blockDim.x * 4) {
+    float4 d[kPfMaxK];
+#pragma unroll
+    for (uint32_t r = 0; r < kPfMaxK; ++r)
+      if (r < k) d[r] = *reinterpret_cast<const float4*>(down + (size_t)pos[r] * H + h);
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (uint32_t r = 0; r < k; ++r) {
-      const float4 d = *reinterpret_cast<const float4*>(a.down + (size_t)pos[r] * H + h);
-      o.x = __builtin_fmaf(d.x, wt[r], o.x);
-      o.y = __builtin_fmaf(d.y, wt[r], o.y);
-      o.z = __builtin_fmaf(d.z, wt[r], o.z);
-      o.w = __builtin_fmaf(d.w, wt[r], o.w);
-    }
-    *reinterpret_cast<float4*>(a.out + (size_t)t * H + h) = o;
+#pragma unroll
+    for (uint32_t r = 0; r < kPfMaxK; ++r)
+      if (r < k) {
+        o.x = __builtin_fmaf(d[r].x, wt[r], o.x);
+        o.y = __builtin_fmaf(d[r].y, wt[r], o.y);
+        o.z = __builtin_fmaf(d[r].z, wt[r], o.z);
+        o.w = __builtin_fmaf(d[r].w, wt[r], o.w);
+      }
+    *reinterpret_cast<float4*>(out + (size_t)t * H + h) = o;
   }
 }
 
