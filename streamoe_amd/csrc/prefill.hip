@@ -10,9 +10,10 @@
 //                 token order), per-token entry positions in ascending
 //                 expert order, and a work list of (expert, <= kPfMC
 //                 entries) items, so a hot expert is spread over many waves.
-//   k_pf_prep_x   entry-ordered x rows in the MFMA k-order (bf16, or f32
-//                 split into bf16 hi + lo) and their group sums, the
-//                 per-group terms of the dequant epilogue.
+//   k_pf_prep_x   one block per token: its x row in the MFMA k-order (bf16,
+//                 or f32 split into bf16 hi + lo) and group sums (the
+//                 per-group terms of the dequant epilogue), written to each
+//                 of the token's entry rows.
 //   k_pf_mm       persistent pipelined grouped GEMM, bf16 MFMA
 //                 (v_mfma_f32_16x16x32_bf16) over (item, column block)
 //                 units: mode 0 gate and up rows of the item's expert ->
@@ -1072,17 +1073,26 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
   }
 }
 
-// Entry e's x row (token ent_token[e]) -> MFMA-ready bf16 hi (and lo for
-// fp32 input) in entry order, and its group sums over what the MFMA sees
-// (hi + lo). One block per entry.
+// Token t's x row -> MFMA-ready bf16 hi (and lo for fp32 input) and its
+// group sums over what the MFMA sees (hi + lo), written to each of the
+// token's k entry rows (entry positions from k_pf_route). One block per
+// token, so the row is read, split and summed once for its k entries.
 __global__ __launch_bounds__(256) void k_pf_prep_x(PfArgs a) {
   __shared__ float part8[kPfMaxGroupsK * 128 / 8];
-  const uint32_t e = blockIdx.x, H = a.g.hidden, G = a.g.group;
-  // In range even when bucketing rejected the input (then *err is set).
-  const uint32_t t = min((uint32_t)a.ent_token[e], a.n_tokens - 1);
+  const uint32_t t = blockIdx.x, H = a.g.hidden, G = a.g.group, k = a.k;
+  const uint32_t nk = a.n_tokens * k;
+  uint16_t* const x_hi = a.x_hi;
+  uint16_t* const x_lo = a.x_lo;
+  float* const xsum = a.xsum;
+  const bool x_bf16 = a.x_bf16;
+  uint32_t pos[kPfMaxK];
+#pragma unroll
+  for (uint32_t r = 0; r < kPfMaxK; ++r)
+    // In range even when bucketing rejected the input (then *err is set).
+    pos[r] = r < k ? min((uint32_t)a.tok_pos[t * k + r], nk - 1) : 0u;
   for (uint32_t k0 = threadIdx.x * 8; k0 < H; k0 += blockDim.x * 8) {
     float f[8];
-    if (a.x_bf16) {
+    if (x_bf16) {
       const u32x4 v = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)t * H + k0);
       const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -1097,24 +1107,30 @@ __global__ __launch_bounds__(256) void k_pf_prep_x(PfArgs a) {
     }
     u32x4 hi, lo;
     split_f32(f, hi, lo);
-    *reinterpret_cast<u32x4*>(a.x_hi + (size_t)e * H + k0) = hi;
-    if (!a.x_bf16) *reinterpret_cast<u32x4*>(a.x_lo + (size_t)e * H + k0) = lo;
+#pragma unroll
+    for (uint32_t r = 0; r < kPfMaxK; ++r)
+      if (r < k) {
+        *reinterpret_cast<u32x4*>(x_hi + (size_t)pos[r] * H + k0) = hi;
+        if (!x_bf16) *reinterpret_cast<u32x4*>(x_lo + (size_t)pos[r] * H + k0) = lo;
+      }
     // Partial sum of these 8 inputs as the MFMA sees them.
     const uint32_t hv[4] = {hi.x, hi.y, hi.z, hi.w}, lv[4] = {lo.x, lo.y, lo.z, lo.w};
     float p = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       p += __uint_as_float(hv[i] << 16) + __uint_as_float(hv[i] & 0xFFFF0000u);
-      if (!a.x_bf16) p += __uint_as_float(lv[i] << 16) + __uint_as_float(lv[i] & 0xFFFF0000u);
+      if (!x_bf16) p += __uint_as_float(lv[i] << 16) + __uint_as_float(lv[i] & 0xFFFF0000u);
     }
     part8[k0 / 8] = p;
   }
   __syncthreads();
   const uint32_t ng = H / G, per = G / 8;
   for (uint32_t g = threadIdx.x; g < ng; g += blockDim.x) {
-    float s = 0.f;
-    for (uint32_t j = 0; j < per; ++j) s += part8[g * per + j];
-    a.xsum[(size_t)e * ng + g] = s;
+    float sum = 0.f;
+    for (uint32_t j = 0; j < per; ++j) sum += part8[g * per + j];
+#pragma unroll
+    for (uint32_t r = 0; r < kPfMaxK; ++r)
+      if (r < k) xsum[(size_t)pos[r] * ng + g] = sum;
   }
 }
 
@@ -1145,7 +1161,7 @@ __global__ __launch_bounds__(256) void k_pf_act_sum(PfArgs a) {
 // ---------------------------------------------------------------------------
 // Combine: out[t, :] = fold over t's entries in ascending expert order.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_pf_combine(PfArgs a) {
+__global__ __launch_bounds__(512) void k_pf_combine(PfArgs a) {
   const uint32_t t = blockIdx.x;
   const uint32_t H = a.g.hidden, k = a.k;
   const float* const down = a.down;
@@ -1274,7 +1290,7 @@ static hipError_t launch_gemms(const PfArgs& a, uint32_t n_cu, hipStream_t st) {
 
 hipError_t launch_prefill(const PfArgs& a, uint32_t n_cu, hipStream_t st) {
   hipLaunchKernelGGL(k_pf_route, dim3(1), dim3(1024), 0, st, a);
-  hipLaunchKernelGGL(k_pf_prep_x, dim3(a.n_tokens * a.k), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(k_pf_prep_x, dim3(a.n_tokens), dim3(256), 0, st, a);
   const uint32_t G = a.g.group;
   hipError_t e;
   if (a.g.bits == 4)
@@ -1284,7 +1300,7 @@ hipError_t launch_prefill(const PfArgs& a, uint32_t n_cu, hipStream_t st) {
     e = G == 32 ? launch_gemms<3, 32>(a, n_cu, st) : G == 64 ? launch_gemms<3, 64>(a, n_cu, st)
                                                    : launch_gemms<3, 128>(a, n_cu, st);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_pf_combine, dim3(a.n_tokens), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(k_pf_combine, dim3(a.n_tokens), dim3(512), 0, st, a);
   return hipGetLastError();
 }
 
