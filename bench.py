@@ -50,9 +50,9 @@ CONFIGS = {
 # WRITE_SIZE passes scaled by a 256 MiB copy calibration (FETCH x 2.0,
 # WRITE x 1.0): profiles/decode_c2_a3b_4bit.md (one layer = the three
 # k_fa_* launches), profiles/lm_head_c1_qmv_argmax.md (k_qmv + argmax) and
-# profiles/prefill_c4_a3b_4bit.md (the six prefill launches of one layer).
+# profiles/prefill_c4_a3b_4bit.md (the five prefill launches of one layer).
 # None where no counter pass was taken.
-MEASURED_TRAFFIC = {"c2": 18_841_805, "c1": 175_961_008, "c4": 596_401_459}
+MEASURED_TRAFFIC = {"c2": 18_841_805, "c1": 175_961_008, "c4": 578_995_832}
 
 
 def stream_read_peak(dev, gib=4):
@@ -483,8 +483,8 @@ def run_prefill(args, c):
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": MEASURED_TRAFFIC.get("c4"),
                      "unit_of_work": f"one layer: {nbytes} algorithmic bytes ({len(hit)} hit experts x {stride} "
                                      f"+ X + Y), {flops} flops",
-                     "kernel": "prefill layer: k_pf_route + k_pf_prep_x + k_pf_mm (gate/up) + k_pf_act_sum + "
-                               "k_pf_mm (down) + k_pf_combine (one HIP graph)"},
+                     "kernel": "prefill layer: k_pf_route + k_pf_prep_x + k_pf_mm (gate/up, with the activation "
+                               "group sums) + k_pf_mm (down) + k_pf_combine (one HIP graph)"},
     }
     if not args.no_cpu:
         # The whole layer (a few seconds of CPU work), timed with all host
