@@ -120,9 +120,8 @@ struct PfArgs {
   // Workspace (prefill_workspace).
   uint32_t* items;         // [max_items, 2]: expert, start | count << 16
   uint32_t* n_items;
-  int32_t* ent_token;      // [n*k] token of each entry (entries sorted by expert, then token)
-  float* ent_weight;       // [n*k]
   int32_t* tok_pos;        // [n, k] entry positions of each token in ascending expert order
+  float* tok_w;            // [n, k] the routing weights in the same order
   float* xsum;             // [n*k, hidden / group] group sums of each entry's x row
   float* asum;             // [n*k, inter / group] group sums of the activations
   uint16_t* x_hi;          // [n*k, hidden] x rows in entry order, bf16, MFMA order

@@ -50,7 +50,6 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 constexpr uint32_t kPfMC = 32;   // entries per work item (two 16-row MFMA tiles)
 constexpr uint32_t kPfKC = 256;  // inputs per pipelined K chunk
-constexpr uint32_t kPfStage = 8192;  // entries k_pf_route stages in LDS
 
 // ---------------------------------------------------------------------------
 // Bucketing (one block of 1024 threads).
@@ -67,8 +66,6 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
   __shared__ uint32_t col[kPfMaxExperts * (kPfMaxTokens / 32)];
   __shared__ uint16_t pre[kPfMaxExperts * (kPfMaxTokens / 32)];
   __shared__ uint32_t offs[kPfMaxExperts];
-  __shared__ int32_t st_tok[kPfStage];
-  __shared__ float st_w[kPfStage];
   const uint32_t tid = threadIdx.x, n = a.n_tokens, k = a.k, E = a.E;
   const uint32_t cw = (n + 31) / 32;
   for (uint32_t i = tid; i < E * cw; i += blockDim.x) col[i] = 0;
@@ -178,13 +175,16 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
   }
   // Every entry places itself: position = the expert's offset + the tokens
   // before t that chose the same expert; rank among t's experts in
-  // ascending expert order = how many of t's experts are smaller. Entries
-  // go through LDS (when they fit) so the global writes are coalesced.
-  const uint32_t total = n * k;
-  const bool staged = total <= kPfStage;
+  // ascending expert order = how many of t's experts are smaller. The token
+  // writes its entry positions and weights in that order (token-major,
+  // coalesced), all the later kernels need of the entries.
   int32_t row[kPfMaxK];
+  float roww[kPfMaxK];
 #pragma unroll
-  for (uint32_t s = 0; s < kPfMaxK; ++s) row[s] = 0;
+  for (uint32_t s = 0; s < kPfMaxK; ++s) {
+    row[s] = 0;
+    roww[s] = 0.f;
+  }
   if (tok) {
 #pragma unroll
     for (uint32_t s = 0; s < kPfMaxK; ++s) {
@@ -195,33 +195,29 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
       uint32_t r = 0;
 #pragma unroll
       for (uint32_t q = 0; q < kPfMaxK; ++q) r += (q < k && ex[q] < e) ? 1u : 0u;
-      if (staged) {
-        st_tok[pos] = (int32_t)tid;
-        st_w[pos] = wt[s];
-      } else {
-        a.ent_token[pos] = (int32_t)tid;
-        a.ent_weight[pos] = wt[s];
-      }
 #pragma unroll
       for (uint32_t q = 0; q < kPfMaxK; ++q)
-        if (q == min(r, k - 1)) row[q] = (int32_t)pos;
+        if (q == min(r, k - 1)) {
+          row[q] = (int32_t)pos;
+          roww[q] = wt[s];
+        }
     }
     if ((k & 3) == 0) {
       int4* tp = reinterpret_cast<int4*>(a.tok_pos + tid * k);
+      float4* tw = reinterpret_cast<float4*>(a.tok_w + tid * k);
 #pragma unroll
       for (uint32_t q = 0; q < kPfMaxK / 4; ++q)
-        if (4 * q < k) tp[q] = make_int4(row[4 * q], row[4 * q + 1], row[4 * q + 2], row[4 * q + 3]);
+        if (4 * q < k) {
+          tp[q] = make_int4(row[4 * q], row[4 * q + 1], row[4 * q + 2], row[4 * q + 3]);
+          tw[q] = make_float4(roww[4 * q], roww[4 * q + 1], roww[4 * q + 2], roww[4 * q + 3]);
+        }
     } else {
 #pragma unroll
       for (uint32_t q = 0; q < kPfMaxK; ++q)
-        if (q < k) a.tok_pos[tid * k + q] = row[q];
-    }
-  }
-  if (staged) {
-    __syncthreads();
-    for (uint32_t i = tid; i < total; i += blockDim.x) {
-      a.ent_token[i] = st_tok[i];
-      a.ent_weight[i] = st_w[i];
+        if (q < k) {
+          a.tok_pos[tid * k + q] = row[q];
+          a.tok_w[tid * k + q] = roww[q];
+        }
     }
   }
   PF_STAMP(5);
@@ -1177,7 +1173,7 @@ __global__ __launch_bounds__(512) void k_pf_combine(PfArgs a) {
     // In range even when bucketing rejected the input (then *err is set).
     pos[r] = r < k ? min((uint32_t)a.tok_pos[t * k + r], nk - 1) : 0u;
 #pragma unroll
-  for (uint32_t r = 0; r < kPfMaxK; ++r) wt[r] = r < k ? a.ent_weight[pos[r]] : 0.f;
+  for (uint32_t r = 0; r < kPfMaxK; ++r) wt[r] = r < k ? a.tok_w[t * k + r] : 0.f;
   for (uint32_t h = threadIdx.x * 4; h < H; h += blockDim.x * 4) {
     float4 d[kPfMaxK];
 #pragma unroll
@@ -1213,7 +1209,6 @@ uint64_t prefill_workspace(uint32_t hidden, uint32_t inter, uint32_t group, uint
   };
   uint8_t* p_items = take(max_items * 2 * 4);
   uint8_t* p_nitems = take(4);
-  uint8_t* p_tok = take(nk * 4);
   uint8_t* p_w = take(nk * 4);
   uint8_t* p_pos = take(nk * 4);
   uint8_t* p_xsum = take(nk * (hidden / group) * 4);
@@ -1226,8 +1221,7 @@ uint64_t prefill_workspace(uint32_t hidden, uint32_t inter, uint32_t group, uint
   if (a) {
     a->items = reinterpret_cast<uint32_t*>(p_items);
     a->n_items = reinterpret_cast<uint32_t*>(p_nitems);
-    a->ent_token = reinterpret_cast<int32_t*>(p_tok);
-    a->ent_weight = reinterpret_cast<float*>(p_w);
+    a->tok_w = reinterpret_cast<float*>(p_w);
     a->tok_pos = reinterpret_cast<int32_t*>(p_pos);
     a->xsum = reinterpret_cast<float*>(p_xsum);
     a->asum = reinterpret_cast<float*>(p_asum);
