@@ -74,6 +74,7 @@ def _case(kernels, n_tokens, H, I, E, k, bits, group, x_bf16, seed, routing="zip
     ("one-token", 1, 2048, 512, 256, 8, 4, 64, True, "zipf"),
     ("k1", 33, 1024, 256 * 2, 16, 1, 4, 64, True, "zipf"),
     ("k10-g32", 48, 1024, 512, 64, 10, 4, 32, True, "zipf"),  # the reference's other supported top-k
+    ("max-n1024-k16", 1024, 2048, 512, 256, 16, 4, 64, True, "zipf"),  # largest tokens x k (16384 entries)
 ])
 def test_prefill_matches_oracle(kernels, name, n, H, I, E, k, bits, group, x_bf16, routing):
     got, want, _ = _case(kernels, n, H, I, E, k, bits, group, x_bf16, seed=sum(map(ord, name)), routing=routing)
