@@ -119,14 +119,39 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
   __syncthreads();
   PF_STAMP(2);
   __shared__ uint32_t scnt[kPfMaxExperts], snch[kPfMaxExperts], sibase[kPfMaxExperts];
-  if (tid < E) {
-    uint32_t cnt = 0;
-    for (uint32_t c = 0; c < cw; ++c) {
-      pre[tid * cw + c] = (uint16_t)cnt;
-      cnt += __popc(col[tid * cw + c]);
+  {
+    // Four threads per expert (lanes 4e .. 4e + 3 of one wave), each over a
+    // quarter of the expert's bitmap words: popcounts, an exclusive scan
+    // across the four, then the running counts before each word.
+    static_assert(kPfMaxTokens / 32 <= 4 * 8 && 4 * kPfMaxExperts <= 1024, "count split");
+    const uint32_t e = tid >> 2, j = tid & 3, per = (cw + 3) / 4;
+    uint32_t pc[8], loc = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < 8; ++i) {
+      const uint32_t c = j * per + i;
+      pc[i] = (e < E && i < per && c < cw) ? __popc(col[e * cw + c]) : 0u;
+      loc += pc[i];
     }
-    scnt[tid] = cnt;
-    snch[tid] = (cnt + kPfMC - 1) / kPfMC;
+    uint32_t incl = loc;
+    const uint32_t t1 = __shfl_up(incl, 1, 4);
+    if (j >= 1) incl += t1;
+    const uint32_t t2 = __shfl_up(incl, 2, 4);
+    if (j >= 2) incl += t2;
+    if (e < E) {
+      uint32_t run = incl - loc;
+#pragma unroll
+      for (uint32_t i = 0; i < 8; ++i) {
+        const uint32_t c = j * per + i;
+        if (i < per && c < cw) {
+          pre[e * cw + c] = (uint16_t)run;
+          run += pc[i];
+        }
+      }
+      if (j == 3) {
+        scnt[e] = incl;
+        snch[e] = (incl + kPfMC - 1) / kPfMC;
+      }
+    }
   }
   __syncthreads();
   PF_STAMP(3);
