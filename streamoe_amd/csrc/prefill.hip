@@ -199,17 +199,11 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
     }
   }
   // Every entry places itself: position = the expert's offset + the tokens
-  // before t that chose the same expert; rank among t's experts in
+  // before t that chose the same expert; rank r among t's experts in
   // ascending expert order = how many of t's experts are smaller. The token
-  // writes its entry positions and weights in that order (token-major,
-  // coalesced), all the later kernels need of the entries.
-  int32_t row[kPfMaxK];
-  float roww[kPfMaxK];
-#pragma unroll
-  for (uint32_t s = 0; s < kPfMaxK; ++s) {
-    row[s] = 0;
-    roww[s] = 0.f;
-  }
+  // writes its entry positions and weights in that order (token-major),
+  // all the later kernels need of the entries: element t k + r of tok_pos
+  // and tok_w, stored directly (no selection of the rank's register).
   if (tok) {
 #pragma unroll
     for (uint32_t s = 0; s < kPfMaxK; ++s) {
@@ -220,29 +214,9 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
       uint32_t r = 0;
 #pragma unroll
       for (uint32_t q = 0; q < kPfMaxK; ++q) r += (q < k && ex[q] < e) ? 1u : 0u;
-#pragma unroll
-      for (uint32_t q = 0; q < kPfMaxK; ++q)
-        if (q == min(r, k - 1)) {
-          row[q] = (int32_t)pos;
-          roww[q] = wt[s];
-        }
-    }
-    if ((k & 3) == 0) {
-      int4* tp = reinterpret_cast<int4*>(a.tok_pos + tid * k);
-      float4* tw = reinterpret_cast<float4*>(a.tok_w + tid * k);
-#pragma unroll
-      for (uint32_t q = 0; q < kPfMaxK / 4; ++q)
-        if (4 * q < k) {
-          tp[q] = make_int4(row[4 * q], row[4 * q + 1], row[4 * q + 2], row[4 * q + 3]);
-          tw[q] = make_float4(roww[4 * q], roww[4 * q + 1], roww[4 * q + 2], roww[4 * q + 3]);
-        }
-    } else {
-#pragma unroll
-      for (uint32_t q = 0; q < kPfMaxK; ++q)
-        if (q < k) {
-          a.tok_pos[tid * k + q] = row[q];
-          a.tok_w[tid * k + q] = roww[q];
-        }
+      r = min(r, k - 1);  // a duplicated expert (already reported) stays in range
+      a.tok_pos[tid * k + r] = (int32_t)pos;
+      a.tok_w[tid * k + r] = wt[s];
     }
   }
   PF_STAMP(5);
