@@ -9,8 +9,7 @@ bf16 N(0,.01)), f32 router N(0,.02), residual stream N(0,1). Between
 layers the next input is RMSNorm(residual) (unit bf16 weights). One step
 = one token through the 40 layers: three kernels per layer (router +
 shared gate/up; top-k + routed gate/up; down + combine) replayed from a
-HIP graph (default), one kernel per phase (--path kernels) or one
-persistent cooperative launch (--path persistent, eager).
+HIP graph (default) or one kernel per phase (--path kernels).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2]
 
@@ -30,6 +29,12 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+
+# The decode arithmetic: 4-/3-bit codes times x as 24-bit block floating
+# point (one exponent per 32 inputs, three int8 limbs, exact int32 sums
+# with v_dot4c_i32_i8), then the bf16 scale and bias and everything after
+# (SwiGLU, the down matvec, the combine) in f32.
+DECODE_DTYPE = "u4/u3 codes x 24-bit block-FP activations (int8 limbs, sdot4 int32 sums), f32 epilogue"
 
 # Algorithmic bytes per unit (weights read once).
 CONFIGS = {
@@ -94,12 +99,38 @@ def layer_bytes(c, tokens=1):
     return tokens * c["k"] * routed + shared + c["E"] * c["H"] * 4
 
 
+# A GPU box grants one GPU's process a share of 16 host CPUs (the harness's
+# worker-pool rule), whatever nproc reports; the baseline uses every CPU of
+# that share that the process may run on.
+BOX_CPU_SHARE = 16
+
+
 def cpu_threads():
-    n = os.cpu_count() or 1
-    env = os.environ.get("OMP_NUM_THREADS")
-    if env and env.isdigit():
-        n = min(n, int(env))
-    return max(1, min(n, 16))
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    return max(1, min(n, BOX_CPU_SHARE))
+
+
+def host_cpu():
+    """What the CPU baseline ran on: CPU model, nproc, the CPUs this
+    process may use, and the threads the baseline used."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        aff = None
+    return {"cpu_model": model, "nproc": os.cpu_count(), "affinity_cpus": aff, "threads_used": cpu_threads(),
+            "box_cpu_share": BOX_CPU_SHARE}
 
 
 def cpu_baseline_decode(c, arena_l0, router_l0, shared_l0, gate_l0, x, seconds):
@@ -126,46 +157,14 @@ def cpu_baseline_decode(c, arena_l0, router_l0, shared_l0, gate_l0, x, seconds):
     med = times[len(times) // 2]
     return dict(value=med * 1e6, unit="us/layer", cores=th, kind="port",
                 sample=f"{len(times)} runs of one {c['name'].split(',')[0]} layer (median), "
-                       f"oracle/oracle.c on {th} threads")
+                       f"oracle/oracle.c with rows (router, gate/up, down) in parallel on {th} threads",
+                host=host_cpu())
 
 
 def _sync_status(kern):
     import streamoe_amd as sa
 
     return sa._lib.smoe_sync(kern.h)
-
-
-def trace_phases(kern, step, nl, nb=256):
-    """Per-block phase timestamps of the persistent decode (100 MHz
-    s_memrealtime ticks) from one traced step, summarised over layers
-    1..nl-1 in microseconds: mean per-phase durations, and for each handoff
-    the gap between the LAST producer and the FIRST consumer."""
-    import numpy as np
-    import torch
-
-    from streamoe_amd import _abi
-
-    buf = torch.zeros(nl * nb * 8 + nl * 2, dtype=torch.int64, device="cuda")
-    kern.set_option(_abi.SMOE_OPT_TRACE_BUFFER, buf.data_ptr())
-    step()
-    torch.cuda.synchronize()
-    kern.set_option(_abi.SMOE_OPT_TRACE_BUFFER, 0)
-    t = buf.cpu().numpy().astype(np.int64)[:nl * nb * 8].reshape(nl, nb, 8).astype(np.float64) * 0.01
-    if not t.any():
-        return None
-    L = slice(1, nl)
-    d = lambda a, b: round(float((t[L, :, b] - t[L, :, a]).mean()), 3)
-    out = {
-        "x_ready": d(0, 1), "router": d(1, 2), "logits_to_set": d(2, 3), "issue_loads": d(3, 7),
-        "gateup": d(7, 4), "act_wait": d(4, 5), "down_combine": d(5, 6),
-        "layer": round(float(np.diff(t[:, 0, 0])[1:].mean()), 3),
-        "logits_last_pub_to_first_set": round(float((t[L, :, 3].min(1) - t[L, :, 2].max(1)).mean()), 3),
-        "act_last_pub_to_first_ready": round(float((t[L, :, 5].min(1) - t[L, :, 4].max(1)).mean()), 3),
-        "hidden_last_pub_to_first_x": round(float((t[2:, :, 1].min(1) - t[1:-1, :, 6].max(1)).mean()), 3),
-        "spread_gateup_done": round(float((t[L, :, 4].max(1) - t[L, :, 4].min(1)).mean()), 3),
-        "spread_set_ready": round(float((t[L, :, 3].max(1) - t[L, :, 3].min(1)).mean()), 3),
-    }
-    return out
 
 
 FA_TRACE_BLOCKS = 4096  # kFaTraceBlocks in streamoe_amd/csrc/kernels.h (8 points per block)
@@ -262,7 +261,7 @@ def run_decode(args, c):
     work = torch.empty_like(x0)
     torch.cuda.synchronize()
 
-    path = {"auto": 0, "kernels": 1, "persistent": 2, "fused": 3}[args.path]
+    path = {"auto": 0, "kernels": 1, "fused": 3}[args.path]
     kern.set_decode_path(path)
 
     def step():
@@ -273,7 +272,7 @@ def run_decode(args, c):
 
     stream = torch.cuda.current_stream(dev)
     graph = None
-    if not args.eager and path != 2:  # a cooperative launch cannot be captured
+    if not args.eager:
         graph = sa.capture_graph(kern, step)
 
     run = graph.replay if graph is not None else step
@@ -295,7 +294,7 @@ def run_decode(args, c):
     assert torch.isfinite(resid).all(), "residual stream is not finite"
     phases = None
     if args.trace and T == 1:
-        phases = trace_phases(kern, step, nl) if path == 2 else trace_fused(kern, step, nl)
+        phases = trace_fused(kern, step, nl) if path in (0, 3) else None
 
     nbytes = layer_bytes(c, T)
     achieved = nbytes / (us_layer * 1e-6) / 1e9
@@ -310,7 +309,7 @@ def run_decode(args, c):
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u4/u3 codes, f32 compute",
+        "dtype": DECODE_DTYPE,
         "data": "synthetic (seeded, generated on the device)",
         "config": {"workload": c["name"], "hidden": H, "experts": E, "top_k": k, "inter": I, "bits": c["bits"],
                    "group": 64, "layers": nl, "shared_expert": c["shared"], "tokens": T,
@@ -414,7 +413,7 @@ def run_lm_head(args, c):
         got = y.cpu().numpy()
         out["cpu_baseline"] = {"value": round(dt * 1e6, 1), "unit": "us/token", "cores": 1, "kind": "port",
                                "sample": "one full LM head matvec, oracle/oracle.c lm_head (single thread, as "
-                                         "io/lm_head.rs:66-122)",
+                                         "io/lm_head.rs:66-122)", "host": host_cpu(),
                                "gpu_speedup": round(dt * 1e6 / us, 1)}
         out["parity"] = {"rel_err": float(np.max(np.abs(got - want)) / np.max(np.abs(want))),
                          "argmax_gpu": int(am.cpu()[0]), "argmax_cpu": int(oracle.argmax(want))}
@@ -502,7 +501,7 @@ def run_prefill(args, c):
         out_d["cpu_baseline"] = {"value": round(cpu_us, 1), "unit": "us/layer (512 tokens)", "cores": nt,
                                  "kind": "port",
                                  "sample": f"all {ns} tokens through oracle moe_permute_fuse "
-                                           f"(moe_cpu.rs:282-339 order), {dt:.2f} s",
+                                           f"(moe_cpu.rs:282-339 order), {dt:.2f} s", "host": host_cpu(),
                                  "gpu_speedup": round(cpu_us / us, 1)}
         out_d["parity"] = {"rel_err": float(np.max(np.abs(got - want)) / np.max(np.abs(want))),
                            "tokens_checked": ns, "tolerance": 1e-3}
@@ -516,9 +515,9 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
-    ap.add_argument("--path", default="auto", choices=["auto", "kernels", "persistent", "fused"],
+    ap.add_argument("--path", default="auto", choices=["auto", "kernels", "fused"],
                     help="decode path: auto (three-kernel where supported), kernels (one per phase), "
-                         "persistent (one cooperative launch), fused (three-kernel only)")
+                         "fused (three-kernel only)")
     ap.add_argument("--eager", action="store_true", help="launch every step eagerly instead of replaying a HIP graph")
     ap.add_argument("--trace", action="store_true", help="report per-phase times from in-kernel timestamps")
     ap.add_argument("--no-cpu", action="store_true")

@@ -57,7 +57,7 @@ typedef enum {
   SMOE_ERR_WORKSPACE_TOO_SMALL = 9, /* caller workspace smaller than *_workspace_size */
   SMOE_ERR_HIP = 10,                /* a HIP runtime call failed (launch, memset, sync) */
   SMOE_ERR_NO_DEVICE = 11,          /* no gfx950 device at that ordinal */
-  SMOE_ERR_DEVICE_TIMEOUT = 12,     /* a bounded device-side wait expired; outputs are invalid */
+  SMOE_ERR_DEVICE_TIMEOUT = 12,     /* reserved (a bounded device-side wait expired); no entry point of this build waits */
   SMOE_ERR_IO = 13                  /* a file could not be opened or read, or is too short (ExpertIoError::Io) */
 } smoe_status;
 
@@ -65,13 +65,13 @@ typedef enum {
 typedef enum {
   SMOE_OPT_DECODE_PATH = 1,  /* 0 auto (default: three-kernel where it has an
                                 instance, else one kernel per phase), 1 one
-                                kernel per phase, 2 persistent cooperative,
-                                3 three-kernel only */
+                                kernel per phase, 3 three-kernel only (2, the
+                                former persistent path, is rejected) */
   SMOE_OPT_TRACE_BUFFER = 2  /* device uint64 buffer for in-kernel timestamps, or 0 =
-                                off. Persistent decode: per layer and block 8 words;
-                                three-kernel decode: per layer 3 * 4096 * 8 words
-                                (kernel, block, point); prefill: 8 words (phase
-                                ends of the bucketing kernel). Diagnostics only. */
+                                off. Three-kernel decode: per layer 3 * 4096 * 8
+                                words (kernel, block, point); prefill: 8 words
+                                (phase ends of the bucketing kernel). Diagnostics
+                                only. */
 } smoe_option;
 
 typedef struct smoe_handle smoe_handle;
@@ -105,7 +105,7 @@ int smoe_set_stream(smoe_handle* h, void* stream);
 int smoe_reserve(smoe_handle* h, uint32_t max_hidden, uint32_t max_inter, uint32_t max_experts);
 
 /* Block until all work enqueued on the handle's stream has finished, then
- * report (and clear) a device-side timeout of the persistent decode.
+ * report (and clear) a routing error found on the device by smoe_moe_prefill.
  * Replaces MetalContext::commit_and_wait_labeled's wait and its
  * command-buffer error check (backend/gpu/metal.rs:343-440). */
 int smoe_sync(smoe_handle* h);
@@ -287,6 +287,7 @@ int smoe_moe_decode_layer(smoe_handle* h, const smoe_layer* layer, const float* 
 int smoe_moe_decode_layers(smoe_handle* h, const smoe_layer* layers, uint32_t n_layers,
                            const void* const* norm_w, float eps, const float* input,
                            float* residual_io, float* work);
+
 
 /* Several decode tokens (1..4) through the same layers at once, each as
  * smoe_moe_decode_layers would decode it alone (own routing, experts,

@@ -86,15 +86,51 @@ typedef struct {
   uint32_t r0, r1;
 } row_job;
 
-static void* row_thread(void* p) {
-  row_job* j = (row_job*)p;
-  j->fn(j->ctx, j->r0, j->r1);
-  return NULL;
-}
-
 static int default_threads(void) {
   long n = sysconf(_SC_NPROCESSORS_ONLN);
   return n > 0 ? (int)n : 1;
+}
+
+/* A persistent pool (rayon keeps its workers alive between parallel     */
+/* iterators): workers sleep on a condition variable between jobs; job  */
+/* share t of `nthreads` goes to worker t - 1, share 0 to the caller.    */
+typedef struct {
+  row_fn fn;
+  void* ctx;
+  uint32_t rows;
+  int nthreads;
+} pool_job;
+
+static pthread_mutex_t pool_call_mu = PTHREAD_MUTEX_INITIALIZER; /* one job at a time */
+static pthread_mutex_t pool_mu = PTHREAD_MUTEX_INITIALIZER;
+static pthread_cond_t pool_go = PTHREAD_COND_INITIALIZER;
+static pthread_cond_t pool_done = PTHREAD_COND_INITIALIZER;
+static int pool_workers = 0;
+static uint64_t pool_gen = 0;
+static int pool_pending = 0;
+static pool_job pool_cur;
+
+static void run_share(const pool_job* j, int t) {
+  uint32_t per = (j->rows + j->nthreads - 1) / j->nthreads;
+  uint32_t a = (uint32_t)t * per, b = a + per > j->rows ? j->rows : a + per;
+  if (a < b) j->fn(j->ctx, a, b);
+}
+
+static void* pool_worker(void* arg) {
+  int id = (int)(intptr_t)arg; /* runs share id + 1 */
+  uint64_t seen = 0;
+  for (;;) {
+    pthread_mutex_lock(&pool_mu);
+    while (pool_gen == seen) pthread_cond_wait(&pool_go, &pool_mu);
+    seen = pool_gen;
+    pool_job j = pool_cur;
+    pthread_mutex_unlock(&pool_mu);
+    if (id + 1 < j.nthreads) run_share(&j, id + 1);
+    pthread_mutex_lock(&pool_mu);
+    if (--pool_pending == 0) pthread_cond_signal(&pool_done);
+    pthread_mutex_unlock(&pool_mu);
+  }
+  return NULL;
 }
 
 static void parallel_rows(row_fn fn, void* ctx, uint32_t rows, int nthreads) {
@@ -104,25 +140,28 @@ static void parallel_rows(row_fn fn, void* ctx, uint32_t rows, int nthreads) {
     fn(ctx, 0, rows);
     return;
   }
-  pthread_t* th = (pthread_t*)malloc(sizeof(pthread_t) * nthreads);
-  row_job* jobs = (row_job*)malloc(sizeof(row_job) * nthreads);
-  uint32_t per = (rows + nthreads - 1) / nthreads;
-  int launched = 0;
-  for (int t = 0; t < nthreads; ++t) {
-    uint32_t a = t * per, b = a + per > rows ? rows : a + per;
-    if (a >= b) break;
-    jobs[t].fn = fn;
-    jobs[t].ctx = ctx;
-    jobs[t].r0 = a;
-    jobs[t].r1 = b;
-    if (t == 0) continue; /* thread 0's share runs on the caller */
-    pthread_create(&th[t], NULL, row_thread, &jobs[t]);
-    launched = t;
+  pthread_mutex_lock(&pool_call_mu);
+  pthread_mutex_lock(&pool_mu);
+  while (pool_workers < nthreads - 1) {
+    pthread_t th;
+    if (pthread_create(&th, NULL, pool_worker, (void*)(intptr_t)pool_workers) != 0) break;
+    pthread_detach(th);
+    ++pool_workers;
   }
-  fn(ctx, jobs[0].r0, jobs[0].r1);
-  for (int t = 1; t <= launched; ++t) pthread_join(th[t], NULL);
-  free(th);
-  free(jobs);
+  if (nthreads - 1 > pool_workers) nthreads = pool_workers + 1;
+  pool_cur.fn = fn;
+  pool_cur.ctx = ctx;
+  pool_cur.rows = rows;
+  pool_cur.nthreads = nthreads;
+  pool_pending = pool_workers;
+  ++pool_gen;
+  pthread_cond_broadcast(&pool_go);
+  pthread_mutex_unlock(&pool_mu);
+  run_share(&pool_cur, 0);
+  pthread_mutex_lock(&pool_mu);
+  while (pool_pending > 0) pthread_cond_wait(&pool_done, &pool_mu);
+  pthread_mutex_unlock(&pool_mu);
+  pthread_mutex_unlock(&pool_call_mu);
 }
 
 /* ------------------------------------------------------------------ */
@@ -193,6 +232,31 @@ int orc_lm_head(const uint32_t* packed, const uint16_t* scales, const uint16_t* 
 /* bf16_matvec_cpu (cpu_matvec.rs:318-357, `acc = w.mul_add(x[c], acc)` */
 /* in column order) with f32 weights in place of bf16 ones.            */
 /* ------------------------------------------------------------------ */
+typedef struct {
+  const float* w;
+  uint32_t in_dim;
+  const float* x;
+  float* out;
+} f32mv_ctx;
+
+static void f32mv_rows(void* p, uint32_t r0, uint32_t r1) {
+  const f32mv_ctx* c = (const f32mv_ctx*)p;
+  for (uint32_t r = r0; r < r1; ++r) {
+    const float* row = c->w + (size_t)r * c->in_dim;
+    float acc = 0.0f;
+    for (uint32_t i = 0; i < c->in_dim; ++i) acc = fmaf(row[i], c->x[i], acc);
+    c->out[r] = acc;
+  }
+}
+
+/* The same, rows in parallel (the reference's row-parallel matvecs,   */
+/* cpu_matvec.rs:150); per-row arithmetic and order are unchanged.     */
+void orc_f32_matvec_mt(const float* w, uint32_t in_dim, uint32_t out_dim, const float* x, float* out,
+                       int nthreads) {
+  f32mv_ctx c = {w, in_dim, x, out};
+  parallel_rows(f32mv_rows, &c, out_dim, nthreads);
+}
+
 void orc_f32_matvec(const float* w, uint32_t in_dim, uint32_t out_dim, const float* x, float* out) {
   for (uint32_t r = 0; r < out_dim; ++r) {
     const float* row = w + (size_t)r * in_dim;
@@ -402,7 +466,7 @@ int orc_moe_decode_layer(const orc_layer* L, const float* x, const float* h_mid,
   if (L->k == 0 || L->k > L->n_experts || L->k > 16) return ORC_ERR_BAD_K;
   uint32_t H = L->hidden;
   float* scores = (float*)malloc(sizeof(float) * L->n_experts);
-  orc_f32_matvec(L->router_w, H, L->n_experts, x, scores);
+  orc_f32_matvec_mt(L->router_w, H, L->n_experts, x, scores, nthreads);
   if (logits_out) memcpy(logits_out, scores, sizeof(float) * L->n_experts);
   int rc = orc_router(scores, L->n_experts, L->k, L->normalize, idx_out, w_out);
   free(scores);

@@ -62,6 +62,8 @@ int orc_dequant_matvec_4bit_gs(const uint32_t* packed, const uint16_t* scales,
 int orc_lm_head(const uint32_t* packed, const uint16_t* scales, const uint16_t* biases,
                 uint32_t hidden, uint32_t vocab, uint32_t group, const float* x, float* out);
 void orc_f32_matvec(const float* w, uint32_t in_dim, uint32_t out_dim, const float* x, float* out);
+void orc_f32_matvec_mt(const float* w, uint32_t in_dim, uint32_t out_dim, const float* x, float* out,
+                       int nthreads);
 uint32_t orc_argmax(const float* v, uint32_t n);
 
 /* ---- 3-bit layout ------------------------------------------------- */

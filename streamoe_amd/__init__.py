@@ -149,7 +149,7 @@ class Kernels:
         check(_lib.smoe_set_option(self.h, option, value), "smoe_set_option")
 
     def set_decode_path(self, path):
-        """0 auto, 1 one kernel per phase, 2 persistent, 3 three-kernel (SMOE_OPT_DECODE_PATH)."""
+        """0 auto, 1 one kernel per phase, 3 three-kernel only (SMOE_OPT_DECODE_PATH)."""
         self.set_option(_abi.SMOE_OPT_DECODE_PATH, path)
 
     def reserve(self, max_hidden, max_inter, max_experts):

@@ -8,7 +8,6 @@
 #include "../../include/smoe.h"
 #include "handle.h"
 #include "kernels.h"
-#include "persist.h"
 
 using namespace smoe;
 
@@ -58,10 +57,8 @@ int reserve(smoe_handle* h, uint32_t H, uint32_t I, uint32_t E) {
   const size_t log_b = al(T * lstride * sizeof(float));
   const size_t tab_b = al(T * sizeof(FfnTable));
   const size_t xl_b = al(T * (size_t)H / 32 * 32 * sizeof(uint32_t));
-  const size_t tr_b = al((size_t)H * 8), tl_b = al(((size_t)E + 1) * 8);
-  const size_t ta_b = al((size_t)kMaxSlotsHost * I * 8), tro_b = al(32 * 8);
   const size_t arg_b = 2 * (size_t)kQmvMaxWaves * sizeof(uint32_t);
-  const size_t total = act_b + log_b + 256 + tab_b + xl_b + arg_b + tr_b + tl_b + ta_b + tro_b + 256;
+  const size_t total = act_b + log_b + 256 + tab_b + xl_b + arg_b + 256;
   void* mem = nullptr;
   if (hipSetDevice(h->device) != hipSuccess) return SMOE_ERR_HIP;
   if (hipMalloc(&mem, total) != hipSuccess) return SMOE_ERR_HIP;
@@ -85,16 +82,7 @@ int reserve(smoe_handle* h, uint32_t H, uint32_t I, uint32_t E) {
   h->arg_v = (float*)q;
   h->arg_i = (uint32_t*)(q + kQmvMaxWaves * sizeof(float));
   q += arg_b;
-  h->tag_resid = (uint64_t*)q;
-  q += tr_b;
-  h->tag_logit = (uint64_t*)q;
-  q += tl_b;
-  h->tag_act = (uint64_t*)q;
-  q += ta_b;
-  h->tag_route = (uint64_t*)q;
-  q += tro_b;
   h->err = (uint32_t*)q;
-  h->epoch = 1;
   h->lstride = (uint32_t)lstride;
   h->astride = (uint32_t)(kMaxSlotsHost * I);
   h->xstride = H / 32 * 32;
@@ -124,7 +112,7 @@ const char* smoe_strerror(int status) {
     case SMOE_ERR_WORKSPACE_TOO_SMALL: return "workspace smaller than the required size";
     case SMOE_ERR_HIP: return "HIP runtime error";
     case SMOE_ERR_NO_DEVICE: return "no gfx950 device at that ordinal";
-    case SMOE_ERR_DEVICE_TIMEOUT: return "a bounded device-side wait expired; outputs are invalid";
+    case SMOE_ERR_DEVICE_TIMEOUT: return "a bounded device-side wait expired (reserved: no entry point of this build waits)";
     case SMOE_ERR_IO: return "file could not be opened or read, or is shorter than asked";
     default: return "unknown status";
   }
@@ -146,6 +134,7 @@ int smoe_create(int device, void* stream, smoe_handle** out) {
   h->stream = (hipStream_t)stream;
   const int rc = reserve(h, 4096, 2048, 1024);
   if (rc) {
+    if (h->mem) (void)hipFree(h->mem);
     delete h;
     return rc;
   }
@@ -193,7 +182,9 @@ int smoe_set_option(smoe_handle* h, int option, int64_t value) {
   if (!h) return SMOE_ERR_INVALID_ARG;
   switch (option) {
     case SMOE_OPT_DECODE_PATH:
-      if (value < 0 || value > 3) return SMOE_ERR_INVALID_ARG;
+      // 2 was the persistent cooperative decode, removed (slower than the
+      // three-kernel path on every shape it covered).
+      if (value < 0 || value > 3 || value == 2) return SMOE_ERR_INVALID_ARG;
       h->decode_path = (int)value;
       return SMOE_OK;
     case SMOE_OPT_TRACE_BUFFER:
@@ -398,7 +389,8 @@ int smoe_experts_decode(smoe_handle* h, const smoe_expert_shape* shape,
   return hip_status(e);
 }
 
-static int check_layer(smoe_handle* h, const smoe_layer* L) {
+// Arguments of one resident layer, independent of any reservation.
+static int check_layer_args(const smoe_layer* L) {
   if (!L || !L->experts || !L->router_w) return SMOE_ERR_INVALID_ARG;
   if (int rc = check_shape(&L->shape)) return rc;
   if (int rc = check_router(1, L->n_experts, L->k)) return rc;
@@ -409,6 +401,11 @@ static int check_layer(smoe_handle* h, const smoe_layer* L) {
   if (!aligned(L->router_w, 0, 16) || (L->shared_gate && !aligned(L->shared_gate, 0, 16)))
     return SMOE_ERR_MISALIGNED;
   if (L->shape.hidden % 4) return SMOE_ERR_UNSUPPORTED_SHAPE;
+  return SMOE_OK;
+}
+
+static int check_layer(smoe_handle* h, const smoe_layer* L) {
+  if (int rc = check_layer_args(L)) return rc;
   if (L->shape.hidden > h->max_hidden || L->shape.inter > h->max_inter ||
       L->n_experts > h->max_experts)
     return SMOE_ERR_SCRATCH_TOO_SMALL;
@@ -454,10 +451,25 @@ static bool fused_ok(const smoe_layer* L) {
   return fused_supported(s.hidden, s.inter, s.group, s.bits, L->n_experts, L->k);
 }
 
-static int decode_fused(smoe_handle* h, const smoe_layer* L, const float* x_in, const float* resid,
-                        const uint16_t* norm, float eps, float* x_out, const float* h_mid,
-                        float* out, int32_t* idx_out, float* w_out, uint32_t layer_index,
-                        uint32_t n_tokens = 1) {
+// Where the three-kernel decode keeps its per-token intermediates (router
+// logits, activations, route table, x limbs) and the stream it runs on.
+struct FaScratch {
+  uint32_t* xl;
+  float* logits;
+  float* act;
+  FfnTable* table;
+  uint32_t lstride, astride, xstride;  // per-token strides (elements)
+  uint64_t* trace;
+  hipStream_t stream;
+};
+
+static FaScratch handle_scratch(const smoe_handle* h) {
+  return FaScratch{h->xl, h->logits, h->act, h->table, h->lstride, h->astride, h->xstride, h->trace, h->stream};
+}
+
+static int decode_fused(const FaScratch& sc, const smoe_layer* L, const float* x_in, const float* resid,
+                        const uint16_t* norm, float eps, const float* h_mid, float* out, int32_t* idx_out,
+                        float* w_out, uint32_t layer_index, uint32_t n_tokens = 1) {
   if (!fused_ok(L)) return SMOE_ERR_UNSUPPORTED_SHAPE;
   const smoe_expert_shape& s = L->shape;
   FusedLayer a{};
@@ -465,8 +477,7 @@ static int decode_fused(smoe_handle* h, const smoe_layer* L, const float* x_in, 
   a.resid = resid;
   a.norm = norm;
   a.eps = eps;
-  a.xl = h->xl;
-  (void)x_out;
+  a.xl = sc.xl;
   a.router = L->router_w;
   a.shared = (const uint8_t*)L->shared_expert;
   a.gate = L->shared_expert ? L->shared_gate : nullptr;
@@ -477,81 +488,33 @@ static int decode_fused(smoe_handle* h, const smoe_layer* L, const float* x_in, 
   a.E = L->n_experts;
   a.k = L->k;
   a.normalize = L->normalize != 0;
-  a.logits = h->logits;
-  a.act = h->act;
-  a.table = h->table;
+  a.logits = sc.logits;
+  a.act = sc.act;
+  a.table = sc.table;
   a.h_mid = h_mid;
   a.out = out;
   a.idx_out = idx_out;
   a.w_out = w_out;
-  a.trace = (h->trace && n_tokens == 1) ? h->trace + (uint64_t)layer_index * kFaTraceLayer : nullptr;
+  a.trace = (sc.trace && n_tokens == 1) ? sc.trace + (uint64_t)layer_index * kFaTraceLayer : nullptr;
   a.n_tokens = n_tokens;
-  a.lstride = h->lstride;
-  a.astride = h->astride;
-  a.xstride = h->xstride;
-  return hip_status(launch_fused_layer(a, h->stream));
+  a.lstride = sc.lstride;
+  a.astride = sc.astride;
+  a.xstride = sc.xstride;
+  return hip_status(launch_fused_layer(a, sc.stream));
 }
 
-// One persistent launch over layers[0..n) (n <= kMaxPLayers). Returns
-// SMOE_ERR_UNSUPPORTED_SHAPE when no instance covers the shapes.
-static int decode_persistent(smoe_handle* h, const smoe_layer* layers, uint32_t n,
-                             const void* const* norm_w, float eps, const float* input,
-                             const float* resid_in, float* out, int32_t* idx_out, float* w_out) {
-  const smoe_layer& L0 = layers[0];
-  const smoe_expert_shape& s = L0.shape;
-  PPlan plan;
-  const bool shared = L0.shared_expert != nullptr;
-  if (n > (uint32_t)kMaxPLayers || s.group < 32 ||
-      !persist_plan(s.hidden, s.inter, L0.n_experts, L0.k, s.bits, shared,
-                    idx_out != nullptr || w_out != nullptr, &plan))
-    return SMOE_ERR_UNSUPPORTED_SHAPE;
-  for (uint32_t l = 1; l < n; ++l) {
-    const smoe_layer& L = layers[l];
-    if (L.shape.hidden != s.hidden || L.shape.inter != s.inter || L.shape.group != s.group ||
-        L.shape.bits != s.bits || L.n_experts != L0.n_experts || L.k != L0.k ||
-        (L.shared_expert != nullptr) != shared || (L.shared_gate != nullptr) != (L0.shared_gate != nullptr) ||
-        (L.normalize != 0) != (L0.normalize != 0))
-      return SMOE_ERR_UNSUPPORTED_SHAPE;
+// n_layers layers of one token on the three-kernel path: layer l reads x_l
+// (input, or RMSNorm(residual) * norm_w[l] inside the router kernel) and
+// adds its MoE output to residual_io.
+static int decode_chain_fused(const FaScratch& sc, const smoe_layer* layers, uint32_t n_layers,
+                              const void* const* norm_w, float eps, const float* input, float* residual_io) {
+  for (uint32_t l = 0; l < n_layers; ++l) {
+    const uint16_t* nw = (norm_w && l > 0) ? (const uint16_t*)norm_w[l] : nullptr;
+    if (int rc = decode_fused(sc, &layers[l], l == 0 ? input : nullptr, residual_io, nw, eps, residual_io,
+                              residual_io, nullptr, nullptr, l))
+      return rc;
   }
-  PArgs a{};
-  for (uint32_t l = 0; l < n; ++l) {
-    const smoe_layer& L = layers[l];
-    a.L[l].experts = (const uint8_t*)L.experts;
-    a.L[l].router = L.router_w;
-    a.L[l].shared = (const uint8_t*)L.shared_expert;
-    a.L[l].gate = L.shared_gate;
-    a.L[l].norm = (norm_w && l > 0) ? (const uint16_t*)norm_w[l] : nullptr;
-    a.L[l].stride = L.stride;
-  }
-  a.geom_routed = blob_geom(s.hidden, s.inter, s.group, s.bits);
-  a.geom_shared = blob_geom(s.hidden, s.inter, s.group, 4);
-  a.n_layers = n;
-  a.E = L0.n_experts;
-  a.k = L0.k;
-  a.group = s.group;
-  a.normalize = L0.normalize != 0;
-  a.has_shared = shared;
-  a.has_gate = shared && L0.shared_gate != nullptr;
-  a.eps = eps;
-  a.input = input;
-  a.resid_in = resid_in;
-  a.out = out;
-  a.idx_out = idx_out;
-  a.w_out = w_out;
-  a.tag_resid = h->tag_resid;
-  a.tag_logit = h->tag_logit;
-  a.tag_act = h->tag_act;
-  a.err = h->err;
-  a.trace = h->trace;
-  if (h->epoch > 0xFFFFFF00u - n) {
-    // Epoch space exhausted: clear the tags and restart at 1.
-    const size_t bytes = (char*)(h->tag_route + 32) - (char*)h->tag_resid;
-    if (hipMemsetAsync(h->tag_resid, 0, bytes, h->stream) != hipSuccess) return SMOE_ERR_HIP;
-    h->epoch = 1;
-  }
-  a.epoch = h->epoch;
-  h->epoch += n;
-  return hip_status(launch_decode_persistent(a, plan, s.bits, h->stream));
+  return SMOE_OK;
 }
 
 int smoe_moe_decode_layer(smoe_handle* h, const smoe_layer* layer, const float* input,
@@ -560,11 +523,8 @@ int smoe_moe_decode_layer(smoe_handle* h, const smoe_layer* layer, const float* 
   if (int rc = check_layer(h, layer)) return rc;
   if (!aligned(input, 0, 16)) return SMOE_ERR_MISALIGNED;
   if (int rc = use_device(h)) return rc;
-  if (h->decode_path == 2) {
-    return decode_persistent(h, layer, 1, nullptr, 0.f, input, h_mid, hidden_out, idx_out, w_out);
-  }
   if (h->decode_path != 1) {
-    const int rc = decode_fused(h, layer, input, nullptr, nullptr, 0.f, nullptr, h_mid, hidden_out,
+    const int rc = decode_fused(handle_scratch(h), layer, input, nullptr, nullptr, 0.f, h_mid, hidden_out,
                                 idx_out, w_out, 0);
     if (rc != SMOE_ERR_UNSUPPORTED_SHAPE || h->decode_path == 3) return rc;
   }
@@ -587,36 +547,8 @@ int smoe_moe_decode_layers(smoe_handle* h, const smoe_layer* layers, uint32_t n_
   if (h->decode_path == 0 || h->decode_path == 3) {
     bool all = true;
     for (uint32_t l = 0; l < n_layers; ++l) all = all && fused_ok(&layers[l]);
-    if (all) {
-      for (uint32_t l = 0; l < n_layers; ++l) {
-        const uint16_t* nw = (norm_w && l > 0) ? (const uint16_t*)norm_w[l] : nullptr;
-        if (int rc = decode_fused(h, &layers[l], l == 0 ? input : nullptr, residual_io, nw, eps,
-                                  work, residual_io, residual_io, nullptr, nullptr, l))
-          return rc;
-      }
-      return SMOE_OK;
-    }
+    if (all) return decode_chain_fused(handle_scratch(h), layers, n_layers, norm_w, eps, input, residual_io);
     if (h->decode_path == 3) return SMOE_ERR_UNSUPPORTED_SHAPE;
-  }
-  if (h->decode_path == 2) {
-    // Persistent launches of up to kMaxPLayers layers; between chunks the
-    // next chunk's input is RMSNorm(residual).
-    int rc = SMOE_OK;
-    for (uint32_t l0 = 0; l0 < n_layers && rc == SMOE_OK; l0 += kMaxPLayers) {
-      const uint32_t n = n_layers - l0 < (uint32_t)kMaxPLayers ? n_layers - l0 : (uint32_t)kMaxPLayers;
-      const float* x = input;
-      if (l0 > 0) {
-        x = residual_io;
-        if (norm_w) {
-          if (launch_rmsnorm(residual_io, (const uint16_t*)norm_w[l0], eps, H, work, h->stream) != hipSuccess)
-            return SMOE_ERR_HIP;
-          x = work;
-        }
-      }
-      rc = decode_persistent(h, layers + l0, n, norm_w ? norm_w + l0 : nullptr, eps, x, residual_io,
-                             residual_io, nullptr, nullptr);
-    }
-    return rc;
   }
   for (uint32_t l = 0; l < n_layers; ++l) {
     const float* x = input;
@@ -653,8 +585,9 @@ int smoe_moe_decode_tokens(smoe_handle* h, const smoe_layer* layers, uint32_t n_
   for (uint32_t l = 0; l < n_layers; ++l) {
     const uint16_t* nw = (norm_w && l > 0) ? (const uint16_t*)norm_w[l] : nullptr;
     const bool last = l + 1 == n_layers;
-    if (int rc = decode_fused(h, &layers[l], l == 0 ? input : nullptr, residual_io, nw, eps, work, residual_io,
-                              residual_io, last ? idx_out : nullptr, last ? w_out : nullptr, l, n_tokens))
+    if (int rc = decode_fused(handle_scratch(h), &layers[l], l == 0 ? input : nullptr, residual_io, nw, eps,
+                              residual_io, residual_io, last ? idx_out : nullptr, last ? w_out : nullptr, l,
+                              n_tokens))
       return rc;
   }
   return SMOE_OK;

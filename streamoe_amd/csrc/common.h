@@ -63,8 +63,20 @@ __device__ __forceinline__ T ld_stream(const T* p) {
 #endif
 }
 
+// Weight load: non-temporal (NT, the routed experts: streamed once per
+// token) or temporal (data reused every token, e.g. router rows and the
+// shared expert, which then stay resident in the memory-side cache).
+template <bool NT, typename T>
+__device__ __forceinline__ T ld_w(const T* p) {
+  if constexpr (NT)
+    return ld_stream(p);
+  else
+    return *p;
+}
+
+template <bool NT = true>
 __device__ __forceinline__ Raw<4> load_raw4(const uint8_t* p) {
-  const u32x4 v = ld_stream(reinterpret_cast<const u32x4*>(p));
+  const u32x4 v = ld_w<NT>(reinterpret_cast<const u32x4*>(p));
   Raw<4> r;
   r.d[0] = v.x;
   r.d[1] = v.y;
@@ -72,23 +84,21 @@ __device__ __forceinline__ Raw<4> load_raw4(const uint8_t* p) {
   r.d[3] = v.w;
   return r;
 }
+template <bool NT = true>
 __device__ __forceinline__ Raw<3> load_raw3(const uint8_t* p) {
   const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
   Raw<3> r;
-  r.d[0] = ld_stream(q + 0);
-  r.d[1] = ld_stream(q + 1);
-  r.d[2] = ld_stream(q + 2);
+  r.d[0] = ld_w<NT>(q + 0);
+  r.d[1] = ld_w<NT>(q + 1);
+  r.d[2] = ld_w<NT>(q + 2);
   return r;
 }
-template <int BITS>
-__device__ __forceinline__ Raw<BITS> load_raw(const uint8_t* p);
-template <>
-__device__ __forceinline__ Raw<4> load_raw<4>(const uint8_t* p) {
-  return load_raw4(p);
-}
-template <>
-__device__ __forceinline__ Raw<3> load_raw<3>(const uint8_t* p) {
-  return load_raw3(p);
+template <int BITS, bool NT = true>
+__device__ __forceinline__ Raw<BITS> load_raw(const uint8_t* p) {
+  if constexpr (BITS == 4)
+    return load_raw4<NT>(p);
+  else
+    return load_raw3<NT>(p);
 }
 
 // Codes of a chunk as exact floats, in input order j = 0..31.

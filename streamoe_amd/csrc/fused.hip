@@ -36,8 +36,10 @@
 //                      residual.
 //
 // Weights are read exactly once per token with 128-bit (4-bit) or 96-bit
-// (3-bit) non-temporal loads; x limbs and logits (<= 10 KB) are re-read
-// from L2 by every wave that needs them, and each K_C block stages the
+// (3-bit) loads: non-temporal for the routed experts, temporal for the
+// router rows and the shared expert (reused by every token, they stay in
+// the memory-side cache); x limbs and logits (<= 10 KB) are re-read from
+// L2 by every wave that needs them, and each K_C block stages the
 // activations (<= 68 KB) in LDS once.
 #include "common.h"
 #include "kernels.h"
@@ -199,10 +201,16 @@ __device__ __forceinline__ FusedLayer token_view(const FusedLayer& a, uint32_t t
 #define FA_ARGS_IN_SGPRS(...) asm volatile("" ::__VA_ARGS__)
 
 // A 2048-wide f32 row (router row or shared-expert gate), chunk c per lane.
+// Router rows and the shared-gate row are read by every token, so they are
+// loaded temporally: all 40 layers' routers and shared experts (155 MB at
+// the A3B shape) then stay in the 256 MB memory-side cache while the routed
+// experts stream past it non-temporally (measured on MI355X: a 2 MB
+// temporal read after a 512 MB non-temporal stream takes 0.74 us, against
+// 1.49 us from HBM).
 __device__ __forceinline__ void fa_row_load(const float* row, uint32_t c, f32x4 (&wr)[kChunk / 4]) {
   const f32x4* rp = reinterpret_cast<const f32x4*>(row + (size_t)c * kChunk);
 #pragma unroll
-  for (int i = 0; i < kChunk / 4; ++i) wr[i] = ld_stream(rp + i);
+  for (int i = 0; i < kChunk / 4; ++i) wr[i] = ld_w<false>(rp + i);
 }
 
 // row . x over the wave (valid in lane 63): four FMA chains per lane, then
@@ -300,7 +308,9 @@ __device__ __forceinline__ void load_logits(const float* logits, uint32_t E, int
 
 // gate and up rows [r0, r0 + kFaRW) of one expert blob against x (limbs),
 // SwiGLU, stored to act[r0 ..]. All loads are issued before any arithmetic.
-template <int BITS>
+// NT: non-temporal weight loads (routed experts) or temporal (the shared
+// expert, reused by every token).
+template <int BITS, bool NT>
 __device__ __forceinline__ void gateup_rows(const FusedLayer& a, FaClock& clk, const uint8_t* blob,
                                             const BlobGeom& g, uint32_t r0, int lane,
                                             const XLimbs& xl, float* act) {
@@ -314,8 +324,8 @@ __device__ __forceinline__ void gateup_rows(const FusedLayer& a, FaClock& clk, c
 #pragma unroll
   for (int p = 0; p < kFaRW; ++p) {
     const uint32_t row = r0 + p;
-    rg[p] = load_raw<BITS>(blob + g.w[0] + (size_t)row * RB + c * CB);
-    ru[p] = load_raw<BITS>(blob + g.w[1] + (size_t)row * RB + c * CB);
+    rg[p] = load_raw<BITS, NT>(blob + g.w[0] + (size_t)row * RB + c * CB);
+    ru[p] = load_raw<BITS, NT>(blob + g.w[1] + (size_t)row * RB + c * CB);
     load_sb(blob, g.s[0], g.b[0], row, gpr, cps, c, sg[p], bg[p]);
     load_sb(blob, g.s[1], g.b[1], row, gpr, cps, c, su[p], bu[p]);
   }
@@ -389,13 +399,13 @@ __global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a_all) {
       id = sid[slot];
     }
     fa_stamp(a, clk, 2, false);
-    gateup_rows<BITS>(a, clk, a.experts + (uint64_t)id * a.stride, a.routed, r0, lane, xl,
-                      a.act + (size_t)slot * I);
+    gateup_rows<BITS, true>(a, clk, a.experts + (uint64_t)id * a.stride, a.routed, r0, lane, xl,
+                            a.act + (size_t)slot * I);
   } else if (blockIdx.x < nrouted + nshared) {
     const uint32_t r0 = (blockIdx.x - nrouted) * kFaRW;
     XLimbs xl;
     load_limbs(a.xl + (size_t)lane * kXLimbWords, xl);
-    gateup_rows<4>(a, clk, a.shared, a.sgeom, r0, lane, xl, a.act + (size_t)k * I);
+    gateup_rows<4, false>(a, clk, a.shared, a.sgeom, r0, lane, xl, a.act + (size_t)k * I);
   } else {
     // Route table (normalize_weights, moe_router.rs:130-141).
     __shared__ float sprob[64 * P];
@@ -497,7 +507,7 @@ struct DownLoads {
   uint16_t sr[NR], br[NR];
 };
 
-template <int BITS, int LI, int NR>
+template <int BITS, int LI, int NR, bool NT = true>
 __device__ __forceinline__ void down_load(const uint8_t* blob, const BlobGeom& g, uint32_t row0,
                                           uint32_t c, DownLoads<BITS, NR>& d) {
   constexpr int CB = chunk_bytes<BITS>();
@@ -507,7 +517,7 @@ __device__ __forceinline__ void down_load(const uint8_t* blob, const BlobGeom& g
 #pragma unroll
   for (int r = 0; r < NR; ++r) {
     const uint32_t row = row0 + r;
-    d.raw[r] = load_raw<BITS>(blob + g.w[2] + (size_t)row * RB + c * CB);
+    d.raw[r] = load_raw<BITS, NT>(blob + g.w[2] + (size_t)row * RB + c * CB);
     const size_t gi = ((size_t)row * gpr + (c >> cps)) * 2;
     d.sr[r] = *reinterpret_cast<const uint16_t*>(blob + g.s[2] + gi);
     d.br[r] = *reinterpret_cast<const uint16_t*>(blob + g.b[2] + gi);
@@ -611,7 +621,7 @@ __global__ __launch_bounds__(1024) void k_fa_down(FusedLayer a_all) {
     }
   } else {
     DownLoads<4, NRS> d;
-    down_load<4, LI, NRS>(blob, a.sgeom, lrow0, c, d);
+    down_load<4, LI, NRS, false>(blob, a.sgeom, lrow0, c, d);
 #pragma unroll
     for (int i = 0; i < kFaStage; ++i) {
       const uint32_t j = threadIdx.x + i * blockDim.x;

@@ -21,18 +21,12 @@ struct smoe_handle {
   uint32_t* xl = nullptr;     // [max_hidden / 32 * kXLimbWords] x as integer limbs
   float* arg_v = nullptr;     // [256] argmax partial values
   uint32_t* arg_i = nullptr;  // [256] argmax partial indices
-  // Persistent decode: tagged handoff buffers (epoch << 32 | value).
-  uint64_t* tag_resid = nullptr;  // [max_hidden]
-  uint64_t* tag_logit = nullptr;  // [max_experts + 1]
-  uint64_t* tag_act = nullptr;    // [kMaxSlots * max_inter]
-  uint64_t* tag_route = nullptr;  // [32]
-  uint32_t* err = nullptr;        // device error word
-  uint32_t epoch = 1;             // next unused epoch (0 is never used)
+  uint32_t* err = nullptr;        // device error word (prefill routing errors)
   uint32_t max_hidden = 0, max_inter = 0, max_experts = 0;
   // Per-token strides (elements) of logits, act and limbs in the scratch.
   uint32_t lstride = 0, astride = 0, xstride = 0;
   // Options.
-  int decode_path = 0;  // 0 auto, 1 per-phase kernels, 2 persistent, 3 three-kernel
+  int decode_path = 0;  // 0 auto, 1 per-phase kernels, 3 three-kernel
   uint64_t* trace = nullptr;
   // File loader: two pinned host staging buffers (allocated on first use,
   // freed by smoe_destroy) and the events that say when a copy out of

@@ -424,28 +424,15 @@ LAYER_CASES = [
     ("k10", 2048, 512, 128, 10, 4, True, True),      # the reference's other supported top-k
 ]
 
-PATHS = [1, 2, 3]
-PATH_IDS = ["per-phase", "persistent", "three-kernel"]
+PATHS = [1, 3]
+PATH_IDS = ["per-phase", "three-kernel"]
 
 
 @pytest.mark.parametrize("path", PATHS, ids=PATH_IDS)
 @pytest.mark.parametrize("name,H,I,E,k,bits,normalize,shared", LAYER_CASES)
 def test_moe_decode_layer_matches_oracle(kernels, path, name, H, I, E, k, bits, normalize, shared):
-    from streamoe_amd import _abi
-
     kernels.set_decode_path(path)
     try:
-        if path == 2 and k > 8:
-            torch = _torch()
-            buf = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
-            import streamoe_amd as sa
-
-            lay = sa.ExpertLayout(H, I, bits, 64)
-            r = torch.zeros((E, H), dtype=torch.float32, device="cuda")
-            x = torch.zeros(H, dtype=torch.float32, device="cuda")
-            L = kernels.layer(lay, buf, lay.expert_size, E, k, normalize, r)
-            assert kernels.moe_decode_layer(L, x, x, x) == _abi.CODES["SMOE_ERR_UNSUPPORTED_SHAPE"]
-            return
         seed = sum(map(ord, name)) * 7 + 1
         got, gi, gw, want, wi, ww, gap = _layer_case(kernels, H, I, E, k, bits, normalize, shared, seed=seed)
         kernels.sync()
@@ -454,39 +441,6 @@ def test_moe_decode_layer_matches_oracle(kernels, path, name, H, I, E, k, bits, 
         assert np.array_equal(gi, wi)
         assert np.max(np.abs(gw - ww)) <= 1e-5 * np.max(np.abs(ww))
         assert err <= TOL
-    finally:
-        kernels.set_decode_path(0)
-
-
-def test_persistent_repeated_launches_are_identical(kernels):
-    """The persistent decode is deterministic: fixed-order reductions, no
-    atomics in the arithmetic; 20 launches give the same bits (and each
-    launch uses fresh epochs for its tagged handoffs)."""
-    import streamoe_amd as sa
-
-    torch = _torch()
-    H, I, E, k = 2048, 512, 256, 8
-    lay = sa.ExpertLayout(H, I, 4, 64)
-    arena = torch.empty(E * lay.expert_size, dtype=torch.uint8, device="cuda")
-    assert kernels.synth_experts(arena, E, lay.expert_size, lay, 77) == 0
-    sh = torch.empty(lay.expert_size, dtype=torch.uint8, device="cuda")
-    assert kernels.synth_experts(sh, 1, lay.expert_size, lay, 78) == 0
-    r = torch.empty((E, H), dtype=torch.float32, device="cuda")
-    g = torch.empty(H, dtype=torch.float32, device="cuda")
-    x = torch.empty(H, dtype=torch.float32, device="cuda")
-    for i, (t, sg) in enumerate([(r, 0.02), (g, 0.02), (x, 1.0)]):
-        assert kernels.synth_normal_f32(t, 900 + i, sg) == 0
-    L = kernels.layer(lay, arena, lay.expert_size, E, k, True, r, sh, g)
-    kernels.set_decode_path(2)
-    try:
-        outs = []
-        for _ in range(20):
-            out = torch.empty(H, dtype=torch.float32, device="cuda")
-            assert kernels.moe_decode_layer(L, x, x, out) == 0
-            outs.append(out)
-        kernels.sync()
-        ref = host(outs[0]).view(np.uint32)
-        assert all(np.array_equal(host(o).view(np.uint32), ref) for o in outs[1:])
     finally:
         kernels.set_decode_path(0)
 
