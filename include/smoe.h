@@ -288,6 +288,22 @@ int smoe_moe_decode_layers(smoe_handle* h, const smoe_layer* layers, uint32_t n_
                            const void* const* norm_w, float eps, const float* input,
                            float* residual_io, float* work);
 
+/* smoe_moe_decode_layers without a handle and without any allocation, for
+ * callers that cannot allocate device memory: code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc. No
+ * counterpart in the reference. Same arguments and results as
+ * smoe_moe_decode_layers (bit for bit), on the CURRENT device, enqueued on
+ * `stream` (a hipStream_t; NULL = the default stream). The three-kernel
+ * shapes only (hidden 2048, inter 512 or 1024, <= 256 experts, k <= 16;
+ * else SMOE_ERR_UNSUPPORTED_SHAPE). Its intermediates live in a fixed
+ * 128 KiB device array that each GPU the library runs on holds until the
+ * process ends; layers needing more return SMOE_ERR_SCRATCH_TOO_SMALL. The
+ * first call on a device without a handle (smoe_create does it for its
+ * device) looks the array's address up once. Calls that overlap on one GPU
+ * share the array and race: serialise them (one stream per GPU). */
+int smoe_moe_decode_layers_noalloc(void* stream, const smoe_layer* layers, uint32_t n_layers,
+                                   const void* const* norm_w, float eps, const float* input,
+                                   float* residual_io);
 
 /* Several decode tokens (1..4) through the same layers at once, each as
  * smoe_moe_decode_layers would decode it alone (own routing, experts,

@@ -119,6 +119,7 @@ PROTOTYPES = {
                                  _P, _P, _P, C.c_float, _P]),
     "smoe_moe_decode_layer": (_I, [_P, C.POINTER(Layer), _P, _P, _P, _P, _P]),
     "smoe_moe_decode_layers": (_I, [_P, C.POINTER(Layer), _U32, C.POINTER(_P), C.c_float, _P, _P, _P]),
+    "smoe_moe_decode_layers_noalloc": (_I, [_P, C.POINTER(Layer), _U32, C.POINTER(_P), C.c_float, _P, _P]),
     "smoe_moe_decode_tokens": (_I, [_P, C.POINTER(Layer), _U32, C.POINTER(_P), C.c_float, _U32, _P, _P, _P, _P,
                                     _P]),
     "smoe_moe_prefill_workspace_size": (_U64, [C.POINTER(ExpertShape), _U32, _U32, _U32]),

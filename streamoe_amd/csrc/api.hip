@@ -3,6 +3,7 @@
 #include <math.h>
 #include <string.h>
 
+#include <mutex>
 #include <new>
 
 #include "../../include/smoe.h"
@@ -94,6 +95,38 @@ int reserve(smoe_handle* h, uint32_t H, uint32_t I, uint32_t E) {
 
 int use_device(smoe_handle* h) { return hipSetDevice(h->device) == hipSuccess ? SMOE_OK : SMOE_ERR_HIP; }
 
+// ---------------------------------------------------------------------------
+// Fixed scratch of the no-allocation decode (smoe_moe_decode_layers_noalloc):
+// one file-scope device array, which every GPU the library runs on holds
+// until the process ends. In host code `scratch` only names the symbol; its
+// address on a device comes from hipGetSymbolAddress with that device
+// current, kept per device in g_noalloc below, and only that address is
+// ever passed to a kernel. Calls that overlap on one GPU share the array
+// and race; nothing in it has to start at zero (every kernel writes what it
+// later reads within the same layer).
+// ---------------------------------------------------------------------------
+constexpr size_t kNoAllocScratchBytes = 128 * 1024;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kNoAllocMaxDevices = 64;
+std::mutex g_noalloc_mu;
+void* g_noalloc[kNoAllocMaxDevices];  // device address of `scratch`, per device
+
+// The device address of `scratch` on the current device `dev`, looked up
+// once per device (smoe_create does it for its device; the entry point for
+// any other).
+int noalloc_scratch(int dev, uint8_t** out) {
+  if (dev < 0 || dev >= kNoAllocMaxDevices) return SMOE_ERR_NO_DEVICE;
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  if (!g_noalloc[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return SMOE_ERR_HIP;
+    g_noalloc[dev] = p;
+  }
+  *out = (uint8_t*)g_noalloc[dev];
+  return SMOE_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -108,7 +141,9 @@ const char* smoe_strerror(int status) {
     case SMOE_ERR_UNSUPPORTED_GROUP: return "unsupported group size (32, 64 or 128)";
     case SMOE_ERR_UNSUPPORTED_SHAPE: return "no kernel instance for this shape";
     case SMOE_ERR_MISALIGNED: return "weight, scale or activation pointer misaligned";
-    case SMOE_ERR_SCRATCH_TOO_SMALL: return "shape exceeds the reserved scratch (smoe_reserve)";
+    case SMOE_ERR_SCRATCH_TOO_SMALL:
+      return "shape exceeds the reserved scratch (smoe_reserve), or the fixed 128 KiB scratch of "
+             "smoe_moe_decode_layers_noalloc";
     case SMOE_ERR_WORKSPACE_TOO_SMALL: return "workspace smaller than the required size";
     case SMOE_ERR_HIP: return "HIP runtime error";
     case SMOE_ERR_NO_DEVICE: return "no gfx950 device at that ordinal";
@@ -132,7 +167,9 @@ int smoe_create(int device, void* stream, smoe_handle** out) {
   if (!h) return SMOE_ERR_HIP;
   h->device = device;
   h->stream = (hipStream_t)stream;
-  const int rc = reserve(h, 4096, 2048, 1024);
+  int rc = reserve(h, 4096, 2048, 1024);
+  uint8_t* fixed = nullptr;
+  if (!rc) rc = noalloc_scratch(device, &fixed);  // set-up of the no-allocation decode on this device
   if (rc) {
     if (h->mem) (void)hipFree(h->mem);
     delete h;
@@ -566,6 +603,47 @@ int smoe_moe_decode_layers(smoe_handle* h, const smoe_layer* layers, uint32_t n_
       return rc;
   }
   return SMOE_OK;
+}
+
+int smoe_moe_decode_layers_noalloc(void* stream, const smoe_layer* layers, uint32_t n_layers,
+                                   const void* const* norm_w, float eps, const float* input, float* residual_io) {
+  if (!layers || !n_layers || !input || !residual_io) return SMOE_ERR_INVALID_ARG;
+  uint32_t max_e = 0, max_i = 0;
+  for (uint32_t l = 0; l < n_layers; ++l) {
+    if (int rc = check_layer_args(&layers[l])) return rc;
+    if (layers[l].shape.hidden != layers[0].shape.hidden) return SMOE_ERR_INVALID_ARG;
+    if (norm_w && l > 0 && !norm_w[l]) return SMOE_ERR_INVALID_ARG;
+    if (!fused_ok(&layers[l])) return SMOE_ERR_UNSUPPORTED_SHAPE;
+    max_e = layers[l].n_experts > max_e ? layers[l].n_experts : max_e;
+    max_i = layers[l].shape.inter > max_i ? layers[l].shape.inter : max_i;
+  }
+  if (!aligned(input, 0, 16) || !aligned(residual_io, 0, 16)) return SMOE_ERR_MISALIGNED;
+  // Layout of the fixed scratch for one token (the handle's layout, sized
+  // to these layers): logits, activations of the k + 1 slots, route table,
+  // x limbs, each 256-byte aligned.
+  auto al = [](size_t n) { return (n + 255) & ~(size_t)255; };
+  const uint32_t H = layers[0].shape.hidden;
+  const size_t lstride = al(((size_t)(max_e + 1 > 256 ? max_e + 1 : 256)) * sizeof(float)) / sizeof(float);
+  const size_t log_b = al(lstride * sizeof(float));
+  const size_t act_b = al((size_t)kMaxSlotsHost * max_i * sizeof(float));
+  const size_t tab_b = al(sizeof(FfnTable));
+  const size_t xl_b = al((size_t)H / 32 * 32 * sizeof(uint32_t));
+  if (log_b + act_b + tab_b + xl_b > kNoAllocScratchBytes) return SMOE_ERR_SCRATCH_TOO_SMALL;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return SMOE_ERR_HIP;
+  uint8_t* base = nullptr;
+  if (int rc = noalloc_scratch(dev, &base)) return rc;
+  FaScratch sc{};
+  sc.logits = (float*)base;
+  sc.act = (float*)(base + log_b);
+  sc.table = (FfnTable*)(base + log_b + act_b);
+  sc.xl = (uint32_t*)(base + log_b + act_b + tab_b);
+  sc.lstride = (uint32_t)lstride;
+  sc.astride = (uint32_t)(kMaxSlotsHost * max_i);
+  sc.xstride = H / 32 * 32;
+  sc.trace = nullptr;
+  sc.stream = (hipStream_t)stream;
+  return decode_chain_fused(sc, layers, n_layers, norm_w, eps, input, residual_io);
 }
 
 int smoe_moe_decode_tokens(smoe_handle* h, const smoe_layer* layers, uint32_t n_layers,

@@ -73,6 +73,20 @@ def test_create_destroy_argument_errors():
     assert lib.smoe_expert_bytes(None) == 0
 
 
+def test_noalloc_decode_argument_errors_without_gpu():
+    """The no-allocation decode validates its arguments on the host before
+    any HIP call."""
+    from streamoe_amd import _abi
+
+    lib = _abi.load()
+    assert lib.smoe_moe_decode_layers_noalloc(None, None, 0, None, C.c_float(0), None, None) == \
+        _abi.CODES["SMOE_ERR_INVALID_ARG"]
+    lay = _abi.Layer()
+    arr = (_abi.Layer * 1)(lay)
+    assert lib.smoe_moe_decode_layers_noalloc(None, arr, 1, None, C.c_float(0), C.c_void_p(16),
+                                              C.c_void_p(16)) == _abi.CODES["SMOE_ERR_INVALID_ARG"]
+
+
 def test_create_without_gpu_reports_no_device():
     import torch
     from streamoe_amd import _abi
