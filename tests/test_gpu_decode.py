@@ -555,15 +555,17 @@ def test_three_kernel_decode_graph_replays_match_eager(kernels):
         kernels.set_decode_path(0)
 
 
+@pytest.mark.parametrize("bits", [4, 3], ids=["c2-4bit", "c3-3bit"])
 @pytest.mark.parametrize("path", PATHS, ids=PATH_IDS)
-def test_decode_40_layers_matches_oracle_chain(kernels, path):
-    """Config 2 at full size: 40 resident layers (256 experts each, 18 GB),
-    one token; between layers x = RMSNorm(residual) with unit bf16 weights.
-    The CPU chain fetches only the experts its router picks. The final
-    residual must agree within 1e-3 (the smallest k-th/(k+1)-th
-    probability gap over the layers is reported)."""
+def test_decode_40_layers_matches_oracle_chain(kernels, path, bits):
+    """Configs 2 and 3 at full size: 40 resident layers (256 experts each,
+    18 GB at 4-bit, 14 GB with packed 3-bit routed experts), one token;
+    between layers x = RMSNorm(residual) with unit bf16 weights. The CPU
+    chain fetches only the experts its router picks. The final residual
+    must agree within 1e-3 (the smallest k-th/(k+1)-th probability gap over
+    the layers is reported)."""
     torch = _torch()
-    c = _chain(kernels, 40, 256, 8, 4, seed=5000)
+    c = _chain(kernels, 40, 256, 8, bits, seed=5000 + bits)
     resid = c["x0"].clone()
     work = torch.empty(c["H"], dtype=torch.float32, device="cuda")
     kernels.set_decode_path(path)
@@ -575,7 +577,7 @@ def test_decode_40_layers_matches_oracle_chain(kernels, path):
     got = host(resid)
     want, min_gap = _chain_oracle(c, 1e-6)
     err = rel_err(got, want)
-    print(f"40-layer chain path={path}: rel_err={err:.3e} min top-k gap={min_gap:.3e}")
+    print(f"40-layer chain path={path} bits={bits}: rel_err={err:.3e} min top-k gap={min_gap:.3e}")
     assert np.all(np.isfinite(got))
     assert err <= TOL
     del c

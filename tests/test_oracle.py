@@ -387,3 +387,23 @@ def test_xorshift_stream_known_values():
         st ^= st >> 27
         want.append((st * 0x2545F4914F6CDD1D) & 0xFFFFFFFFFFFFFFFF)
     assert [int(v) for v in oracle.XorShift64s(1).next_u64(3)] == want
+
+
+@pytest.mark.parametrize("pos", [0, 3, 255])
+def test_router_nan_logit_keeps_start_slots(pos):
+    """moe_router.rs:52-141 with one NaN logit: the softmax sum is NaN, so
+    every probability is NaN; `score > values[min_k]` is then never true,
+    all k slots keep their start (index 0, -1e30), and the guarded
+    renormalisation (sum > 0 fails) leaves the weights as they are. The
+    position of the NaN does not matter (a NaN at index 0 becomes the max
+    and poisons every exp; elsewhere it poisons the sum)."""
+    rng = np.random.default_rng(pos)
+    logits = rng.standard_normal(256).astype(np.float32)
+    logits[pos] = np.nan
+    probs = oracle.softmax(logits)
+    assert np.all(np.isnan(probs))
+    for normalize in (False, True):
+        rc, idx, w = oracle.router(logits, 8, normalize)
+        assert rc == 0
+        assert np.all(idx == 0)
+        assert np.all(w == np.float32(-1e30))
