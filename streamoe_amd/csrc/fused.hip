@@ -278,9 +278,29 @@ __global__ __launch_bounds__(64) void k_fa_route(FusedLayer a) {
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     const FusedLayer at = token_view(a, t);
-    fa_x_finish(at, f[t]);
-    const float s = fa_row_dot(wr, f[t].x);
-    if (lane == 63) at.logits[w] = s;
+    if (at.x_in || !at.norm) {
+      const float s = fa_row_dot(wr, f[t].x);
+      if (lane == 63) at.logits[w] = s;
+    } else {
+      // logit = (1 / rms(r)) * (W . (r * w)): the dot and the sum of
+      // squares run side by side instead of the dot waiting for the norm.
+      float rw[kChunk];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t w4[4] = {f[t].w[i].x, f[t].w[i].y, f[t].w[i].z, f[t].w[i].w};
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          rw[8 * i + 2 * h] = f[t].x[8 * i + 2 * h] * bf16f((uint16_t)(w4[h] & 0xFFFFu));
+          rw[8 * i + 2 * h + 1] = f[t].x[8 * i + 2 * h + 1] * bf16f((uint16_t)(w4[h] >> 16));
+        }
+      }
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < kChunk; ++j) ss = __builtin_fmaf(f[t].x[j], f[t].x[j], ss);
+      const float dot = fa_row_dot(wr, rw);
+      ss = group_sum_last<64>(ss);
+      if (lane == 63) at.logits[w] = dot * (1.0f / sqrtf(__builtin_fmaf(ss, 1.0f / (float)kFaH, at.eps)));
+    }
   }
   fa_stamp(a, clk, 4, false);
   fa_stamp(a, clk, 5, true);
@@ -384,8 +404,10 @@ __global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a_all) {
   const uint32_t nshared = a.shared ? tiles : 0u;
 
   if (blockIdx.x < nrouted) {
-    const uint32_t slot = blockIdx.x / tiles;
-    const uint32_t r0 = (blockIdx.x % tiles) * kFaRW;
+    // tiles is a power of two (inter 512 or 1024): shifts, no division.
+    const uint32_t tsh = __builtin_ctz(tiles);
+    const uint32_t slot = blockIdx.x >> tsh;
+    const uint32_t r0 = (blockIdx.x & (tiles - 1)) * kFaRW;
     float v[P];
     load_logits<P>(a.logits, E, lane, v);
     XLimbs xl;
