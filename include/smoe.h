@@ -142,11 +142,6 @@ int smoe_qmv(smoe_handle* h, const smoe_qweights* w, const float* x, float* y, u
  * pick. Two launches: 256 slice blocks, then one block over the partials. */
 int smoe_argmax(smoe_handle* h, const float* v, uint32_t n, int32_t* out_index);
 
-/* Dequantize rows [row0, row0 + n_rows) of `w` into device
- * f32[n_rows, in_dim]: w = fma(q, s, b), one rounding, exactly the value
- * the reference CPU path forms (crates/streammoe/src/riir/backend/cpu/
- * cpu_matvec.rs:164-165). Verification entry point: the decode kernels
- * use the same code-unpacking routine and never materialise w. */
 /* smoe_qmv and smoe_argmax of its output in one pass (the LM head with
  * the greedy pick, io/gpu_lm_head.rs:130-193): y as smoe_qmv computes it,
  * *out_index = the first index of max(y) as smoe_argmax gives it, from
@@ -170,6 +165,11 @@ uint64_t smoe_qmm_workspace_size(uint32_t in_dim, uint32_t group, uint32_t n_tok
 int smoe_qmm(smoe_handle* h, const smoe_qweights* w, const float* x, float* y, uint32_t out_dim,
              uint32_t in_dim, uint32_t n_tokens, void* workspace, uint64_t workspace_bytes);
 
+/* Dequantize rows [row0, row0 + n_rows) of `w` into device
+ * f32[n_rows, in_dim]: w = fma(q, s, b), one rounding, exactly the value
+ * the reference CPU path forms (crates/streammoe/src/riir/backend/cpu/
+ * cpu_matvec.rs:164-165). Verification entry point: the decode kernels
+ * use the same code-unpacking routine and never materialise w. */
 int smoe_dequant(smoe_handle* h, const smoe_qweights* w, uint32_t in_dim, uint32_t row0,
                  uint32_t n_rows, float* out);
 
