@@ -482,7 +482,7 @@ def run_prefill(args, c):
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": MEASURED_TRAFFIC.get("c4"),
                      "unit_of_work": f"one layer: {nbytes} algorithmic bytes ({len(hit)} hit experts x {stride} "
                                      f"+ X + Y), {flops} flops",
-                     "kernel": "prefill layer: k_pf_route + k_pf_prep_x + k_pf_mm (gate/up, with the activation "
+                     "kernel": "prefill layer: k_pf_route (+ per-token x preparation) + k_pf_mm (gate/up, with the activation "
                                "group sums) + k_pf_mm (down) + k_pf_combine (one HIP graph)"},
     }
     if not args.no_cpu:

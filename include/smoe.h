@@ -262,7 +262,7 @@ typedef struct {
 
 /* Decode one token through one layer with routing on the device:
  * router -> top-k -> routed + shared expert FFN -> combine. For hidden
- * 2048, inter 512 or 1024, <= 256 experts this is three kernels (router +
+ * 2048, inter 512 or 1024, <= 512 experts this is three kernels (router +
  * shared gate/up; top-k + routed gate/up; down + combine) that allocate
  * nothing and set no memory, so a caller can capture them in a HIP graph;
  * other shapes take one kernel per phase. See SMOE_OPT_DECODE_PATH.
@@ -294,7 +294,7 @@ int smoe_moe_decode_layers(smoe_handle* h, const smoe_layer* layers, uint32_t n_
  * counterpart in the reference. Same arguments and results as
  * smoe_moe_decode_layers (bit for bit), on the CURRENT device, enqueued on
  * `stream` (a hipStream_t; NULL = the default stream). The three-kernel
- * shapes only (hidden 2048, inter 512 or 1024, <= 256 experts, k <= 16;
+ * shapes only (hidden 2048, inter 512 or 1024, <= 512 experts, k <= 16;
  * else SMOE_ERR_UNSUPPORTED_SHAPE). Its intermediates live in a fixed
  * 128 KiB device array that each GPU the library runs on holds until the
  * process ends; layers needing more return SMOE_ERR_SCRATCH_TOO_SMALL. The
@@ -337,7 +337,8 @@ uint64_t smoe_moe_prefill_workspace_size(const smoe_expert_shape* shape, uint32_
  * out_sum: device f32[n_tokens, hidden] (overwritten); workspace:
  * device, >= smoe_moe_prefill_workspace_size bytes, 256-byte aligned.
  * Supported: bits 4 or 3, group 32/64/128, hidden and inter multiples of
- * 256, 1..1024 tokens, <= 256 experts, 1 <= k <= min(16, n_experts);
+ * 256 with hidden >= 1024, 1..1024 tokens, <= 512 experts,
+ * 1 <= k <= min(16, n_experts);
  * else SMOE_ERR_UNSUPPORTED_SHAPE / SMOE_ERR_BAD_K. An expert id out of
  * range or repeated within a token is found on the device: the call
  * returns SMOE_OK and the next smoe_sync returns SMOE_ERR_INVALID_ARG.

@@ -51,9 +51,9 @@ int reserve(smoe_handle* h, uint32_t H, uint32_t I, uint32_t E) {
   // act, logits, route table and limbs hold kMaxDecodeTokens tokens
   // (multi-token decode); single-token paths use token 0's.
   const size_t T = kMaxDecodeTokens;
-  // Per token at least E + 1 logits and 256 (the decode kernels read the
-  // logits as 64 lanes x 4).
-  const size_t lstride = al(((size_t)(E + 1 > 256 ? E + 1 : 256)) * sizeof(float)) / sizeof(float);
+  // Per token at least E + 1 logits, and a whole number of 64 lanes x P
+  // (the three-kernel decode reads them unguarded).
+  const size_t lstride = logit_stride(E);
   const size_t act_b = al(T * kMaxSlotsHost * I * sizeof(float));
   const size_t log_b = al(T * lstride * sizeof(float));
   const size_t tab_b = al(T * sizeof(FfnTable));
@@ -623,7 +623,7 @@ int smoe_moe_decode_layers_noalloc(void* stream, const smoe_layer* layers, uint3
   // x limbs, each 256-byte aligned.
   auto al = [](size_t n) { return (n + 255) & ~(size_t)255; };
   const uint32_t H = layers[0].shape.hidden;
-  const size_t lstride = al(((size_t)(max_e + 1 > 256 ? max_e + 1 : 256)) * sizeof(float)) / sizeof(float);
+  const size_t lstride = logit_stride(max_e);
   const size_t log_b = al(lstride * sizeof(float));
   const size_t act_b = al((size_t)kMaxSlotsHost * max_i * sizeof(float));
   const size_t tab_b = al(sizeof(FfnTable));

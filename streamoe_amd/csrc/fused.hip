@@ -311,12 +311,15 @@ __global__ __launch_bounds__(64) void k_fa_route(FusedLayer a) {
 // read as -inf. The logits buffer holds at least 64 * P floats per token.
 template <int P>
 __device__ __forceinline__ void load_logits(const float* logits, uint32_t E, int lane, float (&v)[P]) {
-  if constexpr (P == 4) {
-    const f32x4 q = *reinterpret_cast<const f32x4*>(logits + lane * 4);
-    v[0] = q.x;
-    v[1] = q.y;
-    v[2] = q.z;
-    v[3] = q.w;
+  if constexpr (P == 4 || P == 8) {
+#pragma unroll
+    for (int h = 0; h < P / 4; ++h) {
+      const f32x4 q = *reinterpret_cast<const f32x4*>(logits + lane * P + 4 * h);
+      v[4 * h] = q.x;
+      v[4 * h + 1] = q.y;
+      v[4 * h + 2] = q.z;
+      v[4 * h + 3] = q.w;
+    }
   } else {
 #pragma unroll
     for (int e = 0; e < P; ++e) v[e] = logits[lane * P + e];
@@ -686,7 +689,7 @@ bool fused_supported(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t b
   if (inter != 512 && inter != 1024) return false;
   if (group % kChunk != 0 || (group & (group - 1)) != 0 || inter % group != 0) return false;
   if (bits != 4 && bits != 3) return false;
-  if (n_experts < 1 || n_experts > 256 || k < 1 || k > (uint32_t)kMaxK || k > n_experts) return false;
+  if (n_experts < 1 || n_experts > kFaMaxExperts || k < 1 || k > (uint32_t)kMaxK || k > n_experts) return false;
   return true;
 }
 
@@ -700,8 +703,10 @@ static void launch_gateup_fa_k(const FusedLayer& a, uint32_t blocks, hipStream_t
     hipLaunchKernelGGL((k_fa_gateup<BITS, 1, KC>), grid, dim3(64), 0, st, a);
   else if (p <= 2)
     hipLaunchKernelGGL((k_fa_gateup<BITS, 2, KC>), grid, dim3(64), 0, st, a);
-  else
+  else if (p <= 4)
     hipLaunchKernelGGL((k_fa_gateup<BITS, 4, KC>), grid, dim3(64), 0, st, a);
+  else
+    hipLaunchKernelGGL((k_fa_gateup<BITS, 8, KC>), grid, dim3(64), 0, st, a);
 }
 
 template <int BITS>

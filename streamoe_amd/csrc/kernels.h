@@ -94,6 +94,13 @@ constexpr uint32_t kFaTraceBlocks = 4096;
 constexpr uint32_t kFaTracePoints = 8;
 constexpr uint64_t kFaTraceLayer = 3ull * kFaTraceBlocks * kFaTracePoints;
 
+// Experts per layer of the three-kernel path: the top-k wave holds 8
+// logits per lane, read unguarded from a row of logit_stride(E) floats.
+constexpr uint32_t kFaMaxExperts = 512;
+inline uint32_t logit_stride(uint32_t E) {
+  const uint32_t need = E + 1 > 256 ? (E + 1 > 512 ? E + 1 : 512) : 256;  // >= 64 lanes x P
+  return (need + 63) & ~63u;
+}
 bool fused_supported(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t bits,
                      uint32_t n_experts, uint32_t k);
 // K_A (router + shared gate/up), K_B (top-k + routed gate/up), K_C (down +
@@ -102,9 +109,10 @@ hipError_t launch_fused_layer(const FusedLayer& a, hipStream_t st);
 
 // Prefill (prefill.hip): limits, arguments and workspace.
 constexpr uint32_t kPfMaxTokens = 1024;
-constexpr uint32_t kPfMaxExperts = 256;
+constexpr uint32_t kPfMaxExperts = 512;
 constexpr uint32_t kPfMaxK = 16;
 constexpr uint32_t kPfMaxGroupsK = 128;  // K / group of either GEMM (e.g. 4096 / 32)
+constexpr uint32_t kPfMinHidden = 1024;  // the gate/up GEMM's token-id lookahead needs K / 256 >= 3
 
 struct PfArgs {
   BlobGeom g;              // routed expert geometry
@@ -120,12 +128,13 @@ struct PfArgs {
   // Workspace (prefill_workspace).
   uint32_t* items;         // [max_items, 2]: expert, start | count << 16
   uint32_t* n_items;
+  uint32_t* item_tok;      // [max_items, 32]: token of each item row (token 0 past the count)
   int32_t* tok_pos;        // [n, k] entry positions of each token in ascending expert order
   float* tok_w;            // [n, k] the routing weights in the same order
-  float* xsum;             // [n*k, hidden / group] group sums of each entry's x row
+  float* xsum;             // [n, hidden / group] group sums of each token's x row (as the MFMAs see it)
   float* asum;             // [n*k, inter / group] group sums of the activations
-  uint16_t* x_hi;          // [n*k, hidden] x rows in entry order, bf16, MFMA order
-  uint16_t* x_lo;          // [n*k, hidden] low halves (fp32 input only)
+  uint16_t* x_hi;          // [n, hidden] x rows, bf16, MFMA order
+  uint16_t* x_lo;          // [n, hidden] low halves (fp32 input only)
   uint16_t* act_hi;        // [n*k, inter] SwiGLU output, bf16 hi, MFMA order
   uint16_t* act_lo;        // [n*k, inter] bf16 lo
   float* down;             // [n*k, hidden]

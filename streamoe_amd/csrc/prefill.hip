@@ -5,18 +5,18 @@
 // combine), whose CPU statement is build_expert_buckets (moe_router.rs:
 // 374-436) + moe_permute_fuse_cpu (moe_cpu.rs:282-339).
 //
-//   k_pf_route    one block, one thread per token: bucket the n*k
-//                 assignments by expert (stable in
-//                 token order), per-token entry positions in ascending
-//                 expert order, and a work list of (expert, <= kPfMC
-//                 entries) items, so a hot expert is spread over many waves.
-//   k_pf_prep_x   one block per token: its x row in the MFMA k-order (bf16,
-//                 or f32 split into bf16 hi + lo) and group sums (the
-//                 per-group terms of the dequant epilogue), written to each
-//                 of the token's entry rows.
+//   k_pf_route    block 0, one thread per token: bucket the n*k
+//                 assignments by expert (stable in token order), per-token
+//                 entry positions in ascending expert order, a work list of
+//                 (expert, <= kPfMC entries) items, so a hot expert is spread
+//                 over many waves, and the token of each item row. Blocks
+//                 1..: each token's x row in the MFMA k-order (bf16, or f32
+//                 split into bf16 hi + lo) and its group sums (the per-group
+//                 terms of the dequant epilogue), once per token.
 //   k_pf_mm       persistent pipelined grouped GEMM, bf16 MFMA
 //                 (v_mfma_f32_16x16x32_bf16) over (item, column block)
-//                 units: mode 0 gate and up rows of the item's expert ->
+//                 units: mode 0 gate and up rows of the item's expert over
+//                 its tokens' x rows (copied by token id) ->
 //                 act = silu(gate) * up as bf16 hi + lo, with the down
 //                 GEMM's activation group sums for G <= 64; mode 1 down rows
 //                 over the activations -> f32 per entry.
@@ -50,180 +50,6 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 constexpr uint32_t kPfMC = 32;   // entries per work item (two 16-row MFMA tiles)
 constexpr uint32_t kPfKC = 256;  // inputs per pipelined K chunk
-
-// ---------------------------------------------------------------------------
-// Bucketing (one block of 1024 threads).
-// ---------------------------------------------------------------------------
-#define PF_STAMP(i)                                                         \
-  do {                                                                      \
-    if (a.trace && threadIdx.x == 0) a.trace[i] = __builtin_amdgcn_s_memrealtime(); \
-  } while (0)
-
-__global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
-  PF_STAMP(0);
-  // col[e][c]: bit (t & 31) set when token 32c + (t & 31) chose expert e;
-  // pre[e][c]: tokens before 32c that chose e.
-  __shared__ uint32_t col[kPfMaxExperts * (kPfMaxTokens / 32)];
-  __shared__ uint16_t pre[kPfMaxExperts * (kPfMaxTokens / 32)];
-  __shared__ uint32_t offs[kPfMaxExperts];
-  const uint32_t tid = threadIdx.x, n = a.n_tokens, k = a.k, E = a.E;
-  const uint32_t cw = (n + 31) / 32;
-  for (uint32_t i = tid; i < E * cw; i += blockDim.x) col[i] = 0;
-  // Thread t owns token t: its k experts and weights stay in registers
-  // (one read of the routing input), validated here.
-  int32_t ex[kPfMaxK];
-  float wt[kPfMaxK];
-  const bool tok = tid < n;
-  bool bad = false;
-#pragma unroll
-  for (uint32_t s = 0; s < kPfMaxK; ++s) {
-    ex[s] = -1;
-    wt[s] = 0.f;
-  }
-  const bool vec = (k & 3) == 0 && ((reinterpret_cast<uintptr_t>(a.idx) | reinterpret_cast<uintptr_t>(a.w)) & 15) == 0;
-  if (tok && vec) {
-    // A token's k ids / weights are contiguous and 16-byte aligned: read
-    // them four at a time.
-    const int4* ip = reinterpret_cast<const int4*>(a.idx + tid * k);
-    const float4* wp = reinterpret_cast<const float4*>(a.w + tid * k);
-#pragma unroll
-    for (uint32_t q = 0; q < kPfMaxK / 4; ++q)
-      if (4 * q < k) {
-        const int4 iv = ip[q];
-        const float4 wv = wp[q];
-        ex[4 * q] = iv.x, ex[4 * q + 1] = iv.y, ex[4 * q + 2] = iv.z, ex[4 * q + 3] = iv.w;
-        wt[4 * q] = wv.x, wt[4 * q + 1] = wv.y, wt[4 * q + 2] = wv.z, wt[4 * q + 3] = wv.w;
-      }
-  } else if (tok) {
-#pragma unroll
-    for (uint32_t s = 0; s < kPfMaxK; ++s)
-      if (s < k) {
-        ex[s] = a.idx[tid * k + s];
-        wt[s] = a.w[tid * k + s];
-      }
-  }
-#pragma unroll
-  for (uint32_t s = 0; s < kPfMaxK; ++s)
-    if (tok && s < k) bad |= ex[s] < 0 || (uint32_t)ex[s] >= E;
-  __syncthreads();
-  PF_STAMP(1);
-  if (tok) {
-#pragma unroll
-    for (uint32_t s = 0; s < kPfMaxK; ++s) {
-      if (s >= k || ex[s] < 0 || (uint32_t)ex[s] >= E) continue;
-      const uint32_t old = atomicOr(&col[ex[s] * cw + (tid >> 5)], 1u << (tid & 31));
-      bad |= (old >> (tid & 31)) & 1u;  // an expert twice in one token
-    }
-    if (bad) *a.err = 2u;
-  }
-  __syncthreads();
-  PF_STAMP(2);
-  __shared__ uint32_t scnt[kPfMaxExperts], snch[kPfMaxExperts], sibase[kPfMaxExperts];
-  {
-    // Four threads per expert (lanes 4e .. 4e + 3 of one wave), each over a
-    // quarter of the expert's bitmap words: popcounts, an exclusive scan
-    // across the four, then the running counts before each word.
-    static_assert(kPfMaxTokens / 32 <= 4 * 8 && 4 * kPfMaxExperts <= 1024, "count split");
-    const uint32_t e = tid >> 2, j = tid & 3, per = (cw + 3) / 4;
-    uint32_t pc[8], loc = 0;
-#pragma unroll
-    for (uint32_t i = 0; i < 8; ++i) {
-      const uint32_t c = j * per + i;
-      pc[i] = (e < E && i < per && c < cw) ? __popc(col[e * cw + c]) : 0u;
-      loc += pc[i];
-    }
-    uint32_t incl = loc;
-    const uint32_t t1 = __shfl_up(incl, 1, 4);
-    if (j >= 1) incl += t1;
-    const uint32_t t2 = __shfl_up(incl, 2, 4);
-    if (j >= 2) incl += t2;
-    if (e < E) {
-      uint32_t run = incl - loc;
-#pragma unroll
-      for (uint32_t i = 0; i < 8; ++i) {
-        const uint32_t c = j * per + i;
-        if (i < per && c < cw) {
-          pre[e * cw + c] = (uint16_t)run;
-          run += pc[i];
-        }
-      }
-      if (j == 3) {
-        scnt[e] = incl;
-        snch[e] = (incl + kPfMC - 1) / kPfMC;
-      }
-    }
-  }
-  __syncthreads();
-  PF_STAMP(3);
-  // Wave 0: exclusive scans of the counts (entry offsets) and of the items
-  // per expert (work-list bases), 4 experts per lane and a DPP scan.
-  if (tid < 64) {
-    uint32_t c4[4], n4[4], ca = 0, na = 0;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t e = tid * 4 + q;
-      c4[q] = e < E ? scnt[e] : 0u;
-      n4[q] = e < E ? snch[e] : 0u;
-      ca += c4[q];
-      na += n4[q];
-    }
-    uint32_t ci = ca, ni = na;  // inclusive scans over lanes
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint32_t tc = __shfl_up(ci, o, 64), tn = __shfl_up(ni, o, 64);
-      if (tid >= o) {
-        ci += tc;
-        ni += tn;
-      }
-    }
-    uint32_t co = ci - ca, no = ni - na;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t e = tid * 4 + q;
-      if (e < E) {
-        offs[e] = co;
-        sibase[e] = no;
-      }
-      co += c4[q];
-      no += n4[q];
-    }
-    if (tid == 63) *a.n_items = ni;
-  }
-  __syncthreads();
-  PF_STAMP(4);
-  if (tid < E) {
-    const uint32_t cnt = scnt[tid], nch = snch[tid], off = offs[tid], ibase = sibase[tid];
-    for (uint32_t c = 0; c < nch; ++c) {
-      a.items[2 * (ibase + c)] = tid;
-      a.items[2 * (ibase + c) + 1] = (off + c * kPfMC) | (min(kPfMC, cnt - c * kPfMC) << 16);
-    }
-  }
-  // Every entry places itself: position = the expert's offset + the tokens
-  // before t that chose the same expert; rank r among t's experts in
-  // ascending expert order = how many of t's experts are smaller. The token
-  // writes its entry positions and weights in that order (token-major),
-  // all the later kernels need of the entries: element t k + r of tok_pos
-  // and tok_w, stored directly (no selection of the rank's register).
-  if (tok) {
-#pragma unroll
-    for (uint32_t s = 0; s < kPfMaxK; ++s) {
-      const int32_t e = ex[s];
-      if (s >= k || e < 0 || (uint32_t)e >= E) continue;
-      const uint32_t ci = e * cw + (tid >> 5);
-      const uint32_t pos = offs[e] + pre[ci] + __popc(col[ci] & ((1u << (tid & 31)) - 1u));
-      uint32_t r = 0;
-#pragma unroll
-      for (uint32_t q = 0; q < kPfMaxK; ++q) r += (q < k && ex[q] < e) ? 1u : 0u;
-      r = min(r, k - 1);  // a duplicated expert (already reported) stays in range
-      a.tok_pos[tid * k + r] = (int32_t)pos;
-      a.tok_w[tid * k + r] = wt[s];
-    }
-  }
-  PF_STAMP(5);
-  __syncthreads();
-  __builtin_amdgcn_s_waitcnt(0);
-  PF_STAMP(6);
-}
 
 // ---------------------------------------------------------------------------
 // MFMA operand helpers.
@@ -293,6 +119,260 @@ __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
 template <int BITS>
 __device__ __forceinline__ u32x4 codes_bf16(uint32_t w) {
   return BITS == 4 ? codes_bf16_4(w) : codes_bf16_3(w);
+}
+
+// ---------------------------------------------------------------------------
+// Bucketing (block 0 of k_pf_route, 1024 threads) and the per-token x
+// preparation (blocks 1.., four tokens each), in one launch: the
+// preparation runs on other CUs while the single bucketing block works.
+// ---------------------------------------------------------------------------
+#define PF_STAMP(i)                                                         \
+  do {                                                                      \
+    if (a.trace && threadIdx.x == 0) a.trace[i] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+
+constexpr uint32_t kPfPrepTokens = 4;                    // tokens per preparation block (256 threads each)
+constexpr uint32_t kPfPart8 = kPfMaxGroupsK * 128 / 8;   // 8-input partial sums of one row (H <= 16384)
+
+// Token t's x row -> MFMA-ready bf16 hi (and lo for fp32 input) and its
+// group sums over what the MFMAs see (hi + lo), in row t of x_hi / x_lo /
+// xsum. 256 threads (tid); part8: kPfPart8 floats of LDS. Every thread of
+// the block reaches the barrier (live = false: no work).
+__device__ __forceinline__ void pf_prep_token(const PfArgs& a, uint32_t t, bool live, uint32_t tid, float* part8) {
+  const uint32_t H = a.g.hidden, G = a.g.group;
+  const bool x_bf16 = a.x_bf16;
+  if (live) {
+    for (uint32_t k0 = tid * 8; k0 < H; k0 += 256 * 8) {
+      float f[8];
+      if (x_bf16) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)t * H + k0);
+        const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          f[2 * i] = __uint_as_float(w4[i] << 16);
+          f[2 * i + 1] = __uint_as_float(w4[i] & 0xFFFF0000u);
+        }
+      } else {
+        const f32x4* p = reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(a.x) + (size_t)t * H + k0);
+        const f32x4 u = p[0], v = p[1];
+        f[0] = u.x, f[1] = u.y, f[2] = u.z, f[3] = u.w, f[4] = v.x, f[5] = v.y, f[6] = v.z, f[7] = v.w;
+      }
+      u32x4 hi, lo;
+      split_f32(f, hi, lo);
+      *reinterpret_cast<u32x4*>(a.x_hi + (size_t)t * H + k0) = hi;
+      if (!x_bf16) *reinterpret_cast<u32x4*>(a.x_lo + (size_t)t * H + k0) = lo;
+      // Partial sum of these 8 inputs as the MFMA sees them.
+      const uint32_t hv[4] = {hi.x, hi.y, hi.z, hi.w}, lv[4] = {lo.x, lo.y, lo.z, lo.w};
+      float p = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        p += __uint_as_float(hv[i] << 16) + __uint_as_float(hv[i] & 0xFFFF0000u);
+        if (!x_bf16) p += __uint_as_float(lv[i] << 16) + __uint_as_float(lv[i] & 0xFFFF0000u);
+      }
+      part8[k0 / 8] = p;
+    }
+  }
+  __syncthreads();
+  if (live) {
+    const uint32_t ng = H / G, per = G / 8;
+    for (uint32_t g = tid; g < ng; g += 256) {
+      float sum = 0.f;
+      for (uint32_t j = 0; j < per; ++j) sum += part8[g * per + j];
+      a.xsum[(size_t)t * ng + g] = sum;
+    }
+  }
+}
+
+// LDS of the bucketing block: col [E, cw] u32 then pre [E, cw] u16
+// (cw = ceil(n / 32)); the preparation blocks use the same memory as
+// kPfPrepTokens rows of part sums.
+__host__ __device__ constexpr uint32_t pf_route_lds(uint32_t E, uint32_t n) {
+  return (E * ((n + 31) / 32) * 6 + 15) / 16 * 16 > kPfPrepTokens * kPfPart8 * 4
+             ? (E * ((n + 31) / 32) * 6 + 15) / 16 * 16
+             : kPfPrepTokens * kPfPart8 * 4;
+}
+
+__global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t pf_dyn[];
+  const uint32_t tid = threadIdx.x;
+  if (blockIdx.x > 0) {
+    const uint32_t sub = tid >> 8, t = (blockIdx.x - 1) * kPfPrepTokens + sub;
+    pf_prep_token(a, t, t < a.n_tokens, tid & 255u, reinterpret_cast<float*>(pf_dyn) + sub * kPfPart8);
+    return;
+  }
+  PF_STAMP(0);
+  const uint32_t n = a.n_tokens, k = a.k, E = a.E;
+  const uint32_t cw = (n + 31) / 32;
+  // col[e][c]: bit (t & 31) set when token 32c + (t & 31) chose expert e;
+  // pre[e][c]: tokens before 32c that chose e.
+  uint32_t* const col = reinterpret_cast<uint32_t*>(pf_dyn);
+  uint16_t* const pre = reinterpret_cast<uint16_t*>(pf_dyn + E * cw * 4);
+  __shared__ uint32_t offs[kPfMaxExperts];
+  for (uint32_t i = tid; i < E * cw; i += blockDim.x) col[i] = 0;
+  // Thread t owns token t: its k experts and weights stay in registers
+  // (one read of the routing input), validated here.
+  int32_t ex[kPfMaxK];
+  float wt[kPfMaxK];
+  const bool tok = tid < n;
+  bool bad = false;
+#pragma unroll
+  for (uint32_t s = 0; s < kPfMaxK; ++s) {
+    ex[s] = -1;
+    wt[s] = 0.f;
+  }
+  const bool vec = (k & 3) == 0 && ((reinterpret_cast<uintptr_t>(a.idx) | reinterpret_cast<uintptr_t>(a.w)) & 15) == 0;
+  if (tok && vec) {
+    // A token's k ids / weights are contiguous and 16-byte aligned: read
+    // them four at a time.
+    const int4* ip = reinterpret_cast<const int4*>(a.idx + tid * k);
+    const float4* wp = reinterpret_cast<const float4*>(a.w + tid * k);
+#pragma unroll
+    for (uint32_t q = 0; q < kPfMaxK / 4; ++q)
+      if (4 * q < k) {
+        const int4 iv = ip[q];
+        const float4 wv = wp[q];
+        ex[4 * q] = iv.x, ex[4 * q + 1] = iv.y, ex[4 * q + 2] = iv.z, ex[4 * q + 3] = iv.w;
+        wt[4 * q] = wv.x, wt[4 * q + 1] = wv.y, wt[4 * q + 2] = wv.z, wt[4 * q + 3] = wv.w;
+      }
+  } else if (tok) {
+#pragma unroll
+    for (uint32_t s = 0; s < kPfMaxK; ++s)
+      if (s < k) {
+        ex[s] = a.idx[tid * k + s];
+        wt[s] = a.w[tid * k + s];
+      }
+  }
+#pragma unroll
+  for (uint32_t s = 0; s < kPfMaxK; ++s)
+    if (tok && s < k) bad |= ex[s] < 0 || (uint32_t)ex[s] >= E;
+  __syncthreads();
+  PF_STAMP(1);
+  if (tok) {
+#pragma unroll
+    for (uint32_t s = 0; s < kPfMaxK; ++s) {
+      if (s >= k || ex[s] < 0 || (uint32_t)ex[s] >= E) continue;
+      const uint32_t old = atomicOr(&col[ex[s] * cw + (tid >> 5)], 1u << (tid & 31));
+      bad |= (old >> (tid & 31)) & 1u;  // an expert twice in one token
+    }
+    if (bad) *a.err = 2u;
+  }
+  __syncthreads();
+  PF_STAMP(2);
+  __shared__ uint32_t scnt[kPfMaxExperts], snch[kPfMaxExperts], sibase[kPfMaxExperts];
+  {
+    // TPE = 4 threads per expert (2 above 256 experts), adjacent lanes of
+    // one wave, each over a share of the expert's bitmap words: popcounts,
+    // an exclusive scan across the TPE, then the running counts before
+    // each word.
+    static_assert(kPfMaxTokens / 32 <= 2 * 16 && 2 * kPfMaxExperts <= 1024 && 4 * 256 <= 1024, "count split");
+    const uint32_t tpe = E <= 256 ? 4u : 2u;
+    const uint32_t e = tid / tpe, j = tid % tpe, per = (cw + tpe - 1) / tpe;
+    uint32_t pc[16], loc = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < 16; ++i) {
+      const uint32_t c = j * per + i;
+      pc[i] = (e < E && i < per && c < cw) ? __popc(col[e * cw + c]) : 0u;
+      loc += pc[i];
+    }
+    uint32_t incl = loc;
+    const uint32_t t1 = __shfl_up(incl, 1, tpe);
+    if (j >= 1) incl += t1;
+    if (tpe == 4) {
+      const uint32_t t2 = __shfl_up(incl, 2, 4);
+      if (j >= 2) incl += t2;
+    }
+    if (e < E) {
+      uint32_t run = incl - loc;
+#pragma unroll
+      for (uint32_t i = 0; i < 16; ++i) {
+        const uint32_t c = j * per + i;
+        if (i < per && c < cw) {
+          pre[e * cw + c] = (uint16_t)run;
+          run += pc[i];
+        }
+      }
+      if (j == tpe - 1) {
+        scnt[e] = incl;
+        snch[e] = (incl + kPfMC - 1) / kPfMC;
+      }
+    }
+  }
+  __syncthreads();
+  PF_STAMP(3);
+  // Wave 0: exclusive scans of the counts (entry offsets) and of the items
+  // per expert (work-list bases), 8 experts per lane and a shuffle scan.
+  if (tid < 64) {
+    constexpr int EPL = kPfMaxExperts / 64;
+    uint32_t c8[EPL], n8[EPL], ca = 0, na = 0;
+#pragma unroll
+    for (int q = 0; q < EPL; ++q) {
+      const uint32_t e = tid * EPL + q;
+      c8[q] = e < E ? scnt[e] : 0u;
+      n8[q] = e < E ? snch[e] : 0u;
+      ca += c8[q];
+      na += n8[q];
+    }
+    uint32_t ci = ca, ni = na;  // inclusive scans over lanes
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t tc = __shfl_up(ci, o, 64), tn = __shfl_up(ni, o, 64);
+      if (tid >= o) {
+        ci += tc;
+        ni += tn;
+      }
+    }
+    uint32_t co = ci - ca, no = ni - na;
+#pragma unroll
+    for (int q = 0; q < EPL; ++q) {
+      const uint32_t e = tid * EPL + q;
+      if (e < E) {
+        offs[e] = co;
+        sibase[e] = no;
+      }
+      co += c8[q];
+      no += n8[q];
+    }
+    if (tid == 63) *a.n_items = ni;
+  }
+  __syncthreads();
+  PF_STAMP(4);
+  if (tid < E) {
+    const uint32_t cnt = scnt[tid], nch = snch[tid], off = offs[tid], ibase = sibase[tid];
+    for (uint32_t c = 0; c < nch; ++c) {
+      a.items[2 * (ibase + c)] = tid;
+      a.items[2 * (ibase + c) + 1] = (off + c * kPfMC) | (min(kPfMC, cnt - c * kPfMC) << 16);
+    }
+    // Rows past the count of the expert's last item read token 0's x (their
+    // results are dropped).
+    if (cnt % kPfMC)
+      for (uint32_t m = cnt % kPfMC; m < kPfMC; ++m) a.item_tok[(ibase + nch - 1) * kPfMC + m] = 0u;
+  }
+  // Every entry places itself: position = the expert's offset + the tokens
+  // before t that chose the same expert (its row in the expert's items);
+  // rank r among t's experts in ascending expert order = how many of t's
+  // experts are smaller. The token writes its entry positions and weights
+  // in that order (token-major), and its id into its items' row slots.
+  if (tok) {
+#pragma unroll
+    for (uint32_t s = 0; s < kPfMaxK; ++s) {
+      const int32_t e = ex[s];
+      if (s >= k || e < 0 || (uint32_t)e >= E) continue;
+      const uint32_t ci = e * cw + (tid >> 5);
+      const uint32_t row = pre[ci] + __popc(col[ci] & ((1u << (tid & 31)) - 1u));
+      const uint32_t pos = offs[e] + row;
+      uint32_t r = 0;
+#pragma unroll
+      for (uint32_t q = 0; q < kPfMaxK; ++q) r += (q < k && ex[q] < e) ? 1u : 0u;
+      r = min(r, k - 1);  // a duplicated expert (already reported) stays in range
+      a.tok_pos[tid * k + r] = (int32_t)pos;
+      a.tok_w[tid * k + r] = wt[s];
+      a.item_tok[sibase[e] * kPfMC + row] = tid;
+    }
+  }
+  PF_STAMP(5);
+  __syncthreads();
+  __builtin_amdgcn_s_waitcnt(0);
+  PF_STAMP(6);
 }
 
 // ---------------------------------------------------------------------------
@@ -384,7 +464,13 @@ struct PfMM {
   // last finished unit ([column wave][32 rows] f32), after the unit buffers.
   static constexpr bool ASUM = MODE == 0 && G <= 64;
   static constexpr int OFF_PS = S * STAGE + 2 * UBUF;
-  static constexpr int LDS = OFF_PS + (ASUM ? 4 * kPfMC * 4 : 0);
+  // Gate/up: the token ids of two units' rows (A rows and group sums are
+  // gathered from the per-token arrays), one buffer per unit parity.
+  static constexpr bool GATHER = MODE == 0;
+  static constexpr int OFF_TOK = OFF_PS + (ASUM ? 4 * kPfMC * 4 : 0);
+  static constexpr int LDS = OFF_TOK + (GATHER ? 2 * kPfMC * 4 : 0);
+  // Per-lane row offsets of one unit's group-sum copies.
+  static constexpr int NXR = USB ? N_UXS : N_XS;
   // Accumulators per lane, exchanged between the K halves through LDS.
   static constexpr int NT = NMAT * CT * 2 * 4;
   static_assert(CG % 2 == 0, "K halves");
@@ -725,11 +811,13 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
   const uint32_t my_units = group_units > lb ? (group_units - lb + per - 1) / per : 0;
   const uint32_t total = my_units * nch;
   if (total == 0) return;
-  // A rows are entries (x was gathered into entry order): no indirection.
+  // Gate/up: A rows are token rows of x_hi / x_lo / xsum, looked up by the
+  // unit's token ids; down: entry rows of the activations, in place.
   const uint16_t* const ahi_src = MODE == 0 ? a.x_hi : a.act_hi;
   const uint16_t* const alo_src = MODE == 0 ? a.x_lo : a.act_lo;
   const float* const gsum = MODE == 0 ? a.xsum : a.asum;
   const uint8_t* const experts = a.experts;
+  const uint32_t* const item_tok = a.item_tok;
   const uint64_t stride = a.stride;
   uint16_t* const act_hi = a.act_hi;
   uint16_t* const act_lo = a.act_lo;
@@ -791,35 +879,62 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
     UnitSrc u;
     u.bq = blob + wo0 + (size_t)cb * C::NCOL * rowb;
     u.bs = blob + so0 + (size_t)cb * C::NCOL * ng * 2;
-    u.ah = reinterpret_cast<const uint8_t*>(ahi_src + (size_t)start * K);
-    u.al = reinterpret_cast<const uint8_t*>(alo_src + (size_t)start * K);
-    u.xs = reinterpret_cast<const uint8_t*>(gsum + (size_t)start * ng);
+    const size_t r0 = C::GATHER ? 0 : start;  // gathered rows are addressed by token
+    u.ah = reinterpret_cast<const uint8_t*>(ahi_src + r0 * K);
+    u.al = reinterpret_cast<const uint8_t*>(alo_src + r0 * K);
+    u.xs = reinterpret_cast<const uint8_t*>(gsum + r0 * ng);
     u.cnt = cnt;
     return u;
+  };
+  // Per-lane byte offsets of one unit's A rows (row pair (dw N_A + i,
+  // + 16)) and group-sum rows from its row base: gate/up by the token ids in
+  // token buffer `par` (rows past the count hold token 0), down by the entry
+  // row (rows past the count repeat the last one). Results of rows past the
+  // count are never stored.
+  struct UnitRows {
+    uint32_t a[C::N_A];
+    uint32_t x[C::NXR > 0 ? C::NXR : 1];
+  };
+  auto unit_rows = [=](const UnitSrc& u, uint32_t par) {
+    const uint32_t* tb = reinterpret_cast<const uint32_t*>(lds + C::OFF_TOK) + par * kPfMC;
+    auto row = [&](uint32_t m) { return C::GATHER ? tb[m] : min(m, u.cnt - 1); };
+    UnitRows r;
+#pragma unroll
+    for (int i = 0; i < C::N_A; ++i) r.a[i] = row(dw * C::N_A + i + 16 * (lane >> 5)) * K * 2;
+#pragma unroll
+    for (int i = 0; i < C::NXR; ++i) {
+      const uint32_t p = dw * ((C::USB ? C::P_UXS : C::P_XS) / C::NW) + i * 64 + lane;
+      const uint32_t m = C::USB ? min(p / (uint32_t)(C::NGU / 4), kPfMC - 1) : p % kPfMC;
+      r.x[i] = row(m) * ng * 4;
+    }
+    return r;
+  };
+  // Gate/up: copy unit v's 32 token ids into token buffer `par` (one wave).
+  auto token_dma = [=](uint32_t v, uint32_t par) {
+    if (C::GATHER && dw == 0 && lane < kPfMC)
+      dma4(item_tok + (size_t)(item_lo + v / ncb) * kPfMC + lane, lds + C::OFF_TOK + par * kPfMC * 4);
   };
   // Issue every copy of chunk c of unit u into stage `slot`. Captures by
   // value: a by-reference capture stores the locals' addresses, and the
   // memory clobbers of the waits below would then keep them in scratch.
   // Unit scale copies into unit buffer ub (before the unit's first chunk).
-  auto issue_unit = [=](const UnitSrc& u, uint32_t ub) {
+  auto issue_unit = [=](const UnitSrc& u, const UnitRows& rw, uint32_t ub) {
     uint8_t* ubuf = lds + C::S * C::STAGE + ub * C::UBUF;
 #pragma unroll
     for (int i = 0; i < C::N_US; ++i)
       if ((C::P_US / C::NW) % 64 == 0 || i * 64 + lane < (uint32_t)(C::P_US / C::NW))
         dma16(u.bs + off_us[i], ubuf + (dw * (C::P_US / C::NW) + i * 64) * 16);
-    // Group sums: piece p = (row m, piece in row); rows >= cnt repeat row
-    // cnt - 1.
+    // Group sums: piece p = (row m, piece in row), row offsets from rw.
     constexpr uint32_t XPR = C::NGU / 4;  // pieces per row
 #pragma unroll
     for (int i = 0; i < C::N_UXS; ++i) {
       const uint32_t p = dw * (C::P_UXS / C::NW) + i * 64 + lane;
-      const uint32_t m = p / XPR, pc = p % XPR;
+      const uint32_t pc = p % XPR;
       if ((C::P_UXS / C::NW) % 64 == 0 || i * 64 + lane < (uint32_t)(C::P_UXS / C::NW))
-        dma16(u.xs + (size_t)min(m, u.cnt - 1) * ng * 4 + pc * 16,
-              ubuf + C::OFF_UXS + (dw * (C::P_UXS / C::NW) + i * 64) * 16);
+        dma16(u.xs + rw.x[i] + pc * 16, ubuf + C::OFF_UXS + (dw * (C::P_UXS / C::NW) + i * 64) * 16);
     }
   };
-  auto issue = [=](const UnitSrc& u, uint32_t c, uint32_t slot) {
+  auto issue = [=](const UnitSrc& u, const UnitRows& rw, uint32_t c, uint32_t slot) {
     const uint32_t cnt = u.cnt;
     uint8_t* st = lds + slot * C::STAGE;
     // Weight codes: slot p = (row, slot part) holds the row's part
@@ -846,8 +961,7 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
 #pragma unroll
       for (int i = 0; i < C::N_A; ++i) {
         const uint32_t pair = dw * C::N_A + i, half = lane >> 5, sp = lane & 31;
-        const uint32_t m = pair + 16 * half;
-        const uint32_t off = min(m, cnt - 1) * K * 2 + (sp ^ pair) * 16;
+        const uint32_t off = rw.a[i] + (sp ^ pair) * 16;
         if (half == 0 || cnt > 16)
           dma16(a_base + off, st + (hl ? C::OFF_AL : C::OFF_AH) + pair * 64 * 16);
       }
@@ -858,9 +972,9 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
     for (int i = 0; i < C::N_XS; ++i) {
       const uint32_t o = i * 64 + lane;
       const uint32_t p = dw * (C::P_XS / C::NW) + o;
-      const uint32_t g = p / kPfMC, m = p % kPfMC;
+      const uint32_t g = p / kPfMC;
       if ((C::P_XS / C::NW) % 64 == 0 || o < (uint32_t)(C::P_XS / C::NW))
-        dma4(xs_base + (min(m, cnt - 1) * ng + g) * 4, st + C::OFF_XS + (dw * (C::P_XS / C::NW) + i * 64) * 4);
+        dma4(xs_base + rw.x[i] + g * 4, st + C::OFF_XS + (dw * (C::P_XS / C::NW) + i * 64) * 4);
     }
   };
 
@@ -876,10 +990,27 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
   // of the compute position (unit cv, chunk cc, stage cslot).
   uint32_t iv = lb, ic = 0, islot = 0, issued = 0, iub = 0;
   UnitSrc isrc = unit_src(iv);
+  UnitRows irows;
+  if constexpr (C::GATHER) {
+    // The first unit's token ids, visible to every wave before its copies.
+    // Later units' ids are copied with the previous unit's first chunk, at
+    // least K / 256 - 1 >= S - 1 chunks ahead, so the per-chunk waits and
+    // barriers below have made them visible when that unit starts.
+    if (copier) token_dma(iv, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  }
+  // At a unit's first chunk: its row offsets, and the next unit's token ids.
+  auto start_unit = [&]() {
+    irows = unit_rows(isrc, iub);
+    if (iv + per < group_units) token_dma(iv + per, iub ^ 1u);
+  };
   for (; issued + 1 < (uint32_t)C::S && issued < total; ++issued) {
     if (copier) {
-      if (C::USB && ic == 0) issue_unit(isrc, iub);
-      issue(isrc, ic, islot);
+      if (ic == 0) start_unit();
+      if (C::USB && ic == 0) issue_unit(isrc, irows, iub);
+      issue(isrc, irows, ic, islot);
     }
     islot = islot + 1 == (uint32_t)C::S ? 0u : islot + 1;
     if (++ic == nch) {
@@ -934,8 +1065,9 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
     asm volatile("" ::: "memory");
     if (issued < total) {
       if (copier) {
-        if (C::USB && ic == 0) issue_unit(isrc, iub);
-        issue(isrc, ic, islot);
+        if (ic == 0) start_unit();
+        if (C::USB && ic == 0) issue_unit(isrc, irows, iub);
+        issue(isrc, irows, ic, islot);
       }
       ++issued;
       islot = islot + 1 == (uint32_t)C::S ? 0u : islot + 1;
@@ -1068,67 +1200,6 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
   }
 }
 
-// Token t's x row -> MFMA-ready bf16 hi (and lo for fp32 input) and its
-// group sums over what the MFMA sees (hi + lo), written to each of the
-// token's k entry rows (entry positions from k_pf_route). One block per
-// token, so the row is read, split and summed once for its k entries.
-__global__ __launch_bounds__(256) void k_pf_prep_x(PfArgs a) {
-  __shared__ float part8[kPfMaxGroupsK * 128 / 8];
-  const uint32_t t = blockIdx.x, H = a.g.hidden, G = a.g.group, k = a.k;
-  const uint32_t nk = a.n_tokens * k;
-  uint16_t* const x_hi = a.x_hi;
-  uint16_t* const x_lo = a.x_lo;
-  float* const xsum = a.xsum;
-  const bool x_bf16 = a.x_bf16;
-  uint32_t pos[kPfMaxK];
-#pragma unroll
-  for (uint32_t r = 0; r < kPfMaxK; ++r)
-    // In range even when bucketing rejected the input (then *err is set).
-    pos[r] = r < k ? min((uint32_t)a.tok_pos[t * k + r], nk - 1) : 0u;
-  for (uint32_t k0 = threadIdx.x * 8; k0 < H; k0 += blockDim.x * 8) {
-    float f[8];
-    if (x_bf16) {
-      const u32x4 v = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)t * H + k0);
-      const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        f[2 * i] = __uint_as_float(w4[i] << 16);
-        f[2 * i + 1] = __uint_as_float(w4[i] & 0xFFFF0000u);
-      }
-    } else {
-      const float* p = reinterpret_cast<const float*>(a.x) + (size_t)t * H + k0;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) f[i] = p[i];
-    }
-    u32x4 hi, lo;
-    split_f32(f, hi, lo);
-#pragma unroll
-    for (uint32_t r = 0; r < kPfMaxK; ++r)
-      if (r < k) {
-        *reinterpret_cast<u32x4*>(x_hi + (size_t)pos[r] * H + k0) = hi;
-        if (!x_bf16) *reinterpret_cast<u32x4*>(x_lo + (size_t)pos[r] * H + k0) = lo;
-      }
-    // Partial sum of these 8 inputs as the MFMA sees them.
-    const uint32_t hv[4] = {hi.x, hi.y, hi.z, hi.w}, lv[4] = {lo.x, lo.y, lo.z, lo.w};
-    float p = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      p += __uint_as_float(hv[i] << 16) + __uint_as_float(hv[i] & 0xFFFF0000u);
-      if (!x_bf16) p += __uint_as_float(lv[i] << 16) + __uint_as_float(lv[i] & 0xFFFF0000u);
-    }
-    part8[k0 / 8] = p;
-  }
-  __syncthreads();
-  const uint32_t ng = H / G, per = G / 8;
-  for (uint32_t g = threadIdx.x; g < ng; g += blockDim.x) {
-    float sum = 0.f;
-    for (uint32_t j = 0; j < per; ++j) sum += part8[g * per + j];
-#pragma unroll
-    for (uint32_t r = 0; r < kPfMaxK; ++r)
-      if (r < k) xsum[(size_t)pos[r] * ng + g] = sum;
-  }
-}
-
 // Group sums of the activations (hi + lo) per entry; one block per entry.
 __global__ __launch_bounds__(256) void k_pf_act_sum(PfArgs a) {
   __shared__ float part8[kPfMaxGroupsK * 128 / 8];
@@ -1208,18 +1279,20 @@ uint64_t prefill_workspace(uint32_t hidden, uint32_t inter, uint32_t group, uint
   };
   uint8_t* p_items = take(max_items * 2 * 4);
   uint8_t* p_nitems = take(4);
+  uint8_t* p_itok = take(max_items * kPfMC * 4);
   uint8_t* p_w = take(nk * 4);
   uint8_t* p_pos = take(nk * 4);
-  uint8_t* p_xsum = take(nk * (hidden / group) * 4);
+  uint8_t* p_xsum = take((uint64_t)n_tokens * (hidden / group) * 4);
   uint8_t* p_asum = take(nk * (inter / group) * 4);
-  uint8_t* p_xhi = take(nk * hidden * 2);
-  uint8_t* p_xlo = take(nk * hidden * 2);
+  uint8_t* p_xhi = take((uint64_t)n_tokens * hidden * 2);
+  uint8_t* p_xlo = take((uint64_t)n_tokens * hidden * 2);
   uint8_t* p_ahi = take(nk * inter * 2);
   uint8_t* p_alo = take(nk * inter * 2);
   uint8_t* p_down = take(nk * hidden * 4);
   if (a) {
     a->items = reinterpret_cast<uint32_t*>(p_items);
     a->n_items = reinterpret_cast<uint32_t*>(p_nitems);
+    a->item_tok = reinterpret_cast<uint32_t*>(p_itok);
     a->tok_w = reinterpret_cast<float*>(p_w);
     a->tok_pos = reinterpret_cast<int32_t*>(p_pos);
     a->xsum = reinterpret_cast<float*>(p_xsum);
@@ -1238,7 +1311,7 @@ bool prefill_supported(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t
                        uint32_t n_tokens, uint32_t n_experts, uint32_t k) {
   if (bits != 4 && bits != 3) return false;
   if (group != 32 && group != 64 && group != 128) return false;
-  if (hidden % kPfKC || inter % kPfKC) return false;
+  if (hidden % kPfKC || inter % kPfKC || hidden < kPfMinHidden) return false;
   if (hidden / group > kPfMaxGroupsK || inter / group > kPfMaxGroupsK) return false;
   if (n_tokens < 1 || n_tokens > kPfMaxTokens || n_experts < 1 || n_experts > kPfMaxExperts) return false;
   if (k < 1 || k > kPfMaxK || k > n_experts) return false;
@@ -1282,8 +1355,13 @@ static hipError_t launch_gemms(const PfArgs& a, uint32_t n_cu, hipStream_t st) {
 }
 
 hipError_t launch_prefill(const PfArgs& a, uint32_t n_cu, hipStream_t st) {
-  hipLaunchKernelGGL(k_pf_route, dim3(1), dim3(1024), 0, st, a);
-  hipLaunchKernelGGL(k_pf_prep_x, dim3(a.n_tokens), dim3(256), 0, st, a);
+  const uint32_t route_lds = pf_route_lds(a.E, a.n_tokens);
+  static std::atomic<uint64_t> raised{0};
+  if (route_lds > 64 * 1024) {
+    const hipError_t e = raise_lds_limit(reinterpret_cast<const void*>(&k_pf_route), (int)pf_route_lds(kPfMaxExperts, kPfMaxTokens), raised);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(k_pf_route, dim3(1 + (a.n_tokens + kPfPrepTokens - 1) / kPfPrepTokens), dim3(1024), route_lds, st, a);
   const uint32_t G = a.g.group;
   hipError_t e;
   if (a.g.bits == 4)

@@ -422,6 +422,8 @@ LAYER_CASES = [
     ("olmoe-3bit-e32", 2048, 1024, 32, 2, 3, True, False),
     ("k16-i1024", 2048, 1024, 64, 16, 4, True, True),  # down kernel: 8 rows per lane, > 64 KB LDS
     ("k10", 2048, 512, 128, 10, 4, True, True),      # the reference's other supported top-k
+    ("e512-k10", 2048, 512, 512, 10, 4, True, True),  # 512 experts, top-10, shared expert
+    ("e300-k8", 2048, 512, 300, 8, 4, True, False),   # 8 logits per lane, ragged last lanes
 ]
 
 PATHS = [1, 3]

@@ -75,6 +75,9 @@ def _case(kernels, n_tokens, H, I, E, k, bits, group, x_bf16, seed, routing="zip
     ("k1", 33, 1024, 256 * 2, 16, 1, 4, 64, True, "zipf"),
     ("k10-g32", 48, 1024, 512, 64, 10, 4, 32, True, "zipf"),  # the reference's other supported top-k
     ("max-n1024-k16", 1024, 2048, 512, 256, 16, 4, 64, True, "zipf"),  # largest tokens x k (16384 entries)
+    ("e512-k10", 256, 2048, 512, 512, 10, 4, 64, True, "zipf"),  # 512 experts, top-10
+    ("max-e512-n1024", 1024, 2048, 512, 512, 10, 4, 64, True, "zipf"),  # largest bucketing bitmaps
+    ("e512-f32-x", 64, 1024, 512, 512, 10, 3, 32, False, "zipf"),
 ])
 def test_prefill_matches_oracle(kernels, name, n, H, I, E, k, bits, group, x_bf16, routing):
     got, want, _ = _case(kernels, n, H, I, E, k, bits, group, x_bf16, seed=sum(map(ord, name)), routing=routing)
@@ -118,6 +121,10 @@ def test_prefill_argument_errors(kernels):
     assert kernels.moe_prefill(lay, arena, lay.expert_size, 4, idx, w, x, True, 4, 5, out, ws) == c["SMOE_ERR_BAD_K"]
     assert kernels.moe_prefill(lay, arena, lay.expert_size, 4, idx, w, x, True, 4, 0, out, ws) == c["SMOE_ERR_BAD_K"]
     assert kernels.moe_prefill(lay, arena, lay.expert_size, 4, idx, w, x, True, 2000, 2, out, ws) == \
+        c["SMOE_ERR_UNSUPPORTED_SHAPE"]
+    # Hidden sizes below 1024 have no prefill instance (checked before any launch).
+    small_h = sa.ExpertLayout(768, 512, 4, 64)
+    assert kernels.moe_prefill(small_h, arena, small_h.expert_size, 4, idx, w, x, True, 4, 2, out, ws) == \
         c["SMOE_ERR_UNSUPPORTED_SHAPE"]
     # Invalid routing is caught on the device and reported by smoe_sync.
     bad = torch.tensor([[0, 1], [2, 9], [3, 0], [1, 2]], dtype=torch.int32, device="cuda")
