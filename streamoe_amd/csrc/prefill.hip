@@ -477,6 +477,7 @@ struct PfMM {
   static_assert(P_BQ % NW == 0 && P_BS % NW == 0 && P_XS % NW == 0 && P_US % NW == 0 && P_UXS % NW == 0,
                 "equal shares");
   static_assert(!USB || NGU % 4 == 0, "unit group sums in 16-byte pieces");
+  static_assert(!USB || ((NGU / 4) & (NGU / 4 - 1)) == 0, "unit group-sum rows: a power-of-two piece count (XOR swizzle)");
   static_assert(N_A * NW * 64 == P_A && P_A == 16 * 64, "one row pair per A copy");
   static_assert((S - 2) * D + DU <= 63, "vmcnt range");
   static_assert(NWD == 0 || (MODE == 0 && USB), "copy waves: unit-staged gate/up only");
@@ -771,7 +772,10 @@ __device__ __forceinline__ void pf_unit_bias(const uint8_t* ub, uint32_t nch, ui
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       if ((uint32_t)t >= ntiles) break;
-      const float xa = uxs[(16 * t + r16) * C::NGU + g];
+      // Group g of row m sits in 16-byte slot (g / 4) ^ (m % XPR) of the row.
+      constexpr uint32_t XPR = C::NGU / 4;
+      const uint32_t m = 16 * t + r16;
+      const float xa = uxs[m * C::NGU + ((((g >> 2) ^ (m & (XPR - 1))) << 2) | (g & 3u))];
 #pragma unroll
       for (int mt = 0; mt < C::NMAT; ++mt)
         tot[mt][0][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, bb[mt], tot[mt][0][t], 0, 0, 0);
@@ -871,10 +875,16 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
     const uint8_t* xs;
     uint32_t cnt;
   };
-  auto unit_src = [=](uint32_t v) {
-    const uint32_t item = item_lo + v / ncb, cb = v % ncb;
-    const uint32_t e = items[2 * item];
-    const uint32_t start = items[2 * item + 1] & 0xFFFFu, cnt = items[2 * item + 1] >> 16;
+  // Work-list words (expert, start | count << 16) of unit v's item, a
+  // scalar load; each unit's words are loaded one unit ahead of their use,
+  // so no wave waits on this load when a unit starts.
+  auto item_words = [=](uint32_t v) {
+    return *reinterpret_cast<const uint2*>(items + 2 * (size_t)(item_lo + v / ncb));
+  };
+  auto unit_src = [=](uint32_t v, uint2 iw) {
+    const uint32_t cb = v % ncb;
+    const uint32_t e = iw.x;
+    const uint32_t start = iw.y & 0xFFFFu, cnt = iw.y >> 16;
     const uint8_t* blob = experts + (size_t)e * stride;
     UnitSrc u;
     u.bq = blob + wo0 + (size_t)cb * C::NCOL * rowb;
@@ -924,12 +934,15 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
     for (int i = 0; i < C::N_US; ++i)
       if ((C::P_US / C::NW) % 64 == 0 || i * 64 + lane < (uint32_t)(C::P_US / C::NW))
         dma16(u.bs + off_us[i], ubuf + (dw * (C::P_US / C::NW) + i * 64) * 16);
-    // Group sums: piece p = (row m, piece in row), row offsets from rw.
+    // Group sums: slot p = (row m, slot in row) holds the row's piece
+    // (slot ^ m % XPR) under gate/up (pf_unit_bias reads one group of 16
+    // rows at once: the XOR spreads them over the banks), else piece p;
+    // row offsets from rw.
     constexpr uint32_t XPR = C::NGU / 4;  // pieces per row
 #pragma unroll
     for (int i = 0; i < C::N_UXS; ++i) {
       const uint32_t p = dw * (C::P_UXS / C::NW) + i * 64 + lane;
-      const uint32_t pc = p % XPR;
+      const uint32_t pc = MODE == 0 ? (p % XPR) ^ ((p / XPR) & (XPR - 1)) : p % XPR;
       if ((C::P_UXS / C::NW) % 64 == 0 || i * 64 + lane < (uint32_t)(C::P_UXS / C::NW))
         dma16(u.xs + rw.x[i] + pc * 16, ubuf + C::OFF_UXS + (dw * (C::P_UXS / C::NW) + i * 64) * 16);
     }
@@ -989,7 +1002,8 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
   // Issue position (unit iv, chunk ic, stage islot) runs S - 1 chunks ahead
   // of the compute position (unit cv, chunk cc, stage cslot).
   uint32_t iv = lb, ic = 0, islot = 0, issued = 0, iub = 0;
-  UnitSrc isrc = unit_src(iv);
+  UnitSrc isrc = unit_src(iv, item_words(iv));
+  uint2 inext = iv + per < group_units ? item_words(iv + per) : uint2{0u, 0u};
   UnitRows irows;
   if constexpr (C::GATHER) {
     // The first unit's token ids, visible to every wave before its copies.
@@ -1017,12 +1031,17 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
       ic = 0;
       iub ^= 1u;
       iv += per;
-      if (iv < group_units) isrc = unit_src(iv);
+      if (iv < group_units) {
+        isrc = unit_src(iv, inext);
+        if (iv + per < group_units) inext = item_words(iv + per);
+      }
     }
   }
   uint32_t cv = lb, cc = 0, cslot = 0, cub = 0;
-  uint32_t c_item = item_lo + cv / ncb, c_cb = cv % ncb;
-  uint32_t c_start = items[2 * c_item + 1] & 0xFFFFu, c_cnt = items[2 * c_item + 1] >> 16;
+  uint32_t c_cb = cv % ncb;
+  uint32_t c_w = item_words(cv).y;
+  uint32_t c_start = c_w & 0xFFFFu, c_cnt = c_w >> 16;
+  uint32_t c_next = cv + per < group_units ? item_words(cv + per).y : 0u;
   // Activation group sums of the last finished unit, still to be written by
   // wave 0 once a block barrier has ordered the column waves' row sums.
   bool ps_pend = false;
@@ -1075,7 +1094,10 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
         ic = 0;
         iub ^= 1u;
         iv += per;
-        if (iv < group_units) isrc = unit_src(iv);
+        if (iv < group_units) {
+        isrc = unit_src(iv, inext);
+        if (iv + per < group_units) inext = item_words(iv + per);
+      }
       }
     }
     // The row sums are read before the next unit end writes them again:
@@ -1105,10 +1127,10 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
       cub ^= 1u;
       cv += per;
       if (cv < group_units) {
-        c_item = item_lo + cv / ncb;
         c_cb = cv % ncb;
-        c_start = items[2 * c_item + 1] & 0xFFFFu;
-        c_cnt = items[2 * c_item + 1] >> 16;
+        c_start = c_next & 0xFFFFu;
+        c_cnt = c_next >> 16;
+        if (cv + per < group_units) c_next = item_words(cv + per).y;
       }
       // Every wave is done reading this stage; the upper half parks its sums
       // there ([column wave][accumulator][lane]) for the lower half.
