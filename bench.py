@@ -53,11 +53,12 @@ CONFIGS = {
 
 # HBM bytes actually moved per unit of work, from rocprofv3 FETCH_SIZE and
 # WRITE_SIZE passes scaled by a 256 MiB copy calibration (FETCH x 2.0,
-# WRITE x 1.0): profiles/decode_c2_a3b_4bit.md (one layer = the three
-# k_fa_* launches), profiles/lm_head_c1_qmv_argmax.md (k_qmv + argmax) and
-# profiles/prefill_c4_a3b_4bit.md (the five prefill launches of one layer).
-# None where no counter pass was taken.
-MEASURED_TRAFFIC = {"c2": 18_841_805, "c1": 175_961_008, "c4": 578_790_232}
+# WRITE x 1.0): profiles/decode_c{0,2,3}_*.md (one layer = the three k_fa_*
+# launches), profiles/lm_head_c1_qmv_argmax.md (k_qmv + argmax) and
+# profiles/prefill_c4_a3b_4bit.md (the four prefill launches of one layer).
+# None where no counter pass was taken (multi-token decode, per-phase path).
+MEASURED_TRAFFIC = {"c0": 29_745_023, "c2": 18_873_238, "c3": 15_771_620, "c1": 175_934_641,
+                    "c4": 562_582_175}
 
 
 def stream_read_peak(dev, gib=4):
@@ -317,7 +318,7 @@ def run_decode(args, c):
         "gbps": round(achieved, 1),
         "pct_of_hbm_peak": round(100 * achieved / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": MEASURED_TRAFFIC.get(c.get("key")) if path in (0, 3) else None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": MEASURED_TRAFFIC.get(c.get("key")) if path in (0, 3) and T == 1 else None,
                      "unit_of_work": f"one layer, {T} token(s): {nbytes} algorithmic bytes",
                      "kernel": "decode layer: k_fa_route + k_fa_gateup + k_fa_down (one HIP graph)"
                                if path in (0, 3) else "decode layer (all launches)"},
