@@ -268,7 +268,15 @@ typedef struct {
  * other shapes take one kernel per phase. See SMOE_OPT_DECODE_PATH.
  * input: device f32[hidden] (the post-attention-norm hidden);
  * h_mid: device f32[hidden] (residual); hidden_out: device f32[hidden];
- * idx_out / w_out: device int32[k] / f32[k], or NULL.
+ * idx_out / w_out: device int32[k] / f32[k], or NULL, in the
+ * reference's slot order (the running-minimum replacement order).
+ * Combine order: the per-phase path adds the routed terms in that slot
+ * order, as the reference does (deferred.rs:462-468); the three-kernel
+ * path adds them in ascending expert index (the order its top-k set
+ * comes in), so its hidden_out can differ from the reference's by a few
+ * ULP (same terms, another summation order), never bit-identical by
+ * construction. The renormalisation sum runs in the same order as the
+ * combine.
  * Replaces finish_post_attention's routing (attn/linear_attn_forward.rs:
  * 2123-2165) + moe_dispatch_per_token (:2382-2710) without the host
  * round trip. */

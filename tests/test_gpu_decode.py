@@ -447,6 +447,20 @@ def test_moe_decode_layer_matches_oracle(kernels, path, name, H, I, E, k, bits, 
         kernels.set_decode_path(0)
 
 
+def test_decode_layer_hidden_4096_auto_path(kernels):
+    """The reference's Qwen3.5-397B-A17B shape (hidden 4096, 512 experts,
+    top-10, inter 1024, gated shared expert) has no three-kernel instance;
+    the default path takes the per-phase kernels, same contract."""
+    kernels.set_decode_path(0)
+    got, gi, gw, want, wi, ww, gap = _layer_case(kernels, 4096, 1024, 512, 10, 4, True, True, seed=4096)
+    kernels.sync()
+    err = rel_err(got, want)
+    print(f"hidden 4096 E=512 k=10: idx gpu={list(gi)} cpu={list(wi)} gap={gap:.3e} rel_err={err:.3e}")
+    assert np.array_equal(gi, wi)
+    assert np.max(np.abs(gw - ww)) <= 1e-5 * np.max(np.abs(ww))
+    assert err <= TOL
+
+
 def _chain(kernels, NL, E, k, bits, seed, norm_sigma=0.0, I=512, H=2048):
     """NL resident config-2-style layers (routed `bits`, 4-bit shared expert
     with gate) and per-layer bf16 RMSNorm weights 1 + N(0, norm_sigma)."""
