@@ -137,9 +137,11 @@ typedef struct {
 int smoe_qmv(smoe_handle* h, const smoe_qweights* w, const float* x, float* y, uint32_t out_dim,
              uint32_t in_dim);
 
-/* Greedy argmax of a device f32[n] (16-byte aligned; first index wins on
- * ties, as a sequential scan) into a device int32. The LM head's token
- * pick. Two launches: 256 slice blocks, then one block over the partials. */
+/* Greedy argmax of a device f32[n] (16-byte aligned) into a device int32:
+ * the reference's scan `best = 0; if v[i] > v[best] then best = i`
+ * (first index wins on ties; a NaN never wins, and a NaN at index 0 is
+ * never replaced, so the result is 0 then). The LM head's token pick. Two
+ * launches: 256 slice blocks, then one block over the partials. */
 int smoe_argmax(smoe_handle* h, const float* v, uint32_t n, int32_t* out_index);
 
 /* smoe_qmv and smoe_argmax of its output in one pass (the LM head with

@@ -169,7 +169,7 @@ __global__ __launch_bounds__(256) void k_qmv(const uint8_t* __restrict__ codes,
 
 __global__ __launch_bounds__(1024) void k_argmax_final(const float* __restrict__ pv,
                                                        const uint32_t* __restrict__ pi, uint32_t n,
-                                                       int32_t* __restrict__ out);
+                                                       const float* __restrict__ v0, int32_t* __restrict__ out);
 
 template <int BITS, int CPR>
 static hipError_t qmv_inst(const QView& w, const float* x, float* y, uint32_t rows,
@@ -189,7 +189,8 @@ static hipError_t qmv_inst(const QView& w, const float* x, float* y, uint32_t ro
   n_waves = blocks * wpb;
   hipLaunchKernelGGL((k_qmv<BITS, CPR, U>), dim3(blocks), dim3(wpb * 64), 0, st, w.codes, w.scales,
                      w.biases, x, y, rows, w.group, n_waves, arg_out ? arg_v : nullptr, arg_i);
-  if (arg_out) hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(1024), 0, st, arg_v, arg_i, n_waves, arg_out);
+  if (arg_out)
+    hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(1024), 0, st, arg_v, arg_i, n_waves, (const float*)y, arg_out);
   return hipGetLastError();
 }
 
@@ -305,9 +306,13 @@ __global__ __launch_bounds__(256) void k_argmax_part(const float* __restrict__ v
   }
 }
 
+// The merge of the partials. The reference's greedy pick is the scan
+// `best = 0; if v[i] > v[best] then best = i` (engine_tests.rs:105-107,
+// orc_argmax): NaN never replaces the best, and a NaN at index 0 is never
+// replaced, so the pick is 0 then; v0 = the vector's first element.
 __global__ __launch_bounds__(1024) void k_argmax_final(const float* __restrict__ pv,
                                                        const uint32_t* __restrict__ pi, uint32_t n,
-                                                       int32_t* __restrict__ out) {
+                                                       const float* __restrict__ v0, int32_t* __restrict__ out) {
   float best = -INFINITY;
   uint32_t bi = 0xFFFFFFFFu;
   // Four partials per thread per round, loaded before they are merged (the
@@ -325,13 +330,16 @@ __global__ __launch_bounds__(1024) void k_argmax_final(const float* __restrict__
     for (int j = 0; j < 4; ++j) argmax_merge(best, bi, v[j], ix[j]);
   }
   argmax_block(best, bi);
-  if (threadIdx.x == 0) *out = (int32_t)bi;
+  if (threadIdx.x == 0) {
+    const float first = *v0;
+    *out = first != first ? 0 : (int32_t)bi;
+  }
 }
 
 hipError_t launch_argmax(const float* v, uint32_t n, int32_t* out, float* part_v, uint32_t* part_i,
                          hipStream_t st) {
   hipLaunchKernelGGL(k_argmax_part, dim3(kArgBlocks), dim3(256), 0, st, v, n, part_v, part_i);
-  hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(256), 0, st, part_v, part_i, kArgBlocks, out);
+  hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(256), 0, st, part_v, part_i, kArgBlocks, v, out);
   return hipGetLastError();
 }
 

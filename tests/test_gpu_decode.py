@@ -131,6 +131,56 @@ def test_argmax_first_index_on_ties(kernels, n):
     assert int(host(out)[0]) == int(np.argmax(v)) == oracle.argmax(v)
 
 
+def _ref_argmax(v):
+    """The reference's greedy pick (engine_tests.rs:105-107): fold from
+    index 0, replace only when strictly greater."""
+    best = 0
+    for i in range(1, len(v)):
+        if v[i] > v[best]:
+            best = i
+    return best
+
+
+@pytest.mark.parametrize("case", ["nan-first", "nan-inside", "all-nan", "nan-first-of-one"])
+def test_argmax_nan_like_the_reference(kernels, case):
+    """NaN never wins, and a NaN at index 0 is never replaced (the
+    reference's scan keeps index 0): smoe_argmax over 4097 values (slice
+    borders included) and the oracle agree with the restated scan."""
+    torch = _torch()
+    rng = np.random.default_rng(77)
+    n = 1 if case == "nan-first-of-one" else 4097
+    v = rng.standard_normal(n).astype(np.float32)
+    if case in ("nan-first", "nan-first-of-one"):
+        v[0] = np.nan
+    elif case == "nan-inside":
+        v[[5, 1000, 2100, 4096]] = np.nan
+        v[3000] = 9.0
+    else:
+        v[:] = np.nan
+    want = _ref_argmax(v)
+    out = torch.empty(1, dtype=torch.int32, device="cuda")
+    assert kernels.argmax(dev(v), n, out) == 0
+    assert int(host(out)[0]) == want == oracle.argmax(v)
+
+
+def test_qmv_argmax_nan_first_row(kernels):
+    """smoe_qmv_argmax when row 0's scales are NaN (y[0] = NaN): index 0, as
+    the reference's scan over the logits gives."""
+    torch = _torch()
+    out_dim, in_dim = 9000, 2048
+    rng = np.random.default_rng(9)
+    codes, s, b = gen_quant_matrix(rng, out_dim, in_dim, 64, 4)
+    s[0, :] = 0x7FC0  # bf16 NaN
+    x = rng.standard_normal(in_dim).astype(np.float32)
+    w = qweights(codes, s, b, 64, 4)
+    y = torch.empty(out_dim, dtype=torch.float32, device="cuda")
+    i = torch.empty(1, dtype=torch.int32, device="cuda")
+    assert kernels.qmv_argmax(w, dev(x), y, out_dim, in_dim, i) == 0
+    got = host(y)
+    assert np.isnan(got[0]) and np.all(np.isfinite(got[1:]))
+    assert int(host(i)[0]) == 0 == _ref_argmax(got) == oracle.argmax(got)
+
+
 @pytest.mark.parametrize("out_dim,in_dim,bits", [(151936, 2048, 4), (50000, 1024, 4), (9000, 2048, 3),
                                                  (77, 512, 4)])
 def test_qmv_argmax_fused(kernels, out_dim, in_dim, bits):

@@ -407,3 +407,17 @@ def test_router_nan_logit_keeps_start_slots(pos):
         assert rc == 0
         assert np.all(idx == 0)
         assert np.all(w == np.float32(-1e30))
+
+
+def test_argmax_is_the_reference_scan_with_nan():
+    """orc_argmax is the reference's greedy fold (engine_tests.rs:105-107):
+    first maximal index, NaN never replaces the best, a NaN at index 0 is
+    kept (every comparison with it is false)."""
+    v = np.array([np.nan, 3.0, 5.0, 5.0, 1.0], np.float32)
+    assert oracle.argmax(v) == 0
+    v = np.array([1.0, np.nan, 5.0, np.nan, 5.0], np.float32)
+    assert oracle.argmax(v) == 2
+    v = np.full(7, np.nan, np.float32)
+    assert oracle.argmax(v) == 0
+    v = np.array([-np.inf, -np.inf], np.float32)
+    assert oracle.argmax(v) == 0
