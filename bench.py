@@ -48,6 +48,10 @@ CONFIGS = {
                H=2048, bits=4),
     "c4": dict(name="Qwen3.6-A3B-shape MoE layer prefill, 512 tokens (bf16 x, Zipf 1.1 routing)", H=2048, I=512,
                E=256, k=8, bits=4, tokens=512),
+    # Not a BASELINE config: the reference's largest supported model shape
+    # (Qwen3.5-397B-A17B), 16 of its 60 layers resident (58 GB).
+    "c5": dict(name="Qwen3.5-397B-A17B-shape MoE decode, 16 layers (1 token)", H=4096, I=1024, E=512, k=10,
+               bits=4, normalize=True, shared=True, layers=16),
 }
 
 

@@ -264,7 +264,7 @@ typedef struct {
 
 /* Decode one token through one layer with routing on the device:
  * router -> top-k -> routed + shared expert FFN -> combine. For hidden
- * 2048, inter 512 or 1024, <= 512 experts this is three kernels (router +
+ * 2048 or 4096, inter 512 or 1024, <= 512 experts this is three kernels (router +
  * shared gate/up; top-k + routed gate/up; down + combine) that allocate
  * nothing and set no memory, so a caller can capture them in a HIP graph;
  * other shapes take one kernel per phase. See SMOE_OPT_DECODE_PATH.
@@ -304,7 +304,7 @@ int smoe_moe_decode_layers(smoe_handle* h, const smoe_layer* layers, uint32_t n_
  * counterpart in the reference. Same arguments and results as
  * smoe_moe_decode_layers (bit for bit), on the CURRENT device, enqueued on
  * `stream` (a hipStream_t; NULL = the default stream). The three-kernel
- * shapes only (hidden 2048, inter 512 or 1024, <= 512 experts, k <= 16;
+ * shapes only (hidden 2048 or 4096, inter 512 or 1024, <= 512 experts, k <= 16;
  * else SMOE_ERR_UNSUPPORTED_SHAPE). Its intermediates live in a fixed
  * 128 KiB device array that each GPU the library runs on holds until the
  * process ends; layers needing more return SMOE_ERR_SCRATCH_TOO_SMALL. The
@@ -315,16 +315,17 @@ int smoe_moe_decode_layers_noalloc(void* stream, const smoe_layer* layers, uint3
                                    const void* const* norm_w, float eps, const float* input,
                                    float* residual_io);
 
-/* Several decode tokens (1..4) through the same layers at once, each as
- * smoe_moe_decode_layers would decode it alone (own routing, experts,
- * combine and chained RMSNorm; bit-identical to that): input,
+/* Several decode tokens (1..4; 1..2 at hidden 4096) through the same
+ * layers at once, each as smoe_moe_decode_layers would decode it alone
+ * (own routing, experts, combine and chained RMSNorm; bit-identical to
+ * that): input,
  * residual_io and work are [n_tokens, hidden] rows (16-byte aligned).
  * Every layer is still three launches: the router and shared-expert rows
  * are read once for all tokens and each token's routed experts run side
  * by side in the same grids. idx_out / w_out (nullable): [n_tokens, k] of the last
  * layer in the reference's slot order. Replaces the T-token pass of
- * decode_multi.rs (moe_dispatch_multi, 445-654). Three-kernel shapes only
- * (else SMOE_ERR_UNSUPPORTED_SHAPE). */
+ * decode_multi.rs (moe_dispatch_multi, 445-654). Three-kernel shapes only,
+ * and n_tokens <= 2 at hidden 4096 (else SMOE_ERR_UNSUPPORTED_SHAPE). */
 int smoe_moe_decode_tokens(smoe_handle* h, const smoe_layer* layers, uint32_t n_layers,
                            const void* const* norm_w, float eps, uint32_t n_tokens, const float* input,
                            float* residual_io, float* work, int32_t* idx_out, float* w_out);

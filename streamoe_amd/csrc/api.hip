@@ -510,6 +510,7 @@ static int decode_fused(const FaScratch& sc, const smoe_layer* L, const float* x
   if (!fused_ok(L)) return SMOE_ERR_UNSUPPORTED_SHAPE;
   const smoe_expert_shape& s = L->shape;
   FusedLayer a{};
+  a.hidden = s.hidden;
   a.x_in = x_in;
   a.resid = resid;
   a.norm = norm;
@@ -655,7 +656,8 @@ int smoe_moe_decode_tokens(smoe_handle* h, const smoe_layer* layers, uint32_t n_
     if (int rc = check_layer(h, &layers[l])) return rc;
     if (layers[l].shape.hidden != layers[0].shape.hidden) return SMOE_ERR_INVALID_ARG;
     if (norm_w && l > 0 && !norm_w[l]) return SMOE_ERR_INVALID_ARG;
-    if (!fused_ok(&layers[l])) return SMOE_ERR_UNSUPPORTED_SHAPE;
+    if (!fused_ok(&layers[l]) || n_tokens > fused_max_tokens(layers[l].shape.hidden))
+      return SMOE_ERR_UNSUPPORTED_SHAPE;
   }
   if (!aligned(input, 0, 16) || !aligned(residual_io, 0, 16) || !aligned(work, 0, 16))
     return SMOE_ERR_MISALIGNED;

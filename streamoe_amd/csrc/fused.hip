@@ -47,7 +47,9 @@
 
 namespace smoe {
 
-constexpr uint32_t kFaH = 2048;              // hidden size of this path (64 lanes x 32)
+// Hidden sizes of this path: HC x 2048, HC = 1 or 2 chunks of 32 values
+// per lane (lane l holds chunks l + 64 h, h < HC).
+constexpr uint32_t kFaH = 2048;              // hidden values per chunk column (64 lanes x 32)
 // Work per wave / block. K_B waves take 4 gate/up row pairs (their sums
 // are reduced together, gateup_rows); the K_C row count is a build-time
 // tunable. Both are the measured best on MI355X (2 or 8 rows per K_B wave,
@@ -92,29 +94,38 @@ __device__ __forceinline__ void load_sb(const uint8_t* blob, uint64_t s_off, uin
 // x = r * inv * w), or r itself when w is null. The vector and the norm
 // weights are loaded together (one memory round trip): a missing operand
 // reads a harmless stand-in and is then ignored.
+template <int HC>
 struct FaX {
-  float x[kChunk];
-  u32x4 w[4];
+  float x[HC][kChunk];
+  u32x4 w[HC][4];
 };
 
-__device__ __forceinline__ void fa_x_load(const FusedLayer& a, int lane, FaX& f) {
+template <int HC>
+__device__ __forceinline__ void fa_x_load(const FusedLayer& a, int lane, FaX<HC>& f) {
   const float* src = a.x_in ? a.x_in : a.resid;
   const uint16_t* nw = a.norm ? a.norm : reinterpret_cast<const uint16_t*>(src);
-  const u32x4* wp = reinterpret_cast<const u32x4*>(nw + (size_t)lane * kChunk);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) f.w[i] = wp[i];
-  load_x32(src + (size_t)lane * kChunk, f.x);
+  for (int h = 0; h < HC; ++h) {
+    const size_t c = (size_t)lane + 64 * h;
+    const u32x4* wp = reinterpret_cast<const u32x4*>(nw + c * kChunk);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f.w[h][i] = wp[i];
+    load_x32(src + c * kChunk, f.x[h]);
+  }
 }
 
-// 1 / rms of the hidden vector whose chunk `lane` every lane holds in f.x.
+// 1 / rms of the hidden vector whose chunks every lane holds in f.x.
 // Every rounding is written out (no contraction left to the compiler), so
 // all instantiations (T = 1..4 tokens) compute x bit for bit alike.
-__device__ __forceinline__ float fa_inv_rms(const FusedLayer& a, const FaX& f) {
+template <int HC>
+__device__ __forceinline__ float fa_inv_rms(const FusedLayer& a, const FaX<HC>& f) {
   float ss = 0.f;
 #pragma unroll
-  for (int j = 0; j < kChunk; ++j) ss = __builtin_fmaf(f.x[j], f.x[j], ss);
+  for (int h = 0; h < HC; ++h)
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) ss = __builtin_fmaf(f.x[h][j], f.x[h][j], ss);
   ss = readlane_f(group_sum_last<64>(ss), 63);
-  return 1.0f / sqrtf(__builtin_fmaf(ss, 1.0f / (float)kFaH, a.eps));
+  return 1.0f / sqrtf(__builtin_fmaf(ss, 1.0f / (float)(HC * kFaH), a.eps));
 }
 
 // x[j] = r[j] * inv * w[j] for eight consecutive values (w: 8 bf16).
@@ -127,11 +138,14 @@ __device__ __forceinline__ void fa_norm8(float* x, float inv, const u32x4& w) {
   }
 }
 
-__device__ __forceinline__ void fa_x_finish(const FusedLayer& a, FaX& f) {
+template <int HC>
+__device__ __forceinline__ void fa_x_finish(const FusedLayer& a, FaX<HC>& f) {
   if (a.x_in || !a.norm) return;
-  const float inv = fa_inv_rms(a, f);
+  const float inv = fa_inv_rms<HC>(a, f);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) fa_norm8(f.x + 8 * i, inv, f.w[i]);
+  for (int h = 0; h < HC; ++h)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fa_norm8(f.x[h] + 8 * i, inv, f.w[h][i]);
 }
 
 // x as integer limbs (common.h, make_limbs) with four lanes per 32-value
@@ -177,9 +191,10 @@ __device__ __forceinline__ void store_limbs_quad(uint32_t* dst, const float (&x)
 // Token t's view of a multi-token layer: the same arguments with every
 // per-token pointer moved to token t's rows. Branch-free (selects), so it
 // adds no branch level in front of the first loads.
+template <int HC>
 __device__ __forceinline__ FusedLayer token_view(const FusedLayer& a, uint32_t t) {
   FusedLayer b = a;
-  const size_t hs = (size_t)t * kFaH;
+  const size_t hs = (size_t)t * HC * kFaH;
   b.x_in = a.x_in ? a.x_in + hs : nullptr;
   b.resid = a.resid ? a.resid + hs : nullptr;
   b.h_mid += hs;
@@ -207,32 +222,39 @@ __device__ __forceinline__ FusedLayer token_view(const FusedLayer& a, uint32_t t
 // experts stream past it non-temporally (measured on MI355X: a 2 MB
 // temporal read after a 512 MB non-temporal stream takes 0.74 us, against
 // 1.49 us from HBM).
-__device__ __forceinline__ void fa_row_load(const float* row, uint32_t c, f32x4 (&wr)[kChunk / 4]) {
-  const f32x4* rp = reinterpret_cast<const f32x4*>(row + (size_t)c * kChunk);
+template <int HC>
+__device__ __forceinline__ void fa_row_load(const float* row, uint32_t lane, f32x4 (&wr)[HC][kChunk / 4]) {
 #pragma unroll
-  for (int i = 0; i < kChunk / 4; ++i) wr[i] = ld_w<false>(rp + i);
+  for (int h = 0; h < HC; ++h) {
+    const f32x4* rp = reinterpret_cast<const f32x4*>(row + ((size_t)lane + 64 * h) * kChunk);
+#pragma unroll
+    for (int i = 0; i < kChunk / 4; ++i) wr[h][i] = ld_w<false>(rp + i);
+  }
 }
 
-// row . x over the wave (valid in lane 63): four FMA chains per lane, then
-// the wave sum.
-__device__ __forceinline__ float fa_row_dot(const f32x4 (&wr)[kChunk / 4], const float (&x)[kChunk]) {
+// row . x over the wave (valid in lane 63): four FMA chains per lane over
+// its chunks, then the wave sum.
+template <int HC>
+__device__ __forceinline__ float fa_row_dot(const f32x4 (&wr)[HC][kChunk / 4], const float (&x)[HC][kChunk]) {
   float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
 #pragma unroll
-  for (int i = 0; i < kChunk / 4; ++i) {
-    a0 = __builtin_fmaf(wr[i].x, x[4 * i + 0], a0);
-    a1 = __builtin_fmaf(wr[i].y, x[4 * i + 1], a1);
-    a2 = __builtin_fmaf(wr[i].z, x[4 * i + 2], a2);
-    a3 = __builtin_fmaf(wr[i].w, x[4 * i + 3], a3);
-  }
+  for (int h = 0; h < HC; ++h)
+#pragma unroll
+    for (int i = 0; i < kChunk / 4; ++i) {
+      a0 = __builtin_fmaf(wr[h][i].x, x[h][4 * i + 0], a0);
+      a1 = __builtin_fmaf(wr[h][i].y, x[h][4 * i + 1], a1);
+      a2 = __builtin_fmaf(wr[h][i].z, x[h][4 * i + 2], a2);
+      a3 = __builtin_fmaf(wr[h][i].w, x[h][4 * i + 3], a3);
+    }
   return group_sum_last<64>((a0 + a1) + (a2 + a3));
 }
 
 // ---------------------------------------------------------------------------
 // K_A: router logits for T tokens: each wave reads its
-// router row once and applies it to every token's x. The last 4T waves
+// router row once and applies it to every token's x. The last 4 HC T waves
 // write x of the tokens as integer limbs for K_B.
 // ---------------------------------------------------------------------------
-template <int T>
+template <int T, int HC>
 __global__ __launch_bounds__(64) void k_fa_route(FusedLayer a) {
   FA_ARGS_IN_SGPRS("s"(a.x_in), "s"(a.resid), "s"(a.norm), "s"(a.eps), "s"(a.router), "s"(a.E),
                    "s"(a.logits), "s"(a.xl), "s"(a.trace), "s"(a.lstride), "s"(a.xstride));
@@ -241,18 +263,17 @@ __global__ __launch_bounds__(64) void k_fa_route(FusedLayer a) {
   const int lane = threadIdx.x;
   const uint32_t w = blockIdx.x;
   const uint32_t nrouter = a.E;
-  const uint32_t c = lane;  // this lane's chunk of the hidden vector
 
   if (w >= nrouter) {
-    // Limb waves, four per token: wave p of token t converts chunks
+    // Limb waves, 4 HC per token: wave p of token t converts chunks
     // [16p, 16p + 16), four lanes per chunk (8 values each). Every lane also
-    // loads chunk `lane` for the sum of squares.
+    // loads its own chunks for the sum of squares.
     const uint32_t lw = w - nrouter;
-    const FusedLayer at = token_view(a, lw >> 2);
-    const uint32_t ch = (lw & 3) * 16 + (uint32_t)(lane >> 2);
+    const FusedLayer at = token_view<HC>(a, lw / (4 * HC));
+    const uint32_t ch = (lw % (4 * HC)) * 16 + (uint32_t)(lane >> 2);
     const int q = lane & 3;
-    FaX f;
-    fa_x_load(at, lane, f);
+    FaX<HC> f;
+    fa_x_load<HC>(at, lane, f);
     const float* src = at.x_in ? at.x_in : at.resid;
     const uint16_t* nw = at.norm ? at.norm : reinterpret_cast<const uint16_t*>(src);
     const uint32_t e0 = ch * kChunk + q * 8;
@@ -262,44 +283,49 @@ __global__ __launch_bounds__(64) void k_fa_route(FusedLayer a) {
     __builtin_amdgcn_sched_barrier(0);
     fa_stamp(a, clk, 3, true);
     float x[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-    if (!at.x_in && at.norm) fa_norm8(x, fa_inv_rms(at, f), w8);
+    if (!at.x_in && at.norm) fa_norm8(x, fa_inv_rms<HC>(at, f), w8);
     store_limbs_quad(at.xl + (size_t)ch * kXLimbWords, x, q);
     fa_stamp(a, clk, 5, true);
     fa_flush(a, clk, 0);
     return;
   }
-  f32x4 wr[kChunk / 4];
-  fa_row_load(a.router + (size_t)w * kFaH, c, wr);
-  FaX f[T];
+  f32x4 wr[HC][kChunk / 4];
+  fa_row_load<HC>(a.router + (size_t)w * (HC * kFaH), lane, wr);
+  FaX<HC> f[T];
 #pragma unroll
-  for (int t = 0; t < T; ++t) fa_x_load(token_view(a, t), lane, f[t]);
+  for (int t = 0; t < T; ++t) fa_x_load<HC>(token_view<HC>(a, t), lane, f[t]);
   __builtin_amdgcn_sched_barrier(0);
   fa_stamp(a, clk, 3, true);
 #pragma unroll
   for (int t = 0; t < T; ++t) {
-    const FusedLayer at = token_view(a, t);
+    const FusedLayer at = token_view<HC>(a, t);
     if (at.x_in || !at.norm) {
-      const float s = fa_row_dot(wr, f[t].x);
+      const float s = fa_row_dot<HC>(wr, f[t].x);
       if (lane == 63) at.logits[w] = s;
     } else {
       // logit = (1 / rms(r)) * (W . (r * w)): the dot and the sum of
       // squares run side by side instead of the dot waiting for the norm.
-      float rw[kChunk];
+      float rw[HC][kChunk];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t w4[4] = {f[t].w[i].x, f[t].w[i].y, f[t].w[i].z, f[t].w[i].w};
+      for (int hc = 0; hc < HC; ++hc)
 #pragma unroll
-        for (int h = 0; h < 4; ++h) {
-          rw[8 * i + 2 * h] = f[t].x[8 * i + 2 * h] * bf16f((uint16_t)(w4[h] & 0xFFFFu));
-          rw[8 * i + 2 * h + 1] = f[t].x[8 * i + 2 * h + 1] * bf16f((uint16_t)(w4[h] >> 16));
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t w4[4] = {f[t].w[hc][i].x, f[t].w[hc][i].y, f[t].w[hc][i].z, f[t].w[hc][i].w};
+#pragma unroll
+          for (int h = 0; h < 4; ++h) {
+            rw[hc][8 * i + 2 * h] = f[t].x[hc][8 * i + 2 * h] * bf16f((uint16_t)(w4[h] & 0xFFFFu));
+            rw[hc][8 * i + 2 * h + 1] = f[t].x[hc][8 * i + 2 * h + 1] * bf16f((uint16_t)(w4[h] >> 16));
+          }
         }
-      }
       float ss = 0.f;
 #pragma unroll
-      for (int j = 0; j < kChunk; ++j) ss = __builtin_fmaf(f[t].x[j], f[t].x[j], ss);
-      const float dot = fa_row_dot(wr, rw);
+      for (int hc = 0; hc < HC; ++hc)
+#pragma unroll
+        for (int j = 0; j < kChunk; ++j) ss = __builtin_fmaf(f[t].x[hc][j], f[t].x[hc][j], ss);
+      const float dot = fa_row_dot<HC>(wr, rw);
       ss = group_sum_last<64>(ss);
-      if (lane == 63) at.logits[w] = dot * (1.0f / sqrtf(__builtin_fmaf(ss, 1.0f / (float)kFaH, at.eps)));
+      if (lane == 63)
+        at.logits[w] = dot * (1.0f / sqrtf(__builtin_fmaf(ss, 1.0f / (float)(HC * kFaH), at.eps)));
     }
   }
   fa_stamp(a, clk, 4, false);
@@ -333,32 +359,40 @@ __device__ __forceinline__ void load_logits(const float* logits, uint32_t E, int
 // SwiGLU, stored to act[r0 ..]. All loads are issued before any arithmetic.
 // NT: non-temporal weight loads (routed experts) or temporal (the shared
 // expert, reused by every token).
-template <int BITS, bool NT>
+template <int BITS, bool NT, int HC>
 __device__ __forceinline__ void gateup_rows(const FusedLayer& a, FaClock& clk, const uint8_t* blob,
                                             const BlobGeom& g, uint32_t r0, int lane,
-                                            const XLimbs& xl, float* act) {
+                                            const XLimbs (&xl)[HC], float* act) {
   constexpr int CB = chunk_bytes<BITS>();
-  constexpr uint32_t RB = kFaH / kChunk * CB;  // row bytes
-  const uint32_t c = lane;
-  const uint32_t gpr = kFaH / g.group;
+  constexpr uint32_t RB = HC * kFaH / kChunk * CB;  // row bytes
+  const uint32_t gpr = HC * kFaH / g.group;
   const uint32_t cps = __builtin_ctz(g.group / kChunk);
-  Raw<BITS> rg[kFaRW], ru[kFaRW];
-  uint16_t sg[kFaRW], bg[kFaRW], su[kFaRW], bu[kFaRW];
+  Raw<BITS> rg[kFaRW][HC], ru[kFaRW][HC];
+  uint16_t sg[kFaRW][HC], bg[kFaRW][HC], su[kFaRW][HC], bu[kFaRW][HC];
 #pragma unroll
   for (int p = 0; p < kFaRW; ++p) {
     const uint32_t row = r0 + p;
-    rg[p] = load_raw<BITS, NT>(blob + g.w[0] + (size_t)row * RB + c * CB);
-    ru[p] = load_raw<BITS, NT>(blob + g.w[1] + (size_t)row * RB + c * CB);
-    load_sb(blob, g.s[0], g.b[0], row, gpr, cps, c, sg[p], bg[p]);
-    load_sb(blob, g.s[1], g.b[1], row, gpr, cps, c, su[p], bu[p]);
+#pragma unroll
+    for (int h = 0; h < HC; ++h) {
+      const uint32_t c = lane + 64 * h;
+      rg[p][h] = load_raw<BITS, NT>(blob + g.w[0] + (size_t)row * RB + c * CB);
+      ru[p][h] = load_raw<BITS, NT>(blob + g.w[1] + (size_t)row * RB + c * CB);
+      load_sb(blob, g.s[0], g.b[0], row, gpr, cps, c, sg[p][h], bg[p][h]);
+      load_sb(blob, g.s[1], g.b[1], row, gpr, cps, c, su[p][h], bu[p][h]);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
   fa_stamp(a, clk, 3, true);
   float gp[kFaRW], up[kFaRW];
 #pragma unroll
   for (int p = 0; p < kFaRW; ++p) {
-    gp[p] = chunk_dot_i<BITS>(rg[p], xl, bf16f(sg[p]), bf16f(bg[p]));
-    up[p] = chunk_dot_i<BITS>(ru[p], xl, bf16f(su[p]), bf16f(bu[p]));
+    gp[p] = chunk_dot_i<BITS>(rg[p][0], xl[0], bf16f(sg[p][0]), bf16f(bg[p][0]));
+    up[p] = chunk_dot_i<BITS>(ru[p][0], xl[0], bf16f(su[p][0]), bf16f(bu[p][0]));
+#pragma unroll
+    for (int h = 1; h < HC; ++h) {
+      gp[p] += chunk_dot_i<BITS>(rg[p][h], xl[h], bf16f(sg[p][h]), bf16f(bg[p][h]));
+      up[p] += chunk_dot_i<BITS>(ru[p][h], xl[h], bf16f(su[p][h]), bf16f(bu[p][h]));
+    }
   }
   // The eight rows' lane partials are summed together: after the two swaps
   // the 16-lane rows hold gate/up rows 0, 2, 1, 3, and every lane of a row
@@ -383,7 +417,7 @@ __device__ __forceinline__ void gateup_rows(const FusedLayer& a, FaClock& clk, c
 // gate score) in the order the act slots use, and, when asked, the
 // reference's exact slot order.
 // ---------------------------------------------------------------------------
-template <int BITS, int P, int KC>
+template <int BITS, int P, int KC, int HC>
 __global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a_all) {
   FA_ARGS_IN_SGPRS("s"(a_all.logits), "s"(a_all.xl), "s"(a_all.act), "s"(a_all.table), "s"(a_all.E),
                    "s"(a_all.k), "s"(a_all.normalize), "s"(a_all.experts), "s"(a_all.stride),
@@ -395,7 +429,7 @@ __global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a_all) {
   FA_ARGS_IN_SGPRS("s"(a_all.sgeom.group), "s"(a_all.sgeom.w[0]), "s"(a_all.sgeom.w[1]),
                    "s"(a_all.sgeom.s[0]), "s"(a_all.sgeom.s[1]), "s"(a_all.sgeom.b[0]),
                    "s"(a_all.sgeom.b[1]));
-  const FusedLayer a = token_view(a_all, blockIdx.y);
+  const FusedLayer a = token_view<HC>(a_all, blockIdx.y);
   __shared__ int32_t sid[kMaxK];
   __shared__ float sval[kMaxK];
   FaClock clk;
@@ -413,8 +447,9 @@ __global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a_all) {
     const uint32_t r0 = (blockIdx.x & (tiles - 1)) * kFaRW;
     float v[P];
     load_logits<P>(a.logits, E, lane, v);
-    XLimbs xl;
-    load_limbs(a.xl + (size_t)lane * kXLimbWords, xl);
+    XLimbs xl[HC];
+#pragma unroll
+    for (int h = 0; h < HC; ++h) load_limbs(a.xl + ((size_t)lane + 64 * h) * kXLimbWords, xl[h]);
     fa_stamp(a, clk, 1, true);
     int32_t id;
     if (!topk_slot_logits<P, KC>(v, E, k, slot, lane, id)) {
@@ -424,13 +459,14 @@ __global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a_all) {
       id = sid[slot];
     }
     fa_stamp(a, clk, 2, false);
-    gateup_rows<BITS, true>(a, clk, a.experts + (uint64_t)id * a.stride, a.routed, r0, lane, xl,
-                            a.act + (size_t)slot * I);
+    gateup_rows<BITS, true, HC>(a, clk, a.experts + (uint64_t)id * a.stride, a.routed, r0, lane, xl,
+                                a.act + (size_t)slot * I);
   } else if (blockIdx.x < nrouted + nshared) {
     const uint32_t r0 = (blockIdx.x - nrouted) * kFaRW;
-    XLimbs xl;
-    load_limbs(a.xl + (size_t)lane * kXLimbWords, xl);
-    gateup_rows<4, false>(a, clk, a.shared, a.sgeom, r0, lane, xl, a.act + (size_t)k * I);
+    XLimbs xl[HC];
+#pragma unroll
+    for (int h = 0; h < HC; ++h) load_limbs(a.xl + ((size_t)lane + 64 * h) * kXLimbWords, xl[h]);
+    gateup_rows<4, false, HC>(a, clk, a.shared, a.sgeom, r0, lane, xl, a.act + (size_t)k * I);
   } else {
     // Route table (normalize_weights, moe_router.rs:130-141).
     __shared__ float sprob[64 * P];
@@ -438,10 +474,10 @@ __global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a_all) {
     // critical path (in the router kernel its extra wave ended last): its
     // loads go out with the logits'.
     const bool gated = a.gate != nullptr;
-    f32x4 gw[kChunk / 4];
-    FaX gx;
-    fa_row_load(gated ? a.gate : a.router, lane, gw);
-    fa_x_load(a, lane, gx);
+    f32x4 gw[HC][kChunk / 4];
+    FaX<HC> gx;
+    fa_row_load<HC>(gated ? a.gate : a.router, lane, gw);
+    fa_x_load<HC>(a, lane, gx);
     float v[P];
     load_logits<P>(a.logits, E, lane, v);
     const bool is_set = topk_set_logits<P, KC>(v, E, k, lane, sid);
@@ -462,8 +498,8 @@ __global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a_all) {
       a.table->blob[lane] = a.experts + (uint64_t)sid[lane] * a.stride;
       a.table->weight[lane] = wt;
     }
-    fa_x_finish(a, gx);
-    const float gate_dot = readlane_f(fa_row_dot(gw, gx.x), 63);
+    fa_x_finish<HC>(a, gx);
+    const float gate_dot = readlane_f(fa_row_dot<HC>(gw, gx.x), 63);
     const float gate_score = gated ? gate_dot : __builtin_nanf("");
     if (lane == 0) {
       a.table->k = k;
@@ -575,14 +611,14 @@ __host__ __device__ constexpr uint32_t fa_down_parts(uint32_t k) {
   return 2u * ((k + kWave / LI - 1) / (kWave / LI)) + 1u <= 16u ? 2u : 1u;
 }
 
-template <int BITS, int LI, int H>
+template <int BITS, int LI, int H, int HC>
 __global__ __launch_bounds__(1024) void k_fa_down(FusedLayer a_all) {
   FA_ARGS_IN_SGPRS("s"(a_all.act), "s"(a_all.table), "s"(a_all.h_mid), "s"(a_all.out), "s"(a_all.trace),
                    "s"(a_all.k), "s"(a_all.shared), "s"(a_all.astride), "s"(a_all.routed.inter),
                    "s"(a_all.routed.group), "s"(a_all.routed.w[2]), "s"(a_all.routed.s[2]),
                    "s"(a_all.routed.b[2]), "s"(a_all.sgeom.inter), "s"(a_all.sgeom.group),
                    "s"(a_all.sgeom.w[2]), "s"(a_all.sgeom.s[2]), "s"(a_all.sgeom.b[2]));
-  const FusedLayer a = token_view(a_all, blockIdx.y);
+  const FusedLayer a = token_view<HC>(a_all, blockIdx.y);
   constexpr int SPW = kWave / LI;
   constexpr int NR = kFaRB / H;             // rows per routed lane
   constexpr int NRS = kFaRB / (kWave / LI); // rows per shared lane
@@ -685,7 +721,7 @@ __global__ __launch_bounds__(1024) void k_fa_down(FusedLayer a_all) {
 // ---------------------------------------------------------------------------
 bool fused_supported(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t bits,
                      uint32_t n_experts, uint32_t k) {
-  if (hidden != kFaH) return false;
+  if (hidden != kFaH && hidden != 2 * kFaH) return false;
   if (inter != 512 && inter != 1024) return false;
   if (group % kChunk != 0 || (group & (group - 1)) != 0 || inter % group != 0) return false;
   if (bits != 4 && bits != 3) return false;
@@ -695,32 +731,32 @@ bool fused_supported(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t b
 
 // K_B instance: logits per lane P = ceil(E / 64); k = 8 (the A3B and OLMoE
 // shapes) has its own instance with unrolled top-k rounds.
-template <int BITS, int KC>
+template <int BITS, int KC, int HC>
 static void launch_gateup_fa_k(const FusedLayer& a, uint32_t blocks, hipStream_t st) {
   const uint32_t p = (a.E + 63) / 64;
   const dim3 grid(blocks, a.n_tokens);
   if (p <= 1)
-    hipLaunchKernelGGL((k_fa_gateup<BITS, 1, KC>), grid, dim3(64), 0, st, a);
+    hipLaunchKernelGGL((k_fa_gateup<BITS, 1, KC, HC>), grid, dim3(64), 0, st, a);
   else if (p <= 2)
-    hipLaunchKernelGGL((k_fa_gateup<BITS, 2, KC>), grid, dim3(64), 0, st, a);
+    hipLaunchKernelGGL((k_fa_gateup<BITS, 2, KC, HC>), grid, dim3(64), 0, st, a);
   else if (p <= 4)
-    hipLaunchKernelGGL((k_fa_gateup<BITS, 4, KC>), grid, dim3(64), 0, st, a);
+    hipLaunchKernelGGL((k_fa_gateup<BITS, 4, KC, HC>), grid, dim3(64), 0, st, a);
   else
-    hipLaunchKernelGGL((k_fa_gateup<BITS, 8, KC>), grid, dim3(64), 0, st, a);
+    hipLaunchKernelGGL((k_fa_gateup<BITS, 8, KC, HC>), grid, dim3(64), 0, st, a);
 }
 
-template <int BITS>
+template <int BITS, int HC>
 static void launch_gateup_fa(const FusedLayer& a, uint32_t blocks, hipStream_t st) {
   if (a.k == 8)
-    launch_gateup_fa_k<BITS, 8>(a, blocks, st);
+    launch_gateup_fa_k<BITS, 8, HC>(a, blocks, st);
   else
-    launch_gateup_fa_k<BITS, 0>(a, blocks, st);
+    launch_gateup_fa_k<BITS, 0, HC>(a, blocks, st);
 }
 
 // K_C launch: 8 rows per block; LDS for the staged activations. Blocks of
 // more than 64 KB (k = 16 at inter 1024) need the attribute raised (once
 // per device).
-template <int BITS, int LI, int H>
+template <int BITS, int LI, int H, int HC>
 static hipError_t launch_down_fa_h(const FusedLayer& a, hipStream_t st) {
   constexpr uint32_t SPW = kWave / LI;
   const uint32_t waves = (a.k + SPW - 1) / SPW * H + (a.shared ? 1u : 0u);
@@ -732,40 +768,57 @@ static hipError_t launch_down_fa_h(const FusedLayer& a, hipStream_t st) {
     return hipErrorInvalidValue;
   static std::atomic<uint64_t> raised{0};
   if (lds > 64 * 1024) {
-    const hipError_t e = raise_lds_limit(reinterpret_cast<const void*>(&k_fa_down<BITS, LI, H>), 96 * 1024, raised);
+    const hipError_t e =
+        raise_lds_limit(reinterpret_cast<const void*>(&k_fa_down<BITS, LI, H, HC>), 96 * 1024, raised);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((k_fa_down<BITS, LI, H>), dim3(kFaH / kFaRB, a.n_tokens), dim3(waves * kWave), lds, st, a);
+  hipLaunchKernelGGL((k_fa_down<BITS, LI, H, HC>), dim3(HC * kFaH / kFaRB, a.n_tokens), dim3(waves * kWave), lds,
+                     st, a);
   return hipSuccess;
 }
 
-template <int BITS, int LI>
+template <int BITS, int LI, int HC>
 static hipError_t launch_down_fa(const FusedLayer& a, hipStream_t st) {
-  return fa_down_parts<LI>(a.k) == 2 ? launch_down_fa_h<BITS, LI, 2>(a, st) : launch_down_fa_h<BITS, LI, 1>(a, st);
+  return fa_down_parts<LI>(a.k) == 2 ? launch_down_fa_h<BITS, LI, 2, HC>(a, st)
+                                     : launch_down_fa_h<BITS, LI, 1, HC>(a, st);
 }
 
-hipError_t launch_fused_layer(const FusedLayer& a, hipStream_t st) {
-  if (a.n_tokens < 1 || a.n_tokens > kMaxDecodeTokens || (a.trace && a.n_tokens != 1)) return hipErrorInvalidValue;
+uint32_t fused_max_tokens(uint32_t hidden) { return hidden == kFaH ? kMaxDecodeTokens : kFaMaxTokensH2; }
+
+template <int HC>
+static hipError_t launch_fused_layer_h(const FusedLayer& a, hipStream_t st) {
   const uint32_t I = a.routed.inter;
-  const uint32_t ka = a.E + 4u * a.n_tokens;
+  const uint32_t ka = a.E + 4u * HC * a.n_tokens;
   switch (a.n_tokens) {
-    case 1: hipLaunchKernelGGL(k_fa_route<1>, dim3(ka), dim3(64), 0, st, a); break;
-    case 2: hipLaunchKernelGGL(k_fa_route<2>, dim3(ka), dim3(64), 0, st, a); break;
-    case 3: hipLaunchKernelGGL(k_fa_route<3>, dim3(ka), dim3(64), 0, st, a); break;
-    default: hipLaunchKernelGGL(k_fa_route<4>, dim3(ka), dim3(64), 0, st, a); break;
+    case 1: hipLaunchKernelGGL((k_fa_route<1, HC>), dim3(ka), dim3(64), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((k_fa_route<2, HC>), dim3(ka), dim3(64), 0, st, a); break;
+    case 3:
+      if constexpr (HC == 1) hipLaunchKernelGGL((k_fa_route<3, HC>), dim3(ka), dim3(64), 0, st, a);
+      break;
+    default:
+      if constexpr (HC == 1) hipLaunchKernelGGL((k_fa_route<4, HC>), dim3(ka), dim3(64), 0, st, a);
+      break;
   }
   const uint32_t kb = (a.k + (a.shared ? 1u : 0u)) * (I / kFaRW) + 1u;
   if (a.routed.bits == 4)
-    launch_gateup_fa<4>(a, kb, st);
+    launch_gateup_fa<4, HC>(a, kb, st);
   else
-    launch_gateup_fa<3>(a, kb, st);
+    launch_gateup_fa<3, HC>(a, kb, st);
   hipError_t e;
   if (a.routed.bits == 4)
-    e = I == 512 ? launch_down_fa<4, 16>(a, st) : launch_down_fa<4, 32>(a, st);
+    e = I == 512 ? launch_down_fa<4, 16, HC>(a, st) : launch_down_fa<4, 32, HC>(a, st);
   else
-    e = I == 512 ? launch_down_fa<3, 16>(a, st) : launch_down_fa<3, 32>(a, st);
+    e = I == 512 ? launch_down_fa<3, 16, HC>(a, st) : launch_down_fa<3, 32, HC>(a, st);
   if (e != hipSuccess) return e;
   return hipGetLastError();
+}
+
+hipError_t launch_fused_layer(const FusedLayer& a, hipStream_t st) {
+  const uint32_t H = a.hidden;
+  if ((H != kFaH && H != 2 * kFaH) || a.n_tokens < 1 || a.n_tokens > fused_max_tokens(H) ||
+      (a.trace && a.n_tokens != 1))
+    return hipErrorInvalidValue;
+  return H == kFaH ? launch_fused_layer_h<1>(a, st) : launch_fused_layer_h<2>(a, st);
 }
 
 }  // namespace smoe

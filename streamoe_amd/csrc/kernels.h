@@ -53,6 +53,7 @@ BlobGeom blob_geom(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t bit
 
 // One decode layer for the three-kernel path (fused.hip).
 struct FusedLayer {
+  uint32_t hidden;         // 2048 or 4096
   const float* x_in;       // x given as is, or null: x = RMSNorm(resid) * norm
   const float* resid;      // residual r (when x_in is null)
   const uint16_t* norm;    // bf16 RMSNorm weights, or null: x = r
@@ -84,6 +85,7 @@ struct FusedLayer {
 };
 
 constexpr uint32_t kMaxDecodeTokens = 4;  // tokens per multi-token decode call
+constexpr uint32_t kFaMaxTokensH2 = 2;    // the same at hidden 4096 (the router kernel's registers)
 
 // Trace layout of the three-kernel path: per layer kFaTraceLayer words;
 // kernel q (0 route, 1 gate/up, 2 down), block b at
@@ -103,6 +105,7 @@ inline uint32_t logit_stride(uint32_t E) {
 }
 bool fused_supported(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t bits,
                      uint32_t n_experts, uint32_t k);
+uint32_t fused_max_tokens(uint32_t hidden);  // tokens per multi-token call at this hidden size
 // K_A (router + shared gate/up), K_B (top-k + routed gate/up), K_C (down +
 // combine) on `st`; no allocation, no memset (graph-capturable).
 hipError_t launch_fused_layer(const FusedLayer& a, hipStream_t st);

@@ -474,6 +474,10 @@ LAYER_CASES = [
     ("k10", 2048, 512, 128, 10, 4, True, True),      # the reference's other supported top-k
     ("e512-k10", 2048, 512, 512, 10, 4, True, True),  # 512 experts, top-10, shared expert
     ("e300-k8", 2048, 512, 300, 8, 4, True, False),   # 8 logits per lane, ragged last lanes
+    # Hidden 4096: two 32-value chunks per lane in every wave.
+    ("q397b", 4096, 1024, 512, 10, 4, True, True),    # the reference's Qwen3.5-397B-A17B layer
+    ("h4096-3bit", 4096, 512, 128, 8, 3, True, "ungated"),
+    ("h4096-k16-i1024", 4096, 1024, 64, 16, 4, False, True),  # down kernel: one row part, > 64 KB LDS
 ]
 
 PATHS = [1, 3]
@@ -497,13 +501,21 @@ def test_moe_decode_layer_matches_oracle(kernels, path, name, H, I, E, k, bits, 
         kernels.set_decode_path(0)
 
 
-def test_decode_layer_hidden_4096_auto_path(kernels):
+def test_decode_layer_hidden_4096_default_is_three_kernel(kernels):
     """The reference's Qwen3.5-397B-A17B shape (hidden 4096, 512 experts,
-    top-10, inter 1024, gated shared expert) has no three-kernel instance;
-    the default path takes the per-phase kernels, same contract."""
-    kernels.set_decode_path(0)
-    got, gi, gw, want, wi, ww, gap = _layer_case(kernels, 4096, 1024, 512, 10, 4, True, True, seed=4096)
-    kernels.sync()
+    top-10, inter 1024, gated shared expert): the default path takes the
+    three-kernel decode (same bits as forcing it) and agrees with the
+    oracle."""
+    res = {}
+    try:
+        for path in (0, 3):
+            kernels.set_decode_path(path)
+            res[path] = _layer_case(kernels, 4096, 1024, 512, 10, 4, True, True, seed=4096)
+            kernels.sync()
+    finally:
+        kernels.set_decode_path(0)
+    got, gi, gw, want, wi, ww, gap = res[0]
+    assert np.array_equal(got.view(np.uint32), res[3][0].view(np.uint32))
     err = rel_err(got, want)
     print(f"hidden 4096 E=512 k=10: idx gpu={list(gi)} cpu={list(wi)} gap={gap:.3e} rel_err={err:.3e}")
     assert np.array_equal(gi, wi)

@@ -22,17 +22,15 @@ def _tokens(kernels, c, T, seed):
     return xs
 
 
-@pytest.mark.parametrize("T", [1, 2, 3, 4])
-@pytest.mark.parametrize("bits", [4, 3])
-def test_tokens_match_single_token_decode(kernels, T, bits):
+def _match_single_token(kernels, c, T, bits, seed):
     import torch
 
-    c = _chain(kernels, 3, 256, 8, bits, seed=7100 + 10 * T + bits, norm_sigma=0.1)
-    xs = _tokens(kernels, c, T, 7200 + T)
+    k = c["k"]
+    xs = _tokens(kernels, c, T, seed)
     resid = xs.clone()
     work = torch.empty_like(xs)
-    idx = torch.empty((T, 8), dtype=torch.int32, device="cuda")
-    w = torch.empty((T, 8), dtype=torch.float32, device="cuda")
+    idx = torch.empty((T, k), dtype=torch.int32, device="cuda")
+    w = torch.empty((T, k), dtype=torch.float32, device="cuda")
     assert kernels.moe_decode_tokens(c["layers"], c["norms"], 1e-6, T, xs, resid, work, idx, w) == 0
     kernels.sync()
     got = host(resid)
@@ -45,8 +43,27 @@ def test_tokens_match_single_token_decode(kernels, T, bits):
         ct = dict(c, x0=xs[t].contiguous())
         want, gap = _chain_oracle(ct, 1e-6)
         err = rel_err(got[t], want)
-        print(f"T={T} bits={bits} token {t}: rel_err={err:.3e} gap={gap:.2e}")
+        print(f"H={c['H']} T={T} bits={bits} token {t}: rel_err={err:.3e} gap={gap:.2e}")
         assert err <= TOL
+
+
+@pytest.mark.parametrize("T", [1, 2, 3, 4])
+@pytest.mark.parametrize("bits", [4, 3])
+def test_tokens_match_single_token_decode(kernels, T, bits):
+    c = _chain(kernels, 3, 256, 8, bits, seed=7100 + 10 * T + bits, norm_sigma=0.1)
+    _match_single_token(kernels, c, T, bits, 7200 + T)
+
+
+@pytest.mark.parametrize("T", [1, 2])
+def test_tokens_hidden_4096(kernels, T):
+    """Hidden 4096 (two tokens at most per call): two Qwen3.5-397B-A17B-shaped
+    layers (512 experts, top-10, inter 1024, gated shared expert)."""
+    import torch
+
+    c = _chain(kernels, 2, 512, 10, 4, seed=7500 + T, norm_sigma=0.1, I=1024, H=4096)
+    _match_single_token(kernels, c, T, 4, 7600 + T)
+    del c
+    torch.cuda.empty_cache()
 
 
 def test_tokens_slot_order_of_last_layer(kernels):
@@ -99,4 +116,12 @@ def test_tokens_argument_errors(kernels):
     L = kernels.layer(lay, a, lay.expert_size, 8, 2, True, r)
     x4 = torch.zeros((2, 1024), dtype=torch.float32, device="cuda")
     assert kernels.moe_decode_tokens([L], None, 1e-6, 2, x4, x4.clone(), x4.clone()) == \
+        codes["SMOE_ERR_UNSUPPORTED_SHAPE"]
+    # Hidden 4096 takes two tokens per call at most.
+    lay = sa.ExpertLayout(4096, 512, 4, 64)
+    a = torch.zeros(8 * lay.expert_size, dtype=torch.uint8, device="cuda")
+    r = torch.zeros((8, 4096), dtype=torch.float32, device="cuda")
+    L = kernels.layer(lay, a, lay.expert_size, 8, 2, True, r)
+    x3 = torch.zeros((3, 4096), dtype=torch.float32, device="cuda")
+    assert kernels.moe_decode_tokens([L], None, 1e-6, 3, x3, x3.clone(), x3.clone()) == \
         codes["SMOE_ERR_UNSUPPORTED_SHAPE"]
