@@ -730,7 +730,8 @@ bool fused_supported(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t b
 }
 
 // K_B instance: logits per lane P = ceil(E / 64); k = 8 (the A3B and OLMoE
-// shapes) has its own instance with unrolled top-k rounds.
+// shapes) and k = 10 (Qwen3.5-397B-A17B) have their own instances with
+// unrolled top-k rounds.
 template <int BITS, int KC, int HC>
 static void launch_gateup_fa_k(const FusedLayer& a, uint32_t blocks, hipStream_t st) {
   const uint32_t p = (a.E + 63) / 64;
@@ -749,6 +750,8 @@ template <int BITS, int HC>
 static void launch_gateup_fa(const FusedLayer& a, uint32_t blocks, hipStream_t st) {
   if (a.k == 8)
     launch_gateup_fa_k<BITS, 8, HC>(a, blocks, st);
+  else if (a.k == 10)
+    launch_gateup_fa_k<BITS, 10, HC>(a, blocks, st);
   else
     launch_gateup_fa_k<BITS, 0, HC>(a, blocks, st);
 }
