@@ -340,9 +340,11 @@ uint64_t smoe_moe_prefill_workspace_size(const smoe_expert_shape* shape, uint32_
 
 /* out_sum[t] = sum_s weights[t,s] * FFN_{idx[t,s]}(x[t]) for t < n_tokens:
  * tokens sorted by expert on the device, grouped gate/up GEMM with
- * exact in-kernel dequant on bf16 MFMA (fp32 accumulate), SwiGLU, down
- * GEMM, then a fixed-order per-token combine (ascending expert, no
- * atomics: bit-identical across runs).
+ * exact in-kernel dequant on bf16 MFMA (fp32 accumulate), SwiGLU into
+ * fp16 activations (as the reference's gather GEMM casts them; beyond
+ * +-65504 they become inf), down GEMM on fp16 MFMA, then a fixed-order
+ * per-token combine (ascending expert, no atomics: bit-identical across
+ * runs).
  * x: device, bf16 [n_tokens, hidden] when x_is_bf16 else f32;
  * idx: device int32[n_tokens, k]; weights: device f32[n_tokens, k];
  * out_sum: device f32[n_tokens, hidden] (overwritten); workspace:

@@ -138,8 +138,8 @@ struct PfArgs {
   float* asum;             // [n*k, inter / group] group sums of the activations
   uint16_t* x_hi;          // [n, hidden] x rows, bf16, MFMA order
   uint16_t* x_lo;          // [n, hidden] low halves (fp32 input only)
-  uint16_t* act_hi;        // [n*k, inter] SwiGLU output, bf16 hi, MFMA order
-  uint16_t* act_lo;        // [n*k, inter] bf16 lo
+  uint16_t* act_hi;        // [n*k, inter] SwiGLU output as fp16, MFMA order (qmm: x as bf16 hi)
+  uint16_t* act_lo;        // qmm only: x as bf16 lo (null for the prefill)
   float* down;             // [n*k, hidden]
   uint64_t* trace;         // k_pf_route timestamps (8 words), or null (diagnostics)
 };

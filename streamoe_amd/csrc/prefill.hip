@@ -13,13 +13,14 @@
 //                 1..: each token's x row in the MFMA k-order (bf16, or f32
 //                 split into bf16 hi + lo) and its group sums (the per-group
 //                 terms of the dequant epilogue), once per token.
-//   k_pf_mm       persistent pipelined grouped GEMM, bf16 MFMA
-//                 (v_mfma_f32_16x16x32_bf16) over (item, column block)
-//                 units: mode 0 gate and up rows of the item's expert over
-//                 its tokens' x rows (copied by token id) ->
-//                 act = silu(gate) * up as bf16 hi + lo, with the down
-//                 GEMM's activation group sums for G <= 64; mode 1 down rows
-//                 over the activations -> f32 per entry.
+//   k_pf_mm       persistent pipelined grouped GEMM on MFMA
+//                 (v_mfma_f32_16x16x32_bf16 / _f16) over (item, column
+//                 block) units: mode 0 gate and up rows of the item's expert
+//                 over its tokens' x rows (copied by token id) ->
+//                 act = silu(gate) * up as fp16, with the down GEMM's
+//                 activation group sums for G <= 64; mode 2 down rows over
+//                 the fp16 activations -> f32 per entry (mode 1: the same
+//                 over bf16 hi + lo rows, the dense qmm).
 //   k_pf_act_sum  activation group sums for G > 64 (a group spans more than
 //                 one gate/up unit).
 //   k_pf_combine  out[t] = sum over t's entries in ascending expert order of
@@ -32,7 +33,12 @@
 // the epilogue adds s * (acc - 128 * sum x) + b * sum x = s * acc + (b -
 // 128 s) * sum x, which is sum_k (q_k s + b) x_k up to fp32 rounding. x is
 // bf16 (exact in the MFMA) or an fp32 vector split into bf16 hi + lo (two
-// MFMAs into the same accumulator, ~2^-17 relative).
+// MFMAs into the same accumulator, ~2^-17 relative). The down GEMM's
+// activations are fp16 (one rounding, 2^-11 relative, as the reference's
+// gather GEMM casts them, gather_mm_id.metal:397-402; magnitudes beyond
+// 65504 become inf there as here); its codes enter as the fp16 number
+// 1 + q / 64 (bits 0x3C00 | q << 4, exact) and the epilogue adds
+// 64 s * acc + (b - 64 s) * sum a.
 //
 // K order inside one MFMA (16x16x32: lane l holds row/column l % 16 and 8
 // values at k-block l / 16): within a group, lane block q covers the 8*NU
@@ -45,6 +51,8 @@
 namespace smoe {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
@@ -114,6 +122,38 @@ __device__ __forceinline__ void split_f32(const float (&f)[8], u32x4& hi, u32x4&
 __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4 mfma_f16(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// Codes as fp16 for the down GEMM over fp16 activations: a code q enters as
+// 1 + q / 64 (bits 0x3C00 | q << 4, exact), same order as the bf16 forms.
+// The epilogue then adds 64 s * acc + (b - 64 s) * sum a.
+__device__ __forceinline__ u32x4 codes_f16_4p(uint32_t d) {
+  const uint32_t c3c = 0x3C3C3C3Cu;
+  const uint32_t lo = (d << 4) & 0xF0F0F0F0u;  // q0, q2, q4, q6 in bits 4-7
+  const uint32_t hi = d & 0xF0F0F0F0u;         // q1, q3, q5, q7 in bits 4-7
+  u32x4 r;
+  r.x = __builtin_amdgcn_perm(c3c, lo, 0x04020400u);  // (q0, q4)
+  r.y = __builtin_amdgcn_perm(c3c, hi, 0x04020400u);  // (q1, q5)
+  r.z = __builtin_amdgcn_perm(c3c, lo, 0x04030401u);  // (q2, q6)
+  r.w = __builtin_amdgcn_perm(c3c, hi, 0x04030401u);  // (q3, q7)
+  return r;
+}
+
+__device__ __forceinline__ u32x4 codes_f16_3(uint32_t p) {
+  const uint32_t t = (p & 0x3Fu) | ((p & 0xFC0u) << 2) | ((p & 0x3F000u) << 4) | ((p & 0xFC0000u) << 6);
+  const uint32_t lo = (t << 4) & 0x70707070u;  // [c0, c2, c4, c6] in bits 4-6
+  const uint32_t hi = (t << 1) & 0x70707070u;  // [c1, c3, c5, c7] in bits 4-6
+  u32x4 r;
+  r.x = (lo & 0x00FF00FFu) | 0x3C003C00u;         // (c0, c4)
+  r.y = (hi & 0x00FF00FFu) | 0x3C003C00u;         // (c1, c5)
+  r.z = ((lo >> 8) & 0x00FF00FFu) | 0x3C003C00u;  // (c2, c6)
+  r.w = ((hi >> 8) & 0x00FF00FFu) | 0x3C003C00u;  // (c3, c7)
+  return r;
 }
 
 template <int BITS>
@@ -416,6 +456,9 @@ struct PfMM {
   static constexpr int CG = KC / G;                   // groups per chunk
   static constexpr int CGW = CG / 2;                  // groups per wave (its K half of the chunk)
   static constexpr int NU = G / 32;                   // MFMA steps per group
+  // MODE 0: gate/up (bf16 x, or hi + lo); MODE 1: down over bf16 hi + lo
+  // A rows (the dense qmm); MODE 2: down over fp16 activations (SPLIT false).
+  static constexpr bool F16 = MODE == 2;
   static constexpr int NMAT = MODE == 0 ? 2 : 1;      // weight matrices per column
   static constexpr int CT = MODE == 0 ? 1 : 4;        // 16-column tiles per wave
   static constexpr int NCOL = 64 * CT;                // output columns per unit
@@ -481,6 +524,7 @@ struct PfMM {
   static_assert(N_A * NW * 64 == P_A && P_A == 16 * 64, "one row pair per A copy");
   static_assert((S - 2) * D + DU <= 63, "vmcnt range");
   static_assert(NWD == 0 || (MODE == 0 && USB), "copy waves: unit-staged gate/up only");
+  static_assert(!F16 || !SPLIT, "fp16 activations are one half");
   static_assert(LDS <= 160 * 1024, "LDS per CU");
   static_assert(4 * NT * 64 * 4 <= STAGE, "accumulator exchange fits a stage");
 
@@ -556,7 +600,8 @@ __device__ __forceinline__ void pf_chunk_seq(const uint8_t* st, const uint8_t* s
         // groups start at gofs.
         const uint16_t* sb = reinterpret_cast<const uint16_t*>(sbb + row * C::SB_ROW) + gofs;
         s[mt][ct] = bf16f(sb[gl]);
-        cbias[mt][ct] = __builtin_fmaf(-128.0f, s[mt][ct], bf16f(sb[C::NGU + gl]));
+        cbias[mt][ct] = __builtin_fmaf(C::F16 ? -64.0f : -128.0f, s[mt][ct], bf16f(sb[C::NGU + gl]));
+        if (C::F16) s[mt][ct] *= 64.0f;
       }
     u32x4 bq[C::NMAT][C::CT][C::NU];
 #pragma unroll
@@ -564,8 +609,12 @@ __device__ __forceinline__ void pf_chunk_seq(const uint8_t* st, const uint8_t* s
 #pragma unroll
       for (int ct = 0; ct < C::CT; ++ct)
 #pragma unroll
-        for (int uu = 0; uu < C::NU; ++uu)
-          bq[mt][ct][uu] = BITS == 4 ? codes_bf16_4p(bw[mt][ct][uu], c43) : codes_bf16_3(bw[mt][ct][uu]);
+        for (int uu = 0; uu < C::NU; ++uu) {
+          if constexpr (C::F16)
+            bq[mt][ct][uu] = BITS == 4 ? codes_f16_4p(bw[mt][ct][uu]) : codes_f16_3(bw[mt][ct][uu]);
+          else
+            bq[mt][ct][uu] = BITS == 4 ? codes_bf16_4p(bw[mt][ct][uu], c43) : codes_bf16_3(bw[mt][ct][uu]);
+        }
 #pragma unroll
     for (int t = 0; t < NTL; ++t) {
       f32x4 acc[C::NMAT][C::CT];
@@ -584,8 +633,12 @@ __device__ __forceinline__ void pf_chunk_seq(const uint8_t* st, const uint8_t* s
         for (int mt = 0; mt < C::NMAT; ++mt)
 #pragma unroll
           for (int ct = 0; ct < C::CT; ++ct) {
-            acc[mt][ct] = mfma(ah, bq[mt][ct][uu], acc[mt][ct]);
-            if (SPLIT) acc[mt][ct] = mfma(al, bq[mt][ct][uu], acc[mt][ct]);
+            if constexpr (C::F16) {
+              acc[mt][ct] = mfma_f16(ah, bq[mt][ct][uu], acc[mt][ct]);
+            } else {
+              acc[mt][ct] = mfma(ah, bq[mt][ct][uu], acc[mt][ct]);
+              if (SPLIT) acc[mt][ct] = mfma(al, bq[mt][ct][uu], acc[mt][ct]);
+            }
           }
       }
       // Group sums of rows 16t + 4q .. + 3: one read from the stage
@@ -824,7 +877,6 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
   const uint32_t* const item_tok = a.item_tok;
   const uint64_t stride = a.stride;
   uint16_t* const act_hi = a.act_hi;
-  uint16_t* const act_lo = a.act_lo;
   float* const down = a.down;
   float* const asum_out = a.asum;
   const uint64_t wo0 = a.g.w[MODE == 0 ? 0 : 2], wo1 = a.g.w[MODE == 0 ? 1 : 2];
@@ -1153,7 +1205,7 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
       asm volatile("" ::: "memory");
       if (computer && kh == 0) {
         const uint32_t ntiles = cnt > 16 ? 2 : 1;
-        float hl[2][4] = {};  // gate/up: hi + lo of this lane's activation, rows 16 t + 4 q + r
+        float hl[2][4] = {};  // gate/up: this lane's fp16 activation, rows 16 t + 4 q + r
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
           if ((uint32_t)t >= ntiles) continue;
@@ -1169,14 +1221,13 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
               if (m >= cnt) continue;
               const uint32_t colj = cb * C::NCOL + cw * 16 * C::CT + ct * 16 + n;
               if constexpr (MODE == 0) {
-                // act as bf16 hi + lo in the MFMA order of the down GEMM.
+                // act as fp16 (round to nearest even) in the MFMA order of
+                // the down GEMM.
                 const float v = silu_mul(o[0], o[1]);
-                const uint32_t hi = pk_bf16(v, 0.f) & 0xFFFFu;
-                const uint32_t lo = pk_bf16(v - __uint_as_float(hi << 16), 0.f) & 0xFFFFu;
+                const _Float16 h = (_Float16)v;
                 const size_t at = (size_t)(start + m) * N + (colj & ~7u) + perm8_pos(colj & 7u);
-                act_hi[at] = (uint16_t)hi;
-                act_lo[at] = (uint16_t)lo;
-                hl[t][r] = __uint_as_float(hi << 16) + __uint_as_float(lo << 16);
+                act_hi[at] = __builtin_bit_cast(uint16_t, h);
+                hl[t][r] = (float)h;
               } else {
                 down[(size_t)(start + m) * N + colj] = o[0];
               }
@@ -1184,7 +1235,7 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
           }
         }
         // Gate/up with G <= 64: the down GEMM's activation group sums (over
-        // what its MFMAs see, hi + lo), for the 64 / G groups of this unit's
+        // what its MFMAs see, the fp16 values), for the 64 / G groups of this unit's
         // 64 columns: each column wave sums its 16 columns per row (the
         // lanes of a 16-lane row); wave 0 adds the column waves of a group
         // after the next block barrier (flush_asum).
@@ -1222,19 +1273,19 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
   }
 }
 
-// Group sums of the activations (hi + lo) per entry; one block per entry.
+// Group sums of the fp16 activations per entry; one block per entry.
 __global__ __launch_bounds__(256) void k_pf_act_sum(PfArgs a) {
   __shared__ float part8[kPfMaxGroupsK * 128 / 8];
   const uint32_t r = blockIdx.x, I = a.g.inter, G = a.g.group;
   for (uint32_t k0 = threadIdx.x * 8; k0 < I; k0 += blockDim.x * 8) {
     const u32x4 h = *reinterpret_cast<const u32x4*>(a.act_hi + (size_t)r * I + k0);
-    const u32x4 l = *reinterpret_cast<const u32x4*>(a.act_lo + (size_t)r * I + k0);
-    const uint32_t hv[4] = {h.x, h.y, h.z, h.w}, lv[4] = {l.x, l.y, l.z, l.w};
+    const uint32_t hv[4] = {h.x, h.y, h.z, h.w};
     float p = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      p += __uint_as_float(hv[i] << 16) + __uint_as_float(hv[i] & 0xFFFF0000u) + __uint_as_float(lv[i] << 16) +
-           __uint_as_float(lv[i] & 0xFFFF0000u);
+    for (int i = 0; i < 4; ++i) {
+      const f32x2 f = __builtin_convertvector(__builtin_bit_cast(f16x2, hv[i]), f32x2);
+      p += f.x + f.y;
+    }
     part8[k0 / 8] = p;
   }
   __syncthreads();
@@ -1309,7 +1360,6 @@ uint64_t prefill_workspace(uint32_t hidden, uint32_t inter, uint32_t group, uint
   uint8_t* p_xhi = take((uint64_t)n_tokens * hidden * 2);
   uint8_t* p_xlo = take((uint64_t)n_tokens * hidden * 2);
   uint8_t* p_ahi = take(nk * inter * 2);
-  uint8_t* p_alo = take(nk * inter * 2);
   uint8_t* p_down = take(nk * hidden * 4);
   if (a) {
     a->items = reinterpret_cast<uint32_t*>(p_items);
@@ -1322,7 +1372,7 @@ uint64_t prefill_workspace(uint32_t hidden, uint32_t inter, uint32_t group, uint
     a->x_hi = reinterpret_cast<uint16_t*>(p_xhi);
     a->x_lo = reinterpret_cast<uint16_t*>(p_xlo);
     a->act_hi = reinterpret_cast<uint16_t*>(p_ahi);
-    a->act_lo = reinterpret_cast<uint16_t*>(p_alo);
+    a->act_lo = nullptr;
     a->down = reinterpret_cast<float*>(p_down);
     a->max_items = (uint32_t)max_items;
   }
@@ -1372,8 +1422,8 @@ static hipError_t launch_gemms(const PfArgs& a, uint32_t n_cu, hipStream_t st) {
   // With G <= 64 the gate/up GEMM writes the activation group sums itself.
   if (G > 64) hipLaunchKernelGGL(k_pf_act_sum, dim3(a.n_tokens * a.k), dim3(256), 0, st, a);
   const uint32_t dn_units = a.max_items * (a.g.hidden / 256);
-  if (G == 64 && a.g.inter == 512) return launch_mm<BITS, G, 1, true, G == 64 ? 512 : 0>(a, dn_units, n_cu, st);
-  return launch_mm<BITS, G, 1, true, 0>(a, dn_units, n_cu, st);
+  if (G == 64 && a.g.inter == 512) return launch_mm<BITS, G, 2, false, G == 64 ? 512 : 0>(a, dn_units, n_cu, st);
+  return launch_mm<BITS, G, 2, false, 0>(a, dn_units, n_cu, st);
 }
 
 hipError_t launch_prefill(const PfArgs& a, uint32_t n_cu, hipStream_t st) {
