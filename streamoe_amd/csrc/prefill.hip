@@ -382,10 +382,9 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
       a.items[2 * (ibase + c)] = tid;
       a.items[2 * (ibase + c) + 1] = (off + c * kPfMC) | (min(kPfMC, cnt - c * kPfMC) << 16);
     }
-    // Rows past the count of the expert's last item read token 0's x (their
-    // results are dropped).
-    if (cnt % kPfMC)
-      for (uint32_t m = cnt % kPfMC; m < kPfMC; ++m) a.item_tok[(ibase + nch - 1) * kPfMC + m] = 0u;
+    // Rows past the count of the expert's last item are not written: the
+    // GEMM clamps whatever they hold to a token id (their results are
+    // dropped).
   }
   // Every entry places itself: position = the expert's offset + the tokens
   // before t that chose the same expert (its row in the expert's items);
@@ -875,6 +874,7 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
   const float* const gsum = MODE == 0 ? a.xsum : a.asum;
   const uint8_t* const experts = a.experts;
   const uint32_t* const item_tok = a.item_tok;
+  const uint32_t last_tok = a.n_tokens - 1;
   const uint64_t stride = a.stride;
   uint16_t* const act_hi = a.act_hi;
   float* const down = a.down;
@@ -950,16 +950,16 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
   };
   // Per-lane byte offsets of one unit's A rows (row pair (dw N_A + i,
   // + 16)) and group-sum rows from its row base: gate/up by the token ids in
-  // token buffer `par` (rows past the count hold token 0), down by the entry
-  // row (rows past the count repeat the last one). Results of rows past the
-  // count are never stored.
+  // token buffer `par` (rows past the count hold any value: clamped to a
+  // token id), down by the entry row (rows past the count repeat the last
+  // one). Results of rows past the count are never stored.
   struct UnitRows {
     uint32_t a[C::N_A];
     uint32_t x[C::NXR > 0 ? C::NXR : 1];
   };
   auto unit_rows = [=](const UnitSrc& u, uint32_t par) {
     const uint32_t* tb = reinterpret_cast<const uint32_t*>(lds + C::OFF_TOK) + par * kPfMC;
-    auto row = [&](uint32_t m) { return C::GATHER ? tb[m] : min(m, u.cnt - 1); };
+    auto row = [&](uint32_t m) { return C::GATHER ? min(tb[m], last_tok) : min(m, u.cnt - 1); };
     UnitRows r;
 #pragma unroll
     for (int i = 0; i < C::N_A; ++i) r.a[i] = row(dw * C::N_A + i + 16 * (lane >> 5)) * K * 2;
