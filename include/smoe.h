@@ -315,17 +315,17 @@ int smoe_moe_decode_layers_noalloc(void* stream, const smoe_layer* layers, uint3
                                    const void* const* norm_w, float eps, const float* input,
                                    float* residual_io);
 
-/* Several decode tokens (1..4; 1..2 at hidden 4096) through the same
- * layers at once, each as smoe_moe_decode_layers would decode it alone
- * (own routing, experts, combine and chained RMSNorm; bit-identical to
- * that): input,
- * residual_io and work are [n_tokens, hidden] rows (16-byte aligned).
- * Every layer is still three launches: the router and shared-expert rows
- * are read once for all tokens and each token's routed experts run side
- * by side in the same grids. idx_out / w_out (nullable): [n_tokens, k] of the last
- * layer in the reference's slot order. Replaces the T-token pass of
- * decode_multi.rs (moe_dispatch_multi, 445-654). Three-kernel shapes only,
- * and n_tokens <= 2 at hidden 4096 (else SMOE_ERR_UNSUPPORTED_SHAPE). */
+/* Several decode tokens (1..4) through the same layers at once, each as
+ * smoe_moe_decode_layers would decode it alone (own routing, experts,
+ * combine and chained RMSNorm; bit-identical to that): input, residual_io
+ * and work are [n_tokens, hidden] rows (16-byte aligned). Every layer is
+ * still three launches: the router and shared-expert rows are read once
+ * for all tokens and each token's routed experts run side by side in the
+ * same grids. idx_out / w_out (nullable): [n_tokens, k] of the last layer
+ * in the reference's slot order. Replaces the T-token pass of
+ * decode_multi.rs (moe_dispatch_multi, 445-654). Three-kernel shapes only
+ * (else SMOE_ERR_UNSUPPORTED_SHAPE); at hidden 4096, 3 or 4 tokens take a
+ * fourth launch per layer (the router kernel in two halves). */
 int smoe_moe_decode_tokens(smoe_handle* h, const smoe_layer* layers, uint32_t n_layers,
                            const void* const* norm_w, float eps, uint32_t n_tokens, const float* input,
                            float* residual_io, float* work, int32_t* idx_out, float* w_out);

@@ -656,8 +656,7 @@ int smoe_moe_decode_tokens(smoe_handle* h, const smoe_layer* layers, uint32_t n_
     if (int rc = check_layer(h, &layers[l])) return rc;
     if (layers[l].shape.hidden != layers[0].shape.hidden) return SMOE_ERR_INVALID_ARG;
     if (norm_w && l > 0 && !norm_w[l]) return SMOE_ERR_INVALID_ARG;
-    if (!fused_ok(&layers[l]) || n_tokens > fused_max_tokens(layers[l].shape.hidden))
-      return SMOE_ERR_UNSUPPORTED_SHAPE;
+    if (!fused_ok(&layers[l])) return SMOE_ERR_UNSUPPORTED_SHAPE;
   }
   if (!aligned(input, 0, 16) || !aligned(residual_io, 0, 16) || !aligned(work, 0, 16))
     return SMOE_ERR_MISALIGNED;

@@ -192,7 +192,7 @@ __device__ __forceinline__ void store_limbs_quad(uint32_t* dst, const float (&x)
 // per-token pointer moved to token t's rows. Branch-free (selects), so it
 // adds no branch level in front of the first loads.
 template <int HC>
-__device__ __forceinline__ FusedLayer token_view(const FusedLayer& a, uint32_t t) {
+__host__ __device__ __forceinline__ FusedLayer token_view(const FusedLayer& a, uint32_t t) {
   FusedLayer b = a;
   const size_t hs = (size_t)t * HC * kFaH;
   b.x_in = a.x_in ? a.x_in + hs : nullptr;
@@ -786,11 +786,20 @@ static hipError_t launch_down_fa(const FusedLayer& a, hipStream_t st) {
                                      : launch_down_fa_h<BITS, LI, 1, HC>(a, st);
 }
 
-uint32_t fused_max_tokens(uint32_t hidden) { return hidden == kFaH ? kMaxDecodeTokens : kFaMaxTokensH2; }
-
+// K_A over a.n_tokens tokens. At hidden 4096 a router wave holds two
+// tokens' x at most (289 VGPRs), so 3 or 4 tokens take two launches of 2
+// and n - 2 tokens (the router rows are read twice, from the memory-side
+// cache the second time).
 template <int HC>
-static hipError_t launch_fused_layer_h(const FusedLayer& a, hipStream_t st) {
-  const uint32_t I = a.routed.inter;
+static void launch_route_fa(const FusedLayer& a, hipStream_t st) {
+  if (HC == 2 && a.n_tokens > 2) {
+    FusedLayer lo = a, hi = token_view<HC>(a, 2);
+    lo.n_tokens = 2;
+    hi.n_tokens = a.n_tokens - 2;
+    launch_route_fa<HC>(lo, st);
+    launch_route_fa<HC>(hi, st);
+    return;
+  }
   const uint32_t ka = a.E + 4u * HC * a.n_tokens;
   switch (a.n_tokens) {
     case 1: hipLaunchKernelGGL((k_fa_route<1, HC>), dim3(ka), dim3(64), 0, st, a); break;
@@ -802,6 +811,12 @@ static hipError_t launch_fused_layer_h(const FusedLayer& a, hipStream_t st) {
       if constexpr (HC == 1) hipLaunchKernelGGL((k_fa_route<4, HC>), dim3(ka), dim3(64), 0, st, a);
       break;
   }
+}
+
+template <int HC>
+static hipError_t launch_fused_layer_h(const FusedLayer& a, hipStream_t st) {
+  const uint32_t I = a.routed.inter;
+  launch_route_fa<HC>(a, st);
   const uint32_t kb = (a.k + (a.shared ? 1u : 0u)) * (I / kFaRW) + 1u;
   if (a.routed.bits == 4)
     launch_gateup_fa<4, HC>(a, kb, st);
@@ -818,7 +833,7 @@ static hipError_t launch_fused_layer_h(const FusedLayer& a, hipStream_t st) {
 
 hipError_t launch_fused_layer(const FusedLayer& a, hipStream_t st) {
   const uint32_t H = a.hidden;
-  if ((H != kFaH && H != 2 * kFaH) || a.n_tokens < 1 || a.n_tokens > fused_max_tokens(H) ||
+  if ((H != kFaH && H != 2 * kFaH) || a.n_tokens < 1 || a.n_tokens > kMaxDecodeTokens ||
       (a.trace && a.n_tokens != 1))
     return hipErrorInvalidValue;
   return H == kFaH ? launch_fused_layer_h<1>(a, st) : launch_fused_layer_h<2>(a, st);

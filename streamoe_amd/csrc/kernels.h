@@ -85,7 +85,6 @@ struct FusedLayer {
 };
 
 constexpr uint32_t kMaxDecodeTokens = 4;  // tokens per multi-token decode call
-constexpr uint32_t kFaMaxTokensH2 = 2;    // the same at hidden 4096 (the router kernel's registers)
 
 // Trace layout of the three-kernel path: per layer kFaTraceLayer words;
 // kernel q (0 route, 1 gate/up, 2 down), block b at
@@ -105,7 +104,6 @@ inline uint32_t logit_stride(uint32_t E) {
 }
 bool fused_supported(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t bits,
                      uint32_t n_experts, uint32_t k);
-uint32_t fused_max_tokens(uint32_t hidden);  // tokens per multi-token call at this hidden size
 // K_A (router + shared gate/up), K_B (top-k + routed gate/up), K_C (down +
 // combine) on `st`; no allocation, no memset (graph-capturable).
 hipError_t launch_fused_layer(const FusedLayer& a, hipStream_t st);

@@ -101,10 +101,12 @@ def test_noalloc_decode_argument_errors():
     x = torch.zeros(2048, dtype=torch.float32, device="cuda")
     nw = torch.zeros(2048, dtype=torch.int16, device="cuda")
     ok = sa.Kernels.layer(lay, buf, lay.expert_size, 8, 2, True, r)
-    # hidden 4096 has no three-kernel instance
-    lay4k = sa.ExpertLayout(4096, 512, 4, 64)
-    big = sa.Kernels.layer(lay4k, buf, lay4k.expert_size, 8, 2, True, r)
-    assert _noalloc(sa, torch, [big], [nw], x, x) == _abi.CODES["SMOE_ERR_UNSUPPORTED_SHAPE"]
+    # Hidden 1024 has no three-kernel instance: rejected before any launch
+    # (the buffers below would be too small for a launch at that shape).
+    lay1k = sa.ExpertLayout(1024, 512, 4, 64)
+    r1k = torch.zeros((8, 1024), dtype=torch.float32, device="cuda")
+    small = sa.Kernels.layer(lay1k, buf, lay1k.expert_size, 8, 2, True, r1k)
+    assert _noalloc(sa, torch, [small], [nw], x, x) == _abi.CODES["SMOE_ERR_UNSUPPORTED_SHAPE"]
     assert _noalloc(sa, torch, [ok], [nw], x[1:], x) == _abi.CODES["SMOE_ERR_MISALIGNED"]
     assert sa._lib.smoe_moe_decode_layers_noalloc(None, None, 0, None, C.c_float(0), None, None) == \
         _abi.CODES["SMOE_ERR_INVALID_ARG"]
