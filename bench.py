@@ -13,8 +13,9 @@ HIP graph (default) or one kernel per phase (--path kernels).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2]
 
---config c0/c3 run the other decode shapes, c1 the LM head and c4 the
-512-token prefill layer, each with its own JSON line.
+--config c0/c3 run the other decode shapes, c1 the LM head, c4 the
+512-token prefill layer and c5 the hidden-4096 decode shape (not a
+BASELINE config), each with its own JSON line.
 
 Prints one JSON line. value = µs per layer (lower is better); the
 roofline object gives achieved HBM GB/s from the algorithmic bytes.
@@ -57,12 +58,12 @@ CONFIGS = {
 
 # HBM bytes actually moved per unit of work, from rocprofv3 FETCH_SIZE and
 # WRITE_SIZE passes scaled by a 256 MiB copy calibration (FETCH x 2.0,
-# WRITE x 1.0): profiles/decode_c{0,2,3}_*.md (one layer = the three k_fa_*
+# WRITE x 1.0): profiles/decode_c{0,2,3,5}_*.md (one layer = the three k_fa_*
 # launches), profiles/lm_head_c1_qmv_argmax.md (k_qmv + argmax) and
 # profiles/prefill_c4_a3b_4bit.md (the four prefill launches of one layer).
 # None where no counter pass was taken (multi-token decode, per-phase path).
-MEASURED_TRAFFIC = {"c0": 29_745_023, "c2": 18_873_238, "c3": 15_771_620, "c1": 175_934_641,
-                    "c4": 562_582_175}
+MEASURED_TRAFFIC = {"c0": 29_749_910, "c2": 18_883_732, "c3": 15_758_605, "c1": 175_938_018,
+                    "c4": 554_026_850, "c5": 87_750_848}
 
 
 def stream_read_peak(dev, gib=4):
