@@ -75,10 +75,11 @@ def boundary_logits(E, k, kind, first, second, rng):
     return out
 
 
-def _layer(kernels, logits, k, normalize, shared, seed, inter=512, bits=4):
+def _layer(kernels, logits, k, normalize, shared, seed, inter=512, bits=4, hid=H):
     import streamoe_amd as sa
 
     torch = _torch()
+    H = hid
     E = logits.size
     lay = sa.ExpertLayout(H, inter, bits, 64)
     arena = torch.empty(E * lay.expert_size, dtype=torch.uint8, device="cuda")
@@ -95,11 +96,11 @@ def _layer(kernels, logits, k, normalize, shared, seed, inter=512, bits=4):
     r_dev = _dev(router)
     L = kernels.layer(lay, arena, lay.expert_size, E, k, normalize, r_dev, sh, gate)
     return dict(L=L, arena=arena, router=router, r_dev=r_dev, sh=sh, gate=gate, lay=lay, E=E, k=k,
-                normalize=normalize, bits=bits, inter=inter)
+                normalize=normalize, bits=bits, inter=inter, H=H)
 
 
 def _oracle(c, x, h_mid):
-    return oracle.moe_decode_layer(_host(c["arena"]), c["lay"].expert_size, H, c["inter"], c["E"], c["k"], 64,
+    return oracle.moe_decode_layer(_host(c["arena"]), c["lay"].expert_size, c["H"], c["inter"], c["E"], c["k"], 64,
                                    c["bits"], c["normalize"], c["router"], x, h_mid,
                                    None if c["sh"] is None else _host(c["sh"]),
                                    None if c["gate"] is None else _host(c["gate"]))
@@ -119,13 +120,25 @@ CASES = [
 CASE_IDS = [f"{c[0]}-E{c[1]}-k{c[2]}-{c[3]}-{c[4]}" for c in CASES]
 
 
+CASES_4096 = [
+    # hidden 4096, the Qwen3.5-397B-A17B router width (512 experts, top-10)
+    ("tie", 512, 10, 300, 17),
+    ("tie3", 512, 10, 8, 400),
+    ("margin", 512, 10, 250, 251),
+    ("nan", 512, 10, 5, 6),
+]
+
+
 @pytest.mark.parametrize("path", [1, 3], ids=["per-phase", "three-kernel"])
-@pytest.mark.parametrize("kind,E,k,first,second", CASES, ids=CASE_IDS)
-def test_decode_layer_routing_boundary(kernels, path, kind, E, k, first, second):
+@pytest.mark.parametrize("kind,E,k,first,second,hid",
+                         [c + (2048,) for c in CASES] + [c + (4096,) for c in CASES_4096],
+                         ids=CASE_IDS + [f"h4096-{c[0]}-E{c[1]}-k{c[2]}-{c[3]}-{c[4]}" for c in CASES_4096])
+def test_decode_layer_routing_boundary(kernels, path, kind, E, k, first, second, hid):
     torch = _torch()
+    H = hid
     rng = np.random.default_rng(E * 1000 + first * 7 + second)
     logits = boundary_logits(E, k, kind, first, second, rng)
-    c = _layer(kernels, logits, k, True, True, seed=first * 31 + second)
+    c = _layer(kernels, logits, k, True, True, seed=first * 31 + second, hid=H)
     x = rng.standard_normal(H).astype(np.float32)
     x[0] = 1.0
     h_mid = rng.standard_normal(H).astype(np.float32)
@@ -196,14 +209,15 @@ def outlier_x(rng, n):
 
 
 @pytest.mark.parametrize("path", [1, 3], ids=["per-phase", "three-kernel"])
-@pytest.mark.parametrize("bits", [4, 3])
-def test_decode_layer_outlier_activations(kernels, path, bits):
-    """C2 layer (256 experts, top-8, shared expert) on outlier activations."""
+@pytest.mark.parametrize("bits,H", [(4, 2048), (3, 2048), (4, 4096)], ids=["4bit", "3bit", "4bit-h4096"])
+def test_decode_layer_outlier_activations(kernels, path, bits, H):
+    """C2 layer (256 experts, top-8, shared expert) on outlier activations;
+    the same at hidden 4096 (two 32-value chunks per lane)."""
     import streamoe_amd as sa
 
     torch = _torch()
     E, k = 256, 8
-    rng = np.random.default_rng(900 + bits)
+    rng = np.random.default_rng(900 + bits + H)
     lay = sa.ExpertLayout(H, 512, bits, 64)
     slay = sa.ExpertLayout(H, 512, 4, 64)
     arena = torch.empty(E * lay.expert_size, dtype=torch.uint8, device="cuda")
