@@ -14,11 +14,10 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 
-def _layers(torch, sa, n_layers, E, k, inter, seed):
+def _layers(torch, sa, n_layers, E, k, inter, seed, H=2048):
     """n_layers resident layers generated with torch on the device: 4-bit
     codes uniform, bf16 scales |N(0, .02)| and biases N(0, .01), f32 router
     N(0, .02), a 4-bit shared expert with an f32 gate, bf16 norm weights."""
-    H = 2048
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
     lay = sa.ExpertLayout(H, inter, 4, 64)
@@ -87,6 +86,32 @@ def test_noalloc_decode_matches_handle_decode_twice():
             print(f"case {case}: bit-identical, max|resid| {np.max(np.abs(a)):.3f}")
     finally:
         kern.close()
+
+
+def test_noalloc_decode_hidden_4096():
+    """Two Qwen3.5-397B-A17B-shaped layers (hidden 4096, 512 experts, top-10,
+    inter 1024): the fixed scratch holds them, and the result equals the
+    handle path's bit for bit."""
+    import torch
+
+    import streamoe_amd as sa
+
+    layers, norms, x0, keep = _layers(torch, sa, 2, 512, 10, 1024, 13, H=4096)
+    resid = x0.clone()
+    print("noalloc call: hidden 4096", flush=True)
+    assert _noalloc(sa, torch, layers, norms, x0, resid) == 0
+    torch.cuda.synchronize()
+    kern = sa.Kernels(0)
+    try:
+        r2 = x0.clone()
+        assert kern.moe_decode_layers(layers, norms, 1e-6, x0, r2, torch.empty_like(x0)) == 0
+        kern.sync()
+        a, b = resid.cpu().numpy(), r2.cpu().numpy()
+        assert np.all(np.isfinite(a)) and np.any(a != x0.cpu().numpy())
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    finally:
+        kern.close()
+    del keep
 
 
 def test_noalloc_decode_argument_errors():
