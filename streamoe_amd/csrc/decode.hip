@@ -315,6 +315,10 @@ __global__ __launch_bounds__(1024) void k_argmax_final(const float* __restrict__
                                                        const float* __restrict__ v0, int32_t* __restrict__ out) {
   float best = -INFINITY;
   uint32_t bi = 0xFFFFFFFFu;
+  // v[0] is read with the partials, not after the block reduction: loads
+  // cannot move across its barriers, so a late read is one more memory
+  // round trip at the end of the launch.
+  const float first = *v0;
   // Four partials per thread per round, loaded before they are merged (the
   // merges form a dependency chain; the loads must not).
   for (uint32_t i0 = threadIdx.x; i0 < n; i0 += 4 * blockDim.x) {
@@ -330,10 +334,7 @@ __global__ __launch_bounds__(1024) void k_argmax_final(const float* __restrict__
     for (int j = 0; j < 4; ++j) argmax_merge(best, bi, v[j], ix[j]);
   }
   argmax_block(best, bi);
-  if (threadIdx.x == 0) {
-    const float first = *v0;
-    *out = first != first ? 0 : (int32_t)bi;
-  }
+  if (threadIdx.x == 0) *out = first != first ? 0 : (int32_t)bi;
 }
 
 hipError_t launch_argmax(const float* v, uint32_t n, int32_t* out, float* part_v, uint32_t* part_i,
