@@ -510,11 +510,19 @@ struct PfMM {
   // gathered from the per-token arrays), one buffer per unit parity.
   static constexpr bool GATHER = MODE == 0;
   static constexpr int OFF_TOK = OFF_PS + (ASUM ? 4 * kPfMC * 4 : 0);
-  static constexpr int LDS = OFF_TOK + (GATHER ? 2 * kPfMC * 4 : 0);
+  // Accumulators per lane, exchanged between the K halves at a unit's end:
+  // each half finishes rows r = 2 kh, 2 kh + 1 of every 4-row group and
+  // parks the other half's NT / 2 partial sums, in an area of its own when
+  // the LDS has room for it (then a unit end takes one block barrier), else
+  // in the stage just read (one more barrier, so that no wave still reads
+  // it).
+  static constexpr int NT = NMAT * CT * 2 * 4;
+  static constexpr int EX_BYTES = 4 * NT * 64 * 4;
+  static constexpr int OFF_EX = OFF_TOK + (GATHER ? 2 * kPfMC * 4 : 0);
+  static constexpr bool EXD = OFF_EX + EX_BYTES <= 160 * 1024;
+  static constexpr int LDS = OFF_EX + (EXD ? EX_BYTES : 0);
   // Per-lane row offsets of one unit's group-sum copies.
   static constexpr int NXR = USB ? N_UXS : N_XS;
-  // Accumulators per lane, exchanged between the K halves through LDS.
-  static constexpr int NT = NMAT * CT * 2 * 4;
   static_assert(CG % 2 == 0, "K halves");
   static_assert(P_BQ % NW == 0 && P_BS % NW == 0 && P_XS % NW == 0 && P_US % NW == 0 && P_UXS % NW == 0,
                 "equal shares");
@@ -525,7 +533,7 @@ struct PfMM {
   static_assert(NWD == 0 || (MODE == 0 && USB), "copy waves: unit-staged gate/up only");
   static_assert(!F16 || !SPLIT, "fp16 activations are one half");
   static_assert(LDS <= 160 * 1024, "LDS per CU");
-  static_assert(4 * NT * 64 * 4 <= STAGE, "accumulator exchange fits a stage");
+  static_assert(EXD || EX_BYTES <= STAGE, "accumulator exchange fits a stage");
 
   static_assert(!USB || (2 * NGU) % 16 == 0, "unit scale rows in 16-byte pieces");
 };
@@ -1184,13 +1192,19 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
         c_cnt = c_next >> 16;
         if (cv + per < group_units) c_next = item_words(cv + per).y;
       }
-      // Every wave is done reading this stage; the upper half parks its sums
-      // there ([column wave][accumulator][lane]) for the lower half.
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      __builtin_amdgcn_s_barrier();
-      asm volatile("" ::: "memory");
-      float* ex = reinterpret_cast<float*>(st) + cw * C::NT * 64 + lane;
-      if (computer && kh == 1) {
+      // The K halves swap the partial sums of the rows the other one
+      // finishes ([column wave][receiving half][accumulator][lane]).
+      if constexpr (!C::EXD) {
+        // In the stage just read: every wave must be done reading it.
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+      }
+      constexpr int NTH = C::NT / 2;
+      float* const exb = C::EXD ? reinterpret_cast<float*>(lds + C::OFF_EX) : reinterpret_cast<float*>(st);
+      if (computer) {
+        float* const xo = exb + (cw * 2 + (kh ^ 1u)) * NTH * 64 + lane;
+        const uint32_t rp = 2 * (kh ^ 1u);  // first row the other half finishes
 #pragma unroll
         for (int mt = 0; mt < C::NMAT; ++mt)
 #pragma unroll
@@ -1198,26 +1212,29 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
-              for (int r = 0; r < 4; ++r) ex[(((mt * C::CT + ct) * 2 + t) * 4 + r) * 64] = tot[mt][ct][t][r];
+              for (int rr = 0; rr < 2; ++rr)
+                xo[(((mt * C::CT + ct) * 2 + t) * 2 + rr) * 64] = rp ? tot[mt][ct][t][2 + rr] : tot[mt][ct][t][rr];
       }
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
-      if (computer && kh == 0) {
+      if (computer) {
+        const float* const xi = exb + (cw * 2 + kh) * NTH * 64 + lane;
         const uint32_t ntiles = cnt > 16 ? 2 : 1;
-        float hl[2][4] = {};  // gate/up: this lane's fp16 activation, rows 16 t + 4 q + r
+        float hl[2][2] = {};  // gate/up: this lane's fp16 activation, rows 16 t + 4 q + 2 kh + rr
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
           if ((uint32_t)t >= ntiles) continue;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const uint32_t m = 16 * t + 4 * q + r;
+          for (int rr = 0; rr < 2; ++rr) {
+            const uint32_t m = 16 * t + 4 * q + 2 * kh + rr;
 #pragma unroll
             for (int ct = 0; ct < C::CT; ++ct) {
               float o[C::NMAT];
 #pragma unroll
               for (int mt = 0; mt < C::NMAT; ++mt)
-                o[mt] = tot[mt][ct][t][r] + ex[(((mt * C::CT + ct) * 2 + t) * 4 + r) * 64];
+                o[mt] = (kh ? tot[mt][ct][t][2 + rr] : tot[mt][ct][t][rr]) +
+                        xi[(((mt * C::CT + ct) * 2 + t) * 2 + rr) * 64];
               if (m >= cnt) continue;
               const uint32_t colj = cb * C::NCOL + cw * 16 * C::CT + ct * 16 + n;
               if constexpr (MODE == 0) {
@@ -1227,7 +1244,7 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
                 const _Float16 h = (_Float16)v;
                 const size_t at = (size_t)(start + m) * N + (colj & ~7u) + perm8_pos(colj & 7u);
                 act_hi[at] = __builtin_bit_cast(uint16_t, h);
-                hl[t][r] = (float)h;
+                hl[t][rr] = (float)h;
               } else {
                 down[(size_t)(start + m) * N + colj] = o[0];
               }
@@ -1235,18 +1252,18 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
           }
         }
         // Gate/up with G <= 64: the down GEMM's activation group sums (over
-        // what its MFMAs see, the fp16 values), for the 64 / G groups of this unit's
-        // 64 columns: each column wave sums its 16 columns per row (the
-        // lanes of a 16-lane row); wave 0 adds the column waves of a group
-        // after the next block barrier (flush_asum).
+        // what its MFMAs see, the fp16 values), for the 64 / G groups of this
+        // unit's 64 columns: each column wave sums its 16 columns per row
+        // (the lanes of a 16-lane row); wave 0 adds the column waves of a
+        // group after the next block barrier (flush_asum).
         if constexpr (C::ASUM) {
           float* ps = reinterpret_cast<float*>(lds + C::OFF_PS);
 #pragma unroll
           for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const float rs = row_sum16_all(hl[t][r]);
-              if (n == 0) ps[cw * kPfMC + 16 * t + 4 * q + r] = rs;
+            for (int rr = 0; rr < 2; ++rr) {
+              const float rs = row_sum16_all(hl[t][rr]);
+              if (n == 0) ps[cw * kPfMC + 16 * t + 4 * q + 2 * kh + rr] = rs;
             }
         }
       }
