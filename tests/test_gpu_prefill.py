@@ -78,6 +78,7 @@ def _case(kernels, n_tokens, H, I, E, k, bits, group, x_bf16, seed, routing="zip
     ("e512-k10", 256, 2048, 512, 512, 10, 4, 64, True, "zipf"),  # 512 experts, top-10
     ("max-e512-n1024", 1024, 2048, 512, 512, 10, 4, 64, True, "zipf"),  # largest bucketing bitmaps
     ("e512-f32-x", 64, 1024, 512, 512, 10, 3, 32, False, "zipf"),
+    ("h4096-q397b", 64, 4096, 1024, 512, 10, 4, 64, True, "zipf"),  # Qwen3.5-397B-A17B layer shape
 ])
 def test_prefill_matches_oracle(kernels, name, n, H, I, E, k, bits, group, x_bf16, routing):
     got, want, _ = _case(kernels, n, H, I, E, k, bits, group, x_bf16, seed=sum(map(ord, name)), routing=routing)
