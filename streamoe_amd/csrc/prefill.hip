@@ -1155,9 +1155,9 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
         iub ^= 1u;
         iv += per;
         if (iv < group_units) {
-        isrc = unit_src(iv, inext);
-        if (iv + per < group_units) inext = item_words(iv + per);
-      }
+          isrc = unit_src(iv, inext);
+          if (iv + per < group_units) inext = item_words(iv + per);
+        }
       }
     }
     // The row sums are read before the next unit end writes them again:
