@@ -13,11 +13,12 @@
 // computes in every wave.
 //
 // With T <= 4 tokens (multi-token decode), K_A reads each router row once
-// for all T tokens, and K_B / K_C run one grid slice per token (grid
-// dimension y).
+// for all T tokens (at hidden 4096, once per pair of tokens), and K_B / K_C
+// run one grid slice per token (grid dimension y). Hidden 2048 or 4096: a
+// lane holds HC = hidden / 2048 chunks of 32 values of every row it reads.
 //
 //   K_A  k_fa_route    one wave per router row: x = RMSNorm(r) * w (or the
-//                      given input), logits[e] = W_e . x; four more waves
+//                      given input), logits[e] = W_e . x; 4 HC more waves
 //                      per token store x as integer limbs for K_B
 //                      (common.h, chunk_dot_i).
 //   K_B  k_fa_gateup   one wave per RW rows of one routed slot: the slot's
@@ -38,9 +39,9 @@
 // Weights are read exactly once per token with 128-bit (4-bit) or 96-bit
 // (3-bit) loads: non-temporal for the routed experts, temporal for the
 // router rows and the shared expert (reused by every token, they stay in
-// the memory-side cache); x limbs and logits (<= 10 KB) are re-read from
+// the memory-side cache); x limbs and logits (<= 18 KB) are re-read from
 // L2 by every wave that needs them, and each K_C block stages the
-// activations (<= 68 KB) in LDS once.
+// activations (<= 78 KB) in LDS once.
 #include "common.h"
 #include "kernels.h"
 #include "topk.h"
