@@ -131,6 +131,8 @@ typedef struct {
 
 /* y[r] = sum_c (q[r,c] * s[r,c/g] + b[r,c/g]) * x[c] for r < out_dim,
  * fp32 accumulation. x: device f32[in_dim]; y: device f32[out_dim].
+ * in_dim: a multiple of the group, up to 8192 (as the reference's qmv,
+ * which needs in_dim % 32 == 0, gpu_matvec.rs:94-101).
  * Replaces encode_matvec (gpu_matvec.rs:116-159) and its kernel
  * dequant_matvec_4bit_qmv (shaders.metal:366-423); used for the LM head
  * (crates/streammoe/src/riir/io/gpu_lm_head.rs:130-193). */
@@ -211,7 +213,11 @@ int smoe_topk(smoe_handle* h, const float* scores, uint32_t n_tokens, uint32_t n
 /* ------------------------------------------------------------------ */
 
 /* Shape of one packed expert blob [gate | up | down], each block
- * [codes | bf16 scales | bf16 biases] (variants.rs:401-486). */
+ * [codes | bf16 scales | bf16 biases] (variants.rs:401-486). The decode
+ * entry points take hidden <= 8192 and inter <= 2048, both multiples of
+ * the group: every variant of the reference (variants.rs:620-1040, from the
+ * 256-wide test models to Cogito-V2's 7168 and Qwen3.8-Flash-Next's 2560 x
+ * 640). */
 typedef struct {
   uint32_t hidden; /* H: gate/up in_dim, down out_dim */
   uint32_t inter;  /* I: gate/up out_dim, down in_dim */

@@ -32,10 +32,9 @@ int check_shape(const smoe_expert_shape* s) {
   if (s->bits != 4 && s->bits != 3) return SMOE_ERR_UNSUPPORTED_BITS;
   if (int rc = check_group(s->group)) return rc;
   if (s->hidden % s->group || s->inter % s->group) return SMOE_ERR_IN_DIM_NOT_MULTIPLE;
-  // Kernel instances: hidden/32 in {32, 64, 128}, inter/32 in {8, 16, 32, 64}.
-  const uint32_t ch = s->hidden / 32, ci = s->inter / 32;
-  if (!(ch == 32 || ch == 64 || ch == 128)) return SMOE_ERR_UNSUPPORTED_SHAPE;
-  if (!(ci == 8 || ci == 16 || ci == 32 || ci == 64)) return SMOE_ERR_UNSUPPORTED_SHAPE;
+  // Kernel instances: any hidden up to 8192 and inter up to 2048 (both
+  // multiples of the group, so of 32).
+  if (s->hidden > 8192 || s->inter > 2048) return SMOE_ERR_UNSUPPORTED_SHAPE;
   return SMOE_OK;
 }
 

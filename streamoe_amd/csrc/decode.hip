@@ -50,24 +50,40 @@ __device__ __forceinline__ void argmax_merge(float& bv, uint32_t& bi, float v, u
   }
 }
 
-template <int BITS, int CPR, int U>
+// Padded instances (PAD): CPR is a power of two >= the row's cpr chunks (any
+// multiple of 32 inputs). A lane's chunk c >= cpr reads the row's last
+// chunk instead (in bounds) and multiplies it by a zero input, so it adds
+// nothing; an exact instance (cpr == CPR) compiles without the clamps.
+__device__ __forceinline__ uint32_t pad_chunk(uint32_t c, uint32_t cpr) { return c < cpr ? c : cpr - 1; }
+
+__device__ __forceinline__ void load_x32_pad(const float* base, uint32_t c, uint32_t cpr, float (&x)[kChunk]) {
+  load_x32(base + (size_t)pad_chunk(c, cpr) * kChunk, x);
+  if (c >= cpr) {
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) x[j] = 0.f;
+  }
+}
+
+template <int BITS, int CPR, int U, bool PAD = false>
 __global__ __launch_bounds__(256) void k_qmv(const uint8_t* __restrict__ codes,
                                              const uint16_t* __restrict__ scales,
                                              const uint16_t* __restrict__ biases,
                                              const float* __restrict__ x, float* __restrict__ y,
                                              uint32_t rows, uint32_t group, uint32_t n_waves,
-                                             float* __restrict__ arg_v, uint32_t* __restrict__ arg_i) {
+                                             float* __restrict__ arg_v, uint32_t* __restrict__ arg_i,
+                                             uint32_t cpr_rt) {
   constexpr int L = CPR < kWave ? CPR : kWave;
   constexpr int CPL = CPR / L;
   constexpr int RPP = kWave / L;
   constexpr int CB = chunk_bytes<BITS>();
-  constexpr uint32_t ROW_BYTES = CPR * CB;
+  const uint32_t cpr = PAD ? cpr_rt : (uint32_t)CPR;
+  const uint32_t ROW_BYTES = cpr * CB;
   const int lane = threadIdx.x & 63;
   // Wave-uniform (the compiler cannot tell from threadIdx.x): keeps the step
   // loop and the row bases scalar.
   const uint32_t wave = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
   const int lrow = lane / L, lch = lane % L;
-  const uint32_t gpr = CPR * kChunk / group;  // groups per row
+  const uint32_t gpr = cpr * kChunk / group;  // groups per row
   const uint32_t cpg_shift = __builtin_ctz(group / kChunk);
 
   // x in integer-limb form, built once per wave and reused for every row.
@@ -75,7 +91,10 @@ __global__ __launch_bounds__(256) void k_qmv(const uint8_t* __restrict__ codes,
 #pragma unroll
   for (int i = 0; i < CPL; ++i) {
     float xr[kChunk];
-    load_x32(x + (size_t)(lch + L * i) * kChunk, xr);
+    if (PAD)
+      load_x32_pad(x, lch + L * i, cpr, xr);
+    else
+      load_x32(x + (size_t)(lch + L * i) * kChunk, xr);
     make_limbs(xr, xl[i]);
   }
 
@@ -96,7 +115,7 @@ __global__ __launch_bounds__(256) void k_qmv(const uint8_t* __restrict__ codes,
       row = row < rows ? row : rows - 1;
 #pragma unroll
       for (int i = 0; i < CPL; ++i) {
-        const uint32_t c = lch + L * i;
+        const uint32_t c = PAD ? pad_chunk(lch + L * i, cpr) : lch + L * i;
         raw[u][i] = load_raw<BITS>(codes + (size_t)row * ROW_BYTES + c * CB);
         const size_t gi = (size_t)row * gpr + (c >> cpg_shift);
         sv[u][i] = scales[gi];
@@ -171,9 +190,10 @@ __global__ __launch_bounds__(1024) void k_argmax_final(const float* __restrict__
                                                        const uint32_t* __restrict__ pi, uint32_t n,
                                                        const float* __restrict__ v0, int32_t* __restrict__ out);
 
-template <int BITS, int CPR>
+template <int BITS, int CPR, bool PAD = false>
 static hipError_t qmv_inst(const QView& w, const float* x, float* y, uint32_t rows,
-                           hipStream_t st, float* arg_v, uint32_t* arg_i, int32_t* arg_out) {
+                           hipStream_t st, float* arg_v, uint32_t* arg_i, int32_t* arg_out,
+                           uint32_t cpr = CPR) {
   constexpr int L = CPR < kWave ? CPR : kWave;
   constexpr int RPP = kWave / L;
   // Rows per wave and step, and the persistent grid: 4 rows x 3072 waves
@@ -187,8 +207,8 @@ static hipError_t qmv_inst(const QView& w, const float* x, float* y, uint32_t ro
   const uint32_t wpb = 4;
   const uint32_t blocks = (n_waves + wpb - 1) / wpb;
   n_waves = blocks * wpb;
-  hipLaunchKernelGGL((k_qmv<BITS, CPR, U>), dim3(blocks), dim3(wpb * 64), 0, st, w.codes, w.scales,
-                     w.biases, x, y, rows, w.group, n_waves, arg_out ? arg_v : nullptr, arg_i);
+  hipLaunchKernelGGL((k_qmv<BITS, CPR, U, PAD>), dim3(blocks), dim3(wpb * 64), 0, st, w.codes, w.scales,
+                     w.biases, x, y, rows, w.group, n_waves, arg_out ? arg_v : nullptr, arg_i, cpr);
   if (arg_out)
     hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(1024), 0, st, arg_v, arg_i, n_waves, (const float*)y, arg_out);
   return hipGetLastError();
@@ -198,14 +218,28 @@ template <int BITS>
 static hipError_t qmv_bits(const QView& w, const float* x, float* y, uint32_t rows,
                            uint32_t in_dim, hipStream_t st, bool* unsupported, float* av, uint32_t* ai,
                            int32_t* ao) {
-  switch (in_dim / kChunk) {
+  const uint32_t cpr = in_dim / kChunk;
+  switch (cpr) {
     case 16: return qmv_inst<BITS, 16>(w, x, y, rows, st, av, ai, ao);
     case 32: return qmv_inst<BITS, 32>(w, x, y, rows, st, av, ai, ao);
     case 64: return qmv_inst<BITS, 64>(w, x, y, rows, st, av, ai, ao);
     case 128: return qmv_inst<BITS, 128>(w, x, y, rows, st, av, ai, ao);
     case 256: return qmv_inst<BITS, 256>(w, x, y, rows, st, av, ai, ao);
-    default: *unsupported = true; return hipSuccess;
+    default: break;
   }
+  // Other multiples of 32 inputs up to 8192: the padded instances.
+  if (cpr == 0) {
+    *unsupported = true;
+    return hipSuccess;
+  }
+  if (cpr <= 8) return qmv_inst<BITS, 8, true>(w, x, y, rows, st, av, ai, ao, cpr);
+  if (cpr <= 16) return qmv_inst<BITS, 16, true>(w, x, y, rows, st, av, ai, ao, cpr);
+  if (cpr <= 32) return qmv_inst<BITS, 32, true>(w, x, y, rows, st, av, ai, ao, cpr);
+  if (cpr <= 64) return qmv_inst<BITS, 64, true>(w, x, y, rows, st, av, ai, ao, cpr);
+  if (cpr <= 128) return qmv_inst<BITS, 128, true>(w, x, y, rows, st, av, ai, ao, cpr);
+  if (cpr <= 256) return qmv_inst<BITS, 256, true>(w, x, y, rows, st, av, ai, ao, cpr);
+  *unsupported = true;
+  return hipSuccess;
 }
 
 hipError_t launch_qmv(const QView& w, const float* x, float* y, uint32_t out_dim, uint32_t in_dim,
@@ -525,7 +559,7 @@ hipError_t launch_topk(const float* scores, uint32_t n_tokens, uint32_t n, uint3
 // RW rows (gate and up) of one slot; the block index enumerates
 // (slot, row tile), slots 0..k-1 routed, slot k the shared expert.
 // ---------------------------------------------------------------------------
-template <int BITS, int CPR, int P>
+template <int BITS, int CPR, int P, bool PAD>
 __device__ __forceinline__ void gateup_body(const uint8_t* __restrict__ blob, const BlobGeom& g,
                                             uint32_t row0, const float (&xr)[CPR < 64 ? 1 : CPR / 64][kChunk],
                                             const float (&xs)[CPR < 64 ? 1 : CPR / 64],
@@ -534,7 +568,8 @@ __device__ __forceinline__ void gateup_body(const uint8_t* __restrict__ blob, co
   constexpr int CPL = CPR / L;
   constexpr int RPP = kWave / L;
   constexpr int CB = chunk_bytes<BITS>();
-  constexpr uint32_t ROW_BYTES = CPR * CB;
+  const uint32_t cpr = PAD ? g.hidden / kChunk : (uint32_t)CPR;
+  const uint32_t ROW_BYTES = cpr * CB;
   const int lane = threadIdx.x & 63;
   const int lrow = lane / L, lch = lane % L;
   const uint32_t gpr = g.hidden / g.group;
@@ -549,7 +584,7 @@ __device__ __forceinline__ void gateup_body(const uint8_t* __restrict__ blob, co
     row = row < inter ? row : inter - 1;
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
-      const uint32_t c = lch + L * i;
+      const uint32_t c = PAD ? pad_chunk(lch + L * i, cpr) : lch + L * i;
       const size_t off = (size_t)row * ROW_BYTES + c * CB;
       rg[p][i] = load_raw<BITS>(blob + g.w[0] + off);
       ru[p][i] = load_raw<BITS>(blob + g.w[1] + off);
@@ -575,7 +610,7 @@ __device__ __forceinline__ void gateup_body(const uint8_t* __restrict__ blob, co
   }
 }
 
-template <int BITS, int CPR, int P>
+template <int BITS, int CPR, int P, bool PAD>
 __global__ __launch_bounds__(64) void k_gateup(BlobGeom routed, BlobGeom shared,
                                                const FfnTable* __restrict__ tab_dev,
                                                FfnTable tab_val, uint32_t tiles_per_slot,
@@ -596,29 +631,32 @@ __global__ __launch_bounds__(64) void k_gateup(BlobGeom routed, BlobGeom shared,
   float xs[CPL];
 #pragma unroll
   for (int i = 0; i < CPL; ++i) {
-    load_x32(x + (size_t)(lch + L * i) * kChunk, xr[i]);
+    if (PAD)
+      load_x32_pad(x, lch + L * i, routed.hidden / kChunk, xr[i]);
+    else
+      load_x32(x + (size_t)(lch + L * i) * kChunk, xr[i]);
     xs[i] = xsum(xr[i]);
   }
   const uint32_t row0 = tile * RW;
   if (slot < k) {
     if (row0 >= routed.inter) return;
-    gateup_body<BITS, CPR, P>(blob, routed, row0, xr, xs, act + (size_t)slot * routed.inter);
+    gateup_body<BITS, CPR, P, PAD>(blob, routed, row0, xr, xs, act + (size_t)slot * routed.inter);
   } else {
     if (row0 >= shared.inter) return;
-    gateup_body<4, CPR, P>(blob, shared, row0, xr, xs, act + (size_t)slot * routed.inter);
+    gateup_body<4, CPR, P, PAD>(blob, shared, row0, xr, xs, act + (size_t)slot * routed.inter);
   }
 }
 
-template <int BITS, int CPR>
+template <int BITS, int CPR, bool PAD = false>
 static hipError_t gateup_inst(const BlobGeom& routed, const BlobGeom& shared,
                               const FfnTable* tab_dev, const FfnTable& tab_val, uint32_t n_slots,
                               const float* x, float* act, hipStream_t st) {
   constexpr int L = CPR < kWave ? CPR : kWave;
   constexpr int RPP = kWave / L;
-  constexpr int P = 4;
+  constexpr int P = CPR / L >= 4 ? 2 : 4;  // rows per lane group: 4, or 2 with 4 chunks per lane
   const uint32_t rw = RPP * P;
   const uint32_t tiles = (routed.inter + rw - 1) / rw;
-  hipLaunchKernelGGL((k_gateup<BITS, CPR, P>), dim3(tiles * n_slots), dim3(64), 0, st, routed,
+  hipLaunchKernelGGL((k_gateup<BITS, CPR, P, PAD>), dim3(tiles * n_slots), dim3(64), 0, st, routed,
                      shared, tab_dev, tab_val, tiles, x, act);
   return hipGetLastError();
 }
@@ -627,12 +665,26 @@ template <int BITS>
 static hipError_t gateup_bits(const BlobGeom& routed, const BlobGeom& shared,
                               const FfnTable* tab_dev, const FfnTable& tab_val, uint32_t n_slots,
                               const float* x, float* act, hipStream_t st, bool* unsupported) {
-  switch (routed.hidden / kChunk) {
+  const uint32_t cpr = routed.hidden / kChunk;
+  switch (cpr) {
     case 32: return gateup_inst<BITS, 32>(routed, shared, tab_dev, tab_val, n_slots, x, act, st);
     case 64: return gateup_inst<BITS, 64>(routed, shared, tab_dev, tab_val, n_slots, x, act, st);
     case 128: return gateup_inst<BITS, 128>(routed, shared, tab_dev, tab_val, n_slots, x, act, st);
-    default: *unsupported = true; return hipSuccess;
+    default: break;
   }
+  // Other hidden sizes (multiples of 32 up to 8192): the padded instances.
+  if (cpr == 0) {
+    *unsupported = true;
+    return hipSuccess;
+  }
+  if (cpr <= 8) return gateup_inst<BITS, 8, true>(routed, shared, tab_dev, tab_val, n_slots, x, act, st);
+  if (cpr <= 16) return gateup_inst<BITS, 16, true>(routed, shared, tab_dev, tab_val, n_slots, x, act, st);
+  if (cpr <= 32) return gateup_inst<BITS, 32, true>(routed, shared, tab_dev, tab_val, n_slots, x, act, st);
+  if (cpr <= 64) return gateup_inst<BITS, 64, true>(routed, shared, tab_dev, tab_val, n_slots, x, act, st);
+  if (cpr <= 128) return gateup_inst<BITS, 128, true>(routed, shared, tab_dev, tab_val, n_slots, x, act, st);
+  if (cpr <= 256) return gateup_inst<BITS, 256, true>(routed, shared, tab_dev, tab_val, n_slots, x, act, st);
+  *unsupported = true;
+  return hipSuccess;
 }
 
 hipError_t launch_gateup(const BlobGeom& routed, const BlobGeom& shared, const FfnTable* tab_dev,
@@ -650,7 +702,7 @@ hipError_t launch_gateup(const BlobGeom& routed, const BlobGeom& shared, const F
 // the reference's order: moe = fma(out_k, w_k, moe) (deferred.rs:458-466),
 // then the shared term and the residual.
 // ---------------------------------------------------------------------------
-template <int BITS, int CPR, int MAXS>
+template <int BITS, int CPR, int MAXS, bool PAD>
 __global__ __launch_bounds__(64) void k_down_combine(BlobGeom routed, BlobGeom shared,
                                                      const FfnTable* __restrict__ tab_dev,
                                                      FfnTable tab_val,
@@ -663,8 +715,9 @@ __global__ __launch_bounds__(64) void k_down_combine(BlobGeom routed, BlobGeom s
   constexpr int RPP = kWave / L;
   constexpr int CB = chunk_bytes<BITS>();
   constexpr int CB4 = chunk_bytes<4>();
-  constexpr uint32_t ROW_BYTES = CPR * CB;
-  constexpr uint32_t ROW_BYTES4 = CPR * CB4;
+  const uint32_t cpr = PAD ? routed.inter / kChunk : (uint32_t)CPR;
+  const uint32_t ROW_BYTES = cpr * CB;
+  const uint32_t ROW_BYTES4 = cpr * CB4;
   const int lane = threadIdx.x & 63;
   const int lrow = lane / L, lch = lane % L;
   const uint32_t H = routed.hidden, I = routed.inter;
@@ -686,7 +739,7 @@ __global__ __launch_bounds__(64) void k_down_combine(BlobGeom routed, BlobGeom s
       const uint8_t* blob = tab_dev ? tab_dev->blob[s] : tab_val.blob[s];
 #pragma unroll
       for (int i = 0; i < CPL; ++i) {
-        const uint32_t c = lch + L * i;
+        const uint32_t c = PAD ? pad_chunk(lch + L * i, cpr) : lch + L * i;
         raw[s][i] = load_raw<BITS>(blob + routed.w[2] + (size_t)row * ROW_BYTES + c * CB);
         const size_t gi = ((size_t)row * gpr + (c >> cpg_shift)) * 2;
         sv[s][i] = bf16f(*reinterpret_cast<const uint16_t*>(blob + routed.s[2] + gi));
@@ -698,7 +751,7 @@ __global__ __launch_bounds__(64) void k_down_combine(BlobGeom routed, BlobGeom s
     const uint8_t* blob = tab_dev ? tab_dev->blob[k] : tab_val.blob[k];
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
-      const uint32_t c = lch + L * i;
+      const uint32_t c = PAD ? pad_chunk(lch + L * i, cpr) : lch + L * i;
       rsh[i] = load_raw<4>(blob + shared.w[2] + (size_t)row * ROW_BYTES4 + c * CB4);
       const size_t gi = ((size_t)row * gpr + (c >> cpg_shift)) * 2;
       ssh[i] = bf16f(*reinterpret_cast<const uint16_t*>(blob + shared.s[2] + gi));
@@ -714,7 +767,10 @@ __global__ __launch_bounds__(64) void k_down_combine(BlobGeom routed, BlobGeom s
 #pragma unroll
       for (int i = 0; i < CPL; ++i) {
         float a[kChunk];
-        load_x32(act + (size_t)s * I + (size_t)(lch + L * i) * kChunk, a);
+        if (PAD)
+          load_x32_pad(act + (size_t)s * I, lch + L * i, cpr, a);
+        else
+          load_x32(act + (size_t)s * I + (size_t)(lch + L * i) * kChunk, a);
         part += chunk_dot<BITS>(raw[s][i], a, xsum(a), sv[s][i], bv[s][i]);
       }
       const float o = group_sum<L>(part);
@@ -728,7 +784,10 @@ __global__ __launch_bounds__(64) void k_down_combine(BlobGeom routed, BlobGeom s
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
       float a[kChunk];
-      load_x32(act + (size_t)k * I + (size_t)(lch + L * i) * kChunk, a);
+      if (PAD)
+        load_x32_pad(act + (size_t)k * I, lch + L * i, cpr, a);
+      else
+        load_x32(act + (size_t)k * I + (size_t)(lch + L * i) * kChunk, a);
       part += chunk_dot<4>(rsh[i], a, xsum(a), ssh[i], bsh[i]);
     }
     const float sh = group_sum<L>(part);
@@ -746,7 +805,7 @@ __global__ __launch_bounds__(64) void k_down_combine(BlobGeom routed, BlobGeom s
   if (lch == 0 && valid) hidden_out[row] = res;
 }
 
-template <int BITS, int CPR>
+template <int BITS, int CPR, bool PAD = false>
 static hipError_t down_inst(const BlobGeom& routed, const BlobGeom& shared,
                             const FfnTable* tab_dev, const FfnTable& tab_val, uint32_t k,
                             const float* act, const float* h_mid, const float* shared_out,
@@ -755,10 +814,10 @@ static hipError_t down_inst(const BlobGeom& routed, const BlobGeom& shared,
   constexpr int RPP = kWave / L;
   const uint32_t blocks = (routed.hidden + RPP - 1) / RPP;
   if (k <= 8)
-    hipLaunchKernelGGL((k_down_combine<BITS, CPR, 8>), dim3(blocks), dim3(64), 0, st, routed,
+    hipLaunchKernelGGL((k_down_combine<BITS, CPR, 8, PAD>), dim3(blocks), dim3(64), 0, st, routed,
                        shared, tab_dev, tab_val, act, h_mid, shared_out, hidden_out);
   else
-    hipLaunchKernelGGL((k_down_combine<BITS, CPR, 16>), dim3(blocks), dim3(64), 0, st, routed,
+    hipLaunchKernelGGL((k_down_combine<BITS, CPR, 16, PAD>), dim3(blocks), dim3(64), 0, st, routed,
                        shared, tab_dev, tab_val, act, h_mid, shared_out, hidden_out);
   return hipGetLastError();
 }
@@ -768,13 +827,27 @@ static hipError_t down_bits(const BlobGeom& routed, const BlobGeom& shared,
                             const FfnTable* tab_dev, const FfnTable& tab_val, uint32_t k,
                             const float* act, const float* h_mid, const float* shared_out,
                             float* hidden_out, hipStream_t st, bool* unsupported) {
-  switch (routed.inter / kChunk) {
+  const uint32_t cpr = routed.inter / kChunk;
+  switch (cpr) {
     case 8: return down_inst<BITS, 8>(routed, shared, tab_dev, tab_val, k, act, h_mid, shared_out, hidden_out, st);
     case 16: return down_inst<BITS, 16>(routed, shared, tab_dev, tab_val, k, act, h_mid, shared_out, hidden_out, st);
     case 32: return down_inst<BITS, 32>(routed, shared, tab_dev, tab_val, k, act, h_mid, shared_out, hidden_out, st);
     case 64: return down_inst<BITS, 64>(routed, shared, tab_dev, tab_val, k, act, h_mid, shared_out, hidden_out, st);
-    default: *unsupported = true; return hipSuccess;
+    default: break;
   }
+  // Other intermediate sizes (multiples of 32 up to 2048): the padded instances.
+  if (cpr == 0) {
+    *unsupported = true;
+    return hipSuccess;
+  }
+  if (cpr <= 2) return down_inst<BITS, 2, true>(routed, shared, tab_dev, tab_val, k, act, h_mid, shared_out, hidden_out, st);
+  if (cpr <= 4) return down_inst<BITS, 4, true>(routed, shared, tab_dev, tab_val, k, act, h_mid, shared_out, hidden_out, st);
+  if (cpr <= 8) return down_inst<BITS, 8, true>(routed, shared, tab_dev, tab_val, k, act, h_mid, shared_out, hidden_out, st);
+  if (cpr <= 16) return down_inst<BITS, 16, true>(routed, shared, tab_dev, tab_val, k, act, h_mid, shared_out, hidden_out, st);
+  if (cpr <= 32) return down_inst<BITS, 32, true>(routed, shared, tab_dev, tab_val, k, act, h_mid, shared_out, hidden_out, st);
+  if (cpr <= 64) return down_inst<BITS, 64, true>(routed, shared, tab_dev, tab_val, k, act, h_mid, shared_out, hidden_out, st);
+  *unsupported = true;
+  return hipSuccess;
 }
 
 hipError_t launch_down_combine(const BlobGeom& routed, const BlobGeom& shared,

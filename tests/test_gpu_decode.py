@@ -76,6 +76,11 @@ def oracle_matvec(codes, scales, biases, in_dim, out_dim, group, bits, x):
 @pytest.mark.parametrize("out_dim,in_dim,group,bits", [
     (512, 2048, 64, 4), (2048, 512, 64, 4), (1000, 1024, 32, 4), (77, 4096, 128, 4),
     (512, 2048, 64, 3), (2048, 512, 64, 3), (333, 8192, 64, 4), (5, 2048, 64, 4),
+    # Input widths that are not a power of two times 32 (padded instances):
+    # the reference variants' 2560, 640 and 7168, a 256-wide test model,
+    # three chunks.
+    (1000, 2560, 64, 4), (300, 640, 32, 3), (513, 7168, 64, 4), (129, 7168, 128, 3), (77, 256, 64, 4),
+    (64, 96, 32, 4),
 ])
 def test_qmv_matches_oracle(kernels, out_dim, in_dim, group, bits):
     rng = np.random.default_rng(out_dim * 7 + in_dim + bits)
@@ -359,8 +364,17 @@ def _experts_case(kernels, H, I, k, bits, with_shared, seed):
     (2048, 512, 1, 4, False),
     (4096, 1024, 10, 4, True),
     (1024, 256, 4, 3, False),
+    # The other reference variants (variants.rs): Qwen3.8-Flash-Next
+    # (2560 x 640, top-10), Cogito-V2 (7168 x 2048), the tiny test models.
+    (2560, 640, 10, 4, True),
+    (2560, 640, 10, 3, True),
+    (7168, 2048, 8, 4, True),
+    (256, 64, 3, 4, True),
+    (512, 128, 10, 3, True),
 ])
 def test_experts_decode_matches_oracle(kernels, H, I, k, bits, shared):
+    if H > 4096:
+        kernels.reserve(H, max(I, 2048), 1024)
     got, want = _experts_case(kernels, H, I, k, bits, shared, seed=H + I + k + bits)
     # The expert outputs are small next to h_mid; compare the MoE part too.
     err = rel_err(got, want)
@@ -497,6 +511,49 @@ def test_moe_decode_layer_matches_oracle(kernels, path, name, H, I, E, k, bits, 
         assert np.array_equal(gi, wi)
         assert np.max(np.abs(gw - ww)) <= 1e-5 * np.max(np.abs(ww))
         assert err <= TOL
+    finally:
+        kernels.set_decode_path(0)
+
+
+OTHER_SHAPES = [
+    ("flash-next", 2560, 640, 512, 10, 4, True, True),    # Qwen3.8-Flash-Next-4bit
+    ("flash-next-3bit", 2560, 640, 512, 10, 3, True, True),
+    ("cogito-v2", 7168, 2048, 256, 8, 4, True, True),     # DeepSeek-V3 width (routed by softmax top-k here)
+    ("flash-next-tiny", 256, 64, 8, 3, 4, True, True),
+    ("qwen3-next-tiny", 512, 128, 32, 10, 4, True, True),
+    ("h3072", 3072, 768, 128, 8, 4, False, False),
+]
+
+
+@pytest.mark.parametrize("name,H,I,E,k,bits,normalize,shared", OTHER_SHAPES)
+def test_decode_layer_other_shapes(kernels, name, H, I, E, k, bits, normalize, shared):
+    """Shapes without a three-kernel instance take the per-phase kernels on
+    the default path (padded instances for widths that are not a power of
+    two times 32); forcing the three-kernel path reports them unsupported."""
+    from streamoe_amd import _abi
+
+    if H > 4096:
+        kernels.reserve(H, max(I, 2048), 1024)
+    kernels.set_decode_path(0)
+    seed = sum(map(ord, name)) * 5 + 3
+    got, gi, gw, want, wi, ww, gap = _layer_case(kernels, H, I, E, k, bits, normalize, shared, seed=seed)
+    kernels.sync()
+    err = rel_err(got, want)
+    print(f"layer {name}: idx gpu={list(gi)} cpu={list(wi)} gap={gap:.3e} rel_err={err:.3e}")
+    assert np.array_equal(gi, wi)
+    assert np.max(np.abs(gw - ww)) <= 1e-5 * np.max(np.abs(ww))
+    assert err <= TOL
+    kernels.set_decode_path(3)
+    try:
+        import streamoe_amd as sa
+
+        torch = _torch()
+        lay = sa.ExpertLayout(H, I, bits, 64)
+        a = torch.zeros(E * lay.expert_size, dtype=torch.uint8, device="cuda")
+        r = torch.zeros((E, H), dtype=torch.float32, device="cuda")
+        L = kernels.layer(lay, a, lay.expert_size, E, k, normalize, r)
+        x = torch.zeros(H, dtype=torch.float32, device="cuda")
+        assert kernels.moe_decode_layer(L, x, x, x.clone()) == _abi.CODES["SMOE_ERR_UNSUPPORTED_SHAPE"]
     finally:
         kernels.set_decode_path(0)
 
