@@ -208,6 +208,29 @@ int smoe_softmax_topk(smoe_handle* h, const float* logits, uint32_t n_tokens, ui
 int smoe_topk(smoe_handle* h, const float* scores, uint32_t n_tokens, uint32_t n, uint32_t k,
               int32_t* idx, float* values);
 
+/* noaux_tc routing (DeepSeek-V3 / Cogito-V2) per token t < n_tokens from
+ * the gate logits (device f32[n_tokens, n_experts]) and the per-expert
+ * e_score_correction_bias (device f32[n_experts]): s = sigmoid(logit);
+ * group score = sum of the two largest (s + bias) of each of the n_group
+ * equal groups; the running-minimum top-k of the group scores keeps
+ * topk_group groups; the same top-k over (s + bias) of the kept groups
+ * gives idx (slot order = replacement order); weights = s[idx] * (1 / sum
+ * over the slots, in slot order, when > 0) * routed_scaling_factor.
+ * idx: device int32[n_tokens, k]; weights: device f32[n_tokens, k];
+ * scores_out: device f32[n_tokens, n_experts] receiving s, or NULL; it may
+ * equal logits (the reference leaves the sigmoid scores in place).
+ * Errors: n_experts == 0 -> INVALID_ARG (EmptyScores); n_group == 0 or not
+ * dividing n_experts, topk_group outside 1..=n_group, k outside
+ * 1..=min(n_experts, SMOE_MAX_K) -> BAD_K; n_experts > 1024 or n_group > 64
+ * -> UNSUPPORTED_SHAPE.
+ * Replaces noaux_tc_router_cpu (moe_router.rs:211-330), which the Cogito-V2
+ * MoE paths call on host-copied logits (moe/cogito_moe_gpu.rs:286-300,
+ * moe/moe_cpu.rs:129-140). */
+int smoe_noaux_tc_topk(smoe_handle* h, const float* logits, const float* correction_bias,
+                       uint32_t n_tokens, uint32_t n_experts, uint32_t n_group, uint32_t topk_group,
+                       uint32_t k, float routed_scaling_factor, int32_t* idx, float* weights,
+                       float* scores_out);
+
 /* ------------------------------------------------------------------ */
 /* Decode: K routed experts + shared expert + combine (one token)      */
 /* ------------------------------------------------------------------ */

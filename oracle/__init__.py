@@ -56,6 +56,7 @@ def _declare(L):
         "orc_normalize_weights": (None, [_P, _U32]),
         "orc_router": (C.c_int, [_P, _U32, _U32, C.c_int, _P, _P]),
         "orc_sigmoid": (C.c_float, [C.c_float]),
+        "orc_noaux_tc_router": (C.c_int, [_P, _P, _U32, _U32, _U32, _U32, C.c_float, _P, _P]),
         "orc_combine": (None, [_P, _P, _U32, _P, _P, C.c_float, _U32, _P]),
         "orc_moe_decode_layer": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, C.c_int]),
         "orc_rms_norm_bf16": (None, [_P, _P, _U32, C.c_float, _P]),
@@ -208,6 +209,16 @@ def router(scores, k, normalize):
 
 def sigmoid(x):
     return lib().orc_sigmoid(float(x))
+
+
+def noaux_tc_router(logits, bias, n_group, topk_group, k, scale):
+    """noaux_tc_router_cpu (moe_router.rs:211-330); returns (rc, idx, w,
+    scores) with scores = sigmoid(logits), as the reference leaves them."""
+    s = np.array(logits, np.float32)
+    b = _c(bias, np.float32)
+    idx, w = np.empty(k, np.int32), np.empty(k, np.float32)
+    rc = lib().orc_noaux_tc_router(_p(s), _p(b), s.size, n_group, topk_group, k, float(scale), _p(idx), _p(w))
+    return rc, idx, w, s
 
 
 def combine(expert_out, weights, h_mid, shared_out=None, shared_gate_score=float("nan")):

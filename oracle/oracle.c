@@ -421,6 +421,72 @@ int orc_router(float* scores, uint32_t n, uint32_t k, int normalize, int32_t* id
 /* cpu_sigmoid_scalar, cpu_ops.rs:22-25.                                 */
 float orc_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+/* noaux_tc_router_cpu, moe_router.rs:211-330 (DeepSeek-V3 / Cogito-V2):  */
+/*  1. scores = 1 / (1 + exp(-logit)) in place (the un-biased scores);    */
+/*  2. biased = score + correction_bias (selection only);                 */
+/*  3. group score = top1 + top2 of each group's biased values, by a      */
+/*     linear scan (v > top1: shift; else v > top2);                      */
+/*  4. topk() of the group scores picks topk_group groups;                */
+/*  5. the other groups' biased values become -inf;                       */
+/*  6. topk() of the masked biased values gives idx in slot order;        */
+/*  7. w[s] = scores[idx[s]], summed in slot order, w *= 1/sum when       */
+/*     sum > 0, then w *= routed_scaling_factor.                           */
+int orc_noaux_tc_router(float* scores, const float* bias, uint32_t n, uint32_t n_group,
+                        uint32_t topk_group, uint32_t k, float scale, int32_t* idx, float* w) {
+  if (n == 0) return ORC_ERR_EMPTY;
+  if (n_group == 0 || n % n_group) return ORC_ERR_BAD_K;
+  if (topk_group == 0 || topk_group > n_group) return ORC_ERR_BAD_K;
+  if (k == 0 || k > n) return ORC_ERR_BAD_K;
+  for (uint32_t i = 0; i < n; ++i) scores[i] = 1.0f / (1.0f + expf(-scores[i]));
+  float* biased = (float*)malloc((size_t)n * sizeof(float));
+  float* gscore = (float*)malloc((size_t)n_group * sizeof(float));
+  int32_t* gidx = (int32_t*)malloc((size_t)topk_group * sizeof(int32_t));
+  float* gval = (float*)malloc((size_t)topk_group * sizeof(float));
+  float* tval = (float*)malloc((size_t)k * sizeof(float));
+  unsigned char* keep = (unsigned char*)calloc(n_group, 1);
+  if (!biased || !gscore || !gidx || !gval || !tval || !keep) {
+    free(biased), free(gscore), free(gidx), free(gval), free(tval), free(keep);
+    return ORC_ERR_BAD_ARG;
+  }
+  for (uint32_t i = 0; i < n; ++i) biased[i] = scores[i] + bias[i];
+  const uint32_t gs = n / n_group;
+  for (uint32_t g = 0; g < n_group; ++g) {
+    float top1 = -INFINITY, top2 = -INFINITY;
+    for (uint32_t i = g * gs; i < (g + 1) * gs; ++i) {
+      const float v = biased[i];
+      if (v > top1) {
+        top2 = top1;
+        top1 = v;
+      } else if (v > top2) {
+        top2 = v;
+      }
+    }
+    gscore[g] = top1 + top2;
+  }
+  int rc = orc_topk(gscore, n_group, topk_group, gidx, gval);
+  if (rc == ORC_OK) {
+    for (uint32_t s = 0; s < topk_group; ++s) keep[gidx[s]] = 1;
+    for (uint32_t g = 0; g < n_group; ++g)
+      if (!keep[g])
+        for (uint32_t i = g * gs; i < (g + 1) * gs; ++i) biased[i] = -INFINITY;
+    rc = orc_topk(biased, n, k, idx, tval);
+  }
+  if (rc == ORC_OK) {
+    float sum = 0.0f;
+    for (uint32_t s = 0; s < k; ++s) {
+      w[s] = scores[idx[s]];
+      sum += w[s];
+    }
+    if (sum > 0.0f) {
+      const float inv = 1.0f / sum;
+      for (uint32_t s = 0; s < k; ++s) w[s] *= inv;
+    }
+    for (uint32_t s = 0; s < k; ++s) w[s] *= scale;
+  }
+  free(biased), free(gscore), free(gidx), free(gval), free(tval), free(keep);
+  return rc;
+}
+
 /* ------------------------------------------------------------------ */
 /* cpu_combine: deferred.rs:441-490 (cpu_vec_madd, cpu_ops.rs:12-17):   */
 /*   moe[i] = fma(out_k[i], w_k, moe[i])  for k in slot order;          */

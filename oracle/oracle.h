@@ -81,6 +81,8 @@ int orc_topk(const float* scores, uint32_t n, uint32_t k, int32_t* idx, float* v
 void orc_normalize_weights(float* w, uint32_t k);
 int orc_router(float* scores, uint32_t n, uint32_t k, int normalize, int32_t* idx, float* w);
 float orc_sigmoid(float x);
+int orc_noaux_tc_router(float* scores, const float* bias, uint32_t n, uint32_t n_group,
+                        uint32_t topk_group, uint32_t k, float scale, int32_t* idx, float* w);
 
 /* ---- combine ------------------------------------------------------- */
 void orc_combine(const float* expert_out, const float* weights, uint32_t k, const float* h_mid,

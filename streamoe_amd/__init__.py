@@ -194,6 +194,13 @@ class Kernels:
     def topk(self, scores, n_tokens, n, k, idx, values):
         return _lib.smoe_topk(self.h, _ptr(scores), n_tokens, n, k, _ptr(idx), _ptr(values))
 
+    def noaux_tc_topk(self, logits, correction_bias, n_tokens, n_experts, n_group, topk_group, k,
+                      routed_scaling_factor, idx, weights, scores_out=None):
+        """noaux_tc_router_cpu (moe_router.rs:211-330) on the device."""
+        return _lib.smoe_noaux_tc_topk(self.h, _ptr(logits), _ptr(correction_bias), n_tokens, n_experts,
+                                       n_group, topk_group, k, float(routed_scaling_factor), _ptr(idx),
+                                       _ptr(weights), _ptr(scores_out))
+
     # -- decode experts (encode_experts_mmap_into) --------------------------------
     def experts_decode(self, layout: ExpertLayout, bindings, weights, input, h_mid, shared_out,
                        shared_gate_score, hidden_out):

@@ -114,6 +114,7 @@ PROTOTYPES = {
     "smoe_router": (_I, [_P, _P, _P, _U32, _U32, _U32, _U32, _I, _P, _P, _P]),
     "smoe_softmax_topk": (_I, [_P, _P, _U32, _U32, _U32, _I, _P, _P]),
     "smoe_topk": (_I, [_P, _P, _U32, _U32, _U32, _P, _P]),
+    "smoe_noaux_tc_topk": (_I, [_P, _P, _P, _U32, _U32, _U32, _U32, _U32, C.c_float, _P, _P, _P]),
     "smoe_expert_bytes": (_U64, [C.POINTER(ExpertShape)]),
     "smoe_experts_decode": (_I, [_P, C.POINTER(ExpertShape), C.POINTER(Binding), _U32, C.POINTER(C.c_float),
                                  _P, _P, _P, C.c_float, _P]),

@@ -18,7 +18,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libsmoe.so")
-SOURCES = ["api.hip", "decode.hip", "fused.hip", "loader.hip", "prefill.hip", "synth.hip"]
+SOURCES = ["api.hip", "decode.hip", "fused.hip", "loader.hip", "prefill.hip", "router.hip", "synth.hip"]
 HEADERS = ["common.h", "handle.h", "kernels.h", os.path.join("..", "..", "include", "smoe.h")]
 ARCH = "gfx950"
 

@@ -385,6 +385,24 @@ int smoe_topk(smoe_handle* h, const float* scores, uint32_t n_tokens, uint32_t n
   return hip_status(launch_topk(scores, n_tokens, n, k, false, false, ro, h->stream));
 }
 
+int smoe_noaux_tc_topk(smoe_handle* h, const float* logits, const float* correction_bias,
+                       uint32_t n_tokens, uint32_t n_experts, uint32_t n_group, uint32_t topk_group,
+                       uint32_t k, float routed_scaling_factor, int32_t* idx, float* weights,
+                       float* scores_out) {
+  if (!h || !logits || !correction_bias || !idx || !weights || !n_tokens || !n_experts)
+    return SMOE_ERR_INVALID_ARG;
+  if (n_group == 0 || n_experts % n_group) return SMOE_ERR_BAD_K;
+  if (topk_group == 0 || topk_group > n_group) return SMOE_ERR_BAD_K;
+  if (k < 1 || k > n_experts || k > SMOE_MAX_K) return SMOE_ERR_BAD_K;
+  if (n_experts > kNoauxMaxExperts || n_group > kNoauxMaxGroups) return SMOE_ERR_UNSUPPORTED_SHAPE;
+  if (int rc = use_device(h)) return rc;
+  RouteOut ro{};
+  ro.idx = idx;
+  ro.weight = weights;
+  return hip_status(launch_noaux_topk(logits, correction_bias, n_tokens, n_experts, n_group, topk_group,
+                                      k, routed_scaling_factor, scores_out, ro, h->stream));
+}
+
 uint64_t smoe_expert_bytes(const smoe_expert_shape* s) {
   if (!s || !s->group) return 0;
   const uint64_t w = (uint64_t)s->inter * s->hidden * s->bits / 8;

@@ -181,6 +181,12 @@ hipError_t launch_router_logits(const float* W, const float* gate_w, const float
 // Softmax (optional) + running-min top-k + optional renorm, one wave per token.
 hipError_t launch_topk(const float* scores, uint32_t n_tokens, uint32_t n, uint32_t k,
                        bool softmax, bool normalize, const RouteOut& out, hipStream_t st);
+// noaux_tc routing from logits [n_tokens, n] (router.hip). scores_out may
+// equal logits (each lane reads its scores before writing them) or be null.
+constexpr uint32_t kNoauxMaxExperts = 1024, kNoauxMaxGroups = 64;
+hipError_t launch_noaux_topk(const float* logits, const float* bias, uint32_t n_tokens, uint32_t n,
+                             uint32_t n_group, uint32_t topk_group, uint32_t k, float scale,
+                             float* scores_out, const RouteOut& out, hipStream_t st);
 
 // Expert FFN of every slot in the table: act[slot, r] = silu(gate) * up.
 // Exactly one of tab_dev / tab_val is used (tab_dev when not null).

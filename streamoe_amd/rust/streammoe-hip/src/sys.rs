@@ -108,6 +108,10 @@ extern "C" {
                              normalize: c_int, idx: *mut i32, weights: *mut f32) -> c_int;
     pub fn smoe_topk(h: *mut smoe_handle, scores: *const f32, n_tokens: u32, n: u32, k: u32, idx: *mut i32,
                      values: *mut f32) -> c_int;
+    pub fn smoe_noaux_tc_topk(h: *mut smoe_handle, logits: *const f32, correction_bias: *const f32,
+                              n_tokens: u32, n_experts: u32, n_group: u32, topk_group: u32, k: u32,
+                              routed_scaling_factor: f32, idx: *mut i32, weights: *mut f32,
+                              scores_out: *mut f32) -> c_int;
     pub fn smoe_expert_bytes(shape: *const smoe_expert_shape) -> u64;
     pub fn smoe_experts_decode(h: *mut smoe_handle, shape: *const smoe_expert_shape,
                                bindings: *const smoe_binding, k: u32, weights: *const f32, input: *const f32,

@@ -248,6 +248,104 @@ def test_normalize_guard():
     assert list(oracle.normalize_weights([0.0, 0.0])) == [0.0, 0.0]
 
 
+# --- noaux_tc router (moe_router.rs:211-330) -----------------------------------------------
+
+def test_noaux_tc_hand_reference():
+    """moe_router.rs:528-580: group 1 wins (top-2 sums 2.3128 vs 2.1317 of
+    biased sigmoid scores), idx set {5, 7}, weights gather the UN-biased
+    sigmoid 0.8808 / 0.9820, renormalised and * 2.5 -> 1.1822 / 1.3178."""
+    logits = [3.0, -2.0, 1.0, -1.0, -3.0, 2.0, 0.0, 4.0]
+    bias = [0.1, 0.2, -0.3, 0.0, 0.0, 0.4, -0.1, 0.05]
+    rc, idx, w, s = oracle.noaux_tc_router(logits, bias, 2, 1, 2, 2.5)
+    assert rc == 0
+    pairs = sorted(zip(idx.tolist(), w.tolist()))
+    assert [i for i, _ in pairs] == [5, 7]
+    assert abs(pairs[0][1] - 1.1822) < 1e-3 and abs(pairs[1][1] - 1.3178) < 1e-3
+    assert abs(float(w.sum()) - 2.5) < 1e-3
+    # The logits are left holding the un-biased sigmoid scores.
+    assert all(s[i] == np.float32(oracle.sigmoid(x)) for i, x in enumerate(logits))
+
+
+def test_noaux_tc_cogito_shape():
+    """moe_router.rs:585-640 (256 experts, 8 groups, top-4 groups, k 8,
+    scaling 2.5, logits sin(0.137 i) * 2, bias cos(0.241 i) * 0.5)."""
+    i = np.arange(256, dtype=np.float32)
+    logits = (np.sin(i * np.float32(0.137)) * 2).astype(np.float32)
+    bias = (np.cos(i * np.float32(0.241)) * np.float32(0.5)).astype(np.float32)
+    rc, idx, w, _ = oracle.noaux_tc_router(logits, bias, 8, 4, 8, 2.5)
+    assert rc == 0
+    assert abs(float(w.sum()) - 2.5) < 1e-3
+    assert len({int(j) // 32 for j in idx}) <= 4
+    assert len(set(idx.tolist())) == 8
+
+
+def _noaux_f64(logits, bias, n_group, topk_group, k, scale):
+    """Independent restatement by sorting, in float64 (distinct values)."""
+    s = 1.0 / (1.0 + np.exp(-np.asarray(logits, np.float64)))
+    b = s + np.asarray(bias, np.float64)
+    g = b.reshape(n_group, -1)
+    gsc = np.sort(g, axis=1)[:, -2:].sum(axis=1) if g.shape[1] > 1 else g[:, 0] + -np.inf
+    keep = np.argsort(-gsc, kind="stable")[:topk_group]
+    m = np.full_like(b, -np.inf)
+    gs = b.size // n_group
+    for gi in keep:
+        m[gi * gs:(gi + 1) * gs] = b[gi * gs:(gi + 1) * gs]
+    sel = np.argsort(-m, kind="stable")[:k]
+    return set(sel.tolist()), {int(j): s[j] / s[sel].sum() * scale for j in sel}
+
+
+@pytest.mark.parametrize("n,n_group,topk_group,k", [(256, 8, 4, 8), (64, 4, 2, 6), (512, 16, 3, 10),
+                                                    (128, 1, 1, 8), (96, 3, 3, 4)])
+def test_noaux_tc_vs_sort_f64(n, n_group, topk_group, k):
+    rng = np.random.default_rng(n + k)
+    for _ in range(10):
+        logits = rng.standard_normal(n).astype(np.float32) * 2
+        bias = rng.standard_normal(n).astype(np.float32) * 0.3
+        rc, idx, w, _ = oracle.noaux_tc_router(logits, bias, n_group, topk_group, k, 2.5)
+        want_set, want_w = _noaux_f64(logits, bias, n_group, topk_group, k, 2.5)
+        assert rc == 0 and set(idx.tolist()) == want_set
+        for j, wj in zip(idx.tolist(), w.tolist()):
+            assert abs(wj - want_w[j]) <= 1e-6 * 2.5
+
+
+def test_noaux_tc_group_score_is_top2_sum():
+    """Group 0 holds the single largest score (sigmoid 3 = 0.9526) but its
+    top-2 sum 1.0 loses to group 1's 0.7311 * 2: the winner is expert 2 (the
+    earlier of the tied pair: a later equal value never replaces)."""
+    rc, idx, w, _ = oracle.noaux_tc_router([3.0, -3.0, 1.0, 1.0], [0.0] * 4, 2, 1, 1, 1.5)
+    assert rc == 0 and list(idx) == [2] and w[0] == np.float32(1.5)
+
+
+def test_noaux_tc_bias_selects_but_does_not_weight():
+    """Un-biased, the top-2 would be {0, 2}; the bias lifts expert 1
+    (0.2689 + 0.6) above expert 0 (0.5), and expert 2 (0.6225) then replaces
+    slot 0: idx [2, 1]. The weights still gather the un-biased scores."""
+    rc, idx, w, _ = oracle.noaux_tc_router([0.0, -1.0, 0.5], [0.0, 0.6, 0.0], 1, 1, 2, 1.0)
+    assert rc == 0 and list(idx) == [2, 1]
+    s1, s2 = 1.0 / (1.0 + math.exp(1.0)), 1.0 / (1.0 + math.exp(-0.5))
+    assert abs(w[0] - s2 / (s1 + s2)) < 1e-6 and abs(w[1] - s1 / (s1 + s2)) < 1e-6
+
+
+def test_noaux_tc_more_slots_than_unmasked_experts():
+    """k = 3 with one kept group of 2 experts: the third slot keeps the
+    reference's start entry (index 0), so its weight gathers sigmoid(3)."""
+    rc, idx, w, _ = oracle.noaux_tc_router([3.0, -3.0, 1.0, 1.0], [0.0] * 4, 2, 1, 3, 1.0)
+    assert rc == 0 and list(idx) == [2, 3, 0]
+    s = [1.0 / (1.0 + math.exp(-x)) for x in (1.0, 1.0, 3.0)]
+    for got, want in zip(w, s):
+        assert abs(got - want / sum(s)) < 1e-6
+
+
+@pytest.mark.parametrize("n,n_group,topk_group,k,rc", [
+    (0, 1, 1, 1, 3), (8, 0, 1, 1, 2), (8, 3, 1, 1, 2), (8, 2, 0, 1, 2), (8, 2, 3, 1, 2),
+    (8, 2, 1, 0, 2), (8, 2, 1, 9, 2),
+])
+def test_noaux_tc_errors(n, n_group, topk_group, k, rc):
+    """moe_router.rs:221-255: EmptyScores, then BadK for the group count, the
+    kept-group count and k."""
+    assert oracle.noaux_tc_router([0.0] * n, [0.0] * n, n_group, topk_group, k, 1.0)[0] == rc
+
+
 # --- combine (deferred.rs:441-490) ---------------------------------------------------------
 
 def test_combine_known_answers():
