@@ -93,6 +93,18 @@ __device__ __forceinline__ Raw<3> load_raw3(const uint8_t* p) {
   r.d[2] = ld_w<NT>(q + 2);
   return r;
 }
+// LDS DMA (global_load_lds): each lane's 16 (or 4) bytes at g go to LDS at
+// l + lane * 16 (or 4), without passing through registers. l must be the
+// same for every lane of the wave; completion is counted by vmcnt.
+#define SMOE_GPTR(p) ((const __attribute__((address_space(1))) void*)(p))
+#define SMOE_LPTR(p) ((__attribute__((address_space(3))) void*)(p))
+__device__ __forceinline__ void dma16(const void* g, void* l) {
+  __builtin_amdgcn_global_load_lds(SMOE_GPTR(g), SMOE_LPTR(l), 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void* g, void* l) {
+  __builtin_amdgcn_global_load_lds(SMOE_GPTR(g), SMOE_LPTR(l), 4, 0, 0);
+}
+
 template <int BITS, bool NT = true>
 __device__ __forceinline__ Raw<BITS> load_raw(const uint8_t* p) {
   if constexpr (BITS == 4)

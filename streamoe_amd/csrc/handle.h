@@ -19,8 +19,8 @@ struct smoe_handle {
   float* gate = nullptr;      // [1] shared-expert gate score
   smoe::FfnTable* table = nullptr;  // routing table of the current token
   uint32_t* xl = nullptr;     // [max_hidden / 32 * kXLimbWords] x as integer limbs
-  float* arg_v = nullptr;     // [256] argmax partial values
-  uint32_t* arg_i = nullptr;  // [256] argmax partial indices
+  float* arg_v = nullptr;     // [kQmvMaxWaves] argmax partial values
+  uint32_t* arg_i = nullptr;  // [kQmvMaxWaves] argmax partial indices
   uint32_t* err = nullptr;        // device error word (prefill routing errors)
   uint32_t max_hidden = 0, max_inter = 0, max_experts = 0;
   // Per-token strides (elements) of logits, act and limbs in the scratch.

@@ -429,15 +429,6 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
 // by the row, A rows XOR their parts by the row, so the 16 lanes of an
 // MFMA operand read different banks.
 // ---------------------------------------------------------------------------
-#define PF_GPTR(p) ((const __attribute__((address_space(1))) void*)(p))
-#define PF_LPTR(p) ((__attribute__((address_space(3))) void*)(p))
-
-__device__ __forceinline__ void dma16(const void* g, void* l) {
-  __builtin_amdgcn_global_load_lds(PF_GPTR(g), PF_LPTR(l), 16, 0, 0);
-}
-__device__ __forceinline__ void dma4(const void* g, void* l) {
-  __builtin_amdgcn_global_load_lds(PF_GPTR(g), PF_LPTR(l), 4, 0, 0);
-}
 
 // Position of natural index i (0..7) of an 8-block in the MFMA order
 // [v0, v4, v1, v5, v2, v6, v3, v7].

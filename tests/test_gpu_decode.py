@@ -96,6 +96,41 @@ def test_qmv_matches_oracle(kernels, out_dim, in_dim, group, bits):
     assert err <= TOL
 
 
+@pytest.mark.parametrize("out_dim,in_dim,group,bits", [
+    (40000, 2048, 64, 4), (30001, 2048, 32, 3), (16391, 4096, 128, 4), (20000, 4096, 64, 3),
+    (50003, 2048, 128, 4), (16384, 2048, 64, 4),
+])
+def test_qmv_large_ragged_row_slices(kernels, out_dim, in_dim, group, bits):
+    """Large matrices with ragged row counts (the persistent grid's last
+    steps clamp their rows): within 1e-3 of the oracle, and every row's
+    result independent of the launch that computes it: the same rows as
+    slices of at most 8000 rows (other grids, other wave-to-row mappings)
+    give the same bits."""
+    import streamoe_amd as sa
+
+    rng = np.random.default_rng(out_dim + in_dim + group + bits)
+    codes, s, b = gen_quant_matrix(rng, out_dim, in_dim, group, bits)
+    x = rng.standard_normal(in_dim).astype(np.float32)
+    w = qweights(codes, s, b, group, bits)
+    torch = _torch()
+    xd = dev(x)
+    y = torch.empty(out_dim, dtype=torch.float32, device="cuda")
+    assert kernels.qmv(w, xd, y, out_dim, in_dim) == 0
+    want, _ = oracle_matvec(codes, s, b, in_dim, out_dim, group, bits, x)
+    got = host(y)
+    err = rel_err(got, want)
+    print(f"qmv {out_dim}x{in_dim} g{group} {bits}-bit rel_err={err:.3e}")
+    assert err <= TOL
+    rb, sb = in_dim * bits // 8, in_dim // group * 2
+    ys = torch.empty(out_dim, dtype=torch.float32, device="cuda")
+    for r0 in range(0, out_dim, 8000):
+        n = min(8000, out_dim - r0)
+        ws = sa.QuantWeights(w.buffer, w.packed_offset + r0 * rb, w.scales_offset + r0 * sb,
+                             w.biases_offset + r0 * sb, group, bits)
+        assert kernels.qmv(ws, xd, ys[r0:r0 + n], n, in_dim) == 0
+    assert np.array_equal(host(ys).view(np.uint32), got.view(np.uint32))
+
+
 def test_lm_head_qwen3_shape_and_argmax(kernels):
     """Config 1: 151,936 x 2048 4-bit g64 LM head; greedy argmax bit-exact."""
     V, H, G = 151936, 2048, 64
@@ -168,11 +203,12 @@ def test_argmax_nan_like_the_reference(kernels, case):
     assert int(host(out)[0]) == want == oracle.argmax(v)
 
 
-def test_qmv_argmax_nan_first_row(kernels):
+@pytest.mark.parametrize("out_dim", [9000, 20000])
+def test_qmv_argmax_nan_first_row(kernels, out_dim):
     """smoe_qmv_argmax when row 0's scales are NaN (y[0] = NaN): index 0, as
     the reference's scan over the logits gives."""
     torch = _torch()
-    out_dim, in_dim = 9000, 2048
+    in_dim = 2048
     rng = np.random.default_rng(9)
     codes, s, b = gen_quant_matrix(rng, out_dim, in_dim, 64, 4)
     s[0, :] = 0x7FC0  # bf16 NaN
@@ -187,7 +223,7 @@ def test_qmv_argmax_nan_first_row(kernels):
 
 
 @pytest.mark.parametrize("out_dim,in_dim,bits", [(151936, 2048, 4), (50000, 1024, 4), (9000, 2048, 3),
-                                                 (77, 512, 4)])
+                                                 (77, 512, 4), (40000, 2048, 3), (20000, 4096, 4)])
 def test_qmv_argmax_fused(kernels, out_dim, in_dim, bits):
     """smoe_qmv_argmax: y identical to smoe_qmv, index = numpy's first
     maximal index of y, with the maximum planted on several rows (identical
