@@ -378,10 +378,14 @@ uint64_t smoe_moe_prefill_workspace_size(const smoe_expert_shape* shape, uint32_
  * idx: device int32[n_tokens, k]; weights: device f32[n_tokens, k];
  * out_sum: device f32[n_tokens, hidden] (overwritten); workspace:
  * device, >= smoe_moe_prefill_workspace_size bytes, 256-byte aligned.
- * Supported: bits 4 or 3, group 32/64/128, hidden and inter multiples of
- * 256 with hidden >= 1024, 1..1024 tokens, <= 512 experts,
- * 1 <= k <= min(16, n_experts);
- * else SMOE_ERR_UNSUPPORTED_SHAPE / SMOE_ERR_BAD_K. An expert id out of
+ * Grouped GEMMs for bits 4 or 3, group 32/64/128, hidden and inter
+ * multiples of 256 with hidden >= 1024, <= 512 experts; every other
+ * expert shape of the decode entry points (hidden <= 8192, inter <= 2048,
+ * multiples of the group) and more experts go one token at a time
+ * through the per-phase decode kernels (f32 activations; the combine
+ * again in ascending expert order). 1..1024 tokens, 1 <= k <= min(16,
+ * n_experts); else SMOE_ERR_UNSUPPORTED_SHAPE / SMOE_ERR_BAD_K. The
+ * workspace size covers either path (bf16 x assumed). An expert id out of
  * range or repeated within a token is found on the device: the call
  * returns SMOE_OK and the next smoe_sync returns SMOE_ERR_INVALID_ARG.
  * Enqueue-only, allocates nothing, capturable in a HIP graph.

@@ -692,6 +692,8 @@ int smoe_moe_decode_tokens(smoe_handle* h, const smoe_layer* layers, uint32_t n_
 uint64_t smoe_moe_prefill_workspace_size(const smoe_expert_shape* shape, uint32_t n_tokens,
                                          uint32_t n_experts, uint32_t k) {
   if (!shape || !shape->group || !n_tokens || !n_experts || !k) return 0;
+  if (!prefill_supported(shape->hidden, shape->inter, shape->group, shape->bits, n_tokens, n_experts, k))
+    return prefill_tokens_workspace(shape->hidden, shape->inter, n_tokens, k, true);
   return prefill_workspace(shape->hidden, shape->inter, shape->group, n_tokens, n_experts, k, nullptr,
                            nullptr);
 }
@@ -705,11 +707,24 @@ int smoe_moe_prefill(smoe_handle* h, const smoe_expert_shape* shape, const void*
   if (int rc = check_shape(shape)) return rc;
   if (k < 1 || k > SMOE_MAX_K || k > n_experts) return SMOE_ERR_BAD_K;
   if (stride < smoe_expert_bytes(shape)) return SMOE_ERR_INVALID_ARG;
-  if (!prefill_supported(shape->hidden, shape->inter, shape->group, shape->bits, n_tokens, n_experts, k))
-    return SMOE_ERR_UNSUPPORTED_SHAPE;
+  if (n_tokens > kPfMaxTokens) return SMOE_ERR_UNSUPPORTED_SHAPE;
   if (!blob_aligned(experts, shape->bits) || stride % 16 || !aligned(x, 0, 16) ||
       !aligned(out_sum, 0, 16) || !aligned(workspace, 0, 256))
     return SMOE_ERR_MISALIGNED;
+  if (!prefill_supported(shape->hidden, shape->inter, shape->group, shape->bits, n_tokens, n_experts, k)) {
+    // Shapes without grouped-GEMM tiles: one token at a time through the
+    // per-phase decode kernels.
+    if (workspace_bytes < prefill_tokens_workspace(shape->hidden, shape->inter, n_tokens, k, x_is_bf16 != 0))
+      return SMOE_ERR_WORKSPACE_TOO_SMALL;
+    if (int rc = use_device(h)) return rc;
+    bool unsupported = false;
+    const hipError_t e = launch_prefill_tokens(
+        blob_geom(shape->hidden, shape->inter, shape->group, shape->bits), (const uint8_t*)experts, stride,
+        n_experts, idx, weights, x, x_is_bf16 != 0, n_tokens, k, out_sum, (uint8_t*)workspace, h->err, h->stream,
+        &unsupported);
+    if (unsupported) return SMOE_ERR_UNSUPPORTED_SHAPE;
+    return hip_status(e);
+  }
   PfArgs a{};
   const uint64_t need = prefill_workspace(shape->hidden, shape->inter, shape->group, n_tokens,
                                           n_experts, k, &a, (uint8_t*)workspace);

@@ -864,6 +864,89 @@ hipError_t launch_down_combine(const BlobGeom& routed, const BlobGeom& shared,
 }
 
 // ---------------------------------------------------------------------------
+// Prefill through the per-phase kernels, for expert shapes the grouped GEMMs
+// have no tiles for (hidden or inter not a multiple of 256, hidden below
+// 1024): per token, a route table of its k experts in ascending expert
+// order (the order moe_permute_fuse_cpu, moe_cpu.rs:282-339, adds them in),
+// then k_gateup and k_down_combine over that table with a zero residual.
+// ---------------------------------------------------------------------------
+// One wave: token t's table. An expert id out of range or repeated within
+// the token sets the device error word (as the grouped path's bucketing
+// does) and reads expert 0 instead, so nothing is read out of bounds.
+__global__ __launch_bounds__(64) void k_pt_table(const int32_t* __restrict__ idx, const float* __restrict__ w,
+                                                 uint32_t k, uint32_t E, const uint8_t* experts, uint64_t stride,
+                                                 FfnTable* tab, uint32_t* err) {
+  const int lane = threadIdx.x;
+  const bool live = lane < (int)k;
+  const int32_t id = live ? idx[lane] : 0x7FFFFFFF;
+  const float wt = live ? w[lane] : 0.f;
+  bool bad = live && (id < 0 || (uint32_t)id >= E);
+  // Rank: entries with a smaller id, or the same id in an earlier slot.
+  uint32_t rank = 0;
+  for (uint32_t s = 0; s < k; ++s) {
+    const int32_t o = __shfl(id, s, kWave);
+    rank += (o < id || (o == id && (int)s < lane)) ? 1u : 0u;
+    bad |= live && o == id && (int)s != lane;
+  }
+  if (__ballot(bad) && lane == 0) *err = 2u;
+  if (live) {
+    const uint32_t e = (id >= 0 && (uint32_t)id < E) ? (uint32_t)id : 0u;
+    tab->blob[rank] = experts + (uint64_t)e * stride;
+    tab->weight[rank] = wt;
+  }
+  if (lane == 0) {
+    tab->k = k;
+    tab->has_shared = 0;
+    tab->shared_gate = __builtin_nanf("");
+  }
+}
+
+// x as f32 rows (bf16 widened; f32 input is used in place) and the zero
+// residual.
+__global__ __launch_bounds__(256) void k_pt_prep(const uint16_t* __restrict__ xb, uint64_t n, float* __restrict__ xf,
+                                                 uint32_t hidden, float* __restrict__ zero) {
+  for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256)
+    xf[i] = bf16f(xb[i]);
+  if (blockIdx.x == 0)
+    for (uint32_t i = threadIdx.x; i < hidden; i += 256) zero[i] = 0.f;
+}
+
+uint64_t prefill_tokens_workspace(uint32_t hidden, uint32_t inter, uint32_t n_tokens, uint32_t k, bool x_bf16) {
+  auto al = [](uint64_t b) { return (b + 255) / 256 * 256; };
+  return al(sizeof(FfnTable)) + al((uint64_t)hidden * 4) + al((uint64_t)(k + 1) * inter * 4) +
+         (x_bf16 ? al((uint64_t)n_tokens * hidden * 4) : 0u);
+}
+
+hipError_t launch_prefill_tokens(const BlobGeom& g, const uint8_t* experts, uint64_t stride, uint32_t E,
+                                 const int32_t* idx, const float* w, const void* x, bool x_bf16, uint32_t n,
+                                 uint32_t k, float* out, uint8_t* ws, uint32_t* err, hipStream_t st,
+                                 bool* unsupported) {
+  *unsupported = false;
+  auto al = [](uint64_t b) { return (b + 255) / 256 * 256; };
+  FfnTable* tab = reinterpret_cast<FfnTable*>(ws);
+  float* zero = reinterpret_cast<float*>(ws + al(sizeof(FfnTable)));
+  float* act = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(zero) + al((uint64_t)g.hidden * 4));
+  float* xf = x_bf16 ? reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(act) + al((uint64_t)(k + 1) * g.inter * 4))
+                     : const_cast<float*>(static_cast<const float*>(x));
+  const uint64_t nx = x_bf16 ? (uint64_t)n * g.hidden : 0u;
+  const uint32_t pb = x_bf16 ? (uint32_t)((nx + 255) / 256 < 1024 ? (nx + 255) / 256 : 1024) : 1u;
+  hipLaunchKernelGGL(k_pt_prep, dim3(pb), dim3(256), 0, st, static_cast<const uint16_t*>(x), nx, xf, g.hidden, zero);
+  hipError_t e = hipGetLastError();
+  FfnTable tv{};
+  tv.k = k;
+  for (uint32_t t = 0; t < n && e == hipSuccess; ++t) {
+    hipLaunchKernelGGL(k_pt_table, dim3(1), dim3(64), 0, st, idx + (size_t)t * k, w + (size_t)t * k, k, E, experts,
+                       stride, tab, err);
+    e = hipGetLastError();
+    if (e == hipSuccess) e = launch_gateup(g, g, tab, tv, k, xf + (size_t)t * g.hidden, act, st, unsupported);
+    if (e == hipSuccess && !*unsupported)
+      e = launch_down_combine(g, g, tab, tv, k, act, zero, nullptr, out + (size_t)t * g.hidden, st, unsupported);
+    if (*unsupported) break;
+  }
+  return e;
+}
+
+// ---------------------------------------------------------------------------
 // RMSNorm with bf16 weights (rms_norm_bf16_n_tokens_cpu, backend/cpu/mod.rs:
 // 406-430; GPU rms_norm_sum_sq + rms_norm_apply_bf16, shaders.metal:
 // 1454-1530), or a copy when w is null. One block.

@@ -146,6 +146,14 @@ struct PfArgs {
 // workspace fields into base.
 uint64_t prefill_workspace(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t n_tokens,
                            uint32_t n_experts, uint32_t k, PfArgs* a, uint8_t* base);
+// Prefill through the per-phase decode kernels, one token at a time, for
+// the shapes prefill_supported refuses (decode.hip): workspace bytes and
+// launch.
+uint64_t prefill_tokens_workspace(uint32_t hidden, uint32_t inter, uint32_t n_tokens, uint32_t k, bool x_bf16);
+hipError_t launch_prefill_tokens(const BlobGeom& g, const uint8_t* experts, uint64_t stride, uint32_t E,
+                                 const int32_t* idx, const float* w, const void* x, bool x_bf16, uint32_t n,
+                                 uint32_t k, float* out, uint8_t* ws, uint32_t* err, hipStream_t st,
+                                 bool* unsupported);
 bool prefill_supported(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t bits,
                        uint32_t n_tokens, uint32_t n_experts, uint32_t k);
 hipError_t launch_prefill(const PfArgs& a, uint32_t n_cu, hipStream_t st);

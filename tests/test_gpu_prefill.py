@@ -79,6 +79,14 @@ def _case(kernels, n_tokens, H, I, E, k, bits, group, x_bf16, seed, routing="zip
     ("max-e512-n1024", 1024, 2048, 512, 512, 10, 4, 64, True, "zipf"),  # largest bucketing bitmaps
     ("e512-f32-x", 64, 1024, 512, 512, 10, 3, 32, False, "zipf"),
     ("h4096-q397b", 64, 4096, 1024, 512, 10, 4, 64, True, "zipf"),  # Qwen3.5-397B-A17B layer shape
+    # Shapes without grouped-GEMM tiles (hidden or inter not a multiple of
+    # 256, hidden below 1024, more than 512 experts): one token at a time
+    # through the per-phase decode kernels.
+    ("flash-next", 40, 2560, 640, 512, 10, 4, 64, True, "zipf"),   # Qwen3.8-Flash-Next-4bit
+    ("flash-next-3bit-f32", 24, 2560, 640, 128, 10, 3, 64, False, "zipf"),
+    ("flash-next-tiny", 50, 256, 64, 8, 3, 4, 64, True, "zipf"),
+    ("qwen3-next-tiny", 30, 512, 128, 32, 10, 4, 32, True, "hot"),
+    ("e600", 20, 2048, 512, 600, 8, 4, 64, True, "zipf"),
 ])
 def test_prefill_matches_oracle(kernels, name, n, H, I, E, k, bits, group, x_bf16, routing):
     got, want, _ = _case(kernels, n, H, I, E, k, bits, group, x_bf16, seed=sum(map(ord, name)), routing=routing)
@@ -123,9 +131,9 @@ def test_prefill_argument_errors(kernels):
     assert kernels.moe_prefill(lay, arena, lay.expert_size, 4, idx, w, x, True, 4, 0, out, ws) == c["SMOE_ERR_BAD_K"]
     assert kernels.moe_prefill(lay, arena, lay.expert_size, 4, idx, w, x, True, 2000, 2, out, ws) == \
         c["SMOE_ERR_UNSUPPORTED_SHAPE"]
-    # Hidden sizes below 1024 have no prefill instance (checked before any launch).
-    small_h = sa.ExpertLayout(768, 512, 4, 64)
-    assert kernels.moe_prefill(small_h, arena, small_h.expert_size, 4, idx, w, x, True, 4, 2, out, ws) == \
+    # Hidden sizes above 8192 have no kernel instance (checked before any launch).
+    big_h = sa.ExpertLayout(8256, 512, 4, 64)
+    assert kernels.moe_prefill(big_h, arena, big_h.expert_size, 4, idx, w, x, True, 4, 2, out, ws) == \
         c["SMOE_ERR_UNSUPPORTED_SHAPE"]
     # Invalid routing is caught on the device and reported by smoe_sync.
     bad = torch.tensor([[0, 1], [2, 9], [3, 0], [1, 2]], dtype=torch.int32, device="cuda")
@@ -138,3 +146,37 @@ def test_prefill_argument_errors(kernels):
     with pytest.raises(sa.SmoeError):
         kernels.sync()
     kernels.sync()  # the error word was cleared
+
+
+def test_prefill_per_token_path_errors_and_workspace(kernels):
+    """The per-token path (hidden 768: no grouped-GEMM tiles) reports invalid
+    routing through smoe_sync like the grouped path, needs its own
+    workspace size, and leaves the error word clear after a good call."""
+    import streamoe_amd as sa
+    from streamoe_amd import _abi
+
+    torch = _torch()
+    c = _abi.CODES
+    lay = sa.ExpertLayout(768, 256, 4, 64)
+    E, n, k = 4, 4, 2
+    arena = torch.empty(E * lay.expert_size, dtype=torch.uint8, device="cuda")
+    assert kernels.synth_experts(arena, E, lay.expert_size, lay, 5) == 0
+    w = torch.full((n, k), 0.5, dtype=torch.float32, device="cuda")
+    x = torch.zeros((n, 768), dtype=torch.int16, device="cuda")
+    out = torch.zeros((n, 768), dtype=torch.float32, device="cuda")
+    need = kernels.moe_prefill_workspace_size(lay, n, E, k)
+    assert need > 0
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    small = torch.empty(need // 4, dtype=torch.uint8, device="cuda")
+    good = torch.tensor([[0, 1], [2, 3], [3, 0], [1, 2]], dtype=torch.int32, device="cuda")
+    assert kernels.moe_prefill(lay, arena, lay.expert_size, E, good, w, x, True, n, k, out, small) == \
+        c["SMOE_ERR_WORKSPACE_TOO_SMALL"]
+    assert kernels.moe_prefill(lay, arena, lay.expert_size, E, good, w, x, True, n, k, out, ws) == 0
+    kernels.sync()
+    for bad in ([[0, 1], [2, 9], [3, 0], [1, 2]], [[0, 1], [2, 2], [3, 0], [1, 2]], [[0, -1], [2, 3], [3, 0], [1, 2]]):
+        b = torch.tensor(bad, dtype=torch.int32, device="cuda")
+        assert kernels.moe_prefill(lay, arena, lay.expert_size, E, b, w, x, True, n, k, out, ws) == 0
+        with pytest.raises(sa.SmoeError) as ei:
+            kernels.sync()
+        assert ei.value.status == c["SMOE_ERR_INVALID_ARG"]
+    kernels.sync()
