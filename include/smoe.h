@@ -162,10 +162,12 @@ uint64_t smoe_qmm_workspace_size(uint32_t in_dim, uint32_t group, uint32_t n_tok
  * with exact dequant and fp32 accumulation (x split into bf16 hi + lo):
  * the QmmCall / encode_dense_matmul_n_tokens of metal/lib.rs:357-380,
  * 684-734 and gpu_matvec.rs:256-302 (shared expert and projections at
- * N > 1). Supported: bits 4 or 3, group 32/64/128, in_dim a multiple of
- * 256 (<= 16384), out_dim a multiple of 256; weights, scales, biases, x, y
- * 16-byte aligned, biases after the scales; workspace 256-byte aligned.
- * Enqueue-only, allocates nothing. */
+ * N > 1). The GEMM takes bits 4 or 3, group 32/64/128, in_dim a
+ * multiple of 256 (<= 16384), out_dim a multiple of 256; weights, scales,
+ * biases, x, y 16-byte aligned, biases after the scales; workspace
+ * 256-byte aligned. Other shapes with in_dim <= 8192 (a multiple of the
+ * group) run smoe_qmv's kernel once per token row (x rows 16-byte
+ * aligned; workspace unused). Enqueue-only, allocates nothing. */
 int smoe_qmm(smoe_handle* h, const smoe_qweights* w, const float* x, float* y, uint32_t out_dim,
              uint32_t in_dim, uint32_t n_tokens, void* workspace, uint64_t workspace_bytes);
 

@@ -271,7 +271,21 @@ int smoe_qmm(smoe_handle* h, const smoe_qweights* w, const float* x, float* y, u
   if (!h || !x || !y || !out_dim || !n_tokens || !workspace) return SMOE_ERR_INVALID_ARG;
   QView v;
   if (int rc = qview(w, in_dim, &v)) return rc;
-  if (!qmm_supported(in_dim, out_dim, w->group_size, w->bits, n_tokens)) return SMOE_ERR_UNSUPPORTED_SHAPE;
+  if (!qmm_supported(in_dim, out_dim, w->group_size, w->bits, n_tokens)) {
+    // Shapes without GEMM tiles (in_dim or out_dim not a multiple of 256,
+    // in_dim up to 8192): one k_qmv per token row, as smoe_qmv computes it.
+    if (in_dim > 8192) return SMOE_ERR_UNSUPPORTED_SHAPE;
+    if (!aligned(x, 0, 16)) return SMOE_ERR_MISALIGNED;
+    if (int rc = use_device(h)) return rc;
+    for (uint32_t t = 0; t < n_tokens; ++t) {
+      bool unsupported = false;
+      const hipError_t e = launch_qmv(v, x + (size_t)t * in_dim, y + (size_t)t * out_dim, out_dim, in_dim,
+                                      h->stream, &unsupported);
+      if (unsupported) return SMOE_ERR_UNSUPPORTED_SHAPE;
+      if (e != hipSuccess) return SMOE_ERR_HIP;
+    }
+    return SMOE_OK;
+  }
   // The GEMM copies weights, scales and biases with 16-byte LDS DMA and
   // addresses biases from the scales (biases after them).
   if (!aligned(w->base, w->packed_offset, 16) || !aligned(w->base, w->scales_offset, 16) ||

@@ -18,6 +18,9 @@ TOL = 1e-3
     (4096, 2048, 32, 4, 33),   # two 32-token blocks
     (1024, 1024, 128, 3, 64),  # packed 3-bit
     (256, 256, 64, 4, 100),    # four blocks, last ragged
+    # Without GEMM tiles (one qmv per token row): Flash-Next's 640 and
+    # 2560, a 7168-wide projection, a 96-input matrix.
+    (640, 2560, 64, 4, 9), (2560, 640, 32, 3, 5), (300, 7168, 64, 4, 3), (64, 96, 32, 4, 17),
 ])
 def test_qmm_matches_oracle(kernels, out_dim, in_dim, group, bits, n):
     import torch
@@ -53,6 +56,6 @@ def test_qmm_argument_errors(kernels):
     ws = torch.empty(need, dtype=torch.uint8, device="cuda")
     small = torch.empty(need // 2, dtype=torch.uint8, device="cuda")
     assert kernels.qmm(w, x, y, 512, 2048, 4, small) == c["SMOE_ERR_WORKSPACE_TOO_SMALL"]
-    assert kernels.qmm(w, x, y, 500, 2048, 4, ws) == c["SMOE_ERR_UNSUPPORTED_SHAPE"]  # out_dim % 256
+    assert kernels.qmm(w, x, y, 500, 2048, 4, ws) == 0  # out_dim % 256: one qmv per token row
     assert kernels.qmm(w, x, y, 512, 2048, 0, ws) == c["SMOE_ERR_INVALID_ARG"]
     assert kernels.qmm(w, x[:, 1:], y, 512, 2044, 4, ws) == c["SMOE_ERR_IN_DIM_NOT_MULTIPLE"]
