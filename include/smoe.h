@@ -354,9 +354,12 @@ int smoe_moe_decode_layers_noalloc(void* stream, const smoe_layer* layers, uint3
  * for all tokens and each token's routed experts run side by side in the
  * same grids. idx_out / w_out (nullable): [n_tokens, k] of the last layer
  * in the reference's slot order. Replaces the T-token pass of
- * decode_multi.rs (moe_dispatch_multi, 445-654). Three-kernel shapes only
- * (else SMOE_ERR_UNSUPPORTED_SHAPE); at hidden 4096, 3 or 4 tokens take a
- * fourth launch per layer (the router kernel in two halves). */
+ * decode_multi.rs (moe_dispatch_multi, 445-654). At hidden 4096, 3 or 4
+ * tokens take a fourth launch per layer (the router kernel in two
+ * halves). Shapes without a three-kernel instance (and
+ * SMOE_OPT_DECODE_PATH = 1) decode each token through the per-phase chain
+ * in turn, bit-identical to smoe_moe_decode_layers on that token; with
+ * SMOE_OPT_DECODE_PATH = 3 they return SMOE_ERR_UNSUPPORTED_SHAPE. */
 int smoe_moe_decode_tokens(smoe_handle* h, const smoe_layer* layers, uint32_t n_layers,
                            const void* const* norm_w, float eps, uint32_t n_tokens, const float* input,
                            float* residual_io, float* work, int32_t* idx_out, float* w_out);

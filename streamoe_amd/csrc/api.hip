@@ -600,25 +600,12 @@ int smoe_moe_decode_layer(smoe_handle* h, const smoe_layer* layer, const float* 
   return decode_layer(h, layer, input, h_mid, hidden_out, idx_out, w_out);
 }
 
-int smoe_moe_decode_layers(smoe_handle* h, const smoe_layer* layers, uint32_t n_layers,
-                           const void* const* norm_w, float eps, const float* input,
-                           float* residual_io, float* work) {
-  if (!h || !layers || !n_layers || !input || !residual_io || !work) return SMOE_ERR_INVALID_ARG;
-  for (uint32_t l = 0; l < n_layers; ++l) {
-    if (int rc = check_layer(h, &layers[l])) return rc;
-    if (layers[l].shape.hidden != layers[0].shape.hidden) return SMOE_ERR_INVALID_ARG;
-    if (norm_w && l > 0 && !norm_w[l]) return SMOE_ERR_INVALID_ARG;
-  }
-  if (!aligned(input, 0, 16) || !aligned(residual_io, 0, 16) || !aligned(work, 0, 16))
-    return SMOE_ERR_MISALIGNED;
-  if (int rc = use_device(h)) return rc;
+// One token through the layers on the per-phase kernels (RMSNorm launch,
+// then one layer), with the last layer's idx / w when asked.
+static int decode_chain_phases(smoe_handle* h, const smoe_layer* layers, uint32_t n_layers,
+                               const void* const* norm_w, float eps, const float* input, float* residual_io,
+                               float* work, int32_t* idx_out, float* w_out) {
   const uint32_t H = layers[0].shape.hidden;
-  if (h->decode_path == 0 || h->decode_path == 3) {
-    bool all = true;
-    for (uint32_t l = 0; l < n_layers; ++l) all = all && fused_ok(&layers[l]);
-    if (all) return decode_chain_fused(handle_scratch(h), layers, n_layers, norm_w, eps, input, residual_io);
-    if (h->decode_path == 3) return SMOE_ERR_UNSUPPORTED_SHAPE;
-  }
   for (uint32_t l = 0; l < n_layers; ++l) {
     const float* x = input;
     if (l > 0) {
@@ -631,10 +618,33 @@ int smoe_moe_decode_layers(smoe_handle* h, const smoe_layer* layers, uint32_t n_
         x = residual_io;
       }
     }
-    if (int rc = decode_layer(h, &layers[l], x, residual_io, residual_io, nullptr, nullptr))
+    const bool last = l + 1 == n_layers;
+    if (int rc = decode_layer(h, &layers[l], x, residual_io, residual_io, last ? idx_out : nullptr,
+                              last ? w_out : nullptr))
       return rc;
   }
   return SMOE_OK;
+}
+
+int smoe_moe_decode_layers(smoe_handle* h, const smoe_layer* layers, uint32_t n_layers,
+                           const void* const* norm_w, float eps, const float* input,
+                           float* residual_io, float* work) {
+  if (!h || !layers || !n_layers || !input || !residual_io || !work) return SMOE_ERR_INVALID_ARG;
+  for (uint32_t l = 0; l < n_layers; ++l) {
+    if (int rc = check_layer(h, &layers[l])) return rc;
+    if (layers[l].shape.hidden != layers[0].shape.hidden) return SMOE_ERR_INVALID_ARG;
+    if (norm_w && l > 0 && !norm_w[l]) return SMOE_ERR_INVALID_ARG;
+  }
+  if (!aligned(input, 0, 16) || !aligned(residual_io, 0, 16) || !aligned(work, 0, 16))
+    return SMOE_ERR_MISALIGNED;
+  if (int rc = use_device(h)) return rc;
+  if (h->decode_path == 0 || h->decode_path == 3) {
+    bool all = true;
+    for (uint32_t l = 0; l < n_layers; ++l) all = all && fused_ok(&layers[l]);
+    if (all) return decode_chain_fused(handle_scratch(h), layers, n_layers, norm_w, eps, input, residual_io);
+    if (h->decode_path == 3) return SMOE_ERR_UNSUPPORTED_SHAPE;
+  }
+  return decode_chain_phases(h, layers, n_layers, norm_w, eps, input, residual_io, work, nullptr, nullptr);
 }
 
 int smoe_moe_decode_layers_noalloc(void* stream, const smoe_layer* layers, uint32_t n_layers,
@@ -683,15 +693,29 @@ int smoe_moe_decode_tokens(smoe_handle* h, const smoe_layer* layers, uint32_t n_
                            float* residual_io, float* work, int32_t* idx_out, float* w_out) {
   if (!h || !layers || !n_layers || !input || !residual_io || !work) return SMOE_ERR_INVALID_ARG;
   if (n_tokens < 1 || n_tokens > kMaxDecodeTokens) return SMOE_ERR_INVALID_ARG;
+  bool all = h->decode_path != 1;
   for (uint32_t l = 0; l < n_layers; ++l) {
     if (int rc = check_layer(h, &layers[l])) return rc;
     if (layers[l].shape.hidden != layers[0].shape.hidden) return SMOE_ERR_INVALID_ARG;
     if (norm_w && l > 0 && !norm_w[l]) return SMOE_ERR_INVALID_ARG;
-    if (!fused_ok(&layers[l])) return SMOE_ERR_UNSUPPORTED_SHAPE;
+    all = all && fused_ok(&layers[l]);
   }
+  if (!all && h->decode_path == 3) return SMOE_ERR_UNSUPPORTED_SHAPE;
   if (!aligned(input, 0, 16) || !aligned(residual_io, 0, 16) || !aligned(work, 0, 16))
     return SMOE_ERR_MISALIGNED;
   if (int rc = use_device(h)) return rc;
+  if (!all) {
+    // Shapes without a three-kernel instance (or the per-phase path asked
+    // for): each token through the per-phase chain in turn.
+    const uint32_t H = layers[0].shape.hidden, K = layers[n_layers - 1].k;
+    for (uint32_t t = 0; t < n_tokens; ++t)
+      if (int rc = decode_chain_phases(h, layers, n_layers, norm_w, eps, input + (size_t)t * H,
+                                       residual_io + (size_t)t * H, work + (size_t)t * H,
+                                       idx_out ? idx_out + (size_t)t * K : nullptr,
+                                       w_out ? w_out + (size_t)t * K : nullptr))
+        return rc;
+    return SMOE_OK;
+  }
   for (uint32_t l = 0; l < n_layers; ++l) {
     const uint16_t* nw = (norm_w && l > 0) ? (const uint16_t*)norm_w[l] : nullptr;
     const bool last = l + 1 == n_layers;

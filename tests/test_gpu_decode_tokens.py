@@ -67,6 +67,15 @@ def test_tokens_hidden_4096(kernels, T):
     torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize("T", [1, 3])
+def test_tokens_other_shapes_take_per_token_chain(kernels, T):
+    """Shapes without a three-kernel instance (Qwen3.8-Flash-Next 2560 x 640,
+    top-10): each token through the per-phase chain, bit for bit its own
+    smoe_moe_decode_layers, within 1e-3 of the oracle."""
+    c = _chain(kernels, 2, 64, 10, 4, seed=7700 + T, norm_sigma=0.1, I=640, H=2560)
+    _match_single_token(kernels, c, T, 4, 7800 + T)
+
+
 def test_tokens_slot_order_of_last_layer(kernels):
     """idx_out / w_out of the last layer: the reference's exact slot order
     per token (moe_router.rs:83-141)."""
@@ -110,11 +119,18 @@ def test_tokens_argument_errors(kernels):
     codes = _abi.CODES
     assert kernels.moe_decode_tokens(c["layers"], None, 1e-6, 0, xs, resid, work) == codes["SMOE_ERR_INVALID_ARG"]
     assert kernels.moe_decode_tokens(c["layers"], None, 1e-6, 5, xs, resid, work) == codes["SMOE_ERR_INVALID_ARG"]
-    # No three-kernel instance for hidden 1024: unsupported, not a silent fallback.
+    # No three-kernel instance for hidden 1024: unsupported when only the
+    # three-kernel path is allowed, else each token through the per-phase chain.
     lay = sa.ExpertLayout(1024, 512, 4, 64)
     a = torch.zeros(8 * lay.expert_size, dtype=torch.uint8, device="cuda")
     r = torch.zeros((8, 1024), dtype=torch.float32, device="cuda")
     L = kernels.layer(lay, a, lay.expert_size, 8, 2, True, r)
     x4 = torch.zeros((2, 1024), dtype=torch.float32, device="cuda")
-    assert kernels.moe_decode_tokens([L], None, 1e-6, 2, x4, x4.clone(), x4.clone()) == \
-        codes["SMOE_ERR_UNSUPPORTED_SHAPE"]
+    kernels.set_decode_path(3)
+    try:
+        assert kernels.moe_decode_tokens([L], None, 1e-6, 2, x4, x4.clone(), x4.clone()) == \
+            codes["SMOE_ERR_UNSUPPORTED_SHAPE"]
+    finally:
+        kernels.set_decode_path(0)
+    assert kernels.moe_decode_tokens([L], None, 1e-6, 2, x4, x4.clone(), x4.clone()) == 0
+    kernels.sync()
