@@ -417,7 +417,7 @@ def gpu_batched_experts_forward(kernels: Kernels, layout: ExpertLayout, actual_k
 
     if actual_k < 1 or actual_k > MAX_K:
         raise SmoeError(_abi.CODES["SMOE_ERR_BAD_K"], "gpu_batched_experts_forward")
-    data = np.ascontiguousarray(np.frombuffer(bytes(expert_data), np.uint8))
+    data = np.frombuffer(bytes(expert_data), np.uint8).copy()  # writable, for torch.from_numpy
     if data.size != actual_k * layout.expert_size:
         raise SmoeError(_abi.CODES["SMOE_ERR_INVALID_ARG"], "expert_data length")
     dev = torch.device("cuda", kernels.device)
