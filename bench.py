@@ -317,6 +317,8 @@ def run_decode(args, c):
         "vs_baseline": None,
         "dtype": DECODE_DTYPE,
         "data": "synthetic (seeded, generated on the device)",
+        "seeds": {"experts": "1000 + layer", "router": "2000 + layer", "shared_expert": "3000 + layer",
+                  "shared_gate": "4000 + layer", "x": 5000},
         "config": {"workload": c["name"], "hidden": H, "experts": E, "top_k": k, "inter": I, "bits": c["bits"],
                    "group": 64, "layers": nl, "shared_expert": c["shared"], "tokens": T,
                    "mode": "hipgraph" if graph is not None else "eager"},
@@ -398,7 +400,8 @@ def run_lm_head(args, c):
         "metric": "4-bit MoE expert decode µs/layer + achieved HBM GB/s (% of peak), 1 GPU",
         "value": round(us, 3), "unit": "us/token (LM head qmv + argmax)", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(us / 1e3, 5), "higher_is_better": False, "scaling": "weak",
-        "vs_baseline": None, "dtype": "u4 codes, f32 compute", "data": "synthetic (seeded, generated on the device)",
+        "vs_baseline": None, "dtype": DECODE_DTYPE, "data": "synthetic (seeded, generated on the device)",
+        "seeds": {"codes": "torch.Generator 0xC1", "scales": 0xC11, "biases": 0xC12, "x": 0xC13},
         "config": {"workload": c["name"], "vocab": V, "hidden": H, "bits": 4, "group": G,
                    "mode": "hipgraph" if graph is not None else "eager"},
         "gbps": round(achieved, 1), "pct_of_hbm_peak": round(100 * achieved / HBM_PEAK_GBS, 2),
@@ -477,8 +480,10 @@ def run_prefill(args, c):
         "metric": "4-bit MoE expert decode µs/layer + achieved HBM GB/s (% of peak), 1 GPU",
         "value": round(us, 2), "unit": "us/layer (512-token prefill)", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(us / 1e3, 5), "higher_is_better": False, "scaling": "weak",
-        "vs_baseline": None, "dtype": "u4 codes, bf16 MFMA, f32 accumulate",
+        "vs_baseline": None,
+        "dtype": "u4/u3 codes exact in bf16 (gate/up) and fp16 (down) MFMA, f32 accumulate, fp16 activations",
         "data": "synthetic (seeded, generated on the device)",
+        "seeds": {"experts": 0xC4, "routing": "zipf s=1.1, seed 0xC4", "x": 0xC41},
         "config": {"workload": c["name"], "tokens": n, "hidden": H, "experts": E, "top_k": k, "inter": I,
                    "bits": bits, "group": 64, "experts_hit": int(len(hit)),
                    "mode": "hipgraph" if graph is not None else "eager"},
