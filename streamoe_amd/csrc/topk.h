@@ -43,6 +43,12 @@ __device__ __forceinline__ uint32_t orderable(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// Lane i receives lane i + 1's value (DPP wave_shl:1, one VALU op instead
+// of an LDS-crossbar permute); lane 63 keeps its own.
+__device__ __forceinline__ uint32_t wave_next_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x130, 0xF, 0xF, false);
+}
+
 template <int P>
 __device__ void exact_topk(const float (&v)[P], uint32_t k, int lane, int32_t* out_idx,
                            float* out_val) {
@@ -76,9 +82,9 @@ __device__ void exact_topk(const float (&v)[P], uint32_t k, int lane, int32_t* o
     const bool less = lane >= 1 && lane < (int)k && key < nkey;
     const int p = __popcll(__ballot(less));  // new position among the k
     // Lane q < p takes lane q+1's entry; lane p takes the new one.
-    const uint64_t kn = __shfl_down(key, 1, 64);
-    const int32_t in = __shfl_down(qidx, 1, 64);
-    const float vn = __shfl_down(qval, 1, 64);
+    const uint64_t kn = ((uint64_t)wave_next_u32((uint32_t)(key >> 32)) << 32) | wave_next_u32((uint32_t)key);
+    const int32_t in = (int32_t)wave_next_u32((uint32_t)qidx);
+    const float vn = __uint_as_float(wave_next_u32(__float_as_uint(qval)));
     if (lane < p) {
       key = kn;
       qidx = in;
@@ -97,6 +103,65 @@ __device__ void exact_topk(const float (&v)[P], uint32_t k, int lane, int32_t* o
     out_idx[slot] = qidx;
     out_val[slot] = qval;
   }
+}
+
+// exact_topk on values held transposed: v[e] of lane l is element e * 64 + l.
+// The same scan and result (the reference's running minimum, slot order =
+// replacement order): the 64-index chunks are walked in order, and in each
+// one a compare and a ballot over the lanes not yet passed find the next
+// element that beats the slot minimum, so an event costs a few scalar
+// steps instead of a pass over the lane's P values.
+// Returns, in lanes < k, the element index the lane's queue entry holds
+// (the slots' contents in queue order), -1 elsewhere; out_idx / out_val may
+// be null.
+template <int P>
+__device__ int32_t exact_topk_t(const float (&v)[P], uint32_t k, int lane, int32_t* out_idx, float* out_val) {
+  uint64_t key = lane < (int)k ? (((uint64_t)orderable(-1e30f) << 32) | (uint32_t)lane) : ~0ull;
+  int32_t qidx = 0;
+  float qval = -1e30f;
+  // Queue lanes 1 .. k-1 (k <= 64): where a new entry may be placed.
+  const uint64_t qmask = (k >= 64 ? ~0ull : ((1ull << k) - 1)) & ~1ull;
+#pragma unroll
+  for (int e = 0; e < P; ++e) {
+    uint64_t pend = ~0ull;  // lanes of chunk e not yet passed
+    for (int guard = 0; guard < 64; ++guard) {
+      const float hval = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(qval)));
+      const uint64_t hit = __ballot(v[e] > hval) & pend;
+      if (hit == 0) break;
+      const int first = __builtin_ctzll(hit);
+      pend = first == 63 ? 0ull : pend & (~0ull << (first + 1));
+      const float pj = readlane_f(v[e], first);
+      const uint32_t hslot = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)key);
+      const uint64_t nkey = ((uint64_t)orderable(pj) << 32) | hslot;
+      const int p = __popcll(__ballot(key < nkey) & qmask);  // new position among the k
+      const uint64_t kn = ((uint64_t)wave_next_u32((uint32_t)(key >> 32)) << 32) | wave_next_u32((uint32_t)key);
+      const int32_t in = (int32_t)wave_next_u32((uint32_t)qidx);
+      const float vn = __uint_as_float(wave_next_u32(__float_as_uint(qval)));
+      // Lane q < p takes lane q+1's entry, lane p the new one (selects).
+      const bool sh = lane < p, at = lane == p;
+      key = sh ? kn : (at ? nkey : key);
+      qidx = sh ? in : (at ? e * 64 + first : qidx);
+      qval = sh ? vn : (at ? pj : qval);
+    }
+  }
+  if (lane < (int)k) {
+    const uint32_t slot = (uint32_t)key;
+    if (out_idx) out_idx[slot] = qidx;
+    if (out_val) out_val[slot] = qval;
+  }
+  return lane < (int)k ? qidx : -1;
+}
+
+// Bitwise OR over the wave, valid in lane 63 (DPP row shifts, then the
+// row broadcasts).
+__device__ __forceinline__ uint32_t wave_or_last(uint32_t v) {
+  v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, false);
+  v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, false);
+  v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, false);
+  v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, false);
+  v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false);
+  v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, false);
+  return v;
 }
 
 // Top-k SET: the k largest values (ascending index order in set_ids) when

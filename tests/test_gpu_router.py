@@ -109,6 +109,10 @@ def test_noaux_cogito_fixture(kernels):
 @pytest.mark.parametrize("T,E,n_group,topk_group,k", [
     (1, 256, 8, 4, 8), (64, 256, 8, 4, 8), (16, 64, 4, 2, 6), (8, 512, 16, 3, 10),
     (4, 1024, 64, 8, 16), (6, 128, 1, 1, 8), (5, 96, 3, 3, 4), (9, 8, 2, 1, 2), (3, 160, 32, 32, 16),
+    # every power-of-two group size (1 .. 64 experts per group: the lane
+    # path) and two that are not (the scan path)
+    (4, 64, 64, 16, 8), (4, 128, 64, 9, 8), (4, 256, 64, 7, 8), (4, 256, 32, 5, 8), (4, 256, 16, 3, 8),
+    (4, 256, 4, 2, 8), (4, 192, 16, 5, 8), (4, 240, 5, 2, 8),
 ])
 def test_noaux_random_vs_oracle(kernels, T, E, n_group, topk_group, k):
     rng = np.random.default_rng(E * 7 + T + k)
