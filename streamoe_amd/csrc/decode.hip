@@ -14,6 +14,7 @@
 //                    no atomics.
 #include "common.h"
 #include "kernels.h"
+#include "topk.h"
 
 namespace smoe {
 
@@ -423,18 +424,12 @@ hipError_t launch_router_logits(const float* W, const float* gate_w, const float
 }
 
 // ---------------------------------------------------------------------------
-// Top-k: one wave per token. Lane l holds elements [l*P, l*P + P).
-// Slots live in lanes 0..k-1. The reference scans the scores in index
-// order and replaces the running-minimum slot (lowest slot on ties) with
-// every score strictly greater than it (moe_router.rs:83-124). Scores
-// that do not beat the current minimum can never beat a later one, so
-// the scan jumps straight to the next index whose score beats the
-// current minimum: a ballot over the lanes finds it.
+// Top-k: one wave per token, lane l holding elements l, l + 64, ... The
+// reference scans the scores in index order and replaces the running-
+// minimum slot (lowest slot on ties) with every score strictly greater
+// than it (moe_router.rs:83-124); exact_topk_t does the same scan, one
+// ballot per replacement.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t orderable(float f) {
-  const uint32_t u = __float_as_uint(f);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
 
 template <int P>
 __global__ __launch_bounds__(64) void k_topk(const float* __restrict__ scores, uint32_t n,
@@ -443,10 +438,12 @@ __global__ __launch_bounds__(64) void k_topk(const float* __restrict__ scores, u
   const uint32_t t = blockIdx.x;
   const int lane = threadIdx.x;
   const float* s = scores + (size_t)t * n;
+  // Lane l holds elements l, l + 64, ... (coalesced loads; the layout
+  // exact_topk_t scans).
   float v[P];
 #pragma unroll
   for (int e = 0; e < P; ++e) {
-    const uint32_t j = lane * P + e;
+    const uint32_t j = e * 64 + lane;
     v[e] = j < n ? s[j] : -INFINITY;
   }
   if (softmax) {
@@ -458,7 +455,7 @@ __global__ __launch_bounds__(64) void k_topk(const float* __restrict__ scores, u
     float sum = 0.f;
 #pragma unroll
     for (int e = 0; e < P; ++e) {
-      const uint32_t j = lane * P + e;
+      const uint32_t j = e * 64 + lane;
       v[e] = j < n ? expf(v[e] - m) : 0.f;
       sum += v[e];
     }
@@ -466,56 +463,26 @@ __global__ __launch_bounds__(64) void k_topk(const float* __restrict__ scores, u
     const float inv = 1.0f / sum;
 #pragma unroll
     for (int e = 0; e < P; ++e) {
-      const uint32_t j = lane * P + e;
+      const uint32_t j = e * 64 + lane;
       v[e] = j < n ? v[e] * inv : -INFINITY;
     }
   }
-  // Slot state (lane < k): value and index; other lanes hold +inf so they
-  // never become the minimum.
-  float sval = lane < (int)k ? -1e30f : INFINITY;
-  int32_t sidx = 0;
-  int32_t pos = -1;
-  while (true) {
-    // Minimum slot: smallest value, lowest slot on ties (slots in lanes 0..15).
-    uint64_t key = ((uint64_t)orderable(sval) << 32) | (uint32_t)lane;
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) {
-      const uint64_t other = __shfl_xor(key, o, 64);
-      key = other < key ? other : key;
-    }
-    key = __shfl(key, 0, 64);
-    const int mlane = (int)(key & 0xFFFFFFFFu);
-    const float mval = __shfl(sval, mlane, 64);
-    // First index > pos whose score beats the minimum.
-    int32_t cand = -1;
-    float cval = 0.f;
-#pragma unroll
-    for (int e = P - 1; e >= 0; --e) {
-      const int32_t j = lane * P + e;
-      if (j > pos && v[e] > mval) {
-        cand = j;
-        cval = v[e];
-      }
-    }
-    const uint64_t ball = __ballot(cand >= 0);
-    if (ball == 0) break;
-    const int first = __ffsll((unsigned long long)ball) - 1;
-    const int32_t j = __shfl(cand, first, 64);
-    const float pj = __shfl(cval, first, 64);
-    if (lane == mlane) {
-      sval = pj;
-      sidx = j;
-    }
-    pos = j;
-  }
+  // The reference's running-minimum top-k (moe_router.rs:83-124); lane s < k
+  // then holds slot s.
+  __shared__ int32_t sid[kMaxK];
+  __shared__ float sval[kMaxK];
+  exact_topk_t<P>(v, k, lane, sid, sval);
+  __syncthreads();
+  const int32_t sidx = lane < (int)k ? sid[lane] : 0;
+  const float sv = lane < (int)k ? sval[lane] : 0.f;
   // normalize_weights, moe_router.rs:130-141: sequential sum in slot order.
-  float w = sval;
+  float w = sv;
   if (normalize) {
     float sum = 0.f;
-    for (uint32_t i = 0; i < k; ++i) sum += __shfl(sval, i, 64);
+    for (uint32_t i = 0; i < k; ++i) sum += readlane_f(sv, (int)i);
     if (sum > 0.f) {
       const float inv = 1.0f / sum;
-      w = sval * inv;
+      w = sv * inv;
     }
   }
   if (lane < (int)k) {
