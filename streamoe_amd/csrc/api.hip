@@ -480,12 +480,17 @@ static int check_layer(smoe_handle* h, const smoe_layer* L) {
   return SMOE_OK;
 }
 
+// With norm_w, `input` is the residual: the router kernel normalises it
+// (bf16 weights norm_w, eps) and stores the normalised row in x_norm, which
+// the expert kernels then read.
 static int decode_layer(smoe_handle* h, const smoe_layer* L, const float* input,
-                        const float* h_mid, float* hidden_out, int32_t* idx_out, float* w_out) {
+                        const float* h_mid, float* hidden_out, int32_t* idx_out, float* w_out,
+                        const uint16_t* norm_w = nullptr, float eps = 0.f, float* x_norm = nullptr) {
   const smoe_expert_shape& s = L->shape;
   hipError_t e = launch_router_logits(L->router_w, L->shared_expert ? L->shared_gate : nullptr,
                                       input, 1, L->n_experts, s.hidden, h->logits, h->gate,
-                                      h->stream);
+                                      h->stream, norm_w, eps, x_norm);
+  if (norm_w) input = x_norm;
   if (e != hipSuccess) return SMOE_ERR_HIP;
   RouteOut ro{};
   ro.idx = idx_out;
@@ -605,22 +610,14 @@ int smoe_moe_decode_layer(smoe_handle* h, const smoe_layer* layer, const float* 
 static int decode_chain_phases(smoe_handle* h, const smoe_layer* layers, uint32_t n_layers,
                                const void* const* norm_w, float eps, const float* input, float* residual_io,
                                float* work, int32_t* idx_out, float* w_out) {
-  const uint32_t H = layers[0].shape.hidden;
   for (uint32_t l = 0; l < n_layers; ++l) {
-    const float* x = input;
-    if (l > 0) {
-      if (norm_w) {
-        const hipError_t e =
-            launch_rmsnorm(residual_io, (const uint16_t*)norm_w[l], eps, H, work, h->stream);
-        if (e != hipSuccess) return SMOE_ERR_HIP;
-        x = work;
-      } else {
-        x = residual_io;
-      }
-    }
     const bool last = l + 1 == n_layers;
+    // Layers after the first read the residual; with norm weights their
+    // router kernel applies the RMSNorm and leaves the normalised row in work.
+    const float* x = l > 0 ? residual_io : input;
+    const uint16_t* nw = (l > 0 && norm_w) ? (const uint16_t*)norm_w[l] : nullptr;
     if (int rc = decode_layer(h, &layers[l], x, residual_io, residual_io, last ? idx_out : nullptr,
-                              last ? w_out : nullptr))
+                              last ? w_out : nullptr, nw, eps, work))
       return rc;
   }
   return SMOE_OK;

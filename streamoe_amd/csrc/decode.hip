@@ -383,20 +383,53 @@ hipError_t launch_argmax(const float* v, uint32_t n, int32_t* out, float* part_v
 // Router logits: one 256-thread block per (expert row, token); row
 // n_experts is the shared-expert gate when gate_w is not null.
 // ---------------------------------------------------------------------------
+// With norm_w, x is the residual and every block applies the next layer's
+// RMSNorm itself (rms_norm_bf16_n_tokens_cpu, backend/cpu/mod.rs:406-430:
+// inv = 1 / sqrt(sum_sq / dim + eps), x = r * inv * w; each block forms the
+// same sum in the same order), and block (0, t) stores the normalised row
+// in x_out for the expert kernels: one launch instead of a norm kernel
+// before the router.
 __global__ __launch_bounds__(256) void k_router_logits(const float* __restrict__ W,
                                                        const float* __restrict__ gate_w,
                                                        const float* __restrict__ x,
                                                        uint32_t n_experts, uint32_t hidden,
                                                        float* __restrict__ logits,
-                                                       float* __restrict__ gate_scores) {
+                                                       float* __restrict__ gate_scores,
+                                                       const uint16_t* __restrict__ norm_w, float eps,
+                                                       float* __restrict__ x_out) {
   __shared__ float red[4];
+  __shared__ float inv_sh;
   const uint32_t e = blockIdx.x, t = blockIdx.y;
   const float* row = e < n_experts ? W + (size_t)e * hidden : gate_w;
   const float* xt = x + (size_t)t * hidden;
+  float inv = 1.f;
+  if (norm_w) {
+    float ss = 0.f;
+    for (uint32_t c = threadIdx.x * 4; c < hidden; c += 1024) {
+      const float4 r4 = *reinterpret_cast<const float4*>(xt + c);
+      ss = __builtin_fmaf(r4.x, r4.x, ss);
+      ss = __builtin_fmaf(r4.y, r4.y, ss);
+      ss = __builtin_fmaf(r4.z, r4.z, ss);
+      ss = __builtin_fmaf(r4.w, r4.w, ss);
+    }
+    ss = group_sum<64>(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    if (threadIdx.x == 0) inv_sh = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)hidden + eps);
+    __syncthreads();
+    inv = inv_sh;
+  }
   float acc = 0.f;
   for (uint32_t c = threadIdx.x * 4; c < hidden; c += 1024) {
     const f32x4 w4 = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(row + c));
-    const float4 x4 = *reinterpret_cast<const float4*>(xt + c);
+    float4 x4 = *reinterpret_cast<const float4*>(xt + c);
+    if (norm_w) {
+      x4.x = x4.x * inv * bf16f(norm_w[c]);
+      x4.y = x4.y * inv * bf16f(norm_w[c + 1]);
+      x4.z = x4.z * inv * bf16f(norm_w[c + 2]);
+      x4.w = x4.w * inv * bf16f(norm_w[c + 3]);
+      if (e == 0) *reinterpret_cast<float4*>(x_out + (size_t)t * hidden + c) = x4;
+    }
     acc = __builtin_fmaf(w4.x, x4.x, acc);
     acc = __builtin_fmaf(w4.y, x4.y, acc);
     acc = __builtin_fmaf(w4.z, x4.z, acc);
@@ -416,10 +449,11 @@ __global__ __launch_bounds__(256) void k_router_logits(const float* __restrict__
 
 hipError_t launch_router_logits(const float* W, const float* gate_w, const float* x,
                                 uint32_t n_tokens, uint32_t n_experts, uint32_t hidden,
-                                float* logits, float* gate_scores, hipStream_t st) {
+                                float* logits, float* gate_scores, hipStream_t st,
+                                const uint16_t* norm_w, float eps, float* x_out) {
   const uint32_t rows = n_experts + (gate_w ? 1 : 0);
   hipLaunchKernelGGL(k_router_logits, dim3(rows, n_tokens), dim3(256), 0, st, W, gate_w, x,
-                     n_experts, hidden, logits, gate_scores);
+                     n_experts, hidden, logits, gate_scores, norm_w, eps, x_out);
   return hipGetLastError();
 }
 
@@ -911,41 +945,6 @@ hipError_t launch_prefill_tokens(const BlobGeom& g, const uint8_t* experts, uint
     if (*unsupported) break;
   }
   return e;
-}
-
-// ---------------------------------------------------------------------------
-// RMSNorm with bf16 weights (rms_norm_bf16_n_tokens_cpu, backend/cpu/mod.rs:
-// 406-430; GPU rms_norm_sum_sq + rms_norm_apply_bf16, shaders.metal:
-// 1454-1530), or a copy when w is null. One block.
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(1024) void k_rmsnorm(const float* __restrict__ r,
-                                                  const uint16_t* __restrict__ w, float eps,
-                                                  uint32_t dim, float* __restrict__ x) {
-  __shared__ float red[16];
-  __shared__ float inv_sh;
-  if (w) {
-    float acc = 0.f;
-    for (uint32_t i = threadIdx.x; i < dim; i += blockDim.x) acc += r[i] * r[i];
-    acc = group_sum<64>(acc);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      float s = 0.f;
-      for (uint32_t i = 0; i < (blockDim.x >> 6); ++i) s += red[i];
-      inv_sh = 1.0f / sqrtf(s / (float)dim + eps);
-    }
-    __syncthreads();
-    const float inv = inv_sh;
-    for (uint32_t i = threadIdx.x; i < dim; i += blockDim.x) x[i] = r[i] * inv * bf16f(w[i]);
-  } else {
-    for (uint32_t i = threadIdx.x; i < dim; i += blockDim.x) x[i] = r[i];
-  }
-}
-
-hipError_t launch_rmsnorm(const float* r, const uint16_t* w, float eps, uint32_t dim, float* x_out,
-                          hipStream_t st) {
-  hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(1024), 0, st, r, w, eps, dim, x_out);
-  return hipGetLastError();
 }
 
 }  // namespace smoe

@@ -183,9 +183,12 @@ hipError_t launch_argmax(const float* v, uint32_t n, int32_t* out, float* part_v
 
 // logits[t, e] = W[e] . x[t] for e < n_experts; gate_scores[t] =
 // gate_w . x[t] when gate_w is not null.
+// With norm_w, x is the residual: the kernel applies the bf16-weighted
+// RMSNorm itself and writes the normalised rows to x_out.
 hipError_t launch_router_logits(const float* W, const float* gate_w, const float* x,
                                 uint32_t n_tokens, uint32_t n_experts, uint32_t hidden,
-                                float* logits, float* gate_scores, hipStream_t st);
+                                float* logits, float* gate_scores, hipStream_t st,
+                                const uint16_t* norm_w = nullptr, float eps = 0.f, float* x_out = nullptr);
 // Softmax (optional) + running-min top-k + optional renorm, one wave per token.
 hipError_t launch_topk(const float* scores, uint32_t n_tokens, uint32_t n, uint32_t k,
                        bool softmax, bool normalize, const RouteOut& out, hipStream_t st);
@@ -206,10 +209,6 @@ hipError_t launch_down_combine(const BlobGeom& routed, const BlobGeom& shared,
                                const FfnTable* tab_dev, const FfnTable& tab_val, uint32_t n_slots,
                                const float* act, const float* h_mid, const float* shared_out,
                                float* hidden_out, hipStream_t st, bool* unsupported);
-// x_out = RMSNorm(r) * w (bf16), or a copy of r when w is null.
-hipError_t launch_rmsnorm(const float* r, const uint16_t* w, float eps, uint32_t dim, float* x_out,
-                          hipStream_t st);
-
 // Streaming-read diagnostic over `bytes` (multiple of 16) with
 // kStreamBlocks blocks; sink: kStreamBlocks u32.
 constexpr uint32_t kStreamBlocks = 2048;
