@@ -731,21 +731,23 @@ __global__ __launch_bounds__(64) void k_down_combine(BlobGeom routed, BlobGeom s
   const uint32_t k = tab_dev ? tab_dev->k : tab_val.k;
   const uint32_t has_shared = tab_dev ? tab_dev->has_shared : tab_val.has_shared;
 
+  // Every slot up to MAXS is loaded and computed without a branch (slots
+  // past k re-read slot k - 1 and are not added), so the loads and lane
+  // reductions of different slots overlap instead of running one by one.
   Raw<BITS> raw[MAXS][CPL];
   Raw<4> rsh[CPL];
   float sv[MAXS][CPL], bv[MAXS][CPL], ssh[CPL], bsh[CPL];
 #pragma unroll
   for (int s = 0; s < MAXS; ++s) {
-    if (s < (int)k) {
-      const uint8_t* blob = tab_dev ? tab_dev->blob[s] : tab_val.blob[s];
+    const uint32_t sl = (uint32_t)s < k ? (uint32_t)s : k - 1;
+    const uint8_t* blob = tab_dev ? tab_dev->blob[sl] : tab_val.blob[sl];
 #pragma unroll
-      for (int i = 0; i < CPL; ++i) {
-        const uint32_t c = PAD ? pad_chunk(lch + L * i, cpr) : lch + L * i;
-        raw[s][i] = load_raw<BITS>(blob + routed.w[2] + (size_t)row * ROW_BYTES + c * CB);
-        const size_t gi = ((size_t)row * gpr + (c >> cpg_shift)) * 2;
-        sv[s][i] = bf16f(*reinterpret_cast<const uint16_t*>(blob + routed.s[2] + gi));
-        bv[s][i] = bf16f(*reinterpret_cast<const uint16_t*>(blob + routed.b[2] + gi));
-      }
+    for (int i = 0; i < CPL; ++i) {
+      const uint32_t c = PAD ? pad_chunk(lch + L * i, cpr) : lch + L * i;
+      raw[s][i] = load_raw<BITS>(blob + routed.w[2] + (size_t)row * ROW_BYTES + c * CB);
+      const size_t gi = ((size_t)row * gpr + (c >> cpg_shift)) * 2;
+      sv[s][i] = bf16f(*reinterpret_cast<const uint16_t*>(blob + routed.s[2] + gi));
+      bv[s][i] = bf16f(*reinterpret_cast<const uint16_t*>(blob + routed.b[2] + gi));
     }
   }
   if (has_shared) {
@@ -760,24 +762,32 @@ __global__ __launch_bounds__(64) void k_down_combine(BlobGeom routed, BlobGeom s
     }
   }
 
+  float o[MAXS];
+#pragma unroll
+  for (int s = 0; s < MAXS; ++s) {
+    const uint32_t sl = (uint32_t)s < k ? (uint32_t)s : k - 1;
+    float part = 0.f;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      float a[kChunk];
+      if (PAD)
+        load_x32_pad(act + (size_t)sl * I, lch + L * i, cpr, a);
+      else
+        load_x32(act + (size_t)sl * I + (size_t)(lch + L * i) * kChunk, a);
+      part += chunk_dot<BITS>(raw[s][i], a, xsum(a), sv[s][i], bv[s][i]);
+    }
+    o[s] = part;
+  }
+#pragma unroll
+  for (int st = L / 2; st > 0; st >>= 1)
+#pragma unroll
+    for (int s = 0; s < MAXS; ++s) o[s] += __shfl_xor(o[s], st, kWave);
+  // moe = fma(out_k, w_k, moe) in slot order (deferred.rs:458-466).
   float moe = 0.f;
 #pragma unroll
   for (int s = 0; s < MAXS; ++s) {
-    if (s < (int)k) {
-      float part = 0.f;
-#pragma unroll
-      for (int i = 0; i < CPL; ++i) {
-        float a[kChunk];
-        if (PAD)
-          load_x32_pad(act + (size_t)s * I, lch + L * i, cpr, a);
-        else
-          load_x32(act + (size_t)s * I + (size_t)(lch + L * i) * kChunk, a);
-        part += chunk_dot<BITS>(raw[s][i], a, xsum(a), sv[s][i], bv[s][i]);
-      }
-      const float o = group_sum<L>(part);
-      const float w = tab_dev ? tab_dev->weight[s] : tab_val.weight[s];
-      moe = __builtin_fmaf(o, w, moe);
-    }
+    const float w = tab_dev ? tab_dev->weight[s < (int)k ? s : 0] : tab_val.weight[s < (int)k ? s : 0];
+    moe = s < (int)k ? __builtin_fmaf(o[s], w, moe) : moe;
   }
   float res;
   if (has_shared) {
