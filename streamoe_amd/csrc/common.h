@@ -187,15 +187,6 @@ __device__ __forceinline__ float chunk_dot(const Raw<BITS>& raw, const float (&x
   return __builtin_fmaf(s, qdot(q, x), b * xs);
 }
 
-// Sum over aligned groups of W lanes (W a power of two <= 64). Every lane of
-// a group ends with the same value: the butterfly adds commute exactly.
-template <int W>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
-}
-
 // DPP data movement within a wave (gfx9 encodings): row_shr:n = 0x110+n,
 // row_bcast:15 = 0x142, row_bcast:31 = 0x143. Lanes whose source is out of
 // range keep `identity`.
@@ -203,6 +194,30 @@ template <int CTRL, int ROW_MASK = 0xF>
 __device__ __forceinline__ float dpp_f(float v, float identity) {
   return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(identity), __float_as_int(v), CTRL,
                                                     ROW_MASK, 0xF, false));
+}
+
+// Sum over aligned groups of W lanes (W a power of two <= 64), on DPP and
+// permlane swaps (a shuffle compiles to an LDS permute per step): quad
+// lane ^ 1, quad lane ^ 2, the 8-lane half-row mirror, the 16-lane row
+// mirror, then the row and half exchanges. Each step adds two partial sums
+// over disjoint lane sets of equal size, and both partners form the same
+// sum, so every lane of a group ends with the same value.
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(W >= 1 && W <= 64 && (W & (W - 1)) == 0, "W is a power of two <= 64");
+  if constexpr (W >= 2) v += dpp_f<0xB1>(v, 0.f);
+  if constexpr (W >= 4) v += dpp_f<0x4E>(v, 0.f);
+  if constexpr (W >= 8) v += dpp_f<0x141>(v, 0.f);
+  if constexpr (W >= 16) v += dpp_f<0x140>(v, 0.f);
+  if constexpr (W >= 32) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  if constexpr (W == 64) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  return v;
 }
 
 // Sum over aligned groups of W lanes (16, 32 or 64) with DPP prefix steps.

@@ -129,24 +129,47 @@ __global__ __launch_bounds__(256) void k_qmv(const uint8_t* __restrict__ codes,
   uint32_t best_i = 0xFFFFFFFFu;
   auto compute = [&](uint32_t step, const Raw<BITS>(&raw)[U][CPL], const uint32_t(&sv)[U][CPL],
                      const uint32_t(&bv)[U][CPL]) {
+    if constexpr (L == kWave && U == 4) {
+      // Whole-wave rows: the four rows' lane partials are reduced together
+      // (two permlane swaps leave 16-lane rows holding rows 0, 2, 1, 3, then
+      // one 16-lane sum), ~10 instructions for the four rows instead of four
+      // 6-step butterflies; lane 0 of each 16-lane row stores its row.
+      float part[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      float part = 0.f;
+      for (int u = 0; u < U; ++u) {
+        part[u] = 0.f;
 #pragma unroll
-      for (int i = 0; i < CPL; ++i)
-        part += chunk_dot_i<BITS>(raw[u][i], xl[i], __uint_as_float(sv[u][i] << 16),
-                                  __uint_as_float(bv[u][i] << 16));
-      const float sum = group_sum<L>(part);
-      const uint32_t row = step * STEP_ROWS + u * RPP + lrow;
-      if (lch == 0 && row < rows) {
+        for (int i = 0; i < CPL; ++i)
+          part[u] += chunk_dot_i<BITS>(raw[u][i], xl[i], __uint_as_float(sv[u][i] << 16),
+                                       __uint_as_float(bv[u][i] << 16));
+      }
+      const float sum = row_sum16_all(swap16_add(swap32_add(part[0], part[1]), swap32_add(part[2], part[3])));
+      const int r16 = lane >> 4;
+      const uint32_t row = step * STEP_ROWS + ((r16 >> 1) | ((r16 & 1) << 1));
+      if ((lane & 15) == 0 && row < rows) {
         y[row] = sum;
         argmax_merge(best, best_i, sum, row);
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float part = 0.f;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i)
+          part += chunk_dot_i<BITS>(raw[u][i], xl[i], __uint_as_float(sv[u][i] << 16),
+                                    __uint_as_float(bv[u][i] << 16));
+        const float sum = group_sum<L>(part);
+        const uint32_t row = step * STEP_ROWS + u * RPP + lrow;
+        if (lch == 0 && row < rows) {
+          y[row] = sum;
+          argmax_merge(best, best_i, sum, row);
+        }
       }
     }
   };
   // Fused argmax: the wave's (max, first index) over its rows, written to
-  // arg_v / arg_i[wave] when they are given (lanes other than each row's
-  // lane 0 keep -inf).
+  // arg_v / arg_i[wave] when they are given (lanes that store no row keep
+  // -inf).
   auto publish = [&]() {
     if (!arg_v) return;
 #pragma unroll
@@ -200,8 +223,9 @@ static hipError_t qmv_inst(const QView& w, const float* x, float* y, uint32_t ro
   // Rows per wave and step, and the persistent grid: 4 rows x 3072 waves
   // (12 per CU on 256 CUs, the occupancy this instance's registers allow)
   // measured best on MI355X for the 151,936 x 2048 LM head (45.6 us per
-  // token with the argmax, against 48-69 us for 8 or 16 rows and 1024-5120
-  // waves).
+  // token with the argmax and one butterfly per row, against 48-69 us for
+  // 8 or 16 rows and 1024-5120 waves; 40.6 us with the four rows reduced
+  // together).
   constexpr int U = 4;
   const uint32_t n_steps = (rows + RPP * U - 1) / (RPP * U);
   uint32_t n_waves = n_steps < kQmvMaxWaves ? n_steps : kQmvMaxWaves;
@@ -596,18 +620,40 @@ __device__ __forceinline__ void gateup_body(const uint8_t* __restrict__ blob, co
       bu[p][i] = bf16f(*reinterpret_cast<const uint16_t*>(blob + g.b[1] + gi));
     }
   }
+  if constexpr (L == kWave && P == 4) {
+    // Whole-wave rows: the four gate and four up rows are reduced together
+    // (after the permlane swaps the 16-lane rows hold rows 0, 2, 1, 3), and
+    // one SwiGLU per lane serves the four outputs.
+    float pg[P], pu[P];
 #pragma unroll
-  for (int p = 0; p < P; ++p) {
-    float pg = 0.f, pu = 0.f;
+    for (int p = 0; p < P; ++p) {
+      pg[p] = 0.f;
+      pu[p] = 0.f;
 #pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      pg += chunk_dot<BITS>(rg[p][i], xr[i], xs[i], sg[p][i], bg[p][i]);
-      pu += chunk_dot<BITS>(ru[p][i], xr[i], xs[i], su[p][i], bu[p][i]);
+      for (int i = 0; i < CPL; ++i) {
+        pg[p] += chunk_dot<BITS>(rg[p][i], xr[i], xs[i], sg[p][i], bg[p][i]);
+        pu[p] += chunk_dot<BITS>(ru[p][i], xr[i], xs[i], su[p][i], bu[p][i]);
+      }
     }
-    const float gsum = group_sum<L>(pg);
-    const float usum = group_sum<L>(pu);
-    const uint32_t row = row0 + p * RPP + lrow;
-    if (lch == 0 && row < inter) act_slot[row] = silu_mul(gsum, usum);
+    const float gsum = row_sum16_all(swap16_add(swap32_add(pg[0], pg[1]), swap32_add(pg[2], pg[3])));
+    const float usum = row_sum16_all(swap16_add(swap32_add(pu[0], pu[1]), swap32_add(pu[2], pu[3])));
+    const int r16 = lane >> 4;
+    const uint32_t row = row0 + ((r16 >> 1) | ((r16 & 1) << 1));
+    if ((lane & 15) == 0 && row < inter) act_slot[row] = silu_mul(gsum, usum);
+  } else {
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      float pg = 0.f, pu = 0.f;
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        pg += chunk_dot<BITS>(rg[p][i], xr[i], xs[i], sg[p][i], bg[p][i]);
+        pu += chunk_dot<BITS>(ru[p][i], xr[i], xs[i], su[p][i], bu[p][i]);
+      }
+      const float gsum = group_sum<L>(pg);
+      const float usum = group_sum<L>(pu);
+      const uint32_t row = row0 + p * RPP + lrow;
+      if (lch == 0 && row < inter) act_slot[row] = silu_mul(gsum, usum);
+    }
   }
 }
 
@@ -779,9 +825,7 @@ __global__ __launch_bounds__(64) void k_down_combine(BlobGeom routed, BlobGeom s
     o[s] = part;
   }
 #pragma unroll
-  for (int st = L / 2; st > 0; st >>= 1)
-#pragma unroll
-    for (int s = 0; s < MAXS; ++s) o[s] += __shfl_xor(o[s], st, kWave);
+  for (int s = 0; s < MAXS; ++s) o[s] = group_sum<L>(o[s]);
   // moe = fma(out_k, w_k, moe) in slot order (deferred.rs:458-466).
   float moe = 0.f;
 #pragma unroll
