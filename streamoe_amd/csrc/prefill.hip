@@ -839,7 +839,10 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
                                                           const uint32_t* __restrict__ n_items_p) {
   using C = PfMM<BITS, G, MODE, SPLIT, KU, NWD>;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // The wave index is uniform: in a scalar register, the role branches
+  // below are scalar branches and every LDS destination (M0) of a copy is
+  // scalar arithmetic, with no vector-to-scalar move per copy.
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t cw = wave & 3, kh = (wave >> 2) & 1;  // column wave, K half (compute waves)
   const bool copier = NWD == 0 || wave >= (uint32_t)C::NWC;   // issues copies
   const bool computer = NWD == 0 || wave < (uint32_t)C::NWC;  // runs MFMAs
