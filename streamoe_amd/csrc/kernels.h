@@ -130,8 +130,8 @@ struct PfArgs {
   uint32_t* items;         // [max_items, 2]: expert, start | count << 16
   uint32_t* n_items;
   uint32_t* item_tok;      // [max_items, 32]: token of each item row (token 0 past the count)
-  int32_t* tok_pos;        // [n, k] entry positions of each token in ascending expert order
-  float* tok_w;            // [n, k] the routing weights in the same order
+  uint2* tok_pw;           // [n, k] (entry position, routing weight bits) of each token's
+                           // entries in ascending expert order
   float* xsum;             // [n, hidden / group] group sums of each token's x row (as the MFMAs see it)
   float* asum;             // [n*k, inter / group] group sums of the activations
   uint16_t* x_hi;          // [n, hidden] x rows, bf16, MFMA order

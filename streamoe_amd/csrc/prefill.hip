@@ -232,6 +232,26 @@ __host__ __device__ constexpr uint32_t pf_route_lds(uint32_t E, uint32_t n) {
              : kPfPrepTokens * kPfPart8 * 4;
 }
 
+// Lane l - d's value (DPP row shift right; row_shr:d = 0x110 + d), 0 where
+// the source lies before the 16-lane row or outside ROW_MASK.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint32_t dpp_shr_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xF, false);
+}
+
+// Inclusive prefix sum over the wave: shifts by 1, 2, 4, 8 within each
+// 16-lane row, then row 0's total into row 1 and row 2's into row 3
+// (row_bcast:15), then rows 0-1's total into rows 2-3 (row_bcast:31).
+__device__ __forceinline__ uint32_t wave_scan_incl(uint32_t v) {
+  v += dpp_shr_u<0x111>(v);
+  v += dpp_shr_u<0x112>(v);
+  v += dpp_shr_u<0x114>(v);
+  v += dpp_shr_u<0x118>(v);
+  v += dpp_shr_u<0x142, 0xA>(v);
+  v += dpp_shr_u<0x143, 0xC>(v);
+  return v;
+}
+
 __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t pf_dyn[];
   const uint32_t tid = threadIdx.x;
@@ -314,11 +334,13 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
       pc[i] = (e < E && i < per && c < cw) ? __popc(col[e * cw + c]) : 0u;
       loc += pc[i];
     }
+    // Inclusive scan over the TPE lanes of the expert (aligned groups of
+    // 2 or 4 within a 16-lane row): DPP shifts by 1 and 2.
     uint32_t incl = loc;
-    const uint32_t t1 = __shfl_up(incl, 1, tpe);
+    const uint32_t t1 = dpp_shr_u<0x111>(incl);
     if (j >= 1) incl += t1;
     if (tpe == 4) {
-      const uint32_t t2 = __shfl_up(incl, 2, 4);
+      const uint32_t t2 = dpp_shr_u<0x112>(incl);
       if (j >= 2) incl += t2;
     }
     if (e < E) {
@@ -340,7 +362,7 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
   __syncthreads();
   PF_STAMP(3);
   // Wave 0: exclusive scans of the counts (entry offsets) and of the items
-  // per expert (work-list bases), 8 experts per lane and a shuffle scan.
+  // per expert (work-list bases), 8 experts per lane and a DPP scan.
   if (tid < 64) {
     constexpr int EPL = kPfMaxExperts / 64;
     uint32_t c8[EPL], n8[EPL], ca = 0, na = 0;
@@ -352,15 +374,7 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
       ca += c8[q];
       na += n8[q];
     }
-    uint32_t ci = ca, ni = na;  // inclusive scans over lanes
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint32_t tc = __shfl_up(ci, o, 64), tn = __shfl_up(ni, o, 64);
-      if (tid >= o) {
-        ci += tc;
-        ni += tn;
-      }
-    }
+    const uint32_t ci = wave_scan_incl(ca), ni = wave_scan_incl(na);  // inclusive scans over lanes
     uint32_t co = ci - ca, no = ni - na;
 #pragma unroll
     for (int q = 0; q < EPL; ++q) {
@@ -403,8 +417,7 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
 #pragma unroll
       for (uint32_t q = 0; q < kPfMaxK; ++q) r += (q < k && ex[q] < e) ? 1u : 0u;
       r = min(r, k - 1);  // a duplicated expert (already reported) stays in range
-      a.tok_pos[tid * k + r] = (int32_t)pos;
-      a.tok_w[tid * k + r] = wt[s];
+      a.tok_pw[tid * k + r] = make_uint2(pos, __float_as_uint(wt[s]));
       a.item_tok[sibase[e] * kPfMC + row] = tid;
     }
   }
@@ -1323,11 +1336,12 @@ __global__ __launch_bounds__(512) void k_pf_combine(PfArgs a) {
   float wt[kPfMaxK];
   const uint32_t nk = a.n_tokens * k;
 #pragma unroll
-  for (uint32_t r = 0; r < kPfMaxK; ++r)
+  for (uint32_t r = 0; r < kPfMaxK; ++r) {
+    const uint2 pw = r < k ? a.tok_pw[t * k + r] : make_uint2(0u, 0u);
     // In range even when bucketing rejected the input (then *err is set).
-    pos[r] = r < k ? min((uint32_t)a.tok_pos[t * k + r], nk - 1) : 0u;
-#pragma unroll
-  for (uint32_t r = 0; r < kPfMaxK; ++r) wt[r] = r < k ? a.tok_w[t * k + r] : 0.f;
+    pos[r] = min(pw.x, nk - 1);
+    wt[r] = __uint_as_float(pw.y);
+  }
   for (uint32_t h = threadIdx.x * 4; h < H; h += blockDim.x * 4) {
     float4 d[kPfMaxK];
 #pragma unroll
@@ -1364,8 +1378,7 @@ uint64_t prefill_workspace(uint32_t hidden, uint32_t inter, uint32_t group, uint
   uint8_t* p_items = take(max_items * 2 * 4);
   uint8_t* p_nitems = take(4);
   uint8_t* p_itok = take(max_items * kPfMC * 4);
-  uint8_t* p_w = take(nk * 4);
-  uint8_t* p_pos = take(nk * 4);
+  uint8_t* p_pw = take(nk * 8);
   uint8_t* p_xsum = take((uint64_t)n_tokens * (hidden / group) * 4);
   uint8_t* p_asum = take(nk * (inter / group) * 4);
   uint8_t* p_xhi = take((uint64_t)n_tokens * hidden * 2);
@@ -1376,8 +1389,7 @@ uint64_t prefill_workspace(uint32_t hidden, uint32_t inter, uint32_t group, uint
     a->items = reinterpret_cast<uint32_t*>(p_items);
     a->n_items = reinterpret_cast<uint32_t*>(p_nitems);
     a->item_tok = reinterpret_cast<uint32_t*>(p_itok);
-    a->tok_w = reinterpret_cast<float*>(p_w);
-    a->tok_pos = reinterpret_cast<int32_t*>(p_pos);
+    a->tok_pw = reinterpret_cast<uint2*>(p_pw);
     a->xsum = reinterpret_cast<float*>(p_xsum);
     a->asum = reinterpret_cast<float*>(p_asum);
     a->x_hi = reinterpret_cast<uint16_t*>(p_xhi);
