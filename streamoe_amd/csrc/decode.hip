@@ -51,6 +51,26 @@ __device__ __forceinline__ void argmax_merge(float& bv, uint32_t& bi, float v, u
   }
 }
 
+// One step of a wave argmax on DPP: merge with the lane CTRL names (lanes
+// without a source in range, or outside ROW_MASK, see the identity).
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ void argmax_dpp(float& bv, uint32_t& bi) {
+  const float v = __int_as_float(
+      __builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(bv), CTRL, ROW_MASK, 0xF, false));
+  const uint32_t i = (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)bi, CTRL, ROW_MASK, 0xF, false);
+  argmax_merge(bv, bi, v, i);
+}
+
+// Wave argmax into lane 63: DPP row shifts, then the row broadcasts.
+__device__ __forceinline__ void argmax_wave_last(float& bv, uint32_t& bi) {
+  argmax_dpp<0x111>(bv, bi);
+  argmax_dpp<0x112>(bv, bi);
+  argmax_dpp<0x114>(bv, bi);
+  argmax_dpp<0x118>(bv, bi);
+  argmax_dpp<0x142, 0xA>(bv, bi);
+  argmax_dpp<0x143, 0xC>(bv, bi);
+}
+
 // Padded instances (PAD): CPR is a power of two >= the row's cpr chunks (any
 // multiple of 32 inputs). A lane's chunk c >= cpr reads the row's last
 // chunk instead (in bounds) and multiplies it by a zero input, so it adds
@@ -172,13 +192,8 @@ __global__ __launch_bounds__(256) void k_qmv(const uint8_t* __restrict__ codes,
   // -inf).
   auto publish = [&]() {
     if (!arg_v) return;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ob = __shfl_xor(best, o, 64);
-      const uint32_t oi = __shfl_xor(best_i, o, 64);
-      argmax_merge(best, best_i, ob, oi);
-    }
-    if (lane == 0) {
+    argmax_wave_last(best, best_i);
+    if (lane == 63) {
       arg_v[wave] = best;
       arg_i[wave] = best_i;
     }
@@ -322,28 +337,13 @@ hipError_t launch_dequant(const QView& w, uint32_t in_dim, uint32_t row0, uint32
 constexpr uint32_t kArgBlocks = 256;
 
 // Block-wide (value, index) reduction; result valid in thread 0.
-// One step of a wave argmax on DPP: merge with the lane CTRL names (lanes
-// without a source in range, or outside ROW_MASK, see the identity).
-template <int CTRL, int ROW_MASK = 0xF>
-__device__ __forceinline__ void argmax_dpp(float& bv, uint32_t& bi) {
-  const float v = __int_as_float(
-      __builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(bv), CTRL, ROW_MASK, 0xF, false));
-  const uint32_t i = (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)bi, CTRL, ROW_MASK, 0xF, false);
-  argmax_merge(bv, bi, v, i);
-}
-
 // Block argmax, valid in every lane of wave 0 (threads 0..63): each wave
 // reduces on DPP row shifts and row broadcasts into its last lane (no LDS
 // permutes), then wave 0 merges the waves' results the same way.
 __device__ __forceinline__ void argmax_block(float& best, uint32_t& bi) {
   __shared__ float sv[16];
   __shared__ uint32_t si[16];
-  argmax_dpp<0x111>(best, bi);
-  argmax_dpp<0x112>(best, bi);
-  argmax_dpp<0x114>(best, bi);
-  argmax_dpp<0x118>(best, bi);
-  argmax_dpp<0x142, 0xA>(best, bi);
-  argmax_dpp<0x143, 0xC>(best, bi);
+  argmax_wave_last(best, bi);
   const uint32_t w = threadIdx.x >> 6, nw = blockDim.x >> 6;
   if ((threadIdx.x & 63) == 63) {
     sv[w] = best;
