@@ -443,6 +443,16 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
 // MFMA operand read different banks.
 // ---------------------------------------------------------------------------
 
+// A loop-invariant 32-bit lane offset, made opaque at its use so that the
+// compiler adds it to the scalar base in the copy instruction itself
+// (global_load_lds with a scalar address and a 32-bit vector offset)
+// instead of keeping it widened to 64 bits and adding it with a vector
+// instruction before every copy.
+__device__ __forceinline__ uint32_t pf_voff(uint32_t o) {
+  asm volatile("" : "+v"(o));
+  return o;
+}
+
 // Position of natural index i (0..7) of an 8-block in the MFMA order
 // [v0, v4, v1, v5, v2, v6, v3, v7].
 __device__ __forceinline__ uint32_t perm8_pos(uint32_t i) { return i < 4 ? 2 * i : 2 * (i - 4) + 1; }
@@ -1000,7 +1010,7 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
 #pragma unroll
     for (int i = 0; i < C::N_US; ++i)
       if ((C::P_US / C::NW) % 64 == 0 || i * 64 + lane < (uint32_t)(C::P_US / C::NW))
-        dma16(u.bs + off_us[i], ubuf + (dw * (C::P_US / C::NW) + i * 64) * 16);
+        dma16(u.bs + pf_voff(off_us[i]), ubuf + (dw * (C::P_US / C::NW) + i * 64) * 16);
     // Group sums: slot p = (row m, slot in row) holds the row's piece
     // (slot ^ m % XPR) under gate/up (pf_unit_bias reads one group of 16
     // rows at once: the XOR spreads them over the banks), else piece p;
@@ -1023,14 +1033,14 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
 #pragma unroll
     for (int i = 0; i < C::N_BQ; ++i)
       if ((C::P_BQ / C::NW) % 64 == 0 || i * 64 + lane < (uint32_t)(C::P_BQ / C::NW))
-        dma16(bq_base + off_bq[i], st + C::OFF_BQ + (dw * (C::P_BQ / C::NW) + i * 64) * 16);
+        dma16(bq_base + pf_voff(off_bq[i]), st + C::OFF_BQ + (dw * (C::P_BQ / C::NW) + i * 64) * 16);
     // Scales then biases of each row: [row][array][CG] bf16.
     const uint8_t* bs_base = u.bs + (size_t)c * C::CG * 2;
 #pragma unroll
     for (int i = 0; i < C::N_BS; ++i) {
       uint8_t* dst = st + C::OFF_BS + (dw * (C::P_BS / C::NW) + i * 64) * C::SB_SZ;
       if ((C::P_BS / C::NW) % 64 == 0 || i * 64 + lane < (uint32_t)(C::P_BS / C::NW)) {
-        if (C::SB_SZ == 16) dma16(bs_base + off_bs[i], dst); else dma4(bs_base + off_bs[i], dst);
+        if (C::SB_SZ == 16) dma16(bs_base + pf_voff(off_bs[i]), dst); else dma4(bs_base + pf_voff(off_bs[i]), dst);
       }
     }
     // A rows (bf16, MFMA order), one row pair (m, m + 16) per copy; slot
