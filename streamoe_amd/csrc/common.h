@@ -74,6 +74,14 @@ __device__ __forceinline__ T ld_w(const T* p) {
     return *p;
 }
 
+// A 32-bit lane offset made opaque at its use, so that the compiler adds it
+// to a scalar base inside the load (scalar address + 32-bit vector offset)
+// instead of widening it to 64 bits and adding with a vector instruction.
+__device__ __forceinline__ uint32_t lane_off(uint32_t o) {
+  asm volatile("" : "+v"(o));
+  return o;
+}
+
 template <bool NT = true>
 __device__ __forceinline__ Raw<4> load_raw4(const uint8_t* p) {
   const u32x4 v = ld_w<NT>(reinterpret_cast<const u32x4*>(p));

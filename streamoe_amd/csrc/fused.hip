@@ -78,17 +78,6 @@ __device__ __forceinline__ void fa_flush(const FusedLayer& a, const FaClock& c, 
   for (int p = 0; p < 6; ++p) d[p] = c.t[p];
 }
 
-// Raw bf16 scale and bias of chunk c of `row` in one [rows, in_dim] block.
-// They are widened only where used, so the loads stay in flight together
-// with the codes.
-__device__ __forceinline__ void load_sb(const uint8_t* blob, uint64_t s_off, uint64_t b_off,
-                                        uint32_t row, uint32_t gpr, uint32_t cpg_shift, uint32_t c,
-                                        uint16_t& s, uint16_t& b) {
-  const size_t gi = ((size_t)row * gpr + (c >> cpg_shift)) * 2;
-  s = *reinterpret_cast<const uint16_t*>(blob + s_off + gi);
-  b = *reinterpret_cast<const uint16_t*>(blob + b_off + gi);
-}
-
 // x chunk of this lane: the given input, or RMSNorm(r) * w (bf16 weights)
 // with the sum of squares reduced over the wave (rms_norm_bf16_n_tokens_cpu,
 // backend/cpu/mod.rs:406-430: inv = 1 / sqrt(sum_sq / dim + eps),
@@ -376,10 +365,15 @@ __device__ __forceinline__ void gateup_rows(const FusedLayer& a, FaClock& clk, c
 #pragma unroll
     for (int h = 0; h < HC; ++h) {
       const uint32_t c = lane + 64 * h;
-      rg[p][h] = load_raw<BITS, NT>(blob + g.w[0] + (size_t)row * RB + c * CB);
-      ru[p][h] = load_raw<BITS, NT>(blob + g.w[1] + (size_t)row * RB + c * CB);
-      load_sb(blob, g.s[0], g.b[0], row, gpr, cps, c, sg[p][h], bg[p][h]);
-      load_sb(blob, g.s[1], g.b[1], row, gpr, cps, c, su[p][h], bu[p][h]);
+      // Scalar row bases, 32-bit lane offsets.
+      const uint32_t oc = lane_off(c * CB), os = lane_off((c >> cps) * 2);
+      const size_t rs = (size_t)row * gpr * 2;
+      rg[p][h] = load_raw<BITS, NT>(blob + g.w[0] + (size_t)row * RB + oc);
+      ru[p][h] = load_raw<BITS, NT>(blob + g.w[1] + (size_t)row * RB + oc);
+      sg[p][h] = *reinterpret_cast<const uint16_t*>(blob + g.s[0] + rs + os);
+      bg[p][h] = *reinterpret_cast<const uint16_t*>(blob + g.b[0] + rs + os);
+      su[p][h] = *reinterpret_cast<const uint16_t*>(blob + g.s[1] + rs + os);
+      bu[p][h] = *reinterpret_cast<const uint16_t*>(blob + g.b[1] + rs + os);
     }
   }
   __builtin_amdgcn_sched_barrier(0);
