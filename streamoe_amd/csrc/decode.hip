@@ -137,10 +137,11 @@ __global__ __launch_bounds__(256) void k_qmv(const uint8_t* __restrict__ codes,
 #pragma unroll
       for (int i = 0; i < CPL; ++i) {
         const uint32_t c = PAD ? pad_chunk(lch + L * i, cpr) : lch + L * i;
-        raw[u][i] = load_raw<BITS>(codes + (size_t)row * ROW_BYTES + c * CB);
-        const size_t gi = (size_t)row * gpr + (c >> cpg_shift);
-        sv[u][i] = scales[gi];
-        bv[u][i] = biases[gi];
+        // Row bases (scalar for whole-wave rows) plus 32-bit lane offsets.
+        raw[u][i] = load_raw<BITS>(codes + (size_t)row * ROW_BYTES + lane_off(c * CB));
+        const uint32_t go = lane_off(c >> cpg_shift);
+        sv[u][i] = scales[(size_t)row * gpr + go];
+        bv[u][i] = biases[(size_t)row * gpr + go];
       }
     }
   };
