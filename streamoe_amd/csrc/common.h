@@ -113,6 +113,39 @@ __device__ __forceinline__ void dma4(const void* g, void* l) {
   __builtin_amdgcn_global_load_lds(SMOE_GPTR(g), SMOE_LPTR(l), 4, 0, 0);
 }
 
+// Loads through an explicitly global pointer: a pointer that was itself
+// loaded from memory (an expert blob from a route table) is generic to the
+// compiler, which then emits flat loads, and a pending flat load makes every
+// later wait a full vmcnt(0) (flat operations are not counted in order).
+typedef const __attribute__((address_space(1))) uint8_t* gbytes;
+__device__ __forceinline__ gbytes as_global(const void* p) { return (gbytes)p; }
+
+template <bool NT, typename T>
+__device__ __forceinline__ T gld(gbytes p) {
+  typedef const __attribute__((address_space(1))) T* GT;
+  if constexpr (NT)
+    return __builtin_nontemporal_load((GT)p);
+  else
+    return *(GT)p;
+}
+
+template <int BITS, bool NT = true>
+__device__ __forceinline__ Raw<BITS> load_raw_g(gbytes p) {
+  Raw<BITS> r;
+  if constexpr (BITS == 4) {
+    const u32x4 v = gld<NT, u32x4>(p);
+    r.d[0] = v.x;
+    r.d[1] = v.y;
+    r.d[2] = v.z;
+    r.d[3] = v.w;
+  } else {
+    r.d[0] = gld<NT, uint32_t>(p);
+    r.d[1] = gld<NT, uint32_t>(p + 4);
+    r.d[2] = gld<NT, uint32_t>(p + 8);
+  }
+  return r;
+}
+
 template <int BITS, bool NT = true>
 __device__ __forceinline__ Raw<BITS> load_raw(const uint8_t* p) {
   if constexpr (BITS == 4)
@@ -392,8 +425,16 @@ __device__ __forceinline__ void unpack_bytes(const Raw<3>& r, uint32_t (&b)[8]) 
       p = __builtin_amdgcn_alignbit(r.d[2], r.d[1], 16);
     else
       p = r.d[2] >> 8;
-    // 6-bit field k (codes 2k, 2k+1) to byte k.
-    const uint32_t t = (p & 0x3Fu) | ((p & 0xFC0u) << 2) | ((p & 0x3F000u) << 4) | ((p & 0xFC0000u) << 6);
+    // 6-bit field k (codes 2k, 2k+1) to byte k in two bitfield inserts
+    // (v_bfi_b32): fields 2, 3 move up by 4 bits, then fields 1, 3 by 2.
+    // Bits outside the fields (p's upper byte, copies left between the
+    // fields) end up only in bits 6-7 of each byte, which the masks drop.
+    // (The empty asm keeps the compiler from distributing the final masks
+    // back into the inserts, which costs more instructions than it saves.)
+    uint32_t u = (p & 0x00000FFFu) | ((p << 4) & ~0x00000FFFu);
+    asm volatile("" : "+v"(u));
+    uint32_t t = (u & 0x003F003Fu) | ((u << 2) & ~0x003F003Fu);
+    asm volatile("" : "+v"(t));
     b[2 * i] = t & 0x07070707u;
     b[2 * i + 1] = (t >> 3) & 0x07070707u;
   }

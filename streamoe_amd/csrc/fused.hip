@@ -142,7 +142,7 @@ __device__ __forceinline__ void fa_x_finish(const FusedLayer& a, FaX<HC>& f) {
 // chunk: lane q of the quad holds values 8q .. 8q + 7 and writes limb words
 // 2q and 2q + 1 of every limb; the chunk's exponent and sum come from the
 // quad (DPP).
-__device__ __forceinline__ void store_limbs_quad(uint32_t* dst, const float (&x)[8], int q) {
+__device__ __forceinline__ void store_limbs_quad(uint32_t* dst, const float (&x)[8], int q, bool live = true) {
   float amax = 0.f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(x[j]));
@@ -165,12 +165,12 @@ __device__ __forceinline__ void store_limbs_quad(uint32_t* dst, const float (&x)
     uint2 v;
     v.x = pack_bytes(d[L][0], d[L][2], d[L][4], d[L][6]);
     v.y = pack_bytes(d[L][1], d[L][3], d[L][5], d[L][7]);
-    *reinterpret_cast<uint2*>(dst + 8 * L + 2 * q) = v;
+    if (live) *reinterpret_cast<uint2*>(dst + 8 * L + 2 * q) = v;
   }
   float xs = ((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]));
   xs += dpp_f<0xB1>(xs, 0.f);
   xs += dpp_f<0x4E>(xs, 0.f);
-  if (q == 0) {
+  if (q == 0 && live) {
     uint2 v;
     v.x = __float_as_uint(__builtin_ldexpf(1.0f, -f));
     v.y = __float_as_uint(xs);
@@ -538,8 +538,11 @@ __global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a_all) {
 //
 // One block per kFaRB = 8 hidden rows. Every block needs all (k + 1) * inter
 // activations, so a block stages them in LDS once (one cooperative load, a
-// quarter of what per-wave loads would move through the vector L1) and the
-// lanes read their chunk from there.
+// quarter of what per-wave loads would move through the vector L1), as
+// integer limbs: four lanes per 32-activation chunk convert it while the
+// weights are in flight (common.h, make_limbs; the same block floating
+// point as x in K_B), and every lane's dots then run on v_dot4c_i32_i8
+// (chunk_dot_i) instead of converting each code to a float.
 //
 // Lanes are slot-major: lane (s, c) owns chunk c (LI = inter / 32 chunks per
 // row) of slot s. Routed waves: ceil(k / SPW) slot groups (SPW = 64 / LI
@@ -548,14 +551,14 @@ __global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a_all) {
 // its 64 lanes into 64 / LI row groups. Loads go out in dependency order:
 // the expert pointers (route table), the activation staging, then, once the
 // pointers land, every row's codes, scales and biases; the staging is
-// written to LDS while the weights are in flight.
+// converted and written to LDS while the weights are in flight.
 // Per-(row, slot) sums go through LDS to 8 combine threads, which apply the
 // reference's order: moe = fma(out_s, w_s, moe) over the routed slots, then
 // the shared term and the residual (deferred.rs:441-490).
 // ---------------------------------------------------------------------------
-constexpr int kFaRB = 8;         // hidden rows per K_C block
-constexpr int kFaStage = 8;      // staged float4 per thread, at most
-constexpr int kChunkPad = 36;    // LDS floats per 32-activation chunk (conflict-free reads)
+constexpr int kFaRB = 8;           // hidden rows per K_C block
+constexpr int kFaStageRounds = 4;  // staged chunks per quad of threads, at most
+constexpr int kChunkPad = 36;      // LDS dwords per staged chunk (conflict-free 16-byte reads)
 
 template <int BITS, int NR>
 struct DownLoads {
@@ -568,35 +571,28 @@ __device__ __forceinline__ void down_load(const uint8_t* blob, const BlobGeom& g
                                           uint32_t c, DownLoads<BITS, NR>& d) {
   constexpr int CB = chunk_bytes<BITS>();
   constexpr uint32_t RB = LI * CB;
-  const uint32_t gpr = g.inter / g.group;
+  const uint32_t gpr = g.inter >> __builtin_ctz(g.group);  // groups are powers of two
   const uint32_t cps = __builtin_ctz(g.group / kChunk);
+  const gbytes gb = as_global(blob);
 #pragma unroll
   for (int r = 0; r < NR; ++r) {
     const uint32_t row = row0 + r;
-    d.raw[r] = load_raw<BITS, NT>(blob + g.w[2] + (size_t)row * RB + c * CB);
+    d.raw[r] = load_raw_g<BITS, NT>(gb + g.w[2] + (size_t)row * RB + c * CB);
     const size_t gi = ((size_t)row * gpr + (c >> cps)) * 2;
-    d.sr[r] = *reinterpret_cast<const uint16_t*>(blob + g.s[2] + gi);
-    d.br[r] = *reinterpret_cast<const uint16_t*>(blob + g.b[2] + gi);
+    d.sr[r] = gld<false, uint16_t>(gb + g.s[2] + gi);
+    d.br[r] = gld<false, uint16_t>(gb + g.b[2] + gi);
   }
 }
 
+// The NR rows' sums of this lane's chunk (limbs in LDS), each reduced over
+// the LI lanes of its slot (valid in the last lane of the group).
 template <int BITS, int LI, int NR>
-__device__ __forceinline__ void down_dot(const DownLoads<BITS, NR>& d, const float* sact_chunk,
-                                         float (&o)[NR]) {
-  float act[kChunk];
-  const f32x4* p = reinterpret_cast<const f32x4*>(sact_chunk);
-#pragma unroll
-  for (int i = 0; i < kChunk / 4; ++i) {
-    const f32x4 v = p[i];
-    act[4 * i] = v.x;
-    act[4 * i + 1] = v.y;
-    act[4 * i + 2] = v.z;
-    act[4 * i + 3] = v.w;
-  }
-  const float xs = xsum(act);
+__device__ __forceinline__ void down_dot(const DownLoads<BITS, NR>& d, const uint32_t* limbs, float (&o)[NR]) {
+  XLimbs xl;
+  load_limbs(limbs, xl);
 #pragma unroll
   for (int r = 0; r < NR; ++r)
-    o[r] = group_sum_last<LI>(chunk_dot<BITS>(d.raw[r], act, xs, bf16f(d.sr[r]), bf16f(d.br[r])));
+    o[r] = group_sum_last<LI>(chunk_dot_i<BITS>(d.raw[r], xl, bf16f(d.sr[r]), bf16f(d.br[r])));
 }
 
 // Routed row parts per K_C block: 2 while 2 * ceil(k / SPW) + 1 waves fit in
@@ -617,7 +613,7 @@ __global__ __launch_bounds__(1024) void k_fa_down(FusedLayer a_all) {
   constexpr int SPW = kWave / LI;
   constexpr int NR = kFaRB / H;             // rows per routed lane
   constexpr int NRS = kFaRB / (kWave / LI); // rows per shared lane
-  extern __shared__ f32x4 sact4[];          // staged activations, kChunkPad floats per chunk
+  extern __shared__ f32x4 sact4[];          // staged activation limbs, kChunkPad dwords per chunk
   __shared__ float so[kFaRB][kMaxSlots];
   __shared__ float sw[kMaxSlots];
   FaClock clk;
@@ -646,31 +642,42 @@ __global__ __launch_bounds__(1024) void k_fa_down(FusedLayer a_all) {
   const uint32_t lrow0 = routed ? row0 + (wave % H) * NR : row0 + (lane / LI) * NRS;
   const uint8_t* blob = routed ? a.table->blob[sl] : a.shared;
 
-  // Activation staging: float4 i of the (k + 1) * inter values goes to chunk
-  // i / 8, part i % 8 (out-of-range threads reload the last one).
-  const uint32_t n4 = (k + (a.shared ? 1u : 0u)) * I / 4;
+  // Activation staging: quad qd of the block's threads takes chunks qd,
+  // qd + nquads, ...; lane q of the quad loads values 8q .. 8q + 7 of its
+  // chunk (quads past the last chunk reload it and store nothing).
+  const uint32_t nch = (k + (a.shared ? 1u : 0u)) * (I / kChunk);
+  const uint32_t nquads = blockDim.x >> 2, qd = threadIdx.x >> 2;
+  const int q = threadIdx.x & 3;
   const f32x4* act4 = reinterpret_cast<const f32x4*>(a.act);
-  f32x4 st[kFaStage];
+  f32x4 st[kFaStageRounds][2];
 #pragma unroll
-  for (int i = 0; i < kFaStage; ++i) {
-    const uint32_t j = threadIdx.x + i * blockDim.x;
-    st[i] = act4[j < n4 ? j : n4 - 1];
+  for (int i = 0; i < kFaStageRounds; ++i) {
+    const uint32_t ch = min(qd + i * nquads, nch - 1);
+    st[i][0] = act4[ch * 8 + 2 * q];
+    st[i][1] = act4[ch * 8 + 2 * q + 1];
   }
+  uint32_t* slimbs = reinterpret_cast<uint32_t*>(sact4);
+  const auto stage = [=](void) {
+#pragma unroll
+    for (int i = 0; i < kFaStageRounds; ++i) {
+      const uint32_t ch = qd + i * nquads;
+      if (i * nquads >= nch) break;  // uniform: no quad has a chunk this round
+      const float x[8] = {st[i][0].x, st[i][0].y, st[i][0].z, st[i][0].w,
+                          st[i][1].x, st[i][1].y, st[i][1].z, st[i][1].w};
+      store_limbs_quad(slimbs + (size_t)min(ch, nch - 1) * kChunkPad, x, q, ch < nch);
+    }
+  };
 
   fa_stamp(a, clk, 1, true);
   // One barrier on either path: the staging is complete in LDS after it.
   if (routed) {
     DownLoads<BITS, NR> d;
     down_load<BITS, LI, NR>(blob, a.routed, lrow0, c, d);
-#pragma unroll
-    for (int i = 0; i < kFaStage; ++i) {
-      const uint32_t j = threadIdx.x + i * blockDim.x;
-      if (j < n4) sact4[(j >> 3) * (kChunkPad / 4) + (j & 7)] = st[i];
-    }
+    stage();
     __syncthreads();
     fa_stamp(a, clk, 3, true);
     float od[NR];
-    down_dot<BITS, LI, NR>(d, reinterpret_cast<const float*>(sact4) + (sl * (I / kChunk) + c) * kChunkPad, od);
+    down_dot<BITS, LI, NR>(d, slimbs + (sl * (I / kChunk) + c) * kChunkPad, od);
     if (c == LI - 1 && valid) {
 #pragma unroll
       for (int r = 0; r < NR; ++r) so[lrow0 - row0 + r][slot] = od[r];
@@ -678,14 +685,10 @@ __global__ __launch_bounds__(1024) void k_fa_down(FusedLayer a_all) {
   } else {
     DownLoads<4, NRS> d;
     down_load<4, LI, NRS, false>(blob, a.sgeom, lrow0, c, d);
-#pragma unroll
-    for (int i = 0; i < kFaStage; ++i) {
-      const uint32_t j = threadIdx.x + i * blockDim.x;
-      if (j < n4) sact4[(j >> 3) * (kChunkPad / 4) + (j & 7)] = st[i];
-    }
+    stage();
     __syncthreads();
     float od[NRS];
-    down_dot<4, LI, NRS>(d, reinterpret_cast<const float*>(sact4) + (k * (I / kChunk) + c) * kChunkPad, od);
+    down_dot<4, LI, NRS>(d, slimbs + (k * (I / kChunk) + c) * kChunkPad, od);
     if (c == LI - 1) {
 #pragma unroll
       for (int r = 0; r < NRS; ++r) so[lrow0 - row0 + r][k] = od[r];
@@ -759,10 +762,10 @@ static hipError_t launch_down_fa_h(const FusedLayer& a, hipStream_t st) {
   constexpr uint32_t SPW = kWave / LI;
   const uint32_t waves = (a.k + SPW - 1) / SPW * H + (a.shared ? 1u : 0u);
   const uint32_t chunks = (a.k + (a.shared ? 1u : 0u)) * (a.routed.inter / kChunk);
-  const size_t lds = (size_t)chunks * kChunkPad * sizeof(float);
-  // Every staged float4 has a thread (8 per thread at most); true for all
-  // k <= 16 and inter 512 / 1024, checked anyway.
-  if (chunks * (kChunk / 4) > (uint32_t)kFaStage * waves * kWave || waves > 16 || lds > 96 * 1024)
+  const size_t lds = (size_t)chunks * kChunkPad * sizeof(uint32_t);
+  // Every staged chunk has a quad of threads (kFaStageRounds chunks per quad
+  // at most); true for all k <= 16 and inter 512 / 1024, checked anyway.
+  if (chunks > (uint32_t)kFaStageRounds * waves * (kWave / 4) || waves > 16 || lds > 96 * 1024)
     return hipErrorInvalidValue;
   static std::atomic<uint64_t> raised{0};
   if (lds > 64 * 1024) {
