@@ -205,6 +205,22 @@ int smoe_router(smoe_handle* h, const float* router_w, const float* x, uint32_t 
 int smoe_softmax_topk(smoe_handle* h, const float* logits, uint32_t n_tokens, uint32_t n_experts,
                       uint32_t k, int normalize, int32_t* idx, float* weights);
 
+/* Softmax only: probs[t] = softmax(logits[t]) per token t < n_tokens
+ * (device f32[n_tokens, n], n <= 1024), softmax() of moe_router.rs:52-72
+ * bit for bit: max, e_j = expf(l_j - max) with glibc's expf (the libm
+ * function the reference's f32::exp calls on Linux), the e_j summed one
+ * after another in index order, 1 / sum, e_j * (1 / sum). The routers
+ * above and the decode layers use the same arithmetic wherever the
+ * probabilities decide the routing (the exact scan for ambiguous top-k
+ * sets) or are returned (routing weights). */
+int smoe_softmax(smoe_handle* h, const float* logits, uint32_t n_tokens, uint32_t n, float* probs);
+
+/* The softmax's exponential alone, y[i] = expf(x[i]) for i < n (device
+ * f32): glibc's expf bit for bit (moe_router.rs:64, `(*v - max_val)
+ * .exp()`), for callers that check the device routing against a host
+ * libm. */
+int smoe_expf(smoe_handle* h, const float* x, float* y, uint64_t n);
+
 /* Top-k only, on arbitrary scores (no softmax): topk() of
  * moe_router.rs:83-124 per token. values: device f32[n_tokens, k]. */
 int smoe_topk(smoe_handle* h, const float* scores, uint32_t n_tokens, uint32_t n, uint32_t k,

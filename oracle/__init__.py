@@ -52,6 +52,8 @@ def _declare(L):
         "orc_q3_expert_to_q4": (C.c_int, [_P, _U32, _U32, _U32, _P]),
         "orc_expert_swiglu": (C.c_int, [_P, _U32, _U32, _U32, _U32, _P, _P, C.c_int]),
         "orc_softmax": (C.c_int, [_P, _U32]),
+        "orc_softmax_rows": (C.c_int, [_P, _U32, _U32, C.c_int]),
+        "orc_expf_many": (C.c_int, [_P, _P, C.c_uint64, C.c_int]),
         "orc_topk": (C.c_int, [_P, _U32, _U32, _P, _P]),
         "orc_normalize_weights": (None, [_P, _U32]),
         "orc_router": (C.c_int, [_P, _U32, _U32, C.c_int, _P, _P]),
@@ -185,6 +187,21 @@ def softmax(x):
     x = np.array(x, np.float32)
     assert lib().orc_softmax(_p(x), x.size) == 0
     return x
+
+
+def softmax_rows(x, nthreads=0):
+    """orc_softmax on every row of a 2-D float32 array (rows in parallel)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).copy()
+    assert lib().orc_softmax_rows(_p(x), x.shape[0], x.shape[1], nthreads) == 0
+    return x
+
+
+def expf_many(x, nthreads=0):
+    """The host libm's expf on every element (the reference softmax's exp)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    assert lib().orc_expf_many(_p(x), _p(y), x.size, nthreads) == 0
+    return y
 
 
 def topk(scores, k):

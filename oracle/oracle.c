@@ -377,6 +377,45 @@ int orc_softmax(float* x, uint32_t n) {
   return ORC_OK;
 }
 
+/* Many independent softmax rows (x: rows x n), rows split over threads. */
+typedef struct {
+  float* x;
+  uint32_t n;
+} softmax_rows_ctx;
+
+static void softmax_rows_fn(void* c, uint32_t a, uint32_t b) {
+  softmax_rows_ctx* s = (softmax_rows_ctx*)c;
+  for (uint32_t r = a; r < b; ++r) orc_softmax(s->x + (size_t)r * s->n, s->n);
+}
+
+int orc_softmax_rows(float* x, uint32_t rows, uint32_t n, int nthreads) {
+  if (n == 0) return ORC_ERR_EMPTY;
+  softmax_rows_ctx c = {x, n};
+  parallel_rows(softmax_rows_fn, &c, rows, nthreads);
+  return ORC_OK;
+}
+
+/* The libm expf the softmax calls (moe_router.rs:64), over a buffer in  */
+/* blocks of 4096 values split over threads.                             */
+typedef struct {
+  const float* x;
+  float* y;
+  uint64_t n;
+} expf_ctx;
+
+static void expf_fn(void* c, uint32_t a, uint32_t b) {
+  expf_ctx* e = (expf_ctx*)c;
+  uint64_t lo = (uint64_t)a * 4096u, hi = (uint64_t)b * 4096u;
+  if (hi > e->n) hi = e->n;
+  for (uint64_t i = lo; i < hi; ++i) e->y[i] = expf(e->x[i]);
+}
+
+int orc_expf_many(const float* x, float* y, uint64_t n, int nthreads) {
+  expf_ctx c = {x, y, n};
+  parallel_rows(expf_fn, &c, (uint32_t)((n + 4095u) / 4096u), nthreads);
+  return ORC_OK;
+}
+
 /* topk, moe_router.rs:83-124: slots start at (-1e30, 0); each score    */
 /* replaces the running-minimum slot (lowest slot on ties) when strictly */
 /* greater. Slot order is the replacement order.                         */

@@ -78,6 +78,10 @@ int orc_expert_swiglu(const uint8_t* blob, uint32_t bits, uint32_t hidden, uint3
 /* ---- router -------------------------------------------------------- */
 int orc_softmax(float* x, uint32_t n);
 int orc_topk(const float* scores, uint32_t n, uint32_t k, int32_t* idx, float* val);
+/* orc_softmax over `rows` independent rows of n values, rows in parallel. */
+int orc_softmax_rows(float* x, uint32_t rows, uint32_t n, int nthreads);
+/* y[i] = expf(x[i]): the host libm's expf, the function moe_router.rs:64 calls. */
+int orc_expf_many(const float* x, float* y, uint64_t n, int nthreads);
 void orc_normalize_weights(float* w, uint32_t k);
 int orc_router(float* scores, uint32_t n, uint32_t k, int normalize, int32_t* idx, float* w);
 float orc_sigmoid(float x);

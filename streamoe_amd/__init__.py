@@ -191,6 +191,14 @@ class Kernels:
         return _lib.smoe_softmax_topk(self.h, _ptr(logits), n_tokens, n_experts, k, int(normalize),
                                       _ptr(idx), _ptr(weights))
 
+    def softmax(self, logits, n_tokens, n, probs):
+        """softmax() of moe_router.rs:52-72 per row, the reference's bits."""
+        return _lib.smoe_softmax(self.h, _ptr(logits), n_tokens, n, _ptr(probs))
+
+    def expf(self, x, y, n):
+        """glibc's expf (the reference softmax's exponential) on the device."""
+        return _lib.smoe_expf(self.h, _ptr(x), _ptr(y), n)
+
     def topk(self, scores, n_tokens, n, k, idx, values):
         return _lib.smoe_topk(self.h, _ptr(scores), n_tokens, n, k, _ptr(idx), _ptr(values))
 

@@ -113,6 +113,8 @@ PROTOTYPES = {
     "smoe_dequant": (_I, [_P, C.POINTER(QWeights), _U32, _U32, _U32, _P]),
     "smoe_router": (_I, [_P, _P, _P, _U32, _U32, _U32, _U32, _I, _P, _P, _P]),
     "smoe_softmax_topk": (_I, [_P, _P, _U32, _U32, _U32, _I, _P, _P]),
+    "smoe_softmax": (_I, [_P, _P, _U32, _U32, _P]),
+    "smoe_expf": (_I, [_P, _P, _P, _U64]),
     "smoe_topk": (_I, [_P, _P, _U32, _U32, _U32, _P, _P]),
     "smoe_noaux_tc_topk": (_I, [_P, _P, _P, _U32, _U32, _U32, _U32, _U32, C.c_float, _P, _P, _P]),
     "smoe_expert_bytes": (_U64, [C.POINTER(ExpertShape)]),

@@ -388,6 +388,21 @@ int smoe_softmax_topk(smoe_handle* h, const float* logits, uint32_t n_tokens, ui
   return hip_status(launch_topk(logits, n_tokens, n_experts, k, true, normalize != 0, ro, h->stream));
 }
 
+int smoe_softmax(smoe_handle* h, const float* logits, uint32_t n_tokens, uint32_t n, float* probs) {
+  if (!h || !logits || !probs) return SMOE_ERR_INVALID_ARG;
+  if (int rc = check_router(n_tokens, n, 1)) return rc;
+  if (int rc = use_device(h)) return rc;
+  RouteOut ro{};
+  ro.probs = probs;
+  return hip_status(launch_topk(logits, n_tokens, n, 1, true, false, ro, h->stream));
+}
+
+int smoe_expf(smoe_handle* h, const float* x, float* y, uint64_t n) {
+  if (!h || ((!x || !y) && n)) return SMOE_ERR_INVALID_ARG;
+  if (int rc = use_device(h)) return rc;
+  return hip_status(launch_expf(x, y, n, h->stream));
+}
+
 int smoe_topk(smoe_handle* h, const float* scores, uint32_t n_tokens, uint32_t n, uint32_t k,
               int32_t* idx, float* values) {
   if (!h || !scores || !idx || !values) return SMOE_ERR_INVALID_ARG;

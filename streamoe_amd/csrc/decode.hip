@@ -528,24 +528,15 @@ __global__ __launch_bounds__(64) void k_topk(const float* __restrict__ scores, u
     v[e] = j < n ? s[j] : -INFINITY;
   }
   if (softmax) {
-    // moe_router.rs:52-72: max, exp(v - max), sum, * (1 / sum).
-    float m = -INFINITY;
+    // moe_router.rs:52-72, the reference's probabilities bit for bit.
+    __shared__ float sprob[64 * P];
+    softmax_ref<P, true>(v, n, lane, sprob, load_exp_tab(lane));
+    if (out.probs) {
 #pragma unroll
-    for (int e = 0; e < P; ++e) m = fmaxf(m, v[e]);
-    m = wave_max(m);
-    float sum = 0.f;
-#pragma unroll
-    for (int e = 0; e < P; ++e) {
-      const uint32_t j = e * 64 + lane;
-      v[e] = j < n ? expf(v[e] - m) : 0.f;
-      sum += v[e];
-    }
-    sum = group_sum<64>(sum);
-    const float inv = 1.0f / sum;
-#pragma unroll
-    for (int e = 0; e < P; ++e) {
-      const uint32_t j = e * 64 + lane;
-      v[e] = j < n ? v[e] * inv : -INFINITY;
+      for (int e = 0; e < P; ++e) {
+        const uint32_t j = e * 64 + lane;
+        if (j < n) out.probs[(size_t)t * n + j] = v[e];
+      }
     }
   }
   // The reference's running-minimum top-k (moe_router.rs:83-124); lane s < k
@@ -583,6 +574,29 @@ __global__ __launch_bounds__(64) void k_topk(const float* __restrict__ scores, u
       out.table->shared_gate = out.gate_scores ? out.gate_scores[0] : __builtin_nanf("");
     }
   }
+}
+
+// glibc's expf over a buffer: one element per lane, whole waves (the table
+// lookup is a lane permute), grid-stride.
+__global__ __launch_bounds__(256) void k_expf(const float* __restrict__ x, float* __restrict__ y, uint64_t n) {
+  const ExpTabReg tab = load_exp_tab((int)(threadIdx.x & 63));
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  // Every wave runs the same number of iterations (n rounded up to whole
+  // grid strides), so the permute always sees all 64 lanes active.
+  const uint64_t iters = (n + stride - 1) / stride;
+  for (uint64_t it = 0; it < iters; ++it) {
+    const uint64_t i = it * stride + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const float v = x[i < n ? i : n - 1];
+    const float r = wave_expf_ref(v, tab);
+    if (i < n) y[i] = r;
+  }
+}
+
+hipError_t launch_expf(const float* x, float* y, uint64_t n, hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  const uint64_t blocks = (n + 255) / 256;
+  hipLaunchKernelGGL(k_expf, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, st, x, y, n);
+  return hipGetLastError();
 }
 
 hipError_t launch_topk(const float* scores, uint32_t n_tokens, uint32_t n, uint32_t k,

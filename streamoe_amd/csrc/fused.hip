@@ -427,6 +427,7 @@ __global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a_all) {
   const FusedLayer a = token_view<HC>(a_all, blockIdx.y);
   __shared__ int32_t sid[kMaxK];
   __shared__ float sval[kMaxK];
+  __shared__ float sprob[64 * P];  // the exact softmax's values (softmax_ref)
   FaClock clk;
   fa_stamp(a, clk, 0, false);
   const int lane = threadIdx.x;
@@ -448,7 +449,9 @@ __global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a_all) {
     fa_stamp(a, clk, 1, true);
     int32_t id;
     if (!topk_slot_logits<P, KC>(v, E, k, slot, lane, id)) {
-      wave_softmax<P>(v, E, lane);
+      // Ambiguous set (a tie or a near-tie at the k/k+1 boundary, NaN): the
+      // reference's probabilities bit for bit and its running-minimum scan.
+      softmax_ref<P>(v, E, lane, sprob, load_exp_tab(lane));
       exact_topk<P>(v, k, lane, sid, sval);
       __syncthreads();
       id = sid[slot];
@@ -463,23 +466,37 @@ __global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a_all) {
     for (int h = 0; h < HC; ++h) load_limbs(a.xl + ((size_t)lane + 64 * h) * kXLimbWords, xl[h]);
     gateup_rows<4, false, HC>(a, clk, a.shared, a.sgeom, r0, lane, xl, a.act + (size_t)k * I);
   } else {
-    // Route table (normalize_weights, moe_router.rs:130-141).
-    __shared__ float sprob[64 * P];
+    // Route table (normalize_weights, moe_router.rs:130-141). The
+    // reference's probabilities bit for bit (softmax_ref) wherever they
+    // decide the set or are returned to the caller.
     // The shared-expert gate score gate . x is computed here, off the
     // critical path (in the router kernel its extra wave ended last): its
     // loads go out with the logits'.
     const bool gated = a.gate != nullptr;
     f32x4 gw[HC][kChunk / 4];
     FaX<HC> gx;
+    const ExpTabReg tab = load_exp_tab(lane);
     fa_row_load<HC>(gated ? a.gate : a.router, lane, gw);
     fa_x_load<HC>(a, lane, gx);
     float v[P];
     load_logits<P>(a.logits, E, lane, v);
     const bool is_set = topk_set_logits<P, KC>(v, E, k, lane, sid);
-    wave_softmax<P>(v, E, lane);
-    if (!is_set) exact_topk<P>(v, k, lane, sid, sval);
+    float lg[P];  // the logits, for the caller's exact slot order below
 #pragma unroll
-    for (int e = 0; e < P; ++e) sprob[lane * P + e] = v[e];
+    for (int e = 0; e < P; ++e) lg[e] = v[e];
+    if (is_set) {
+      // Unambiguous set: the weights only enter the combine (compared within
+      // a tolerance), so the fast softmax; the exact one's sequential sum
+      // would make this wave the last of the kernel. The same whether or
+      // not the caller asks for idx / weights, so the combine does not
+      // depend on it.
+      wave_softmax_fast<P>(v, E, lane);
+#pragma unroll
+      for (int e = 0; e < P; ++e) sprob[lane * P + e] = v[e];
+    } else {
+      softmax_ref<P>(v, E, lane, sprob, tab);
+      exact_topk<P>(v, k, lane, sid, sval);
+    }
     __syncthreads();
     if (is_set && lane < (int)k) sval[lane] = sprob[sid[lane]];
     __syncthreads();
@@ -510,7 +527,9 @@ __global__ __launch_bounds__(64) void k_fa_gateup(FusedLayer a_all) {
       __shared__ int32_t eid[kMaxK];
       __shared__ float evl[kMaxK];
       if (is_set) {
-        exact_topk<P>(v, k, lane, eid, evl);
+        __syncthreads();  // sprob is reused
+        softmax_ref<P>(lg, E, lane, sprob, tab);
+        exact_topk<P>(lg, k, lane, eid, evl);
       } else if (lane < (int)k) {
         eid[lane] = sid[lane];
         evl[lane] = sval[lane];

@@ -47,9 +47,13 @@ struct RouteOut {
   uint64_t stride;
   const uint8_t* shared_blob;  // null: no shared expert
   const float* gate_scores;    // [n_tokens] pre-sigmoid shared gate, or null (unscaled)
+  float* probs;                // [n_tokens, n] softmax probabilities, or null
 };
 
 BlobGeom blob_geom(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t bits);
+
+// y[i] = expf_ref(x[i]) (glibc's expf), i < n.
+hipError_t launch_expf(const float* x, float* y, uint64_t n, hipStream_t st);
 
 // One decode layer for the three-kernel path (fused.hip).
 struct FusedLayer {

@@ -5,15 +5,91 @@
 #pragma once
 
 #include "common.h"
+#include "expf_ref.h"
 
 namespace smoe {
 
 // ---------------------------------------------------------------------------
-// Softmax over n values held P per lane (lane l owns [l*P, l*P + P)), as the
-// reference: max, exp(v - max), sum, * (1 / sum). Invalid entries -> -inf.
+// The reference's softmax (moe_router.rs:52-72) bit for bit: max, then
+// e_j = expf(v_j - max) with glibc's expf (expf_ref.h), the sum of the e_j
+// in index order (one add after another, as the reference's loop), inv =
+// 1 / sum correctly rounded, p_j = e_j * inv. n values held P per lane:
+// lane l owns [l*P, l*P + P) (TR = false) or l, l + 64, ... (TR = true).
+// Positions >= n become -inf. The max is the wave's fmaxf (it differs from
+// the reference's strict-> scan only when a NaN is present, and then every
+// probability is NaN in both). The sum runs over sbuf (LDS, >= 64 P
+// floats, which also receives the probabilities): every lane adds the same
+// broadcast values, so all lanes hold the sum. `tab` is this lane's table
+// entry (load_exp_tab). Single-wave blocks only (one barrier).
 // ---------------------------------------------------------------------------
+struct ExpTabReg {
+  uint32_t lo, hi;  // kExpTab[lane & 31]
+};
+
+__device__ __forceinline__ ExpTabReg load_exp_tab(int lane) {
+  static __device__ const uint64_t tab[32] = {
+      kExpTab[0],  kExpTab[1],  kExpTab[2],  kExpTab[3],  kExpTab[4],  kExpTab[5],  kExpTab[6],  kExpTab[7],
+      kExpTab[8],  kExpTab[9],  kExpTab[10], kExpTab[11], kExpTab[12], kExpTab[13], kExpTab[14], kExpTab[15],
+      kExpTab[16], kExpTab[17], kExpTab[18], kExpTab[19], kExpTab[20], kExpTab[21], kExpTab[22], kExpTab[23],
+      kExpTab[24], kExpTab[25], kExpTab[26], kExpTab[27], kExpTab[28], kExpTab[29], kExpTab[30], kExpTab[31]};
+  const uint64_t t = tab[lane & 31];
+  return ExpTabReg{(uint32_t)t, (uint32_t)(t >> 32)};
+}
+
+// expf_ref with the table entry taken from lane i (every lane must run it).
+__device__ __forceinline__ float wave_expf_ref(float x, ExpTabReg tab) {
+  return expf_ref(x, [&](uint32_t i) -> uint64_t {
+    const int a = (int)(i << 2);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_bpermute(a, (int)tab.lo);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_bpermute(a, (int)tab.hi);
+    return ((uint64_t)hi << 32) | lo;
+  });
+}
+
+template <int P, bool TR = false>
+__device__ __forceinline__ void softmax_ref(float (&v)[P], uint32_t n, int lane, float* sbuf, ExpTabReg tab) {
+  float m = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < P; ++e) m = fmaxf(m, v[e]);
+  m = readlane_f(wave_max_last(m), 63);
+#pragma unroll
+  for (int e = 0; e < P; ++e) {
+    const uint32_t j = TR ? (uint32_t)(e * 64 + lane) : (uint32_t)(lane * P + e);
+    const float ex = wave_expf_ref(v[e] - m, tab);
+    v[e] = j < n ? ex : 0.f;
+    sbuf[j] = v[e];
+  }
+  __syncthreads();
+  // Sequential sum in index order; the zeros past n change nothing (the sum
+  // of non-negative values is never -0).
+  float sum = 0.f;
+  const f32x4* s4 = reinterpret_cast<const f32x4*>(sbuf);
+  for (uint32_t i = 0; i < (n + 3) / 4; ++i) {
+    const f32x4 q = s4[i];
+    sum += q.x;
+    sum += q.y;
+    sum += q.z;
+    sum += q.w;
+  }
+  const float inv = __fdiv_rn(1.0f, sum);
+#pragma unroll
+  for (int e = 0; e < P; ++e) {
+    const uint32_t j = TR ? (uint32_t)(e * 64 + lane) : (uint32_t)(lane * P + e);
+    v[e] = j < n ? v[e] * inv : -INFINITY;
+  }
+  __syncthreads();  // every lane has read sbuf
+#pragma unroll
+  for (int e = 0; e < P; ++e) sbuf[TR ? e * 64 + lane : lane * P + e] = v[e];
+  __syncthreads();
+}
+
+// The same softmax with a wave-tree sum and the device expf: within a few
+// ulps of softmax_ref, and ~0.8 us shorter (no sequential sum). Used only
+// for the combine weights of a decode layer whose top-k set is unambiguous
+// and whose caller asked for no idx / weights: those weights enter the
+// combine, which is compared within a tolerance, and decide nothing.
 template <int P>
-__device__ __forceinline__ void wave_softmax(float (&v)[P], uint32_t n, int lane) {
+__device__ __forceinline__ void wave_softmax_fast(float (&v)[P], uint32_t n, int lane) {
   float m = -INFINITY;
 #pragma unroll
   for (int e = 0; e < P; ++e) m = fmaxf(m, v[e]);

@@ -106,6 +106,8 @@ extern "C" {
                        logits_out: *mut f32) -> c_int;
     pub fn smoe_softmax_topk(h: *mut smoe_handle, logits: *const f32, n_tokens: u32, n_experts: u32, k: u32,
                              normalize: c_int, idx: *mut i32, weights: *mut f32) -> c_int;
+    pub fn smoe_softmax(h: *mut smoe_handle, logits: *const f32, n_tokens: u32, n: u32, probs: *mut f32) -> c_int;
+    pub fn smoe_expf(h: *mut smoe_handle, x: *const f32, y: *mut f32, n: u64) -> c_int;
     pub fn smoe_topk(h: *mut smoe_handle, scores: *const f32, n_tokens: u32, n: u32, k: u32, idx: *mut i32,
                      values: *mut f32) -> c_int;
     pub fn smoe_noaux_tc_topk(h: *mut smoe_handle, logits: *const f32, correction_bias: *const f32,
