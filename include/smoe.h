@@ -419,6 +419,36 @@ int smoe_moe_prefill(smoe_handle* h, const smoe_expert_shape* shape, const void*
                      const float* weights, const void* x, int x_is_bf16, uint32_t n_tokens,
                      uint32_t k, float* out_sum, void* workspace, uint64_t workspace_bytes);
 
+/* Device workspace bytes smoe_moe_prefill_block needs (0: a shape
+ * without grouped-GEMM tiles, which the block entry does not take). */
+uint64_t smoe_moe_prefill_block_workspace_size(const smoe_expert_shape* shape, uint32_t n_tokens,
+                                               uint32_t n_experts, uint32_t k, int has_shared);
+
+/* The prefill MoE block of one layer (linear_attn_forward.rs:3998-4075):
+ * the routed experts as smoe_moe_prefill, an optional shared expert over
+ * all n_tokens (4-bit, the routed hidden / inter / group; its gate/up and
+ * down run as further work items of the same grouped GEMMs when the routed
+ * experts are 4-bit, so its weights are read once per pass, else through
+ * the 4-bit GEMM instances of their own), then per token t
+ *   hidden_out[t] = (h_mid[t] + moe_sum[t]) + sigmoid(g_t) * shared_out[t]
+ * with g_t = shared_gate . x[t] (f32 [hidden]; NULL: the shared term
+ * unscaled), or hidden_out[t] = h_mid[t] + moe_sum[t] without a shared
+ * expert: moe_combine_residual_n_tokens_cpu / _noshared_ (backend/cpu/
+ * mod.rs:657-695, the Metal moe_combine_residual_n_tokens,
+ * shaders.metal:3318-3355), added in that order with no fused
+ * multiply-add, the sigmoid with glibc's expf (cpu_ops.rs:22-25). The
+ * shared expert's SwiGLU and down projection are the reference's
+ * MatvecNTokens + SwigluFusedBatched + MatvecNTokens ops in one pass.
+ * h_mid, hidden_out: device f32 [n_tokens, hidden] (hidden_out may alias
+ * h_mid). Grouped-GEMM shapes only (see smoe_moe_prefill); others return
+ * SMOE_ERR_UNSUPPORTED_SHAPE. Enqueue-only, allocates nothing, capturable
+ * in a HIP graph. */
+int smoe_moe_prefill_block(smoe_handle* h, const smoe_expert_shape* shape, const void* experts,
+                           uint64_t stride, uint32_t n_experts, const int32_t* idx, const float* weights,
+                           const void* x, int x_is_bf16, uint32_t n_tokens, uint32_t k,
+                           const void* shared_expert, const float* shared_gate, const float* h_mid,
+                           float* hidden_out, void* workspace, uint64_t workspace_bytes);
+
 /* ------------------------------------------------------------------ */
 /* Expert arena loader: packed_experts/layer_NN.bin -> device memory    */
 /* ------------------------------------------------------------------ */

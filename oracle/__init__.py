@@ -53,6 +53,7 @@ def _declare(L):
         "orc_expert_swiglu": (C.c_int, [_P, _U32, _U32, _U32, _U32, _P, _P, C.c_int]),
         "orc_softmax": (C.c_int, [_P, _U32]),
         "orc_softmax_rows": (C.c_int, [_P, _U32, _U32, C.c_int]),
+        "orc_moe_combine_residual_n_tokens": (None, [_P, _P, _P, _P, _P, _U32, _U32]),
         "orc_expf_many": (C.c_int, [_P, _P, C.c_uint64, C.c_int]),
         "orc_topk": (C.c_int, [_P, _U32, _U32, _P, _P]),
         "orc_normalize_weights": (None, [_P, _U32]),
@@ -299,6 +300,38 @@ def moe_permute_fuse(experts, stride, bits, hidden, inter, group, x, buckets, n_
                                     _p(offs), eids.size, _p(tok), _p(ws), _p(out), nthreads)
     assert rc == 0, rc
     return out
+
+
+def moe_combine_residual_n_tokens(h_mid, moe_sum, shared_out=None, shared_gate=None):
+    """hidden = (h_mid + moe_sum) + sigmoid(gate[t]) * shared_out per token
+    (backend/cpu/mod.rs:657-695)."""
+    h_mid, moe_sum = _c(h_mid, np.float32), _c(moe_sum, np.float32)
+    n, dim = h_mid.shape
+    so = None if shared_out is None else _c(shared_out, np.float32)
+    sg = None if shared_gate is None else _c(shared_gate, np.float32)
+    out = np.empty_like(h_mid)
+    lib().orc_moe_combine_residual_n_tokens(_p(h_mid), _p(moe_sum), _p(so), _p(sg), _p(out), n, dim)
+    return out
+
+
+def moe_prefill_block(experts, stride, bits, hidden, inter, group, n_experts, x, idx, w, h_mid,
+                      shared=None, gate=None, nthreads=0):
+    """The prefill MoE block (linear_attn_forward.rs:3998-4075) on the CPU:
+    moe_permute_fuse over the routed experts; the shared expert's FFN per
+    token (run_packed_expert_swiglu, 4-bit); its gate score gate . x_t (an
+    f32 matvec, sequential FMA); moe_combine_residual_n_tokens."""
+    x = _c(x, np.float32)
+    n, k = idx.shape
+    rc, *b = build_expert_buckets(idx, w, n, k, n_experts)
+    assert rc == 0, rc
+    moe = moe_permute_fuse(experts, stride, bits, hidden, inter, group, x, (rc, *b), n, nthreads)
+    so = sg = None
+    if shared is not None:
+        so = np.stack([expert_swiglu(shared, 4, hidden, inter, group, x[t], nthreads) for t in range(n)])
+        if gate is not None:
+            sg = np.array([f32_matvec(np.asarray(gate, np.float32)[None, :], x[t])[0] for t in range(n)],
+                          np.float32)
+    return moe_combine_residual_n_tokens(h_mid, moe, so, sg), moe, so, sg
 
 
 # ---- test-input generator ---------------------------------------------------------

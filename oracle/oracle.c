@@ -557,6 +557,29 @@ void orc_combine(const float* expert_out, const float* weights, uint32_t k, cons
   free(moe);
 }
 
+/* moe_combine_residual_n_tokens_cpu, backend/cpu/mod.rs:657-680, and   */
+/* its no-shared sibling (682-695): per token t, g = sigmoid(gate[t])    */
+/* (cpu_ops.rs:22-25), hidden = h_mid + moe_sum + g * shared_out,       */
+/* evaluated left to right as Rust does: (h_mid + moe_sum) + (g * s),   */
+/* no fused multiply-add. shared_out NULL: hidden = h_mid + moe_sum.    */
+/* shared_gate NULL with shared_out: the shared term unscaled (g = 1).  */
+void orc_moe_combine_residual_n_tokens(const float* h_mid, const float* moe_sum, const float* shared_out,
+                                       const float* shared_gate, float* hidden_out, uint32_t n_tokens,
+                                       uint32_t dim) {
+  for (uint32_t t = 0; t < n_tokens; ++t) {
+    const float g = shared_gate ? orc_sigmoid(shared_gate[t]) : 1.0f;
+    for (uint32_t i = 0; i < dim; ++i) {
+      const size_t idx = (size_t)t * dim + i;
+      float v = h_mid[idx] + moe_sum[idx];
+      if (shared_out) {
+        const float gs = g * shared_out[idx];
+        v = v + gs;
+      }
+      hidden_out[idx] = v;
+    }
+  }
+}
+
 /* ------------------------------------------------------------------ */
 /* One decode layer, the per-token path (attn/linear_attn_forward.rs:  */
 /* 2123-2170 then moe_dispatch_per_token) restated on the CPU — router */

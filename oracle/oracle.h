@@ -112,6 +112,11 @@ int orc_moe_decode_layer(const orc_layer* L, const float* x, const float* h_mid,
 void orc_rms_norm_bf16(const float* x, const uint16_t* w, uint32_t dim, float eps, float* out);
 
 /* ---- prefill --------------------------------------------------------- */
+/* moe_combine_residual_n_tokens_cpu (backend/cpu/mod.rs:657-695):     */
+/* hidden = (h_mid + moe_sum) + sigmoid(gate[t]) * shared_out, no FMA.  */
+void orc_moe_combine_residual_n_tokens(const float* h_mid, const float* moe_sum, const float* shared_out,
+                                       const float* shared_gate, float* hidden_out, uint32_t n_tokens,
+                                       uint32_t dim);
 int orc_build_expert_buckets(const int32_t* idx, const float* w, uint32_t n_tokens, uint32_t k,
                              uint32_t n_experts, int32_t* expert_ids, uint32_t* offsets,
                              int32_t* token_idx, float* weights, uint32_t* n_buckets);

@@ -268,6 +268,20 @@ class Kernels:
                                      _ptr(out_sum), _ptr(workspace),
                                      0 if workspace is None else workspace.numel() * workspace.element_size())
 
+    def moe_prefill_block_workspace_size(self, layout, n_tokens, n_experts, k, has_shared):
+        shape = layout.shape()
+        return _lib.smoe_moe_prefill_block_workspace_size(C.byref(shape), n_tokens, n_experts, k, int(has_shared))
+
+    def moe_prefill_block(self, layout, experts, stride, n_experts, idx, weights, x, x_is_bf16, n_tokens, k,
+                          shared, gate, h_mid, hidden_out, workspace):
+        """The prefill MoE block (linear_attn_forward.rs:3998-4075): routed
+        experts, optional shared expert with sigmoid gate, residual."""
+        shape = layout.shape()
+        return _lib.smoe_moe_prefill_block(self.h, C.byref(shape), _ptr(experts), stride, n_experts, _ptr(idx),
+                                           _ptr(weights), _ptr(x), int(x_is_bf16), n_tokens, k, _ptr(shared),
+                                           _ptr(gate), _ptr(h_mid), _ptr(hidden_out), _ptr(workspace),
+                                           0 if workspace is None else workspace.numel() * workspace.element_size())
+
     # -- expert files -------------------------------------------------------------
     def load_file(self, path, dst, offset=0, nbytes=0):
         """Copy bytes [offset, offset + nbytes) of the file (nbytes 0: to its

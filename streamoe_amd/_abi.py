@@ -128,6 +128,9 @@ PROTOTYPES = {
     "smoe_moe_prefill_workspace_size": (_U64, [C.POINTER(ExpertShape), _U32, _U32, _U32]),
     "smoe_moe_prefill": (_I, [_P, C.POINTER(ExpertShape), _P, _U64, _U32, _P, _P, _P, _I, _U32, _U32, _P, _P,
                               _U64]),
+    "smoe_moe_prefill_block_workspace_size": (_U64, [C.POINTER(ExpertShape), _U32, _U32, _U32, _I]),
+    "smoe_moe_prefill_block": (_I, [_P, C.POINTER(ExpertShape), _P, _U64, _U32, _P, _P, _P, _I, _U32, _U32, _P,
+                                    _P, _P, _P, _P, _U64]),
     "smoe_layer_file_layout": (_I, [_U64, _U32, _U32, _U32, _U32, _U64, _U64, C.POINTER(FileLayout)]),
     "smoe_load_file": (_I, [_P, C.c_char_p, _U64, _U64, _P, _U64, C.POINTER(_U64)]),
     "smoe_stream_read": (_I, [_P, _P, C.c_uint64, _P]),

@@ -744,8 +744,16 @@ uint64_t smoe_moe_prefill_workspace_size(const smoe_expert_shape* shape, uint32_
   if (!shape || !shape->group || !n_tokens || !n_experts || !k) return 0;
   if (!prefill_supported(shape->hidden, shape->inter, shape->group, shape->bits, n_tokens, n_experts, k))
     return prefill_tokens_workspace(shape->hidden, shape->inter, n_tokens, k, true);
-  return prefill_workspace(shape->hidden, shape->inter, shape->group, n_tokens, n_experts, k, nullptr,
+  return prefill_workspace(shape->hidden, shape->inter, shape->group, n_tokens, n_experts, k, false, nullptr,
                            nullptr);
+}
+
+uint64_t smoe_moe_prefill_block_workspace_size(const smoe_expert_shape* shape, uint32_t n_tokens,
+                                               uint32_t n_experts, uint32_t k, int has_shared) {
+  if (!shape || !shape->group || !n_tokens || !n_experts || !k) return 0;
+  if (!prefill_supported(shape->hidden, shape->inter, shape->group, shape->bits, n_tokens, n_experts, k)) return 0;
+  return prefill_workspace(shape->hidden, shape->inter, shape->group, n_tokens, n_experts, k, has_shared != 0,
+                           nullptr, nullptr);
 }
 
 int smoe_moe_prefill(smoe_handle* h, const smoe_expert_shape* shape, const void* experts,
@@ -777,7 +785,7 @@ int smoe_moe_prefill(smoe_handle* h, const smoe_expert_shape* shape, const void*
   }
   PfArgs a{};
   const uint64_t need = prefill_workspace(shape->hidden, shape->inter, shape->group, n_tokens,
-                                          n_experts, k, &a, (uint8_t*)workspace);
+                                          n_experts, k, false, &a, (uint8_t*)workspace);
   if (workspace_bytes < need) return SMOE_ERR_WORKSPACE_TOO_SMALL;
   if (int rc = use_device(h)) return rc;
   a.g = blob_geom(shape->hidden, shape->inter, shape->group, shape->bits);
@@ -793,6 +801,53 @@ int smoe_moe_prefill(smoe_handle* h, const smoe_expert_shape* shape, const void*
   a.out = out_sum;
   a.err = h->err;
   a.trace = h->trace;
+  int n_cu = 0;
+  if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, h->device) != hipSuccess || n_cu <= 0)
+    return SMOE_ERR_HIP;
+  return hip_status(launch_prefill(a, (uint32_t)n_cu, h->stream));
+}
+
+int smoe_moe_prefill_block(smoe_handle* h, const smoe_expert_shape* shape, const void* experts,
+                           uint64_t stride, uint32_t n_experts, const int32_t* idx, const float* weights,
+                           const void* x, int x_is_bf16, uint32_t n_tokens, uint32_t k,
+                           const void* shared_expert, const float* shared_gate, const float* h_mid,
+                           float* hidden_out, void* workspace, uint64_t workspace_bytes) {
+  if (!h || !experts || !idx || !weights || !x || !h_mid || !hidden_out || !workspace || !n_tokens || !n_experts)
+    return SMOE_ERR_INVALID_ARG;
+  if (shared_gate && !shared_expert) return SMOE_ERR_INVALID_ARG;
+  if (int rc = check_shape(shape)) return rc;
+  if (k < 1 || k > SMOE_MAX_K || k > n_experts) return SMOE_ERR_BAD_K;
+  if (stride < smoe_expert_bytes(shape)) return SMOE_ERR_INVALID_ARG;
+  if (n_tokens > kPfMaxTokens) return SMOE_ERR_UNSUPPORTED_SHAPE;
+  if (!prefill_supported(shape->hidden, shape->inter, shape->group, shape->bits, n_tokens, n_experts, k))
+    return SMOE_ERR_UNSUPPORTED_SHAPE;
+  if (!blob_aligned(experts, shape->bits) || stride % 16 || !aligned(x, 0, 16) || !aligned(h_mid, 0, 16) ||
+      !aligned(hidden_out, 0, 16) || !aligned(workspace, 0, 256) || (shared_expert && !blob_aligned(shared_expert, 4)) ||
+      (shared_gate && !aligned(shared_gate, 0, 16)))
+    return SMOE_ERR_MISALIGNED;
+  PfArgs a{};
+  const uint64_t need = prefill_workspace(shape->hidden, shape->inter, shape->group, n_tokens, n_experts, k,
+                                          shared_expert != nullptr, &a, (uint8_t*)workspace);
+  if (workspace_bytes < need) return SMOE_ERR_WORKSPACE_TOO_SMALL;
+  if (int rc = use_device(h)) return rc;
+  a.g = blob_geom(shape->hidden, shape->inter, shape->group, shape->bits);
+  a.experts = (const uint8_t*)experts;
+  a.stride = stride;
+  a.E = n_experts;
+  a.k = k;
+  a.n_tokens = n_tokens;
+  a.idx = idx;
+  a.w = weights;
+  a.x = x;
+  a.x_bf16 = x_is_bf16 != 0;
+  a.out = hidden_out;
+  a.err = h->err;
+  a.trace = h->trace;
+  a.shared = (const uint8_t*)shared_expert;
+  a.sg = blob_geom(shape->hidden, shape->inter, shape->group, 4);
+  a.shared_in_list = shared_expert && shape->bits == 4;
+  a.gate = shared_expert ? shared_gate : nullptr;
+  a.h_mid = h_mid;
   int n_cu = 0;
   if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, h->device) != hipSuccess || n_cu <= 0)
     return SMOE_ERR_HIP;

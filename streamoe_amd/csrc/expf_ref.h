@@ -45,6 +45,15 @@ static constexpr uint64_t kExpTab[32] = {
     0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
 
+#if defined(__HIPCC__) || defined(__HIP__)
+// The table in device memory, for lookups by index (expf_ref_dev).
+static __device__ const uint64_t kExpTabDev[32] = {
+    kExpTab[0],  kExpTab[1],  kExpTab[2],  kExpTab[3],  kExpTab[4],  kExpTab[5],  kExpTab[6],  kExpTab[7],
+    kExpTab[8],  kExpTab[9],  kExpTab[10], kExpTab[11], kExpTab[12], kExpTab[13], kExpTab[14], kExpTab[15],
+    kExpTab[16], kExpTab[17], kExpTab[18], kExpTab[19], kExpTab[20], kExpTab[21], kExpTab[22], kExpTab[23],
+    kExpTab[24], kExpTab[25], kExpTab[26], kExpTab[27], kExpTab[28], kExpTab[29], kExpTab[30], kExpTab[31]};
+#endif
+
 SMOE_HD inline double expref_asd(uint64_t u) {
   double d;
   memcpy(&d, &u, 8);
@@ -92,5 +101,17 @@ SMOE_HD inline float expf_ref(float x, Lookup lookup) {
   }
   return res;
 }
+
+#if defined(__HIPCC__) || defined(__HIP__)
+// expf_ref with the table read from device memory (one load per call, any
+// lanes active).
+__device__ inline float expf_ref_dev(float x) {
+  return expf_ref(x, [](uint32_t i) { return kExpTabDev[i]; });
+}
+
+// The reference's sigmoid, 1 / (1 + exp(-x)) (cpu_ops.rs:22-25), with
+// glibc's expf and a correctly rounded division.
+__device__ inline float sigmoid_ref(float x) { return __fdiv_rn(1.0f, 1.0f + expf_ref_dev(-x)); }
+#endif
 
 }  // namespace smoe

@@ -142,14 +142,29 @@ struct PfArgs {
   uint16_t* x_lo;          // [n, hidden] low halves (fp32 input only)
   uint16_t* act_hi;        // [n*k, inter] SwiGLU output as fp16, MFMA order (qmm: x as bf16 hi)
   uint16_t* act_lo;        // qmm only: x as bf16 lo (null for the prefill)
-  float* down;             // [n*k, hidden]
+  float* down;             // [n*k (+ n), hidden]
   uint64_t* trace;         // k_pf_route timestamps (8 words), or null (diagnostics)
+  // The MoE block's tail (linear_attn_forward.rs:3998-4075): an optional
+  // shared expert over all n tokens (its entries at positions n*k + t),
+  // its pre-sigmoid gate scores gate . x_t, and the residual h_mid.
+  const uint8_t* shared;   // shared expert blob (4-bit, routed hidden/inter/group), or null
+  BlobGeom sg;             // its geometry
+  int shared_in_list;      // 1: its items ride in the routed work list (routed bits 4);
+                           // 0: a list of their own (sitems, ...) and 4-bit GEMM launches
+  const float* gate;       // [hidden] shared-expert gate vector, or null (unscaled)
+  const float* h_mid;      // [n_tokens, hidden] residual, or null (out = the routed sum)
+  float* gscore;           // [n] gate . x_t
+  uint32_t* xr;            // [9] per-XCD ranges of the work list (null: even split)
+  uint32_t* sitems;        // shared-only work list (shared_in_list == 0): items, count, token rows, ranges
+  uint32_t* sn_items;
+  uint32_t* sitem_tok;
+  uint32_t* sxr;
 };
 
 // Workspace bytes for these sizes; with `a` and `base`, also points a's
 // workspace fields into base.
 uint64_t prefill_workspace(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t n_tokens,
-                           uint32_t n_experts, uint32_t k, PfArgs* a, uint8_t* base);
+                           uint32_t n_experts, uint32_t k, bool shared, PfArgs* a, uint8_t* base);
 // Prefill through the per-phase decode kernels, one token at a time, for
 // the shapes prefill_supported refuses (decode.hip): workspace bytes and
 // launch.

@@ -46,6 +46,7 @@
 // and the 8 values of one MFMA step are in the order of the code unpack,
 // [v0, v4, v1, v5, v2, v6, v3, v7]; activations are permuted to match.
 #include "common.h"
+#include "expf_ref.h"
 #include "kernels.h"
 
 namespace smoe {
@@ -181,6 +182,8 @@ constexpr uint32_t kPfPart8 = kPfMaxGroupsK * 128 / 8;   // 8-input partial sums
 __device__ __forceinline__ void pf_prep_token(const PfArgs& a, uint32_t t, bool live, uint32_t tid, float* part8) {
   const uint32_t H = a.g.hidden, G = a.g.group;
   const bool x_bf16 = a.x_bf16;
+  const float* const gate = a.gate;
+  float gdot = 0.f;  // this thread's share of the shared-expert gate score gate . x_t
   if (live) {
     for (uint32_t k0 = tid * 8; k0 < H; k0 += 256 * 8) {
       float f[8];
@@ -196,6 +199,13 @@ __device__ __forceinline__ void pf_prep_token(const PfArgs& a, uint32_t t, bool 
         const f32x4* p = reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(a.x) + (size_t)t * H + k0);
         const f32x4 u = p[0], v = p[1];
         f[0] = u.x, f[1] = u.y, f[2] = u.z, f[3] = u.w, f[4] = v.x, f[5] = v.y, f[6] = v.z, f[7] = v.w;
+      }
+      if (gate) {
+        const f32x4* gp = reinterpret_cast<const f32x4*>(gate + k0);
+        const f32x4 g0 = gp[0], g1 = gp[1];
+        const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) gdot = __builtin_fmaf(gv[i], f[i], gdot);
       }
       u32x4 hi, lo;
       split_f32(f, hi, lo);
@@ -219,6 +229,17 @@ __device__ __forceinline__ void pf_prep_token(const PfArgs& a, uint32_t t, bool 
       float sum = 0.f;
       for (uint32_t j = 0; j < per; ++j) sum += part8[g * per + j];
       a.xsum[(size_t)t * ng + g] = sum;
+    }
+  }
+  if (gate) {
+    // The 256 thread shares, summed in thread order.
+    __syncthreads();
+    part8[tid] = gdot;
+    __syncthreads();
+    if (live && tid == 0) {
+      float sum = 0.f;
+      for (uint32_t j = 0; j < 256; ++j) sum += part8[j];
+      a.gscore[t] = sum;
     }
   }
 }
@@ -268,6 +289,7 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
   uint32_t* const col = reinterpret_cast<uint32_t*>(pf_dyn);
   uint16_t* const pre = reinterpret_cast<uint16_t*>(pf_dyn + E * cw * 4);
   __shared__ uint32_t offs[kPfMaxExperts];
+  __shared__ uint32_t s_nr;  // routed work items
   for (uint32_t i = tid; i < E * cw; i += blockDim.x) col[i] = 0;
   // Thread t owns token t: its k experts and weights stay in registers
   // (one read of the routing input), validated here.
@@ -386,15 +408,45 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
       co += c8[q];
       no += n8[q];
     }
-    if (tid == 63) *a.n_items = ni;
+    if (tid == 63) s_nr = ni;
   }
   __syncthreads();
   PF_STAMP(4);
+  // Work-list order: the routed items in expert order, cut into 8 XCD
+  // ranges [nr x / 8, nr (x + 1) / 8) (the GEMMs give range x to XCD x);
+  // a shared expert's items (all n tokens, entries n k + t, expert id E)
+  // are spread over the ranges, ns x / 8 .. ns (x + 1) / 8 after range x's
+  // routed items, so that no XCD takes all of them.
+  const uint32_t nr = s_nr;
+  const uint32_t ns = a.shared && a.shared_in_list ? (n + kPfMC - 1) / kPfMC : 0u;
+  auto fidx = [=](uint32_t i) { return i + ns * ((8u * (i + 1u) - 1u) / nr) / 8u; };
+  if (tid < 9) a.xr[tid] = nr * tid / 8u + ns * tid / 8u;
+  if (tid == 0) *a.n_items = nr + ns;
+  for (uint32_t j = tid; j < ns; j += blockDim.x) {
+    const uint32_t x = (8u * (j + 1u) - 1u) / ns, f = nr * (x + 1u) / 8u + j;
+    const uint32_t cnt = min(kPfMC, n - j * kPfMC);
+    a.items[2 * f] = E;
+    a.items[2 * f + 1] = (n * k + j * kPfMC) | (cnt << 16);
+    for (uint32_t r = 0; r < cnt; ++r) a.item_tok[f * kPfMC + r] = j * kPfMC + r;
+  }
+  if (a.shared && !a.shared_in_list) {
+    // A list of its own for 4-bit GEMM launches (routed bits 3).
+    const uint32_t ms = (n + kPfMC - 1) / kPfMC;
+    for (uint32_t j = tid; j < ms; j += blockDim.x) {
+      const uint32_t cnt = min(kPfMC, n - j * kPfMC);
+      a.sitems[2 * j] = 0;
+      a.sitems[2 * j + 1] = (n * k + j * kPfMC) | (cnt << 16);
+      for (uint32_t r = 0; r < cnt; ++r) a.sitem_tok[j * kPfMC + r] = j * kPfMC + r;
+    }
+    if (tid < 9) a.sxr[tid] = ms * tid / 8u;
+    if (tid == 0) *a.sn_items = ms;
+  }
   if (tid < E) {
     const uint32_t cnt = scnt[tid], nch = snch[tid], off = offs[tid], ibase = sibase[tid];
     for (uint32_t c = 0; c < nch; ++c) {
-      a.items[2 * (ibase + c)] = tid;
-      a.items[2 * (ibase + c) + 1] = (off + c * kPfMC) | (min(kPfMC, cnt - c * kPfMC) << 16);
+      const uint32_t f = fidx(ibase + c);
+      a.items[2 * f] = tid;
+      a.items[2 * f + 1] = (off + c * kPfMC) | (min(kPfMC, cnt - c * kPfMC) << 16);
     }
     // Rows past the count of the expert's last item are not written: the
     // GEMM clamps whatever they hold to a token id (their results are
@@ -418,7 +470,7 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
       for (uint32_t q = 0; q < kPfMaxK; ++q) r += (q < k && ex[q] < e) ? 1u : 0u;
       r = min(r, k - 1);  // a duplicated expert (already reported) stays in range
       a.tok_pw[tid * k + r] = make_uint2(pos, __float_as_uint(wt[s]));
-      a.item_tok[sibase[e] * kPfMC + row] = tid;
+      a.item_tok[fidx(sibase[e] + row / kPfMC) * kPfMC + row % kPfMC] = tid;
     }
   }
   PF_STAMP(5);
@@ -859,7 +911,8 @@ __device__ __forceinline__ void pf_unit_bias(const uint8_t* ub, uint32_t nch, ui
 
 template <int BITS, int G, int MODE, bool SPLIT, int KU, int NWD>
 __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32_t* __restrict__ items,
-                                                          const uint32_t* __restrict__ n_items_p) {
+                                                          const uint32_t* __restrict__ n_items_p,
+                                                          const uint32_t* __restrict__ xr) {
   using C = PfMM<BITS, G, MODE, SPLIT, KU, NWD>;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   // The wave index is uniform: in a scalar register, the role branches
@@ -886,8 +939,10 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
   // that XCD's L2 once instead of once per item.
   const uint32_t nx = gridDim.x % 8 == 0 ? 8 : 1, per = gridDim.x / nx;
   const uint32_t xg = blockIdx.x % nx, lb = blockIdx.x / nx;
+  // The ranges come from the bucketing launch (xr), or split evenly.
   const uint32_t n_items = *n_items_p;
-  const uint32_t item_lo = n_items * xg / nx, item_hi = n_items * (xg + 1) / nx;
+  const uint32_t item_lo = xr && nx == 8 ? xr[xg] : n_items * xg / nx;
+  const uint32_t item_hi = xr && nx == 8 ? xr[xg + 1] : n_items * (xg + 1) / nx;
   const uint32_t group_units = (item_hi - item_lo) * ncb;
   const uint32_t my_units = group_units > lb ? (group_units - lb + per - 1) / per : 0;
   const uint32_t total = my_units * nch;
@@ -898,6 +953,9 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
   const uint16_t* const alo_src = MODE == 0 ? a.x_lo : a.act_lo;
   const float* const gsum = MODE == 0 ? a.xsum : a.asum;
   const uint8_t* const experts = a.experts;
+  // Items of expert id E are the shared expert's (same geometry).
+  const uint8_t* const shared = a.shared_in_list ? a.shared : nullptr;
+  const uint32_t e_shared = a.E;
   const uint32_t* const item_tok = a.item_tok;
   const uint32_t last_tok = a.n_tokens - 1;
   const uint64_t stride = a.stride;
@@ -962,7 +1020,7 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
     const uint32_t cb = v % ncb;
     const uint32_t e = iw.x;
     const uint32_t start = iw.y & 0xFFFFu, cnt = iw.y >> 16;
-    const uint8_t* blob = experts + (size_t)e * stride;
+    const uint8_t* blob = shared && e == e_shared ? shared : experts + (size_t)e * stride;
     UnitSrc u;
     u.bq = blob + wo0 + (size_t)cb * C::NCOL * rowb;
     u.bs = blob + so0 + (size_t)cb * C::NCOL * ng * 2;
@@ -1308,9 +1366,9 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
 }
 
 // Group sums of the fp16 activations per entry; one block per entry.
-__global__ __launch_bounds__(256) void k_pf_act_sum(PfArgs a) {
+__global__ __launch_bounds__(256) void k_pf_act_sum(PfArgs a, uint32_t row0) {
   __shared__ float part8[kPfMaxGroupsK * 128 / 8];
-  const uint32_t r = blockIdx.x, I = a.g.inter, G = a.g.group;
+  const uint32_t r = row0 + blockIdx.x, I = a.g.inter, G = a.g.group;
   for (uint32_t k0 = threadIdx.x * 8; k0 < I; k0 += blockDim.x * 8) {
     const u32x4 h = *reinterpret_cast<const u32x4*>(a.act_hi + (size_t)r * I + k0);
     const uint32_t hv[4] = {h.x, h.y, h.z, h.w};
@@ -1332,13 +1390,21 @@ __global__ __launch_bounds__(256) void k_pf_act_sum(PfArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Combine: out[t, :] = fold over t's entries in ascending expert order.
+// Combine: moe[t, :] = fold over t's entries in ascending expert order
+// (moe_cpu.rs:330-337); the MoE block adds the residual and the shared
+// expert as moe_combine_residual_n_tokens_cpu does (backend/cpu/mod.rs:
+// 657-680): out = (h_mid + moe) + sigmoid(gate . x_t) * shared (no fused
+// multiply-add; the sigmoid with glibc's expf), without a shared expert
+// out = h_mid + moe, without h_mid out = moe.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(512) void k_pf_combine(PfArgs a) {
+#pragma clang fp contract(off)
   const uint32_t t = blockIdx.x;
   const uint32_t H = a.g.hidden, k = a.k;
   const float* const down = a.down;
   float* const out = a.out;
+  const float* const h_mid = a.h_mid;
+  const bool shared = a.shared != nullptr;
   // Loops over the k slots run to kPfMaxK with a guard, so that the arrays
   // stay in registers and every load of a pass is issued before the first
   // FMA waits for one.
@@ -1352,11 +1418,16 @@ __global__ __launch_bounds__(512) void k_pf_combine(PfArgs a) {
     pos[r] = min(pw.x, nk - 1);
     wt[r] = __uint_as_float(pw.y);
   }
+  const float sg = shared && a.gate ? sigmoid_ref(a.gscore[t]) : 1.0f;
+  const float* const sh_row = down + (size_t)(nk + t) * H;
   for (uint32_t h = threadIdx.x * 4; h < H; h += blockDim.x * 4) {
     float4 d[kPfMaxK];
 #pragma unroll
     for (uint32_t r = 0; r < kPfMaxK; ++r)
       if (r < k) d[r] = *reinterpret_cast<const float4*>(down + (size_t)pos[r] * H + h);
+    float4 hm = make_float4(0.f, 0.f, 0.f, 0.f), sh = hm;
+    if (h_mid) hm = *reinterpret_cast<const float4*>(h_mid + (size_t)t * H + h);
+    if (h_mid && shared) sh = *reinterpret_cast<const float4*>(sh_row + h);
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (uint32_t r = 0; r < kPfMaxK; ++r)
@@ -1366,6 +1437,18 @@ __global__ __launch_bounds__(512) void k_pf_combine(PfArgs a) {
         o.z = __builtin_fmaf(d[r].z, wt[r], o.z);
         o.w = __builtin_fmaf(d[r].w, wt[r], o.w);
       }
+    if (h_mid) {
+      o.x = hm.x + o.x;
+      o.y = hm.y + o.y;
+      o.z = hm.z + o.z;
+      o.w = hm.w + o.w;
+      if (shared) {
+        o.x = o.x + sg * sh.x;
+        o.y = o.y + sg * sh.y;
+        o.z = o.z + sg * sh.z;
+        o.w = o.w + sg * sh.w;
+      }
+    }
     *reinterpret_cast<float4*>(out + (size_t)t * H + h) = o;
   }
 }
@@ -1376,9 +1459,11 @@ __global__ __launch_bounds__(512) void k_pf_combine(PfArgs a) {
 static uint64_t al256(uint64_t n) { return (n + 255) & ~255ull; }
 
 uint64_t prefill_workspace(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t n_tokens,
-                           uint32_t n_experts, uint32_t k, PfArgs* a, uint8_t* base) {
+                           uint32_t n_experts, uint32_t k, bool shared, PfArgs* a, uint8_t* base) {
   const uint64_t nk = (uint64_t)n_tokens * k;
-  const uint64_t max_items = n_experts + nk / kPfMC + 1;
+  const uint64_t ns = shared ? (n_tokens + kPfMC - 1) / kPfMC : 0;  // shared-expert items
+  const uint64_t ne = nk + (shared ? n_tokens : 0);                 // entry rows
+  const uint64_t max_items = n_experts + nk / kPfMC + 1 + ns;
   uint64_t off = 0;
   auto take = [&](uint64_t bytes) {
     const uint64_t o = off;
@@ -1390,12 +1475,24 @@ uint64_t prefill_workspace(uint32_t hidden, uint32_t inter, uint32_t group, uint
   uint8_t* p_itok = take(max_items * kPfMC * 4);
   uint8_t* p_pw = take(nk * 8);
   uint8_t* p_xsum = take((uint64_t)n_tokens * (hidden / group) * 4);
-  uint8_t* p_asum = take(nk * (inter / group) * 4);
+  uint8_t* p_asum = take(ne * (inter / group) * 4);
   uint8_t* p_xhi = take((uint64_t)n_tokens * hidden * 2);
   uint8_t* p_xlo = take((uint64_t)n_tokens * hidden * 2);
-  uint8_t* p_ahi = take(nk * inter * 2);
-  uint8_t* p_down = take(nk * hidden * 4);
+  uint8_t* p_ahi = take(ne * inter * 2);
+  uint8_t* p_down = take(ne * hidden * 4);
+  uint8_t* p_xr = take(9 * 4);
+  uint8_t* p_gs = take(shared ? (uint64_t)n_tokens * 4 : 0);
+  uint8_t* p_sitems = take(ns * 2 * 4);
+  uint8_t* p_snitems = take(shared ? 4 : 0);
+  uint8_t* p_sitok = take(ns * kPfMC * 4);
+  uint8_t* p_sxr = take(shared ? 9 * 4 : 0);
   if (a) {
+    a->xr = reinterpret_cast<uint32_t*>(p_xr);
+    a->gscore = shared ? reinterpret_cast<float*>(p_gs) : nullptr;
+    a->sitems = shared ? reinterpret_cast<uint32_t*>(p_sitems) : nullptr;
+    a->sn_items = shared ? reinterpret_cast<uint32_t*>(p_snitems) : nullptr;
+    a->sitem_tok = shared ? reinterpret_cast<uint32_t*>(p_sitok) : nullptr;
+    a->sxr = shared ? reinterpret_cast<uint32_t*>(p_sxr) : nullptr;
     a->items = reinterpret_cast<uint32_t*>(p_items);
     a->n_items = reinterpret_cast<uint32_t*>(p_nitems);
     a->item_tok = reinterpret_cast<uint32_t*>(p_itok);
@@ -1434,15 +1531,17 @@ static hipError_t launch_mm(const PfArgs& a, uint32_t n_units_max, uint32_t n_cu
   if (e != hipSuccess) return e;
   const uint32_t grid = n_units_max < n_cu ? n_units_max : n_cu;
   hipLaunchKernelGGL((k_pf_mm<BITS, G, MODE, SPLIT, KU, NWD>), dim3(grid), dim3(64 * C::NWT), lds, st, a,
-                     (const uint32_t*)a.items, (const uint32_t*)a.n_items);
+                     (const uint32_t*)a.items, (const uint32_t*)a.n_items, (const uint32_t*)a.xr);
   return hipGetLastError();
 }
 
 // Per-unit scale staging (KU = K) where it fits in LDS: the A3B-shape gate/up
 // GEMM (bf16 x, hidden 2048, group 64 or 128) and down GEMM (inter 512,
 // group 64); other shapes copy scales per chunk.
+// act_rows: the entry rows [row0, row0 + n_rows) whose activation group
+// sums the G > 64 pass computes.
 template <int BITS, int G>
-static hipError_t launch_gemms(const PfArgs& a, uint32_t n_cu, hipStream_t st) {
+static hipError_t launch_gemms(const PfArgs& a, uint32_t row0, uint32_t n_rows, uint32_t n_cu, hipStream_t st) {
   const uint32_t gu_units = a.max_items * (a.g.inter / 64);
   hipError_t e;
   if (!a.x_bf16)
@@ -1453,7 +1552,7 @@ static hipError_t launch_gemms(const PfArgs& a, uint32_t n_cu, hipStream_t st) {
     e = launch_mm<BITS, G, 0, false, 0>(a, gu_units, n_cu, st);
   if (e != hipSuccess) return e;
   // With G <= 64 the gate/up GEMM writes the activation group sums itself.
-  if (G > 64) hipLaunchKernelGGL(k_pf_act_sum, dim3(a.n_tokens * a.k), dim3(256), 0, st, a);
+  if (G > 64) hipLaunchKernelGGL(k_pf_act_sum, dim3(n_rows), dim3(256), 0, st, a, row0);
   const uint32_t dn_units = a.max_items * (a.g.hidden / 256);
   if (G == 64 && a.g.inter == 512) return launch_mm<BITS, G, 2, false, G == 64 ? 512 : 0>(a, dn_units, n_cu, st);
   return launch_mm<BITS, G, 2, false, 0>(a, dn_units, n_cu, st);
@@ -1467,15 +1566,35 @@ hipError_t launch_prefill(const PfArgs& a, uint32_t n_cu, hipStream_t st) {
     if (e != hipSuccess) return e;
   }
   hipLaunchKernelGGL(k_pf_route, dim3(1 + (a.n_tokens + kPfPrepTokens - 1) / kPfPrepTokens), dim3(1024), route_lds, st, a);
-  const uint32_t G = a.g.group;
+  const uint32_t G = a.g.group, nk = a.n_tokens * a.k;
+  const uint32_t rows = nk + (a.shared && a.shared_in_list ? a.n_tokens : 0u);
   hipError_t e;
   if (a.g.bits == 4)
-    e = G == 32 ? launch_gemms<4, 32>(a, n_cu, st) : G == 64 ? launch_gemms<4, 64>(a, n_cu, st)
-                                                   : launch_gemms<4, 128>(a, n_cu, st);
+    e = G == 32 ? launch_gemms<4, 32>(a, 0, rows, n_cu, st) : G == 64 ? launch_gemms<4, 64>(a, 0, rows, n_cu, st)
+                                                              : launch_gemms<4, 128>(a, 0, rows, n_cu, st);
   else
-    e = G == 32 ? launch_gemms<3, 32>(a, n_cu, st) : G == 64 ? launch_gemms<3, 64>(a, n_cu, st)
-                                                   : launch_gemms<3, 128>(a, n_cu, st);
+    e = G == 32 ? launch_gemms<3, 32>(a, 0, rows, n_cu, st) : G == 64 ? launch_gemms<3, 64>(a, 0, rows, n_cu, st)
+                                                              : launch_gemms<3, 128>(a, 0, rows, n_cu, st);
   if (e != hipSuccess) return e;
+  if (a.shared && !a.shared_in_list) {
+    // The 4-bit shared expert beside 3-bit routed experts: its own work list
+    // through the 4-bit GEMM instances (entry rows n k + t).
+    PfArgs s = a;
+    s.g = a.sg;
+    s.experts = a.shared;
+    s.stride = 0;
+    s.E = 1;
+    s.items = a.sitems;
+    s.n_items = a.sn_items;
+    s.item_tok = a.sitem_tok;
+    s.xr = a.sxr;
+    s.max_items = (a.n_tokens + kPfMC - 1) / kPfMC;
+    s.shared = nullptr;
+    e = G == 32 ? launch_gemms<4, 32>(s, nk, a.n_tokens, n_cu, st)
+                : G == 64 ? launch_gemms<4, 64>(s, nk, a.n_tokens, n_cu, st)
+                          : launch_gemms<4, 128>(s, nk, a.n_tokens, n_cu, st);
+    if (e != hipSuccess) return e;
+  }
   hipLaunchKernelGGL(k_pf_combine, dim3(a.n_tokens), dim3(512), 0, st, a);
   return hipGetLastError();
 }

@@ -27,12 +27,7 @@ struct ExpTabReg {
 };
 
 __device__ __forceinline__ ExpTabReg load_exp_tab(int lane) {
-  static __device__ const uint64_t tab[32] = {
-      kExpTab[0],  kExpTab[1],  kExpTab[2],  kExpTab[3],  kExpTab[4],  kExpTab[5],  kExpTab[6],  kExpTab[7],
-      kExpTab[8],  kExpTab[9],  kExpTab[10], kExpTab[11], kExpTab[12], kExpTab[13], kExpTab[14], kExpTab[15],
-      kExpTab[16], kExpTab[17], kExpTab[18], kExpTab[19], kExpTab[20], kExpTab[21], kExpTab[22], kExpTab[23],
-      kExpTab[24], kExpTab[25], kExpTab[26], kExpTab[27], kExpTab[28], kExpTab[29], kExpTab[30], kExpTab[31]};
-  const uint64_t t = tab[lane & 31];
+  const uint64_t t = kExpTabDev[lane & 31];
   return ExpTabReg{(uint32_t)t, (uint32_t)(t >> 32)};
 }
 

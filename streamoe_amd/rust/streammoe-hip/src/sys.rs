@@ -138,6 +138,13 @@ extern "C" {
                             stride: u64, n_experts: u32, idx: *const i32, weights: *const f32,
                             x: *const c_void, x_is_bf16: c_int, n_tokens: u32, k: u32, out_sum: *mut f32,
                             workspace: *mut c_void, workspace_bytes: u64) -> c_int;
+    pub fn smoe_moe_prefill_block_workspace_size(shape: *const smoe_expert_shape, n_tokens: u32, n_experts: u32,
+                                                 k: u32, has_shared: c_int) -> u64;
+    pub fn smoe_moe_prefill_block(h: *mut smoe_handle, shape: *const smoe_expert_shape, experts: *const c_void,
+                                  stride: u64, n_experts: u32, idx: *const i32, weights: *const f32,
+                                  x: *const c_void, x_is_bf16: c_int, n_tokens: u32, k: u32,
+                                  shared_expert: *const c_void, shared_gate: *const f32, h_mid: *const f32,
+                                  hidden_out: *mut f32, workspace: *mut c_void, workspace_bytes: u64) -> c_int;
     pub fn smoe_layer_file_layout(file_bytes: u64, n_experts: u32, hidden: u32, inter: u32, group: u32,
                                   declared_size: u64, declared_stride: u64,
                                   out: *mut smoe_file_layout) -> c_int;

@@ -519,3 +519,63 @@ def test_argmax_is_the_reference_scan_with_nan():
     assert oracle.argmax(v) == 0
     v = np.array([-np.inf, -np.inf], np.float32)
     assert oracle.argmax(v) == 0
+
+
+# ---- prefill MoE block tail: moe_combine_residual_n_tokens_cpu ------------------
+def test_combine_residual_n_tokens_known_answers():
+    """backend/cpu/mod.rs:657-695: hidden = h_mid + moe_sum + sigmoid(g) *
+    shared; sigmoid(0) = 0.5 exactly (exp(-0) = 1)."""
+    h = np.array([[1.0, -2.0]], np.float32)
+    m = np.array([[2.0, 0.5]], np.float32)
+    s = np.array([[4.0, 8.0]], np.float32)
+    out = oracle.moe_combine_residual_n_tokens(h, m, s, np.zeros(1, np.float32))
+    assert np.array_equal(out, np.array([[5.0, 2.5]], np.float32))
+    # no shared expert: h_mid + moe_sum
+    assert np.array_equal(oracle.moe_combine_residual_n_tokens(h, m), np.array([[3.0, -1.5]], np.float32))
+    # no gate: the shared term unscaled
+    assert np.array_equal(oracle.moe_combine_residual_n_tokens(h, m, s), np.array([[7.0, 6.5]], np.float32))
+
+
+def test_combine_residual_n_tokens_addition_order():
+    """Left to right, (h_mid + moe_sum) + g * shared: with h_mid = 1e8,
+    moe_sum = -1e8 and g * shared = 1 the result is 1; summing the other
+    way, h_mid + (moe_sum + 1) rounds -1e8 + 1 back to -1e8 and gives 0."""
+    h = np.array([[1e8]], np.float32)
+    m = np.array([[-1e8]], np.float32)
+    s = np.array([[2.0]], np.float32)
+    out = oracle.moe_combine_residual_n_tokens(h, m, s, np.zeros(1, np.float32))
+    assert out[0, 0] == np.float32(1.0)
+    assert np.float32(h[0, 0] + np.float32(m[0, 0] + np.float32(1.0))) == np.float32(0.0)
+
+
+def test_combine_residual_n_tokens_no_fused_multiply_add():
+    """g * shared is rounded before the add (Rust does not contract): on
+    inputs where fma(g, s, a) and a + round(g * s) differ, the oracle gives
+    the latter."""
+    rng = np.random.default_rng(11)
+    found = 0
+    for _ in range(2000):
+        gate = np.float32(rng.uniform(-3, 3))
+        g = np.float32(oracle.sigmoid(float(gate)))
+        s = np.float32(rng.uniform(0.5, 2.0))
+        a = -np.float32(np.float64(g) * np.float64(s))  # cancels the product to about one ulp
+        fused = np.float32(np.float64(a) + np.float64(g) * np.float64(s))
+        unfused = np.float32(a + np.float32(g * s))
+        if fused == unfused:
+            continue
+        found += 1
+        out = oracle.moe_combine_residual_n_tokens(np.array([[a]], np.float32), np.zeros((1, 1), np.float32),
+                                                   np.array([[s]], np.float32), np.array([gate], np.float32))
+        assert out[0, 0] == unfused and out[0, 0] != fused
+    assert found >= 20
+
+
+def test_combine_residual_n_tokens_vs_f64():
+    rng = np.random.default_rng(12)
+    n, d = 7, 300
+    h, m, s = (rng.standard_normal((n, d)).astype(np.float32) for _ in range(3))
+    gate = rng.standard_normal(n).astype(np.float32)
+    out = oracle.moe_combine_residual_n_tokens(h, m, s, gate)
+    g64 = 1.0 / (1.0 + np.exp(-gate.astype(np.float64)))
+    want = h.astype(np.float64) + m + g64[:, None] * s
+    assert rel_err(out, want) <= 1e-6
