@@ -167,6 +167,67 @@ def cpu_baseline_decode(c, arena_l0, router_l0, shared_l0, gate_l0, x, seconds):
                 host=host_cpu())
 
 
+def decode_parity(kern, c, layers, arenas, routers, shareds, gates, norms, x0):
+    """The timed computation checked against the oracle after the timing:
+    one fresh token through all the layers (smoe_moe_decode_layers, the
+    step the graph replays) against the oracle chain (router, the chosen
+    experts' FFNs, combine, RMSNorm between layers; only the chosen experts'
+    blobs are copied to the host), and layer 0 alone with the routing
+    returned (idx in the reference's slot order, weights bit for bit)."""
+    import numpy as np
+    import torch
+
+    import oracle
+
+    H, I, k, bits = c["H"], c["I"], c["k"], c["bits"]
+    stride = arenas[0].numel() // c["E"]
+    resid = x0.clone()
+    work = torch.empty_like(x0)
+    sa_check = __import__("streamoe_amd").check
+    sa_check(kern.moe_decode_layers(layers, norms, 1e-6, x0, resid, work), "smoe_moe_decode_layers")
+    torch.cuda.synchronize()
+    got = resid.cpu().numpy()
+    r = x0.cpu().numpy().copy()
+    x = r.copy()
+    min_gap = 1.0
+    for l in range(len(layers)):
+        if l > 0:
+            x = oracle.rms_norm_bf16(r, norms[l].cpu().numpy().view(np.uint16), 1e-6)
+        logits = oracle.f32_matvec(routers[l].cpu().numpy(), x)
+        p = np.sort(oracle.softmax(logits))[::-1]
+        min_gap = min(min_gap, float(p[k - 1] - p[k]))
+        _, idx, w = oracle.router(logits, k, c["normalize"])
+        outs = np.stack([oracle.expert_swiglu(arenas[l][int(e) * stride:(int(e) + 1) * stride].cpu().numpy(), bits,
+                                              H, I, 64, x) for e in idx])
+        sh = score = None
+        if shareds[l] is not None:
+            sh = oracle.expert_swiglu(shareds[l].cpu().numpy(), 4, H, I, 64, x)
+            score = float(oracle.f32_matvec(gates[l].cpu().numpy()[None, :], x)[0])
+        r = oracle.combine(outs, w, r, sh, float("nan") if score is None else score)
+    chain_err = float(np.max(np.abs(got - r)) / np.max(np.abs(r)))
+    # Layer 0 with idx / weights returned.
+    zeros = torch.zeros(H, dtype=torch.float32, device=x0.device)
+    out0 = torch.empty(H, dtype=torch.float32, device=x0.device)
+    idx0 = torch.empty(k, dtype=torch.int32, device=x0.device)
+    w0 = torch.empty(k, dtype=torch.float32, device=x0.device)
+    sa_check(kern.moe_decode_layer(layers[0], x0, zeros, out0, idx0, w0), "smoe_moe_decode_layer")
+    torch.cuda.synchronize()
+    want0, widx, ww, _ = oracle.moe_decode_layer(
+        arenas[0].cpu().numpy(), stride, H, I, c["E"], k, 64, bits, c["normalize"], routers[0].cpu().numpy(),
+        x0.cpu().numpy(), np.zeros(H, np.float32), None if shareds[0] is None else shareds[0].cpu().numpy(),
+        None if gates[0] is None else gates[0].cpu().numpy())
+    g0 = out0.cpu().numpy()
+    return {"chain_rel_err": chain_err, "chain_layers": len(layers), "min_topk_prob_gap": min_gap,
+            "layer0_rel_err": float(np.max(np.abs(g0 - want0)) / np.max(np.abs(want0))),
+            "layer0_idx_equal": bool(np.array_equal(idx0.cpu().numpy(), widx)),
+            # The logits come from the device's router matvec (another
+            # summation order than the oracle's), so the weights agree to a
+            # few ulps; with equal logits they are bit-identical
+            # (tests/test_gpu_softmax.py).
+            "layer0_weights_max_rel_diff": float(np.max(np.abs(w0.cpu().numpy() - ww) / np.abs(ww))),
+            "tolerance": 1e-3}
+
+
 def _sync_status(kern):
     import streamoe_amd as sa
 
@@ -336,6 +397,8 @@ def run_decode(args, c):
         out["roofline"]["traffic"] = None
     if phases:
         out["phases_us"] = phases
+    if T == 1 and not args.no_parity:
+        out["parity"] = decode_parity(kern, c, layers, arenas, routers, shareds, gates, norms, x0)
     if not args.no_cpu and T == 1:
         a0 = arenas[0].cpu().numpy()
         r0 = routers[0].cpu().numpy()
@@ -453,24 +516,44 @@ def run_prefill(args, c):
     sa.check(kern.synth_normal_bf16(x, 0xC41, 1.0), "synth")
     out = torch.empty((n, H), dtype=torch.float32, device=dev)
     ws = torch.empty(kern.moe_prefill_workspace_size(lay, n, E, k), dtype=torch.uint8, device=dev)
+    # The whole MoE block variant: plus a 4-bit shared expert with its f32
+    # gate (config 2's distributions) and the residual h_mid.
+    slay = sa.ExpertLayout(H, I, 4, 64)
+    shared = torch.empty(slay.expert_size, dtype=torch.uint8, device=dev)
+    sa.check(kern.synth_experts(shared, 1, slay.expert_size, slay, 0xC45), "synth")
+    gate = torch.empty(H, dtype=torch.float32, device=dev)
+    sa.check(kern.synth_normal_f32(gate, 0xC46, 0.02), "synth")
+    h_mid = torch.empty((n, H), dtype=torch.float32, device=dev)
+    sa.check(kern.synth_normal_f32(h_mid, 0xC47, 1.0), "synth")
+    hidden = torch.empty((n, H), dtype=torch.float32, device=dev)
+    wsb = torch.empty(kern.moe_prefill_block_workspace_size(lay, n, E, k, True), dtype=torch.uint8, device=dev)
 
     def step():
         sa.check(kern.moe_prefill(lay, arena, stride, E, idx_d, w_d, x, True, n, k, out, ws), "smoe_moe_prefill")
 
-    graph = None if args.eager else sa.capture_graph(kern, step)
-    run = graph.replay if graph is not None else step
-    for _ in range(args.warmup):
-        run()
-    torch.cuda.synchronize()
+    def step_block():
+        sa.check(kern.moe_prefill_block(lay, arena, stride, E, idx_d, w_d, x, True, n, k, shared, gate, h_mid,
+                                        hidden, wsb), "smoe_moe_prefill_block")
+
     stream = torch.cuda.current_stream(dev)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(args.steps):
-        run()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / args.steps
-    sa.check(_sync_status(kern), "smoe_sync")
+
+    def time_steps(fn):
+        graph = None if args.eager else sa.capture_graph(kern, fn)
+        run = graph.replay if graph is not None else fn
+        for _ in range(args.warmup):
+            run()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(args.steps):
+            run()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        sa.check(_sync_status(kern), "smoe_sync")
+        return e0.elapsed_time(e1) * 1e3 / args.steps, graph
+
+    us, graph = time_steps(step)
+    us_blk, _ = time_steps(step_block)
     hit = np.unique(idx)
     nbytes = len(hit) * stride + n * H * 2 + n * H * 4  # weights of hit experts + bf16 X + f32 Y
     flops = 2 * n * k * (2 * H * I + I * H)
@@ -496,6 +579,16 @@ def run_prefill(args, c):
                      "kernel": "prefill layer: k_pf_route (+ per-token x preparation) + k_pf_mm (gate/up, with the activation "
                                "group sums) + k_pf_mm (down) + k_pf_combine (one HIP graph)"},
     }
+    blk_bytes = nbytes + slay.expert_size + 2 * n * H * 4  # + shared expert, h_mid read, gate
+    blk_flops = flops + 2 * n * (2 * H * I + I * H)
+    out_d["block_variant"] = {
+        "what": "smoe_moe_prefill_block: the same routed experts plus a 4-bit shared expert over all tokens (extra "
+                "work items of the same grouped GEMMs), its f32 sigmoid gate and the residual "
+                "(h_mid + moe_sum) + sigmoid(g) * shared",
+        "us_per_layer": round(us_blk, 2), "algorithmic_bytes": blk_bytes, "flops": blk_flops,
+        "gbps": round(blk_bytes / (us_blk * 1e-6) / 1e9, 1),
+        "frac_of_hbm_peak": round(blk_bytes / (us_blk * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "mfma_tflops": round(blk_flops / (us_blk * 1e-6) / 1e12, 2)}
     if not args.no_cpu:
         # The whole layer (a few seconds of CPU work), timed with all host
         # threads; doubles as a parity check of every token.
@@ -516,6 +609,17 @@ def run_prefill(args, c):
                                  "gpu_speedup": round(cpu_us / us, 1)}
         out_d["parity"] = {"rel_err": float(np.max(np.abs(got - want)) / np.max(np.abs(want))),
                            "tokens_checked": ns, "tolerance": 1e-3}
+        # The block: the routed sum above, the shared expert and gate per
+        # token, the reference's combine.
+        sh_h, g_h, hm = shared.cpu().numpy(), gate.cpu().numpy(), h_mid.cpu().numpy()
+        so = np.stack([oracle.expert_swiglu(sh_h, 4, H, I, 64, xs[t], nt) for t in range(n)])
+        sg = np.array([oracle.f32_matvec(g_h[None, :], xs[t])[0] for t in range(n)], np.float32)
+        want_b = oracle.moe_combine_residual_n_tokens(hm, want, so, sg)
+        got_b = hidden.cpu().numpy()
+        out_d["block_variant"]["parity"] = {
+            "rel_err": float(np.max(np.abs(got_b - want_b)) / np.max(np.abs(want_b))),
+            "moe_part_rel_err": float(np.max(np.abs((got_b - hm) - (want_b - hm))) / np.max(np.abs(want_b - hm))),
+            "tokens_checked": n, "tolerance": 1e-3}
     kern.close()
     return out_d
 
@@ -532,6 +636,7 @@ def main():
     ap.add_argument("--eager", action="store_true", help="launch every step eagerly instead of replaying a HIP graph")
     ap.add_argument("--trace", action="store_true", help="report per-phase times from in-kernel timestamps")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-parity", action="store_true", help="skip the parity check of the timed work after timing")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-stream-peak", action="store_true", help="skip the measured streaming-read peak")
     ap.add_argument("--tokens", type=int, default=1, choices=[1, 2, 3, 4],
