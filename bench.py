@@ -105,6 +105,10 @@ def layer_bytes(c, tokens=1):
     return tokens * c["k"] * routed + shared + c["E"] * c["H"] * 4
 
 
+# LM head (config 1): decode tokens per timed graph replay.
+LM_TOKENS = 20
+
+
 # A GPU box grants one GPU's process a share of 16 host CPUs (the harness's
 # worker-pool rule), whatever nproc reports; the baseline uses every CPU of
 # that share that the process may run on.
@@ -434,38 +438,55 @@ def run_lm_head(args, c):
     sa.check(kern.synth_normal_bf16(scales, 0xC11, 0.02), "synth")
     scales.bitwise_and_(0x7FFF)  # |N(0, 0.02)|
     sa.check(kern.synth_normal_bf16(biases, 0xC12, 0.01), "synth")
-    x = torch.empty(H, dtype=torch.float32, device=dev)
-    sa.check(kern.synth_normal_f32(x, 0xC13, 1.0), "synth")
-    y = torch.empty(V, dtype=torch.float32, device=dev)
-    am = torch.empty(1, dtype=torch.int32, device=dev)
+    # One step = the LM head of LM_TOKENS decode tokens, each with its own
+    # x, in one HIP graph (as in a decode loop, where the LM head sits in the
+    # token's graph with the layers); value = µs per token. One graph per
+    # token is timed too: it adds the graph launch (~7 µs) to every token.
+    T = LM_TOKENS
+    xs = torch.empty((T, H), dtype=torch.float32, device=dev)
+    sa.check(kern.synth_normal_f32(xs, 0xC13, 1.0), "synth")
+    ys = torch.empty((T, V), dtype=torch.float32, device=dev)
+    ams = torch.empty(T, dtype=torch.int32, device=dev)
+    x, y, am = xs[0], ys[0], ams[0:1]
     w = sa.QuantWeights(buf, 0, codes_b, codes_b + sc_b, G, 4)
 
     def step():
+        for t in range(T):
+            sa.check(kern.qmv_argmax(w, xs[t], ys[t], V, H, ams[t:t + 1]), "smoe_qmv_argmax")
+
+    def step1():
         sa.check(kern.qmv_argmax(w, x, y, V, H, am), "smoe_qmv_argmax")
 
-    graph = None if args.eager else sa.capture_graph(kern, step)
-    run = graph.replay if graph is not None else step
-    for _ in range(args.warmup):
-        run()
-    torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(args.steps):
-        run()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / args.steps
-    sa.check(_sync_status(kern), "smoe_sync")
+
+    def time_steps(fn, steps):
+        graph = None if args.eager else sa.capture_graph(kern, fn)
+        run = graph.replay if graph is not None else fn
+        for _ in range(args.warmup):
+            run()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            run()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        sa.check(_sync_status(kern), "smoe_sync")
+        return e0.elapsed_time(e1) * 1e3 / steps, graph
+
+    us_step, graph = time_steps(step, args.steps)
+    us = us_step / T
+    us_one, _ = time_steps(step1, args.steps * T)
     nbytes = codes_b + 2 * sc_b
     achieved = nbytes / (us * 1e-6) / 1e9
     out = {
         "metric": "4-bit MoE expert decode µs/layer + achieved HBM GB/s (% of peak), 1 GPU",
         "value": round(us, 3), "unit": "us/token (LM head qmv + argmax)", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(us / 1e3, 5), "higher_is_better": False, "scaling": "weak",
+        "warmup": args.warmup, "ms_per_step": round(us_step / 1e3, 5), "higher_is_better": False, "scaling": "weak",
+        "tokens_per_step": T, "us_per_token_one_graph_each": round(us_one, 3),
         "vs_baseline": None, "dtype": DECODE_DTYPE, "data": "synthetic (seeded, generated on the device)",
         "seeds": {"codes": "torch.Generator 0xC1", "scales": 0xC11, "biases": 0xC12, "x": 0xC13},
-        "config": {"workload": c["name"], "vocab": V, "hidden": H, "bits": 4, "group": G,
+        "config": {"workload": c["name"], "vocab": V, "hidden": H, "bits": 4, "group": G, "tokens_per_graph": T,
                    "mode": "hipgraph" if graph is not None else "eager"},
         "gbps": round(achieved, 1), "pct_of_hbm_peak": round(100 * achieved / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
