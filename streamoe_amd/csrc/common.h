@@ -356,7 +356,9 @@ __device__ __forceinline__ float sigmoidf_ref(float x) { return 1.0f / (1.0f + e
 // in int32 (|sum| <= 32 * 15 * 128). The dot product is then
 //     sum_j q_j x_j = 2^-f * (S0 + 2^8 S1 + 2^16 S2)
 // rounded once or twice at f32 precision: 1.1 VALU ops per 4-bit weight
-// instead of 2.4 for convert-and-FMA.
+// instead of 2.4 for convert-and-FMA. A chunk whose largest |x| is below
+// 2^-128 gets a scale 2^-f that underflows to 0 and contributes 0 (an
+// absolute error below 480 * 2^-128).
 //
 // Byte order: code word i (inputs 8i .. 8i+7) unpacks to lo = bytes
 // [q(8i), q(8i+2), q(8i+4), q(8i+6)] and hi = [q(8i+1), q(8i+3), q(8i+5),

@@ -55,12 +55,17 @@ pub struct BufferRef {
 }
 
 impl BufferRef {
-    fn at(&self, offset: u64) -> *mut c_void {
-        debug_assert!(offset <= self.len);
-        (self.ptr as *mut u8).wrapping_add(offset as usize) as *mut c_void
+    /// The address `offset` bytes into the buffer when `bytes` more bytes
+    /// from there lie inside it; else `SMOE_ERR_INVALID_ARG` (checked in
+    /// every build: the pointer goes to the device unverified).
+    fn span(&self, offset: u64, bytes: u64, what: &'static str) -> Result<*mut c_void, SmoeError> {
+        match offset.checked_add(bytes) {
+            Some(end) if end <= self.len => Ok((self.ptr as *mut u8).wrapping_add(offset as usize) as *mut c_void),
+            _ => Err(SmoeError { status: sys::SMOE_ERR_INVALID_ARG, what }),
+        }
     }
-    fn f32_at(&self, offset: u64) -> *mut f32 {
-        self.at(offset) as *mut f32
+    fn f32_span(&self, offset: u64, n: u64, what: &'static str) -> Result<*mut f32, SmoeError> {
+        Ok(self.span(offset, n.checked_mul(4).unwrap_or(u64::MAX), what)? as *mut f32)
     }
 }
 
@@ -84,15 +89,23 @@ pub struct QuantWeights<'a> {
 pub const QMM_GROUP_SIZES: &[u32] = &[64, 32, 128];
 
 impl QuantWeights<'_> {
-    fn raw(&self) -> sys::smoe_qweights {
-        sys::smoe_qweights {
+    /// The C view, after checking that the codes, scales and biases of an
+    /// `out_dim` x `in_dim` matrix lie inside the buffer.
+    fn raw(&self, out_dim: u32, in_dim: u32, what: &'static str) -> Result<sys::smoe_qweights, SmoeError> {
+        let g = self.group_size.max(1) as u64;
+        let codes = out_dim as u64 * in_dim as u64 * self.bits as u64 / 8;
+        let sb = out_dim as u64 * (in_dim as u64 / g) * 2;
+        self.buffer.span(self.packed_offset, codes, what)?;
+        self.buffer.span(self.scales_offset, sb, what)?;
+        self.buffer.span(self.biases_offset, sb, what)?;
+        Ok(sys::smoe_qweights {
             base: self.buffer.ptr,
             packed_offset: self.packed_offset,
             scales_offset: self.scales_offset,
             biases_offset: self.biases_offset,
             group_size: self.group_size,
             bits: self.bits,
-        }
+        })
     }
 }
 
@@ -142,6 +155,14 @@ impl Kernels {
     pub fn moe_prefill_workspace_size(shape: &ExpertShape, n_tokens: u32, n_experts: u32, k: u32) -> u64 {
         let s = shape.raw();
         unsafe { sys::smoe_moe_prefill_workspace_size(&s, n_tokens, n_experts, k) }
+    }
+
+    /// Device workspace bytes a [`MoePrefillBlockCall`] needs (0: a shape
+    /// the block call does not take).
+    pub fn moe_prefill_block_workspace_size(shape: &ExpertShape, n_tokens: u32, n_experts: u32, k: u32,
+                                            has_shared: bool) -> u64 {
+        let s = shape.raw();
+        unsafe { sys::smoe_moe_prefill_block_workspace_size(&s, n_tokens, n_experts, k, has_shared as c_int) }
     }
 
     /// Copy a byte range of a layer file into device memory (the resident
@@ -204,11 +225,11 @@ pub struct MatvecCall<'a> {
 
 impl KernelCall for MatvecCall<'_> {
     fn encode(&self, k: &Kernels) -> Result<(), SmoeError> {
-        let w = self.weights.raw();
-        check(unsafe {
-            sys::smoe_qmv(k.h, &w, self.input.f32_at(self.input_offset), self.output.f32_at(self.output_offset),
-                          self.out_dim, self.in_dim)
-        }, "smoe_qmv")
+        let what = "smoe_qmv";
+        let w = self.weights.raw(self.out_dim, self.in_dim, what)?;
+        let x = self.input.f32_span(self.input_offset, self.in_dim as u64, what)?;
+        let y = self.output.f32_span(self.output_offset, self.out_dim as u64, what)?;
+        check(unsafe { sys::smoe_qmv(k.h, &w, x, y, self.out_dim, self.in_dim) }, what)
     }
 }
 
@@ -222,11 +243,12 @@ pub struct LmHeadCall<'a> {
 impl KernelCall for LmHeadCall<'_> {
     fn encode(&self, k: &Kernels) -> Result<(), SmoeError> {
         let m = &self.matvec;
-        let w = m.weights.raw();
-        check(unsafe {
-            sys::smoe_qmv_argmax(k.h, &w, m.input.f32_at(m.input_offset), m.output.f32_at(m.output_offset),
-                                 m.out_dim, m.in_dim, self.token.ptr as *mut i32)
-        }, "smoe_qmv_argmax")
+        let what = "smoe_qmv_argmax";
+        let w = m.weights.raw(m.out_dim, m.in_dim, what)?;
+        let x = m.input.f32_span(m.input_offset, m.in_dim as u64, what)?;
+        let y = m.output.f32_span(m.output_offset, m.out_dim as u64, what)?;
+        let t = self.token.span(0, 4, what)? as *mut i32;
+        check(unsafe { sys::smoe_qmv_argmax(k.h, &w, x, y, m.out_dim, m.in_dim, t) }, what)
     }
 }
 
@@ -247,11 +269,14 @@ pub struct QmmCall<'a> {
 
 impl KernelCall for QmmCall<'_> {
     fn encode(&self, k: &Kernels) -> Result<(), SmoeError> {
-        let w = self.weights.raw();
+        let what = "smoe_qmm";
+        let w = self.weights.raw(self.out_dim, self.in_dim, what)?;
+        let x = self.input.f32_span(self.input_offset, self.n_tokens as u64 * self.in_dim as u64, what)?;
+        let y = self.output.f32_span(self.output_offset, self.n_tokens as u64 * self.out_dim as u64, what)?;
         check(unsafe {
-            sys::smoe_qmm(k.h, &w, self.input.f32_at(self.input_offset), self.output.f32_at(self.output_offset),
-                          self.out_dim, self.in_dim, self.n_tokens, self.workspace.ptr, self.workspace.len)
-        }, "smoe_qmm")
+            sys::smoe_qmm(k.h, &w, x, y, self.out_dim, self.in_dim, self.n_tokens, self.workspace.ptr,
+                          self.workspace.len)
+        }, what)
     }
 }
 
@@ -382,17 +407,22 @@ pub struct MoeDecodeLayersCall<'a> {
 }
 
 impl MoeDecodeLayersCall<'_> {
-    fn raw(&self) -> (Vec<sys::smoe_layer>, Option<Vec<*const c_void>>) {
+    /// The C arrays; `norm_w` must have one entry per layer (the C side
+    /// reads norm_w[l] for every layer).
+    fn raw(&self) -> Result<(Vec<sys::smoe_layer>, Option<Vec<*const c_void>>), SmoeError> {
+        if self.norm_w.is_some_and(|v| v.len() != self.layers.len()) {
+            return Err(SmoeError { status: sys::SMOE_ERR_INVALID_ARG, what: "MoeDecodeLayersCall::norm_w" });
+        }
         let l: Vec<sys::smoe_layer> = self.layers.iter().map(|x| x.raw()).collect();
         let n = self.norm_w.map(|v| v.iter().map(|b| b.ptr as *const c_void).collect());
-        (l, n)
+        Ok((l, n))
     }
 
     /// The same chain without a handle or any allocation, on the current
     /// device and `stream` (smoe_moe_decode_layers_noalloc): for code under
     /// graph capture or loops that may not allocate.
     pub fn encode_noalloc(&self, stream: HipStream) -> Result<(), SmoeError> {
-        let (l, n) = self.raw();
+        let (l, n) = self.raw()?;
         let np = n.as_ref().map_or(ptr::null(), |v| v.as_ptr());
         check(unsafe {
             sys::smoe_moe_decode_layers_noalloc(stream.0, l.as_ptr(), l.len() as u32, np, self.eps,
@@ -403,7 +433,7 @@ impl MoeDecodeLayersCall<'_> {
 
 impl KernelCall for MoeDecodeLayersCall<'_> {
     fn encode(&self, k: &Kernels) -> Result<(), SmoeError> {
-        let (l, n) = self.raw();
+        let (l, n) = self.raw()?;
         let np = n.as_ref().map_or(ptr::null(), |v| v.as_ptr());
         check(unsafe {
             sys::smoe_moe_decode_layers(k.h, l.as_ptr(), l.len() as u32, np, self.eps, self.input.ptr as *const f32,
@@ -424,7 +454,7 @@ pub struct MoeDecodeTokensCall<'a> {
 impl KernelCall for MoeDecodeTokensCall<'_> {
     fn encode(&self, k: &Kernels) -> Result<(), SmoeError> {
         let c = &self.chain;
-        let (l, n) = c.raw();
+        let (l, n) = c.raw()?;
         let np = n.as_ref().map_or(ptr::null(), |v| v.as_ptr());
         check(unsafe {
             sys::smoe_moe_decode_tokens(k.h, l.as_ptr(), l.len() as u32, np, c.eps, self.n_tokens,
@@ -465,6 +495,54 @@ impl KernelCall for MoePrefillCall<'_> {
                                   self.input_is_bf16 as c_int, self.n_tokens, self.k,
                                   self.out_sum.ptr as *mut f32, self.workspace.ptr, self.workspace.len)
         }, "smoe_moe_prefill")
+    }
+}
+
+/// The whole prefill MoE block of one layer (linear_attn_forward.rs:
+/// 3998-4075): the routed experts as [`MoePrefillCall`], an optional 4-bit
+/// shared expert over all tokens with an optional f32 gate vector, and the
+/// residual: `hidden_out = (h_mid + moe_sum) + sigmoid(gate . x_t) *
+/// shared_out` (`Op::MoeCombineResidualNTokens`). Workspace:
+/// [`Kernels::moe_prefill_block_workspace_size`] bytes.
+pub struct MoePrefillBlockCall<'a> {
+    pub routed: MoePrefillCall<'a>,
+    pub shared_expert: Option<&'a BufferRef>,
+    pub shared_gate: Option<&'a BufferRef>,
+    pub h_mid: &'a BufferRef,
+}
+
+impl KernelCall for MoePrefillBlockCall<'_> {
+    fn encode(&self, k: &Kernels) -> Result<(), SmoeError> {
+        let r = &self.routed;
+        let s = r.shape.raw();
+        check(unsafe {
+            sys::smoe_moe_prefill_block(k.h, &s, r.experts.ptr, r.stride, r.n_experts, r.indices.ptr as *const i32,
+                                        r.weights.ptr as *const f32, r.input.ptr, r.input_is_bf16 as c_int,
+                                        r.n_tokens, r.k,
+                                        self.shared_expert.map_or(ptr::null(), |b| b.ptr as *const c_void),
+                                        self.shared_gate.map_or(ptr::null(), |b| b.ptr as *const f32),
+                                        self.h_mid.ptr as *const f32, r.out_sum.ptr as *mut f32, r.workspace.ptr,
+                                        r.workspace.len)
+        }, "smoe_moe_prefill_block")
+    }
+}
+
+/// The router softmax alone (`softmax`, moe_router.rs:52-72), the
+/// reference's probabilities bit for bit, per row of `n` logits.
+pub struct SoftmaxCall<'a> {
+    pub logits: &'a BufferRef,
+    pub n_tokens: u32,
+    pub n: u32,
+    pub probs: &'a BufferRef,
+}
+
+impl KernelCall for SoftmaxCall<'_> {
+    fn encode(&self, k: &Kernels) -> Result<(), SmoeError> {
+        let what = "smoe_softmax";
+        let m = self.n_tokens as u64 * self.n as u64;
+        let l = self.logits.f32_span(0, m, what)?;
+        let p = self.probs.f32_span(0, m, what)?;
+        check(unsafe { sys::smoe_softmax(k.h, l, self.n_tokens, self.n, p) }, what)
     }
 }
 

@@ -389,7 +389,7 @@ def _experts_case(kernels, H, I, k, bits, with_shared, seed):
     assert rc == 0
     outs = np.stack([oracle.expert_swiglu(b, bits, H, I, 64, x) for b in blobs])
     want = oracle.combine(outs, wts, h_mid, shared, score if with_shared else float("nan"))
-    return host(out), want
+    return host(out), want, h_mid
 
 
 @pytest.mark.parametrize("H,I,k,bits,shared", [
@@ -411,11 +411,13 @@ def _experts_case(kernels, H, I, k, bits, with_shared, seed):
 def test_experts_decode_matches_oracle(kernels, H, I, k, bits, shared):
     if H > 4096:
         kernels.reserve(H, max(I, 2048), 1024)
-    got, want = _experts_case(kernels, H, I, k, bits, shared, seed=H + I + k + bits)
-    # The expert outputs are small next to h_mid; compare the MoE part too.
+    got, want, h_mid = _experts_case(kernels, H, I, k, bits, shared, seed=H + I + k + bits)
+    # The expert outputs are small next to h_mid: the MoE part (output -
+    # h_mid) is compared on its own as well.
     err = rel_err(got, want)
-    print(f"experts H={H} I={I} k={k} {bits}-bit rel_err={err:.3e}")
-    assert err <= TOL
+    moe_err = rel_err(got - h_mid, want - h_mid)
+    print(f"experts H={H} I={I} k={k} {bits}-bit rel_err={err:.3e} MoE part {moe_err:.3e}")
+    assert err <= TOL and moe_err <= TOL
 
 
 def test_packed_3bit_bit_identical_to_nibbles(kernels):

@@ -14,10 +14,15 @@ S0)) rounded once in f32. Hence, per chunk,
 the first term from rounding x to the grid 2^-f (half a step, at most
 2^-23 * 2^e <= 2^-22 * max|x|), the second from the one f32 rounding of t,
 the last from t * 2^-f landing below the normal f32 range (tiny chunks).
+When the chunk's largest |x| is below 2^-128 (f >= 150), the scale 2^-f
+itself underflows to 0 in f32 and the chunk contributes 0: the error is
+then sum_j q_j |x_j| < 480 * 2^-128 in absolute terms, and the bound's
+last term is that sum instead.
 This test restates that arithmetic in numpy (integer parts exact in int64,
 the f32 steps as float32) and checks the bound on random and adversarial
 chunks: N(0, 1), +-100 outliers, magnitudes spread over 2^20, signed
-zeros, subnormal-sized values, and all-zero chunks. It also reports the
+zeros, values near the bottom of the normal range, all-subnormal chunks,
+and all-zero chunks. It also reports the
 worst error relative to sum_j q_j |x_j| (the scale of the f32 sequential
 sum's own error)."""
 import numpy as np
@@ -60,8 +65,9 @@ def chunks(rng):
     yield x
     yield np.sign(rng.standard_normal(32)) * 2.0 ** (-np.linspace(0, 20, 32))
     yield np.sign(rng.standard_normal(32)) * 2.0 ** rng.uniform(-30, 10, 32)
-    x = rng.standard_normal(32) * 1e-38  # subnormal-sized values
+    x = rng.standard_normal(32) * 1e-38  # near the bottom of the normal range
     yield x
+    yield rng.standard_normal(32) * 1e-40  # all subnormal: the scale underflows
     x = np.zeros(32)
     x[::3] = -0.0
     yield x
@@ -80,10 +86,11 @@ def test_limb_dot_error_within_bound():
             exact = float(np.sum(q.astype(np.float64) * x.astype(np.float64)))
             mag = float(np.sum(q * np.abs(x.astype(np.float64))))
             amax = float(np.max(np.abs(x)))
-            bound = 2.0 ** -22 * amax * float(np.sum(q)) + 2.0 ** -24 * mag + 2.0 ** -150
+            f = 22 - int(np.frexp(np.float32(amax))[1]) if amax > 0 else 0
+            bound = 2.0 ** -22 * amax * float(np.sum(q)) + 2.0 ** -24 * mag + (mag if f >= 150 else 2.0 ** -150)
             err = abs(got - exact)
             assert err <= bound * (1 + 1e-12), (x, q, err, bound)
-            if mag > 0:
+            if mag > 0 and f < 150:
                 worst = max(worst, err / mag)
                 if kind == 0:
                     worst_normal = max(worst_normal, err / mag)

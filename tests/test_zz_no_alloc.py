@@ -1,12 +1,18 @@
 """smoe_moe_decode_layers_noalloc: the decode chain with no handle and no
 allocation (fixed device scratch) gives smoe_moe_decode_layers' result bit
-for bit, on two calls in a row, the second with a smaller input.
+for bit, on two calls in a row, the second with a smaller input; captured
+in a HIP graph after a first call and replayed (with eager work between the
+replays), every replay equals the handle path's result bit for bit.
 
-The first call is made before this test creates any handle, so in a fresh
-process it also covers the entry point's own per-device set-up (the
-scratch address lookup); after other tests the set-up was done by
-smoe_create."""
+Inside a test run a handle already exists (smoe_create looks up the
+scratch address), so the entry point's own first-call lookup is covered by
+running the two-call check once more in a fresh process that creates no
+handle before its first no-allocation call
+(test_noalloc_first_call_in_a_fresh_process)."""
 import ctypes as C
+import os
+import subprocess
+import sys
 
 import numpy as np
 import pytest
@@ -58,6 +64,10 @@ def _noalloc(sa, torch, layers, norms, x0, resid):
 
 
 def test_noalloc_decode_matches_handle_decode_twice():
+    _two_calls_then_handle()
+
+
+def _two_calls_then_handle():
     import torch
 
     import streamoe_amd as sa
@@ -136,3 +146,59 @@ def test_noalloc_decode_argument_errors():
     assert sa._lib.smoe_moe_decode_layers_noalloc(None, None, 0, None, C.c_float(0), None, None) == \
         _abi.CODES["SMOE_ERR_INVALID_ARG"]
     torch.cuda.synchronize()
+
+
+def test_noalloc_graph_capture_and_replay():
+    """A first call outside capture (the per-device set-up), then the chain
+    captured into a HIP graph and replayed three times, the residual reset
+    by eager work between replays: every replay equals the handle path."""
+    import torch
+
+    import streamoe_amd as sa
+
+    layers, norms, x0, keep = _layers(torch, sa, 3, 256, 8, 512, 21)
+    resid = x0.clone()
+    assert _noalloc(sa, torch, layers, norms, x0, resid) == 0  # outside capture
+    torch.cuda.synchronize()
+    kern = sa.Kernels(0)
+    try:
+        want = x0.clone()
+        assert kern.moe_decode_layers(layers, norms, 1e-6, x0, want, torch.empty_like(x0)) == 0
+        kern.sync()
+        want = want.cpu().numpy()
+    finally:
+        kern.close()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        resid.copy_(x0)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            assert _noalloc(sa, torch, layers, norms, x0, resid) == 0
+    torch.cuda.synchronize()
+    for rep in range(3):
+        resid.copy_(x0)          # eager work between the replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = resid.cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"replay {rep}"
+    del keep
+
+
+def test_noalloc_first_call_in_a_fresh_process():
+    """The two-call check in a new Python process that creates no handle
+    before its first no-allocation call, so that call does the per-device
+    scratch lookup itself."""
+    env = dict(os.environ)
+    r = subprocess.run([sys.executable, "-u", os.path.abspath(__file__), "--fresh"], capture_output=True,
+                       text=True, timeout=600, env=env)
+    print(r.stdout[-2000:], r.stderr[-2000:])
+    assert r.returncode == 0 and "fresh process: ok" in r.stdout
+
+
+if __name__ == "__main__" and "--fresh" in sys.argv:
+    sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+    _two_calls_then_handle()
+    print("fresh process: ok", flush=True)
