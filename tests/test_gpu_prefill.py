@@ -69,6 +69,8 @@ def _case(kernels, n_tokens, H, I, E, k, bits, group, x_bf16, seed, routing="zip
     ("f32-x", 96, 2048, 512, 64, 8, 4, 64, False, "zipf"),
     ("olmoe-shape", 64, 2048, 1024, 64, 8, 4, 64, True, "zipf"),
     ("g32", 40, 1024, 512, 32, 4, 4, 32, True, "zipf"),
+    ("g128", 72, 2048, 512, 64, 8, 4, 128, True, "zipf"),
+    ("g128-hot", 300, 1024, 1024, 32, 4, 4, 128, True, "hot"),
     ("g128-3bit", 40, 1024, 512, 32, 4, 3, 128, False, "zipf"),
     ("hot-expert", 200, 2048, 512, 64, 8, 4, 64, True, "hot"),
     ("one-token", 1, 2048, 512, 256, 8, 4, 64, True, "zipf"),
