@@ -62,8 +62,8 @@ CONFIGS = {
 # launches), profiles/lm_head_c1_qmv_argmax.md (k_qmv + argmax) and
 # profiles/prefill_c4_a3b_4bit.md (the four prefill launches of one layer).
 # None where no counter pass was taken (multi-token decode, per-phase path).
-MEASURED_TRAFFIC = {"c0": 29_749_910, "c2": 18_883_732, "c3": 15_758_605, "c1": 175_938_018,
-                    "c4": 554_026_850, "c5": 87_750_848}
+MEASURED_TRAFFIC = {"c0": 29_732_534, "c2": 18_897_532, "c3": 15_786_871, "c1": 175_922_937,
+                    "c4": 569_328_147, "c5": 87_783_971}
 
 
 def stream_read_peak(dev, gib=4):
