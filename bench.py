@@ -597,8 +597,8 @@ def run_prefill(args, c):
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": MEASURED_TRAFFIC.get("c4"),
                      "unit_of_work": f"one layer: {nbytes} algorithmic bytes ({len(hit)} hit experts x {stride} "
                                      f"+ X + Y), {flops} flops",
-                     "kernel": "prefill layer: k_pf_route (+ per-token x preparation) + k_pf_mm (gate/up, with the activation "
-                               "group sums) + k_pf_mm (down) + k_pf_combine (one HIP graph)"},
+                     "kernel": "prefill layer: k_pf_route (+ per-token x preparation) + k_pf_gu64 (gate/up on 32x32 tiles, with "
+                               "the activation group sums) + k_pf_mm (down) + k_pf_combine (one HIP graph)"},
     }
     blk_bytes = nbytes + slay.expert_size + 2 * n * H * 4  # + shared expert, h_mid read, gate
     blk_flops = flops + 2 * n * (2 * H * I + I * H)

@@ -67,11 +67,17 @@ typedef enum {
                                 instance, else one kernel per phase), 1 one
                                 kernel per phase, 3 three-kernel only (2, the
                                 former persistent path, is rejected) */
-  SMOE_OPT_TRACE_BUFFER = 2  /* device uint64 buffer for in-kernel timestamps, or 0 =
+  SMOE_OPT_TRACE_BUFFER = 2, /* device uint64 buffer for in-kernel timestamps, or 0 =
                                 off. Three-kernel decode: per layer 3 * 4096 * 8
                                 words (kernel, block, point); prefill: 8 words
                                 (phase ends of the bucketing kernel). Diagnostics
                                 only. */
+  SMOE_OPT_PREFILL_GEMM = 3  /* prefill gate/up GEMM: 0 auto (default: 32 x 32
+                                MFMA tiles over 128-column units for 4-bit
+                                group-64 experts over bf16 x, else 16 x 16
+                                tiles over 64-column units), 1 the 16 x 16
+                                tiles always. Both give the same results up
+                                to fp32 rounding order. */
 } smoe_option;
 
 typedef struct smoe_handle smoe_handle;

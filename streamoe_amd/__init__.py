@@ -152,6 +152,10 @@ class Kernels:
         """0 auto, 1 one kernel per phase, 3 three-kernel only (SMOE_OPT_DECODE_PATH)."""
         self.set_option(_abi.SMOE_OPT_DECODE_PATH, path)
 
+    def set_prefill_gemm(self, path):
+        """0 auto (32 x 32 gate/up tiles where they apply), 1 k_pf_mm only (SMOE_OPT_PREFILL_GEMM)."""
+        self.set_option(_abi.SMOE_OPT_PREFILL_GEMM, path)
+
     def reserve(self, max_hidden, max_inter, max_experts):
         check(_lib.smoe_reserve(self.h, max_hidden, max_inter, max_experts), "smoe_reserve")
 

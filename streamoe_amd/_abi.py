@@ -31,6 +31,7 @@ STATUS = {
 }
 SMOE_OPT_DECODE_PATH = 1
 SMOE_OPT_TRACE_BUFFER = 2
+SMOE_OPT_PREFILL_GEMM = 3
 CODES = {v: k for k, v in STATUS.items()}
 
 

@@ -226,6 +226,10 @@ int smoe_set_option(smoe_handle* h, int option, int64_t value) {
     case SMOE_OPT_TRACE_BUFFER:
       h->trace = (uint64_t*)(uintptr_t)value;
       return SMOE_OK;
+    case SMOE_OPT_PREFILL_GEMM:
+      if (value < 0 || value > 1) return SMOE_ERR_INVALID_ARG;
+      h->prefill_gemm = (int)value;
+      return SMOE_OK;
     default:
       return SMOE_ERR_INVALID_ARG;
   }
@@ -801,6 +805,7 @@ int smoe_moe_prefill(smoe_handle* h, const smoe_expert_shape* shape, const void*
   a.out = out_sum;
   a.err = h->err;
   a.trace = h->trace;
+  a.gemm_path = h->prefill_gemm;
   int n_cu = 0;
   if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, h->device) != hipSuccess || n_cu <= 0)
     return SMOE_ERR_HIP;
@@ -843,6 +848,7 @@ int smoe_moe_prefill_block(smoe_handle* h, const smoe_expert_shape* shape, const
   a.out = hidden_out;
   a.err = h->err;
   a.trace = h->trace;
+  a.gemm_path = h->prefill_gemm;
   a.shared = (const uint8_t*)shared_expert;
   a.sg = blob_geom(shape->hidden, shape->inter, shape->group, 4);
   a.shared_in_list = shared_expert && shape->bits == 4;

@@ -28,6 +28,7 @@ struct smoe_handle {
   // Options.
   int decode_path = 0;  // 0 auto, 1 per-phase kernels, 3 three-kernel
   uint64_t* trace = nullptr;
+  int prefill_gemm = 0;  // 0 the 32 x 32 gate/up tile where it applies, 1 k_pf_mm only
   // File loader: two pinned host staging buffers (allocated on first use,
   // freed by smoe_destroy) and the events that say when a copy out of
   // each has finished.

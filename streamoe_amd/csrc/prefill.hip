@@ -21,6 +21,10 @@
 //                 activation group sums for G <= 64; mode 2 down rows over
 //                 the fp16 activations -> f32 per entry (mode 1: the same
 //                 over bf16 hi + lo rows, the dense qmm).
+//   k_pf_gu64     the gate/up GEMM for 4-bit group-64 experts over bf16 x
+//                 (the reference models' format): the same pipeline on
+//                 v_mfma_f32_32x32x16_bf16 tiles over (item, 128 column)
+//                 units, so a chunk's token rows are a third of its copies.
 //   k_pf_act_sum  activation group sums for G > 64 (a group spans more than
 //                 one gate/up unit).
 //   k_pf_combine  out[t] = sum over t's entries in ascending expert order of
@@ -1365,6 +1369,345 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
   }
 }
 
+// ---------------------------------------------------------------------------
+// Gate/up GEMM on 32 x 32 tiles (k_pf_gu64): 4-bit codes, group 64, bf16 x.
+//
+// The same staged pipeline as k_pf_mm (persistent block per CU, LDS ring of
+// three stages filled by LDS DMA two chunks ahead, one block barrier per
+// 256-input chunk, four copy-only waves beside eight compute waves, the
+// XCD-aware work list), with a wider unit: (item, 128 output columns) =
+// 256 weight rows. Its 32 token rows are copied once per chunk for all 256
+// rows, so they are a third of a chunk's copies instead of a half (16 KB
+// next to 32 KB of codes and 4 KB of scales). Compute wave (cw, kh) owns
+// columns 32 cw .. 32 cw + 31 of both matrices (one v_mfma_f32_32x32x16_bf16
+// tile each, the 32 item rows by 32 columns, so SwiGLU pairs are in the same
+// lane) and the chunk's groups 2 kh, 2 kh + 1; each A fragment read feeds
+// both tiles. The dequant term (b - 128 s) * sum x of the wave's two groups
+// is exactly one v_mfma_f32_32x32x2_f32 per tile and chunk (K = 2 groups).
+// At a unit's end the K halves swap partial sums through the stage just
+// read (each finishes 16 of the 32 rows), then SwiGLU, fp16 activations in
+// the down GEMM's order, and the activations' 64-column group sums.
+//
+// Lane l: column (or A row) l % 32, k half kq = l / 32. Code words: lane
+// (c, kq) reads the 16 bytes of row c at k half kq of group g (words 0-3 =
+// MFMA steps 0-3); the A fragment of step s is the 8-input block 8 g + 4 kq
+// + s of the item row, stored in the unpack order as for k_pf_mm.
+// ---------------------------------------------------------------------------
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                 0, 0, 0);
+}
+
+struct Gu64 {
+  static constexpr int NWC = 8, NWD = 4, NWT = NWC + NWD;  // compute, copy, all waves
+  static constexpr int G = 64, KC = 256, CG = KC / G;       // inputs per chunk, groups per chunk
+  static constexpr int NCOL = 128, ROWS = 2 * NCOL;         // output columns, weight rows per unit
+  static constexpr int RB = KC / 2;                         // code bytes per row and chunk
+  static constexpr int OFF_BQ = 0;                          // [row][8 parts of 16 B], part ^ (row & 7)
+  static constexpr int OFF_A = OFF_BQ + ROWS * RB;          // [32 rows][32 parts of 16 B], part ^ (row & 15)
+  static constexpr int OFF_S = OFF_A + 32 * KC * 2;         // [row][scale, bias][CG] bf16
+  static constexpr int OFF_XS = OFF_S + ROWS * 2 * CG * 2;  // [32 rows][CG] f32 group sums of x
+  static constexpr int STAGE = OFF_XS + 32 * CG * 4;
+  static constexpr int S = 3;                               // stages
+  static constexpr int OFF_TOK = S * STAGE;                 // [2][32] token ids of two units
+  static constexpr int OFF_PS = OFF_TOK + 2 * 32 * 4;       // [4 column waves][32 rows] activation row sums
+  static constexpr int LDS = OFF_PS + 4 * 32 * 4;
+  // Copies per copy wave and chunk: codes (16 B pieces), A rows (16 B),
+  // scales and biases (4 B), x group sums (16 B, 8 lanes).
+  static constexpr int N_BQ = ROWS * RB / 16 / NWD / 64;
+  static constexpr int N_A = 32 * KC * 2 / 16 / NWD / 64;
+  static constexpr int N_S = ROWS * 2 * CG * 2 / 4 / NWD / 64;
+  static constexpr int D = N_BQ + N_A + N_S + 1;
+  static constexpr int EX = 8 * 16 * 64 * 4;  // K-half exchange: [cw][receiving half][16 values][lane] f32
+  static_assert(N_BQ * NWD * 64 * 16 == ROWS * RB && N_A * NWD * 64 * 16 == 32 * KC * 2, "equal copy shares");
+  static_assert(N_S * NWD * 64 * 4 == ROWS * 2 * CG * 2, "equal copy shares");
+  static_assert(EX <= STAGE, "exchange fits a stage");
+  static_assert(LDS <= 160 * 1024, "LDS per CU");
+  static_assert(2 * D + 1 <= 63, "vmcnt range");
+};
+
+__global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint32_t* __restrict__ items,
+                                                             const uint32_t* __restrict__ n_items_p,
+                                                             const uint32_t* __restrict__ xr) {
+  using C = Gu64;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool copier = wave >= (uint32_t)C::NWC;
+  const uint32_t dw = copier ? wave - C::NWC : 0u;           // copy share
+  const uint32_t cw = wave & 3, kh = (wave >> 2) & 1;        // compute waves: column block, K half
+  const uint32_t c32 = lane & 31, kq = lane >> 5;
+  const uint32_t K = a.g.hidden, N = a.g.inter;
+  const uint32_t ng = K / C::G, nch = K / C::KC, rowb = K / 2;
+  const uint32_t ncb = N / C::NCOL;
+  const uint32_t nx = gridDim.x % 8 == 0 ? 8 : 1, per = gridDim.x / nx;
+  const uint32_t xg = blockIdx.x % nx, lb = blockIdx.x / nx;
+  const uint32_t n_items = *n_items_p;
+  const uint32_t item_lo = xr && nx == 8 ? xr[xg] : n_items * xg / nx;
+  const uint32_t item_hi = xr && nx == 8 ? xr[xg + 1] : n_items * (xg + 1) / nx;
+  const uint32_t group_units = (item_hi - item_lo) * ncb;
+  const uint32_t my_units = group_units > lb ? (group_units - lb + per - 1) / per : 0;
+  const uint32_t total = my_units * nch;
+  if (total == 0) return;
+  // Kernel arguments into scalar locals (nothing takes the argument
+  // block's address).
+  const uint8_t* const experts = a.experts;
+  const uint8_t* const shared = a.shared_in_list ? a.shared : nullptr;
+  const uint32_t e_shared = a.E;
+  const uint32_t* const item_tok = a.item_tok;
+  const uint32_t last_tok = a.n_tokens - 1;
+  const uint64_t stride = a.stride;
+  const uint8_t* const xh = reinterpret_cast<const uint8_t*>(a.x_hi);
+  const uint8_t* const xsum = reinterpret_cast<const uint8_t*>(a.xsum);
+  uint16_t* const act_out = a.act_hi;
+  float* const asum_out = a.asum;
+  const uint64_t wo0 = a.g.w[0], wo1 = a.g.w[1], so0 = a.g.s[0], so1 = a.g.s[1];
+  const uint64_t bso = a.g.b[0] - so0;
+  const uint32_t c43 = 0x43434343u;
+
+  struct Unit {
+    uint32_t e, start, cnt, cb, item;
+  };
+  auto unit = [=](uint32_t i) {  // unit i of this block (scalar loads of its work-list words)
+    const uint32_t v = lb + per * i;
+    Unit u;
+    u.item = item_lo + v / ncb;
+    u.cb = v % ncb;
+    const uint2 iw = *reinterpret_cast<const uint2*>(items + 2 * (size_t)u.item);
+    u.e = iw.x;
+    u.start = iw.y & 0xFFFFu;
+    u.cnt = iw.y >> 16;
+    return u;
+  };
+  // Token ids of unit i into token buffer `par`: copy wave d, lanes 0-7,
+  // rows 8 d .. 8 d + 7.
+  auto token_dma = [=](uint32_t i, uint32_t par) {
+    if (lane < 8) dma4(item_tok + (size_t)unit(i).item * kPfMC + 8 * dw + lane, lds + C::OFF_TOK + (par * 32 + 8 * dw) * 4);
+  };
+  // Per-lane source offsets of one unit's copies (fixed while the unit
+  // lasts; the chunk adds a scalar offset). Copy wave d's code pieces are
+  // rows 64 d + 8 i + l / 8 (gate rows for d < 2, up rows for d >= 2) at
+  // 16-byte part (l % 8) ^ (l / 8 % 8), so copy i adds 8 i rows to one lane
+  // offset; its scale pieces are rows 64 d + 16 i + l / 4 likewise; its A
+  // rows are 8 d + 2 i + l / 32, one token row each.
+  struct Src {
+    const uint8_t* blob;
+    uint32_t bq, s;        // from the blob, copy 0
+    uint32_t ar[C::N_A];   // from x_hi (token row + part)
+    uint32_t xs;           // from xsum
+  };
+  static_assert(C::N_BQ * 8 * C::NWD == C::ROWS && C::N_S * 16 * C::NWD == C::ROWS, "copy rows per wave");
+  auto src_of = [=](const Unit& u, uint32_t par) {
+    Src r;
+    r.blob = shared && u.e == e_shared ? shared : experts + (size_t)u.e * stride;
+    const uint32_t* tb = reinterpret_cast<const uint32_t*>(lds + C::OFF_TOK) + par * 32;
+    const uint32_t mat = dw >= 2, row0 = u.cb * C::NCOL + 64 * (dw & 1u);
+    r.bq = (uint32_t)(mat ? wo1 : wo0) + (row0 + lane / 8) * rowb + (((lane & 7u) ^ ((lane >> 3) & 7u)) * 16);
+    r.s = (uint32_t)((mat ? so1 : so0) + ((lane >> 1) & 1u) * bso) + (row0 + lane / 4) * ng * 2 + (lane & 1u) * 4;
+#pragma unroll
+    for (int i = 0; i < C::N_A; ++i) {
+      const uint32_t row = 8 * dw + 2 * i + lane / 32, part = (lane % 32) ^ (row & 15u);
+      r.ar[i] = min(tb[row], last_tok) * K * 2 + part * 16;
+    }
+    r.xs = min(tb[8 * dw + min(lane, 7u)], last_tok) * ng * 4;
+    return r;
+  };
+  // Every copy of chunk c of a unit into stage `slot`.
+  auto issue = [=](const Src& r, uint32_t c, uint32_t slot) {
+    uint8_t* st = lds + slot * C::STAGE;
+    const uint8_t* bq = r.blob + (size_t)c * C::RB;
+#pragma unroll
+    for (int i = 0; i < C::N_BQ; ++i)
+      dma16(bq + (size_t)(8 * i) * rowb + pf_voff(r.bq), st + C::OFF_BQ + (dw * C::N_BQ + i) * 64 * 16);
+    const uint8_t* ab = xh + (size_t)c * C::KC * 2;
+#pragma unroll
+    for (int i = 0; i < C::N_A; ++i) dma16(ab + r.ar[i], st + C::OFF_A + (dw * C::N_A + i) * 64 * 16);
+    const uint8_t* sb = r.blob + (size_t)c * C::CG * 2;
+#pragma unroll
+    for (int i = 0; i < C::N_S; ++i)
+      dma4(sb + (size_t)(16 * i) * ng * 2 + pf_voff(r.s), st + C::OFF_S + (dw * C::N_S + i) * 64 * 4);
+    if (lane < 8) dma16(xsum + (size_t)c * C::CG * 4 + r.xs, st + C::OFF_XS + 8 * dw * 16);
+  };
+
+  f32x16 tot[2];
+  tot[0] = f32x16{};
+  tot[1] = f32x16{};
+  // The first unit's token ids, visible to every wave before its copies.
+  if (copier) token_dma(0, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  // Issue position (unit iu, chunk ic, token buffer ipar, stage islot)
+  // runs S - 1 chunks ahead of the compute position; the next unit's token
+  // ids are copied with a unit's first chunk.
+  uint32_t iu = 0, ic = 0, ipar = 0, islot = 0, issued = 0;
+  Src src{};
+  uint32_t cc = 0, cslot = 0, cu = 0;
+  Unit ucur = unit(0);
+  // Activation row sums of the last finished unit, written out by wave 0
+  // after the next block barrier.
+  bool ps_pend = false;
+  uint32_t ps_start = 0, ps_cnt = 0, ps_cb = 0;
+  // Iterations -(S - 1) .. -1 only issue (the prologue); iteration j >= 0
+  // waits for chunk j, issues chunk j + S - 1 and computes chunk j.
+  for (int jj = 1 - C::S; jj < (int)total; ++jj) {
+    const uint32_t j = (uint32_t)jj;
+    if (jj >= 0) {
+      if (!copier)
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      else if (j + 1 < total)
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(C::D) : "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+    }
+    if (issued < total) {
+      if (copier) {
+        if (ic == 0) {
+          src = src_of(unit(iu), ipar);
+          if (iu + 1 < my_units) token_dma(iu + 1, ipar ^ 1u);
+        }
+        issue(src, ic, islot);
+      }
+      ++issued;
+      islot = islot + 1 == (uint32_t)C::S ? 0u : islot + 1;
+      if (++ic == nch) {
+        ic = 0;
+        ++iu;
+        ipar ^= 1u;
+      }
+    }
+    if (jj < 0) continue;
+    if (ps_pend) {
+      if (wave == 0) {
+        const float* ps = reinterpret_cast<const float*>(lds + C::OFF_PS);
+        const uint32_t m = lane & 31, gq = lane >> 5;  // group of 64 columns within the unit
+        if (m < ps_cnt)
+          asum_out[(size_t)(ps_start + m) * (N / C::G) + ps_cb * 2 + gq] = ps[(2 * gq) * 32 + m] + ps[(2 * gq + 1) * 32 + m];
+      }
+      ps_pend = false;
+    }
+    const uint8_t* st = lds + cslot * C::STAGE;
+    cslot = cslot + 1 == (uint32_t)C::S ? 0u : cslot + 1;
+    if (!copier) {
+      // Scales and biases of this wave's two groups for both tiles: bf16
+      // pairs (group 2 kh, 2 kh + 1).
+      uint32_t sw[2], bw[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const uint32_t row = t * C::NCOL + 32 * cw + c32;
+        const uint32_t* sp = reinterpret_cast<const uint32_t*>(st + C::OFF_S + row * 16 + 4 * kh);
+        sw[t] = sp[0];
+        bw[t] = sp[2];
+      }
+#pragma unroll
+      for (int gi = 0; gi < 2; ++gi) {
+        const uint32_t g = 2 * kh + gi;
+        u32x4 af[4], bq[2];
+        const uint8_t* ar = st + C::OFF_A + c32 * (C::KC * 2);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) af[s] = *reinterpret_cast<const u32x4*>(ar + (((8 * g + 4 * kq + s) ^ (c32 & 15u)) * 16));
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const uint32_t row = t * C::NCOL + 32 * cw + c32;
+          bq[t] = *reinterpret_cast<const u32x4*>(st + C::OFF_BQ + row * C::RB + (((2 * g + kq) ^ (row & 7u)) * 16));
+        }
+        f32x16 acc0 = f32x16{}, acc1 = f32x16{};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          acc0 = mfma32(af[s], codes_bf16_4p(bq[0][s], c43), acc0);
+          acc1 = mfma32(af[s], codes_bf16_4p(bq[1][s], c43), acc1);
+        }
+        const float s0 = bf16f((uint16_t)(sw[0] >> (16 * gi))), s1 = bf16f((uint16_t)(sw[1] >> (16 * gi)));
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          tot[0][v] = __builtin_fmaf(s0, acc0[v], tot[0][v]);
+          tot[1][v] = __builtin_fmaf(s1, acc1[v], tot[1][v]);
+        }
+      }
+      // Dequant term of the two groups: A = x group sums [32 rows x 2
+      // groups], B = (b - 128 s) [2 groups x 32 columns].
+      const float xa = reinterpret_cast<const float*>(st + C::OFF_XS)[c32 * C::CG + 2 * kh + kq];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const uint32_t sh = 16 * kq;
+        const float cb = __builtin_fmaf(-128.0f, bf16f((uint16_t)(sw[t] >> sh)), bf16f((uint16_t)(bw[t] >> sh)));
+        tot[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa, cb, tot[t], 0, 0, 0);
+      }
+    }
+    if (++cc == nch) {  // unit complete
+      cc = 0;
+      const uint32_t start = ucur.start, cnt = ucur.cnt, cb = ucur.cb;
+      if (++cu < my_units) ucur = unit(cu);
+      // Every wave is done reading this stage; the K halves swap the rows
+      // the other one finishes (values 8 kh' .. 8 kh' + 7 of each tile).
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      float* ex = reinterpret_cast<float*>(const_cast<uint8_t*>(st));
+      if (!copier) {
+        float* xo = ex + (cw * 2 + (kh ^ 1u)) * 16 * 64 + lane;
+        const uint32_t vo = 8 * (kh ^ 1u);
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) xo[(t * 8 + i) * 64] = tot[t][vo + i];
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (!copier) {
+        const float* xi = ex + (cw * 2 + kh) * 16 * 64 + lane;
+        const uint32_t vm = 8 * kh;
+        const uint32_t col = cb * C::NCOL + 32 * cw + c32;
+        const uint32_t pc = (col & ~7u) + perm8_pos(col & 7u);
+        float rs[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t v = vm + i;
+          const uint32_t m = 8 * (v / 4) + 4 * kq + (v % 4);
+          const float g = tot[0][v] + xi[i * 64], u = tot[1][v] + xi[(8 + i) * 64];
+          const _Float16 h = (_Float16)silu_mul(g, u);
+          if (m < cnt) act_out[(size_t)(start + m) * N + pc] = __builtin_bit_cast(uint16_t, h);
+          rs[i] = (float)h;
+        }
+        // Row sums over the wave's 32 columns (the lanes of one k half).
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          rs[i] = row_sum16_all(rs[i]);
+          rs[i] += __shfl_xor(rs[i], 16, kWave);
+        }
+        if (c32 == 0) {
+          float* ps = reinterpret_cast<float*>(lds + C::OFF_PS) + cw * 32;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const uint32_t v = vm + i;
+            ps[8 * (v / 4) + 4 * kq + (v % 4)] = rs[i];
+          }
+        }
+      }
+      ps_pend = true;
+      ps_start = start;
+      ps_cnt = cnt;
+      ps_cb = cb;
+      tot[0] = f32x16{};
+      tot[1] = f32x16{};
+    }
+  }
+  // The last unit's sums (every wave leaves the loop after the same chunk).
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  if (ps_pend && wave == 0) {
+    const float* ps = reinterpret_cast<const float*>(lds + C::OFF_PS);
+    const uint32_t m = lane & 31, gq = lane >> 5;
+    if (m < ps_cnt)
+      asum_out[(size_t)(ps_start + m) * (N / C::G) + ps_cb * 2 + gq] = ps[(2 * gq) * 32 + m] + ps[(2 * gq + 1) * 32 + m];
+  }
+}
+
 // Group sums of the fp16 activations per entry; one block per entry.
 __global__ __launch_bounds__(256) void k_pf_act_sum(PfArgs a, uint32_t row0) {
   __shared__ float part8[kPfMaxGroupsK * 128 / 8];
@@ -1540,11 +1883,24 @@ static hipError_t launch_mm(const PfArgs& a, uint32_t n_units_max, uint32_t n_cu
 // group 64); other shapes copy scales per chunk.
 // act_rows: the entry rows [row0, row0 + n_rows) whose activation group
 // sums the G > 64 pass computes.
+static hipError_t launch_gu64(const PfArgs& a, uint32_t n_units_max, uint32_t n_cu, hipStream_t st) {
+  const auto fn = reinterpret_cast<const void*>(&k_pf_gu64);
+  static std::atomic<uint64_t> raised{0};
+  const hipError_t e = raise_lds_limit(fn, Gu64::LDS, raised);
+  if (e != hipSuccess) return e;
+  const uint32_t grid = n_units_max < n_cu ? n_units_max : n_cu;
+  hipLaunchKernelGGL(k_pf_gu64, dim3(grid), dim3(64 * Gu64::NWT), (size_t)Gu64::LDS, st, a, (const uint32_t*)a.items,
+                     (const uint32_t*)a.n_items, (const uint32_t*)a.xr);
+  return hipGetLastError();
+}
+
 template <int BITS, int G>
 static hipError_t launch_gemms(const PfArgs& a, uint32_t row0, uint32_t n_rows, uint32_t n_cu, hipStream_t st) {
   const uint32_t gu_units = a.max_items * (a.g.inter / 64);
   hipError_t e;
-  if (!a.x_bf16)
+  if (BITS == 4 && G == 64 && a.x_bf16 && a.gemm_path == 0 && a.g.inter % Gu64::NCOL == 0)
+    e = launch_gu64(a, a.max_items * (a.g.inter / Gu64::NCOL), n_cu, st);
+  else if (!a.x_bf16)
     e = launch_mm<BITS, G, 0, true, 0>(a, gu_units, n_cu, st);
   else if ((G == 64 || G == 128) && a.g.hidden == 2048)
     e = launch_mm<BITS, G, 0, false, (G == 64 || G == 128) ? 2048 : 0, (G == 64 || G == 128) ? 4 : 0>(a, gu_units, n_cu, st);

@@ -25,6 +25,7 @@ pub const SMOE_ERR_IO: c_int = 13;
 
 pub const SMOE_OPT_DECODE_PATH: c_int = 1;
 pub const SMOE_OPT_TRACE_BUFFER: c_int = 2;
+pub const SMOE_OPT_PREFILL_GEMM: c_int = 3;
 
 /// Opaque handle (`smoe_handle`).
 #[repr(C)]

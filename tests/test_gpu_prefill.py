@@ -98,6 +98,40 @@ def test_prefill_matches_oracle(kernels, name, n, H, I, E, k, bits, group, x_bf1
     assert err <= TOL
 
 
+@pytest.mark.parametrize("name,n,H,I,E,k,routing", [
+    ("c4-a3b", 512, 2048, 512, 256, 8, "zipf"),
+    ("hot-expert", 200, 2048, 512, 64, 8, "hot"),
+    ("olmoe-inter1024", 64, 2048, 1024, 64, 8, "zipf"),
+    ("h1024-k4", 40, 1024, 512, 32, 4, "zipf"),
+])
+def test_prefill_gate_up_tiles_agree(kernels, name, n, H, I, E, k, routing):
+    """The 32 x 32 gate/up tile (default for 4-bit group-64 experts over
+    bf16 x) and the 16 x 16 one (SMOE_OPT_PREFILL_GEMM = 1) both meet the
+    oracle bar and agree with each other to fp32 rounding-order
+    differences (and the fp16 rounding of the activations they feed)."""
+    seed = sum(map(ord, name)) + 3
+    got_a, want, _ = _case(kernels, n, H, I, E, k, 4, 64, True, seed=seed, routing=routing)
+    kernels.set_prefill_gemm(1)
+    try:
+        got_b, want_b, _ = _case(kernels, n, H, I, E, k, 4, 64, True, seed=seed, routing=routing)
+    finally:
+        kernels.set_prefill_gemm(0)
+    assert np.array_equal(want, want_b)
+    e_a, e_b, e_ab = rel_err(got_a, want), rel_err(got_b, want), rel_err(got_a, got_b)
+    print(f"prefill {name}: 32x32 {e_a:.3e} 16x16 {e_b:.3e} between {e_ab:.3e}")
+    assert e_a <= TOL and e_b <= TOL
+    assert e_ab <= 2e-4
+
+
+def test_prefill_gemm_option_values(kernels):
+    import streamoe_amd as sa
+
+    with pytest.raises(sa.SmoeError):
+        kernels.set_prefill_gemm(2)
+    kernels.set_prefill_gemm(1)
+    kernels.set_prefill_gemm(0)
+
+
 def test_prefill_is_deterministic(kernels):
     """Fixed-order reductions and no atomics in the arithmetic: two runs give
     the same bits."""
