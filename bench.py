@@ -63,7 +63,7 @@ CONFIGS = {
 # profiles/prefill_c4_a3b_4bit.md (the four prefill launches of one layer).
 # None where no counter pass was taken (multi-token decode, per-phase path).
 MEASURED_TRAFFIC = {"c0": 29_732_534, "c2": 18_897_532, "c3": 15_786_871, "c1": 175_922_937,
-                    "c4": 569_328_147, "c5": 87_783_971}
+                    "c4": 571_822_881, "c5": 87_783_971}
 
 
 def stream_read_peak(dev, gib=4):
@@ -573,6 +573,12 @@ def run_prefill(args, c):
         sa.check(_sync_status(kern), "smoe_sync")
         return e0.elapsed_time(e1) * 1e3 / args.steps, graph
 
+    # The other gate/up tile on the same inputs (its own graph), for
+    # comparison; timed first, so that the reported value does not carry
+    # the clock ramp of the first timed loop.
+    kern.set_prefill_gemm(0 if args.prefill_gemm == "16x16" else 1)
+    us_other, _ = time_steps(step)
+    kern.set_prefill_gemm(1 if args.prefill_gemm == "16x16" else 0)
     us, graph = time_steps(step)
     us_blk, _ = time_steps(step_block)
     hit = np.unique(idx)
@@ -597,8 +603,13 @@ def run_prefill(args, c):
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": MEASURED_TRAFFIC.get("c4"),
                      "unit_of_work": f"one layer: {nbytes} algorithmic bytes ({len(hit)} hit experts x {stride} "
                                      f"+ X + Y), {flops} flops",
-                     "kernel": "prefill layer: k_pf_route (+ per-token x preparation) + k_pf_gu64 (gate/up on 32x32 tiles, with "
-                               "the activation group sums) + k_pf_mm (down) + k_pf_combine (one HIP graph)"},
+                     "kernel": ("prefill layer: k_pf_route (+ per-token x preparation) + k_pf_gu64 (gate/up on 32x32 tiles, "
+                                "with the activation group sums) + k_pf_mm (down) + k_pf_combine (one HIP graph)")
+                               if args.prefill_gemm == "auto" else
+                               ("prefill layer: k_pf_route (+ per-token x preparation) + k_pf_mm (gate/up on 16x16 "
+                                "tiles, with the activation group sums) + k_pf_mm (down) + k_pf_combine (one HIP graph)")},
+        "gate_up_tile": "32x32" if args.prefill_gemm == "auto" else "16x16",
+        "other_tile_us_per_layer": {"16x16" if args.prefill_gemm == "auto" else "32x32": round(us_other, 2)},
     }
     blk_bytes = nbytes + slay.expert_size + 2 * n * H * 4  # + shared expert, h_mid read, gate
     blk_flops = flops + 2 * n * (2 * H * I + I * H)
@@ -654,6 +665,9 @@ def main():
     ap.add_argument("--path", default="auto", choices=["auto", "kernels", "fused"],
                     help="decode path: auto (three-kernel where supported), kernels (one per phase), "
                          "fused (three-kernel only)")
+    ap.add_argument("--prefill-gemm", default="auto", choices=["auto", "16x16"],
+                    help="c4: the default gate/up tile (32x32 where it applies) or the 16x16 one "
+                         "(SMOE_OPT_PREFILL_GEMM = 1); the other one is timed beside it")
     ap.add_argument("--eager", action="store_true", help="launch every step eagerly instead of replaying a HIP graph")
     ap.add_argument("--trace", action="store_true", help="report per-phase times from in-kernel timestamps")
     ap.add_argument("--no-cpu", action="store_true")
