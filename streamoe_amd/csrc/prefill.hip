@@ -1405,27 +1405,34 @@ struct Gu64 {
   static constexpr int G = 64, KC = 256, CG = KC / G;       // inputs per chunk, groups per chunk
   static constexpr int NCOL = 128, ROWS = 2 * NCOL;         // output columns, weight rows per unit
   static constexpr int RB = KC / 2;                         // code bytes per row and chunk
-  static constexpr int OFF_BQ = 0;                          // [row][8 parts of 16 B], part ^ (row & 7)
-  static constexpr int OFF_A = OFF_BQ + ROWS * RB;          // [32 rows][32 parts of 16 B], part ^ (row & 15)
-  static constexpr int OFF_S = OFF_A + 32 * KC * 2;         // [row][scale, bias][CG] bf16
-  static constexpr int OFF_XS = OFF_S + ROWS * 2 * CG * 2;  // [32 rows][CG] f32 group sums of x
-  static constexpr int STAGE = OFF_XS + 32 * CG * 4;
-  static constexpr int S = 3;                               // stages
-  static constexpr int OFF_TOK = S * STAGE;                 // [2][32] token ids of two units
+  // Three rings: codes two chunks ahead; token rows and their group sums
+  // one chunk ahead (they come from L2); scales and biases per chunk pair,
+  // copied with the pair's first chunk's token rows in 16-byte pieces (the
+  // 8 bytes a chunk needs per row and array would be 4-byte pieces, twice
+  // the cache lines per chunk).
+  static constexpr int SC = 3, SA = 2, SS = 2;
+  static constexpr int BQ_SLOT = ROWS * RB;                 // [row][8 parts of 16 B], part ^ (row & 7)
+  static constexpr int OFF_BQ = 0;
+  static constexpr int A_BYTES = 32 * KC * 2;               // [32 rows][32 parts of 16 B], part ^ (row & 15)
+  static constexpr int A_SLOT = A_BYTES + 32 * CG * 4;      // + [32 rows][CG] f32 group sums of x
+  static constexpr int OFF_A = OFF_BQ + SC * BQ_SLOT;
+  static constexpr int S_SLOT = ROWS * 2 * 2 * CG * 2;      // [row][scale, bias][2 CG] bf16
+  static constexpr int OFF_S = OFF_A + SA * A_SLOT;
+  static constexpr int OFF_TOK = OFF_S + SS * S_SLOT;       // [2][32] token ids of two units
   static constexpr int OFF_PS = OFF_TOK + 2 * 32 * 4;       // [4 column waves][32 rows] activation row sums
   static constexpr int LDS = OFF_PS + 4 * 32 * 4;
-  // Copies per copy wave and chunk: codes (16 B pieces), A rows (16 B),
-  // scales and biases (4 B), x group sums (16 B, 8 lanes).
+  // Copies per copy wave: codes (16 B pieces) per chunk, A rows (16 B) and
+  // x group sums (16 B, 8 lanes) per chunk, scales and biases (16 B) per
+  // chunk pair.
   static constexpr int N_BQ = ROWS * RB / 16 / NWD / 64;
-  static constexpr int N_A = 32 * KC * 2 / 16 / NWD / 64;
-  static constexpr int N_S = ROWS * 2 * CG * 2 / 4 / NWD / 64;
-  static constexpr int D = N_BQ + N_A + N_S + 1;
+  static constexpr int N_A = A_BYTES / 16 / NWD / 64;
+  static constexpr int N_S = S_SLOT / 16 / NWD / 64;
   static constexpr int EX = 8 * 16 * 64 * 4;  // K-half exchange: [cw][receiving half][16 values][lane] f32
-  static_assert(N_BQ * NWD * 64 * 16 == ROWS * RB && N_A * NWD * 64 * 16 == 32 * KC * 2, "equal copy shares");
-  static_assert(N_S * NWD * 64 * 4 == ROWS * 2 * CG * 2, "equal copy shares");
-  static_assert(EX <= STAGE, "exchange fits a stage");
+  static_assert(N_BQ * NWD * 64 * 16 == BQ_SLOT && N_A * NWD * 64 * 16 == A_BYTES, "equal copy shares");
+  static_assert(N_S * NWD * 64 * 16 == S_SLOT, "equal copy shares");
+  static_assert(N_BQ * 8 * NWD == ROWS && N_S * 32 * NWD == ROWS, "copy rows per wave");
+  static_assert(EX <= BQ_SLOT, "exchange fits a code slot");
   static_assert(LDS <= 160 * 1024, "LDS per CU");
-  static_assert(2 * D + 1 <= 63, "vmcnt range");
 };
 
 __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint32_t* __restrict__ items,
@@ -1489,22 +1496,31 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
   // lasts; the chunk adds a scalar offset). Copy wave d's code pieces are
   // rows 64 d + 8 i + l / 8 (gate rows for d < 2, up rows for d >= 2) at
   // 16-byte part (l % 8) ^ (l / 8 % 8), so copy i adds 8 i rows to one lane
-  // offset; its scale pieces are rows 64 d + 16 i + l / 4 likewise; its A
-  // rows are 8 d + 2 i + l / 32, one token row each.
-  struct Src {
+  // offset; its scale pieces are rows 64 d + 32 i + l / 2, array l % 2,
+  // likewise; its A rows are 8 d + 2 i + l / 32, one token row each.
+  struct SrcC {
     const uint8_t* blob;
-    uint32_t bq, s;        // from the blob, copy 0
+    uint32_t bq;  // from the blob, copy 0
+  };
+  struct SrcA {
+    const uint8_t* blob;
+    uint32_t s;            // from the blob, copy 0
     uint32_t ar[C::N_A];   // from x_hi (token row + part)
     uint32_t xs;           // from xsum
   };
-  static_assert(C::N_BQ * 8 * C::NWD == C::ROWS && C::N_S * 16 * C::NWD == C::ROWS, "copy rows per wave");
-  auto src_of = [=](const Unit& u, uint32_t par) {
-    Src r;
+  auto srcc_of = [=](const Unit& u) {
+    SrcC r;
+    r.blob = shared && u.e == e_shared ? shared : experts + (size_t)u.e * stride;
+    const uint32_t mat = dw >= 2, row0 = u.cb * C::NCOL + 64 * (dw & 1u);
+    r.bq = (uint32_t)(mat ? wo1 : wo0) + (row0 + lane / 8) * rowb + (((lane & 7u) ^ ((lane >> 3) & 7u)) * 16);
+    return r;
+  };
+  auto srca_of = [=](const Unit& u, uint32_t par) {
+    SrcA r;
     r.blob = shared && u.e == e_shared ? shared : experts + (size_t)u.e * stride;
     const uint32_t* tb = reinterpret_cast<const uint32_t*>(lds + C::OFF_TOK) + par * 32;
     const uint32_t mat = dw >= 2, row0 = u.cb * C::NCOL + 64 * (dw & 1u);
-    r.bq = (uint32_t)(mat ? wo1 : wo0) + (row0 + lane / 8) * rowb + (((lane & 7u) ^ ((lane >> 3) & 7u)) * 16);
-    r.s = (uint32_t)((mat ? so1 : so0) + ((lane >> 1) & 1u) * bso) + (row0 + lane / 4) * ng * 2 + (lane & 1u) * 4;
+    r.s = (uint32_t)((mat ? so1 : so0) + (lane & 1u) * bso) + (row0 + lane / 2) * ng * 2;
 #pragma unroll
     for (int i = 0; i < C::N_A; ++i) {
       const uint32_t row = 8 * dw + 2 * i + lane / 32, part = (lane % 32) ^ (row & 15u);
@@ -1513,21 +1529,29 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
     r.xs = min(tb[8 * dw + min(lane, 7u)], last_tok) * ng * 4;
     return r;
   };
-  // Every copy of chunk c of a unit into stage `slot`.
-  auto issue = [=](const Src& r, uint32_t c, uint32_t slot) {
-    uint8_t* st = lds + slot * C::STAGE;
+  // Chunk c's codes into code slot `slot`.
+  auto issue_codes = [=](const SrcC& r, uint32_t c, uint32_t slot) {
+    uint8_t* st = lds + C::OFF_BQ + slot * C::BQ_SLOT;
     const uint8_t* bq = r.blob + (size_t)c * C::RB;
 #pragma unroll
     for (int i = 0; i < C::N_BQ; ++i)
-      dma16(bq + (size_t)(8 * i) * rowb + pf_voff(r.bq), st + C::OFF_BQ + (dw * C::N_BQ + i) * 64 * 16);
+      dma16(bq + (size_t)(8 * i) * rowb + pf_voff(r.bq), st + (dw * C::N_BQ + i) * 64 * 16);
+  };
+  // Chunk c's token rows and x group sums into A slot `slot`; with `pair`,
+  // the scales and biases of chunks c and c + 1 into scale slot `sslot`.
+  auto issue_a = [=](const SrcA& r, uint32_t c, uint32_t slot, bool pair, uint32_t sslot) {
+    uint8_t* st = lds + C::OFF_A + slot * C::A_SLOT;
     const uint8_t* ab = xh + (size_t)c * C::KC * 2;
 #pragma unroll
-    for (int i = 0; i < C::N_A; ++i) dma16(ab + r.ar[i], st + C::OFF_A + (dw * C::N_A + i) * 64 * 16);
-    const uint8_t* sb = r.blob + (size_t)c * C::CG * 2;
+    for (int i = 0; i < C::N_A; ++i) dma16(ab + r.ar[i], st + (dw * C::N_A + i) * 64 * 16);
+    if (lane < 8) dma16(xsum + (size_t)c * C::CG * 4 + r.xs, st + C::A_BYTES + 8 * dw * 16);
+    if (pair) {
+      uint8_t* ss = lds + C::OFF_S + sslot * C::S_SLOT;
+      const uint8_t* sb = r.blob + (size_t)c * C::CG * 2;
 #pragma unroll
-    for (int i = 0; i < C::N_S; ++i)
-      dma4(sb + (size_t)(16 * i) * ng * 2 + pf_voff(r.s), st + C::OFF_S + (dw * C::N_S + i) * 64 * 4);
-    if (lane < 8) dma16(xsum + (size_t)c * C::CG * 4 + r.xs, st + C::OFF_XS + 8 * dw * 16);
+      for (int i = 0; i < C::N_S; ++i)
+        dma16(sb + (size_t)(32 * i) * ng * 2 + pf_voff(r.s), ss + (dw * C::N_S + i) * 64 * 16);
+    }
   };
 
   f32x16 tot[2];
@@ -1538,45 +1562,65 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  // Issue position (unit iu, chunk ic, token buffer ipar, stage islot)
-  // runs S - 1 chunks ahead of the compute position; the next unit's token
-  // ids are copied with a unit's first chunk.
-  uint32_t iu = 0, ic = 0, ipar = 0, islot = 0, issued = 0;
-  Src src{};
-  uint32_t cc = 0, cslot = 0, cu = 0;
+  // Issue positions: token rows and scales (unit au, chunk ac, token
+  // buffer apar) one chunk ahead of the compute position, codes (unit qu,
+  // chunk qc) two chunks ahead. The next unit's token ids are copied when
+  // the first issue position enters a unit.
+  uint32_t au = 0, ac = 0, apar = 0, aiss = 0;
+  uint32_t qu = 0, qc = 0, qiss = 0;
+  SrcA srca{};
+  SrcC srcc{};
+  uint32_t cc = 0, cu = 0;
   Unit ucur = unit(0);
   // Activation row sums of the last finished unit, written out by wave 0
   // after the next block barrier.
   bool ps_pend = false;
   uint32_t ps_start = 0, ps_cnt = 0, ps_cb = 0;
-  // Iterations -(S - 1) .. -1 only issue (the prologue); iteration j >= 0
-  // waits for chunk j, issues chunk j + S - 1 and computes chunk j.
-  for (int jj = 1 - C::S; jj < (int)total; ++jj) {
+  // Iterations -2 and -1 only issue (the prologue); iteration j >= 0 waits
+  // for chunk j (its codes, issued two iterations earlier, and its token
+  // rows, issued one earlier before the next chunk's codes: N_BQ copies
+  // follow them), issues chunk j + 1's token rows and chunk j + 2's codes,
+  // and computes chunk j.
+  for (int jj = -2; jj < (int)total; ++jj) {
     const uint32_t j = (uint32_t)jj;
     if (jj >= 0) {
       if (!copier)
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       else if (j + 1 < total)
-        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(C::D) : "memory");
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(C::N_BQ) : "memory");
       else
         asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
     }
-    if (issued < total) {
-      if (copier) {
-        if (ic == 0) {
-          src = src_of(unit(iu), ipar);
-          if (iu + 1 < my_units) token_dma(iu + 1, ipar ^ 1u);
+    if (copier) {
+      bool tok_next = false;
+      if (jj >= -1 && aiss < total) {
+        if (ac == 0) {
+          srca = srca_of(unit(au), apar);
+          tok_next = au + 1 < my_units;
         }
-        issue(src, ic, islot);
+        issue_a(srca, ac, aiss & 1u, (aiss & 1u) == 0, (aiss >> 1) & 1u);
       }
-      ++issued;
-      islot = islot + 1 == (uint32_t)C::S ? 0u : islot + 1;
-      if (++ic == nch) {
-        ic = 0;
-        ++iu;
-        ipar ^= 1u;
+      if (qiss < total) {
+        if (qc == 0) srcc = srcc_of(unit(qu));
+        issue_codes(srcc, qc, qiss % C::SC);
+      }
+      if (tok_next) token_dma(au + 1, apar ^ 1u);
+    }
+    if (jj >= -1 && aiss < total) {
+      ++aiss;
+      if (++ac == nch) {
+        ac = 0;
+        ++au;
+        apar ^= 1u;
+      }
+    }
+    if (qiss < total) {
+      ++qiss;
+      if (++qc == nch) {
+        qc = 0;
+        ++qu;
       }
     }
     if (jj < 0) continue;
@@ -1589,8 +1633,9 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
       }
       ps_pend = false;
     }
-    const uint8_t* st = lds + cslot * C::STAGE;
-    cslot = cslot + 1 == (uint32_t)C::S ? 0u : cslot + 1;
+    const uint8_t* st = lds + C::OFF_BQ + (j % C::SC) * C::BQ_SLOT;      // codes
+    const uint8_t* sa = lds + C::OFF_A + (j & 1u) * C::A_SLOT;            // token rows, x sums
+    const uint8_t* ss = lds + C::OFF_S + ((j >> 1) & 1u) * C::S_SLOT;     // scales, biases
     if (!copier) {
       // Scales and biases of this wave's two groups for both tiles: bf16
       // pairs (group 2 kh, 2 kh + 1).
@@ -1598,21 +1643,21 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const uint32_t row = t * C::NCOL + 32 * cw + c32;
-        const uint32_t* sp = reinterpret_cast<const uint32_t*>(st + C::OFF_S + row * 16 + 4 * kh);
+        const uint32_t* sp = reinterpret_cast<const uint32_t*>(ss + row * 32 + 8 * (j & 1u) + 4 * kh);
         sw[t] = sp[0];
-        bw[t] = sp[2];
+        bw[t] = sp[4];
       }
 #pragma unroll
       for (int gi = 0; gi < 2; ++gi) {
         const uint32_t g = 2 * kh + gi;
         u32x4 af[4], bq[2];
-        const uint8_t* ar = st + C::OFF_A + c32 * (C::KC * 2);
+        const uint8_t* ar = sa + c32 * (C::KC * 2);
 #pragma unroll
         for (int s = 0; s < 4; ++s) af[s] = *reinterpret_cast<const u32x4*>(ar + (((8 * g + 4 * kq + s) ^ (c32 & 15u)) * 16));
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
           const uint32_t row = t * C::NCOL + 32 * cw + c32;
-          bq[t] = *reinterpret_cast<const u32x4*>(st + C::OFF_BQ + row * C::RB + (((2 * g + kq) ^ (row & 7u)) * 16));
+          bq[t] = *reinterpret_cast<const u32x4*>(st + row * C::RB + (((2 * g + kq) ^ (row & 7u)) * 16));
         }
         f32x16 acc0 = f32x16{}, acc1 = f32x16{};
 #pragma unroll
@@ -1629,7 +1674,7 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
       }
       // Dequant term of the two groups: A = x group sums [32 rows x 2
       // groups], B = (b - 128 s) [2 groups x 32 columns].
-      const float xa = reinterpret_cast<const float*>(st + C::OFF_XS)[c32 * C::CG + 2 * kh + kq];
+      const float xa = reinterpret_cast<const float*>(sa + C::A_BYTES)[c32 * C::CG + 2 * kh + kq];
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const uint32_t sh = 16 * kq;
