@@ -1372,19 +1372,20 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
 // ---------------------------------------------------------------------------
 // Gate/up GEMM on 32 x 32 tiles (k_pf_gu64): 4-bit codes, group 64, bf16 x.
 //
-// The same staged pipeline as k_pf_mm (persistent block per CU, LDS ring of
-// three stages filled by LDS DMA two chunks ahead, one block barrier per
-// 256-input chunk, four copy-only waves beside eight compute waves, the
-// XCD-aware work list), with a wider unit: (item, 128 output columns) =
-// 256 weight rows. Its 32 token rows are copied once per chunk for all 256
-// rows, so they are a third of a chunk's copies instead of a half (16 KB
-// next to 32 KB of codes and 4 KB of scales). Compute wave (cw, kh) owns
+// The staged pipeline of k_pf_mm (persistent block per CU, LDS DMA rings,
+// one block barrier per 256-input chunk, four copy-only waves beside eight
+// compute waves, the XCD-aware work list), with a wider unit: (item, 128
+// output columns) = 256 weight rows. Its 32 token rows are copied once per
+// chunk for all 256 rows, so they are a third of a chunk's copies instead
+// of a half (16 KB next to 32 KB of codes and 4 KB of scales). The codes
+// ring runs two chunks ahead, the token rows (from L2) one, and scales
+// with biases go per chunk pair in 16-byte pieces (Gu64). Compute wave (cw, kh) owns
 // columns 32 cw .. 32 cw + 31 of both matrices (one v_mfma_f32_32x32x16_bf16
 // tile each, the 32 item rows by 32 columns, so SwiGLU pairs are in the same
 // lane) and the chunk's groups 2 kh, 2 kh + 1; each A fragment read feeds
 // both tiles. The dequant term (b - 128 s) * sum x of the wave's two groups
 // is exactly one v_mfma_f32_32x32x2_f32 per tile and chunk (K = 2 groups).
-// At a unit's end the K halves swap partial sums through the stage just
+// At a unit's end the K halves swap partial sums through the code slot just
 // read (each finishes 16 of the 32 rows), then SwiGLU, fp16 activations in
 // the down GEMM's order, and the activations' 64-column group sums.
 //
@@ -1686,8 +1687,8 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
       cc = 0;
       const uint32_t start = ucur.start, cnt = ucur.cnt, cb = ucur.cb;
       if (++cu < my_units) ucur = unit(cu);
-      // Every wave is done reading this stage; the K halves swap the rows
-      // the other one finishes (values 8 kh' .. 8 kh' + 7 of each tile).
+      // Every wave is done reading this code slot; the K halves swap the
+      // rows the other one finishes (values 8 kh' .. 8 kh' + 7 of each tile).
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
