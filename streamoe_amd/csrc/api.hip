@@ -227,7 +227,7 @@ int smoe_set_option(smoe_handle* h, int option, int64_t value) {
       h->trace = (uint64_t*)(uintptr_t)value;
       return SMOE_OK;
     case SMOE_OPT_PREFILL_GEMM:
-      if (value < 0 || value > 1) return SMOE_ERR_INVALID_ARG;
+      if (value < 0 || value > 2) return SMOE_ERR_INVALID_ARG;
       h->prefill_gemm = (int)value;
       return SMOE_OK;
     default:

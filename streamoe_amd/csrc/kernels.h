@@ -159,7 +159,7 @@ struct PfArgs {
   uint32_t* sn_items;
   uint32_t* sitem_tok;
   uint32_t* sxr;
-  int gemm_path;           // 0: the 32 x 32 gate/up tile where it applies, 1: k_pf_mm only
+  int gemm_path;           // 0: the 32 x 32 gate/up tile where it applies, 1: k_pf_mm only, 2: 32 x 32 gate/up and down tiles
 };
 
 // Workspace bytes for these sizes; with `a` and `base`, also points a's

@@ -1370,7 +1370,8 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
 }
 
 // ---------------------------------------------------------------------------
-// Gate/up GEMM on 32 x 32 tiles (k_pf_gu64): 4-bit codes, group 64, bf16 x.
+// Gate/up and down GEMMs on 32 x 32 tiles (k_pf_gu64): 4-bit codes, group
+// 64; gate/up over bf16 x, down over the fp16 activations.
 //
 // The staged pipeline of k_pf_mm (persistent block per CU, LDS DMA rings,
 // one block barrier per 256-input chunk, four copy-only waves beside eight
@@ -1393,12 +1394,25 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
 // (c, kq) reads the 16 bytes of row c at k half kq of group g (words 0-3 =
 // MFMA steps 0-3); the A fragment of step s is the 8-input block 8 g + 4 kq
 // + s of the item row, stored in the unpack order as for k_pf_mm.
+//
+// Down (DOWN = true): the same rings over one matrix, a unit = (item, 256
+// output columns) = 256 rows of the down matrix, A = the item's entry rows
+// of the fp16 activations (rows start .. start + cnt - 1, no token ids) with
+// their group sums. Tile t of wave (cw, kh) is columns 128 t + 32 cw ..
+// + 31; codes enter the fp16 MFMA as 1 + q / 64, so the scale is 64 s and
+// the dequant term (b - 64 s) * sum a. The unit's end stores the f32 sums
+// per entry (the combine reads them).
 // ---------------------------------------------------------------------------
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
                                                  0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 mfma32_f16(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                0, 0, 0);
 }
 
 struct Gu64 {
@@ -1436,6 +1450,7 @@ struct Gu64 {
   static_assert(LDS <= 160 * 1024, "LDS per CU");
 };
 
+template <bool DOWN>
 __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint32_t* __restrict__ items,
                                                              const uint32_t* __restrict__ n_items_p,
                                                              const uint32_t* __restrict__ xr) {
@@ -1446,9 +1461,10 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
   const uint32_t dw = copier ? wave - C::NWC : 0u;           // copy share
   const uint32_t cw = wave & 3, kh = (wave >> 2) & 1;        // compute waves: column block, K half
   const uint32_t c32 = lane & 31, kq = lane >> 5;
-  const uint32_t K = a.g.hidden, N = a.g.inter;
+  const uint32_t K = DOWN ? a.g.inter : a.g.hidden, N = DOWN ? a.g.hidden : a.g.inter;
   const uint32_t ng = K / C::G, nch = K / C::KC, rowb = K / 2;
-  const uint32_t ncb = N / C::NCOL;
+  constexpr uint32_t UCOL = DOWN ? C::ROWS : C::NCOL;  // output columns per unit
+  const uint32_t ncb = N / UCOL;
   const uint32_t nx = gridDim.x % 8 == 0 ? 8 : 1, per = gridDim.x / nx;
   const uint32_t xg = blockIdx.x % nx, lb = blockIdx.x / nx;
   const uint32_t n_items = *n_items_p;
@@ -1466,12 +1482,16 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
   const uint32_t* const item_tok = a.item_tok;
   const uint32_t last_tok = a.n_tokens - 1;
   const uint64_t stride = a.stride;
-  const uint8_t* const xh = reinterpret_cast<const uint8_t*>(a.x_hi);
-  const uint8_t* const xsum = reinterpret_cast<const uint8_t*>(a.xsum);
+  // A rows and their group sums: token rows of x, or entry rows of the
+  // activations.
+  const uint8_t* const xh = reinterpret_cast<const uint8_t*>(DOWN ? a.act_hi : a.x_hi);
+  const uint8_t* const xsum = reinterpret_cast<const uint8_t*>(DOWN ? a.asum : a.xsum);
   uint16_t* const act_out = a.act_hi;
   float* const asum_out = a.asum;
-  const uint64_t wo0 = a.g.w[0], wo1 = a.g.w[1], so0 = a.g.s[0], so1 = a.g.s[1];
-  const uint64_t bso = a.g.b[0] - so0;
+  float* const down_out = a.down;
+  const uint64_t wo0 = a.g.w[DOWN ? 2 : 0], wo1 = a.g.w[DOWN ? 2 : 1];
+  const uint64_t so0 = a.g.s[DOWN ? 2 : 0], so1 = a.g.s[DOWN ? 2 : 1];
+  const uint64_t bso = a.g.b[DOWN ? 2 : 0] - so0;
   const uint32_t c43 = 0x43434343u;
 
   struct Unit {
@@ -1491,14 +1511,14 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
   // Token ids of unit i into token buffer `par`: copy wave d, lanes 0-7,
   // rows 8 d .. 8 d + 7.
   auto token_dma = [=](uint32_t i, uint32_t par) {
-    if (lane < 8) dma4(item_tok + (size_t)unit(i).item * kPfMC + 8 * dw + lane, lds + C::OFF_TOK + (par * 32 + 8 * dw) * 4);
+    if (!DOWN && lane < 8) dma4(item_tok + (size_t)unit(i).item * kPfMC + 8 * dw + lane, lds + C::OFF_TOK + (par * 32 + 8 * dw) * 4);
   };
   // Per-lane source offsets of one unit's copies (fixed while the unit
   // lasts; the chunk adds a scalar offset). Copy wave d's code pieces are
-  // rows 64 d + 8 i + l / 8 (gate rows for d < 2, up rows for d >= 2) at
-  // 16-byte part (l % 8) ^ (l / 8 % 8), so copy i adds 8 i rows to one lane
-  // offset; its scale pieces are rows 64 d + 32 i + l / 2, array l % 2,
-  // likewise; its A rows are 8 d + 2 i + l / 32, one token row each.
+  // rows 64 d + 8 i + l / 8 (gate/up: gate rows for d < 2, up rows for d >=
+  // 2) at 16-byte part (l % 8) ^ (l / 8 % 8), so copy i adds 8 i rows to one
+  // lane offset; its scale pieces are rows 64 d + 32 i + l / 2, array l % 2,
+  // likewise; its A rows are 8 d + 2 i + l / 32, one token (entry) row each.
   struct SrcC {
     const uint8_t* blob;
     uint32_t bq;  // from the blob, copy 0
@@ -1512,22 +1532,35 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
   auto srcc_of = [=](const Unit& u) {
     SrcC r;
     r.blob = shared && u.e == e_shared ? shared : experts + (size_t)u.e * stride;
-    const uint32_t mat = dw >= 2, row0 = u.cb * C::NCOL + 64 * (dw & 1u);
+    const uint32_t mat = DOWN ? 0u : dw >= 2;
+    const uint32_t row0 = DOWN ? u.cb * C::ROWS + 64 * dw : u.cb * C::NCOL + 64 * (dw & 1u);
     r.bq = (uint32_t)(mat ? wo1 : wo0) + (row0 + lane / 8) * rowb + (((lane & 7u) ^ ((lane >> 3) & 7u)) * 16);
     return r;
   };
   auto srca_of = [=](const Unit& u, uint32_t par) {
     SrcA r;
     r.blob = shared && u.e == e_shared ? shared : experts + (size_t)u.e * stride;
-    const uint32_t* tb = reinterpret_cast<const uint32_t*>(lds + C::OFF_TOK) + par * 32;
-    const uint32_t mat = dw >= 2, row0 = u.cb * C::NCOL + 64 * (dw & 1u);
+    const uint32_t mat = DOWN ? 0u : dw >= 2;
+    const uint32_t row0 = DOWN ? u.cb * C::ROWS + 64 * dw : u.cb * C::NCOL + 64 * (dw & 1u);
     r.s = (uint32_t)((mat ? so1 : so0) + (lane & 1u) * bso) + (row0 + lane / 2) * ng * 2;
+    if constexpr (DOWN) {
+      // Entry rows past the item's count repeat its last row.
+      const uint32_t last = u.cnt - 1;
 #pragma unroll
-    for (int i = 0; i < C::N_A; ++i) {
-      const uint32_t row = 8 * dw + 2 * i + lane / 32, part = (lane % 32) ^ (row & 15u);
-      r.ar[i] = min(tb[row], last_tok) * K * 2 + part * 16;
+      for (int i = 0; i < C::N_A; ++i) {
+        const uint32_t row = 8 * dw + 2 * i + lane / 32, part = (lane % 32) ^ (row & 15u);
+        r.ar[i] = (u.start + min(row, last)) * K * 2 + part * 16;
+      }
+      r.xs = (u.start + min(8 * dw + min(lane, 7u), last)) * ng * 4;
+    } else {
+      const uint32_t* tb = reinterpret_cast<const uint32_t*>(lds + C::OFF_TOK) + par * 32;
+#pragma unroll
+      for (int i = 0; i < C::N_A; ++i) {
+        const uint32_t row = 8 * dw + 2 * i + lane / 32, part = (lane % 32) ^ (row & 15u);
+        r.ar[i] = min(tb[row], last_tok) * K * 2 + part * 16;
+      }
+      r.xs = min(tb[8 * dw + min(lane, 7u)], last_tok) * ng * 4;
     }
-    r.xs = min(tb[8 * dw + min(lane, 7u)], last_tok) * ng * 4;
     return r;
   };
   // Chunk c's codes into code slot `slot`.
@@ -1559,7 +1592,7 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
   tot[0] = f32x16{};
   tot[1] = f32x16{};
   // The first unit's token ids, visible to every wave before its copies.
-  if (copier) token_dma(0, 0);
+  if (!DOWN && copier) token_dma(0, 0);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
@@ -1599,7 +1632,7 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
       if (jj >= -1 && aiss < total) {
         if (ac == 0) {
           srca = srca_of(unit(au), apar);
-          tok_next = au + 1 < my_units;
+          tok_next = !DOWN && au + 1 < my_units;
         }
         issue_a(srca, ac, aiss & 1u, (aiss & 1u) == 0, (aiss >> 1) & 1u);
       }
@@ -1663,23 +1696,29 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
         f32x16 acc0 = f32x16{}, acc1 = f32x16{};
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-          acc0 = mfma32(af[s], codes_bf16_4p(bq[0][s], c43), acc0);
-          acc1 = mfma32(af[s], codes_bf16_4p(bq[1][s], c43), acc1);
+          if constexpr (DOWN) {
+            acc0 = mfma32_f16(af[s], codes_f16_4p(bq[0][s]), acc0);
+            acc1 = mfma32_f16(af[s], codes_f16_4p(bq[1][s]), acc1);
+          } else {
+            acc0 = mfma32(af[s], codes_bf16_4p(bq[0][s], c43), acc0);
+            acc1 = mfma32(af[s], codes_bf16_4p(bq[1][s], c43), acc1);
+          }
         }
-        const float s0 = bf16f((uint16_t)(sw[0] >> (16 * gi))), s1 = bf16f((uint16_t)(sw[1] >> (16 * gi)));
+        constexpr float SQ = DOWN ? 64.0f : 1.0f;  // code scale of the MFMA form
+        const float s0 = SQ * bf16f((uint16_t)(sw[0] >> (16 * gi))), s1 = SQ * bf16f((uint16_t)(sw[1] >> (16 * gi)));
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           tot[0][v] = __builtin_fmaf(s0, acc0[v], tot[0][v]);
           tot[1][v] = __builtin_fmaf(s1, acc1[v], tot[1][v]);
         }
       }
-      // Dequant term of the two groups: A = x group sums [32 rows x 2
-      // groups], B = (b - 128 s) [2 groups x 32 columns].
+      // Dequant term of the two groups: A = the A rows' group sums [32 rows
+      // x 2 groups], B = (b - 128 s), down (b - 64 s) [2 groups x 32 columns].
       const float xa = reinterpret_cast<const float*>(sa + C::A_BYTES)[c32 * C::CG + 2 * kh + kq];
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const uint32_t sh = 16 * kq;
-        const float cb = __builtin_fmaf(-128.0f, bf16f((uint16_t)(sw[t] >> sh)), bf16f((uint16_t)(bw[t] >> sh)));
+        const float cb = __builtin_fmaf(DOWN ? -64.0f : -128.0f, bf16f((uint16_t)(sw[t] >> sh)), bf16f((uint16_t)(bw[t] >> sh)));
         tot[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa, cb, tot[t], 0, 0, 0);
       }
     }
@@ -1704,7 +1743,21 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
-      if (!copier) {
+      if (DOWN && !copier) {
+        const float* xi = ex + (cw * 2 + kh) * 16 * 64 + lane;
+        const uint32_t vm = 8 * kh;
+        const uint32_t col = cb * C::ROWS + 32 * cw + c32;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t v = vm + i;
+          const uint32_t m = 8 * (v / 4) + 4 * kq + (v % 4);
+          if (m < cnt) {
+            float* o = down_out + (size_t)(start + m) * N + col;
+            o[0] = tot[0][v] + xi[i * 64];
+            o[C::NCOL] = tot[1][v] + xi[(8 + i) * 64];
+          }
+        }
+      } else if (!copier) {
         const float* xi = ex + (cw * 2 + kh) * 16 * 64 + lane;
         const uint32_t vm = 8 * kh;
         const uint32_t col = cb * C::NCOL + 32 * cw + c32;
@@ -1734,7 +1787,7 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
           }
         }
       }
-      ps_pend = true;
+      ps_pend = !DOWN;
       ps_start = start;
       ps_cnt = cnt;
       ps_cb = cb;
@@ -1929,13 +1982,14 @@ static hipError_t launch_mm(const PfArgs& a, uint32_t n_units_max, uint32_t n_cu
 // group 64); other shapes copy scales per chunk.
 // act_rows: the entry rows [row0, row0 + n_rows) whose activation group
 // sums the G > 64 pass computes.
+template <bool DOWN>
 static hipError_t launch_gu64(const PfArgs& a, uint32_t n_units_max, uint32_t n_cu, hipStream_t st) {
-  const auto fn = reinterpret_cast<const void*>(&k_pf_gu64);
+  const auto fn = reinterpret_cast<const void*>(&k_pf_gu64<DOWN>);
   static std::atomic<uint64_t> raised{0};
   const hipError_t e = raise_lds_limit(fn, Gu64::LDS, raised);
   if (e != hipSuccess) return e;
   const uint32_t grid = n_units_max < n_cu ? n_units_max : n_cu;
-  hipLaunchKernelGGL(k_pf_gu64, dim3(grid), dim3(64 * Gu64::NWT), (size_t)Gu64::LDS, st, a, (const uint32_t*)a.items,
+  hipLaunchKernelGGL(k_pf_gu64<DOWN>, dim3(grid), dim3(64 * Gu64::NWT), (size_t)Gu64::LDS, st, a, (const uint32_t*)a.items,
                      (const uint32_t*)a.n_items, (const uint32_t*)a.xr);
   return hipGetLastError();
 }
@@ -1944,8 +1998,12 @@ template <int BITS, int G>
 static hipError_t launch_gemms(const PfArgs& a, uint32_t row0, uint32_t n_rows, uint32_t n_cu, hipStream_t st) {
   const uint32_t gu_units = a.max_items * (a.g.inter / 64);
   hipError_t e;
-  if (BITS == 4 && G == 64 && a.x_bf16 && a.gemm_path == 0 && a.g.inter % Gu64::NCOL == 0)
-    e = launch_gu64(a, a.max_items * (a.g.inter / Gu64::NCOL), n_cu, st);
+  // The 32 x 32 tiles take the chunks of a unit in pairs (their scales
+  // come per pair): K a multiple of 512. Gate/up on them by default, down
+  // on them with gemm_path 2.
+  const bool tiles32 = BITS == 4 && G == 64 && a.gemm_path != 1;
+  if (tiles32 && a.x_bf16 && a.g.inter % Gu64::NCOL == 0 && a.g.hidden % (2 * Gu64::KC) == 0)
+    e = launch_gu64<false>(a, a.max_items * (a.g.inter / Gu64::NCOL), n_cu, st);
   else if (!a.x_bf16)
     e = launch_mm<BITS, G, 0, true, 0>(a, gu_units, n_cu, st);
   else if ((G == 64 || G == 128) && a.g.hidden == 2048)
@@ -1956,6 +2014,8 @@ static hipError_t launch_gemms(const PfArgs& a, uint32_t row0, uint32_t n_rows, 
   // With G <= 64 the gate/up GEMM writes the activation group sums itself.
   if (G > 64) hipLaunchKernelGGL(k_pf_act_sum, dim3(n_rows), dim3(256), 0, st, a, row0);
   const uint32_t dn_units = a.max_items * (a.g.hidden / 256);
+  if (tiles32 && a.gemm_path == 2 && a.g.hidden % Gu64::ROWS == 0 && a.g.inter % (2 * Gu64::KC) == 0)
+    return launch_gu64<true>(a, a.max_items * (a.g.hidden / Gu64::ROWS), n_cu, st);
   if (G == 64 && a.g.inter == 512) return launch_mm<BITS, G, 2, false, G == 64 ? 512 : 0>(a, dn_units, n_cu, st);
   return launch_mm<BITS, G, 2, false, 0>(a, dn_units, n_cu, st);
 }

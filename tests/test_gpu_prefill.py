@@ -103,33 +103,41 @@ def test_prefill_matches_oracle(kernels, name, n, H, I, E, k, bits, group, x_bf1
     ("hot-expert", 200, 2048, 512, 64, 8, "hot"),
     ("olmoe-inter1024", 64, 2048, 1024, 64, 8, "zipf"),
     ("h1024-k4", 40, 1024, 512, 32, 4, "zipf"),
+    ("inter768", 48, 2048, 768, 32, 8, "zipf"),  # down on 16 x 16 tiles under every option
 ])
 def test_prefill_gate_up_tiles_agree(kernels, name, n, H, I, E, k, routing):
-    """The 32 x 32 gate/up tile (default for 4-bit group-64 experts over
-    bf16 x) and the 16 x 16 one (SMOE_OPT_PREFILL_GEMM = 1) both meet the
-    oracle bar and agree with each other to fp32 rounding-order
-    differences (and the fp16 rounding of the activations they feed)."""
+    """The GEMM tile choices of SMOE_OPT_PREFILL_GEMM on the same inputs:
+    0 (gate/up on 32 x 32 tiles, the default for 4-bit group-64 experts
+    over bf16 x), 1 (16 x 16 tiles only) and 2 (gate/up and down on 32 x 32
+    tiles) each meet the oracle bar and agree with each other to fp32
+    rounding-order differences (and the fp16 rounding of the activations
+    they feed)."""
     seed = sum(map(ord, name)) + 3
-    got_a, want, _ = _case(kernels, n, H, I, E, k, 4, 64, True, seed=seed, routing=routing)
-    kernels.set_prefill_gemm(1)
+    got = {}
     try:
-        got_b, want_b, _ = _case(kernels, n, H, I, E, k, 4, 64, True, seed=seed, routing=routing)
+        for path in (0, 1, 2):
+            kernels.set_prefill_gemm(path)
+            got[path], want_p, _ = _case(kernels, n, H, I, E, k, 4, 64, True, seed=seed, routing=routing)
+            if path == 0:
+                want = want_p
+            assert np.array_equal(want, want_p)
     finally:
         kernels.set_prefill_gemm(0)
-    assert np.array_equal(want, want_b)
-    e_a, e_b, e_ab = rel_err(got_a, want), rel_err(got_b, want), rel_err(got_a, got_b)
-    print(f"prefill {name}: 32x32 {e_a:.3e} 16x16 {e_b:.3e} between {e_ab:.3e}")
-    assert e_a <= TOL and e_b <= TOL
-    assert e_ab <= 2e-4
+    errs = {p: rel_err(g, want) for p, g in got.items()}
+    between = {p: rel_err(got[p], got[0]) for p in (1, 2)}
+    print(f"prefill {name}: vs oracle {errs}, vs path 0 {between}")
+    assert all(e <= TOL for e in errs.values())
+    assert all(e <= 2e-4 for e in between.values())
 
 
 def test_prefill_gemm_option_values(kernels):
     import streamoe_amd as sa
 
-    with pytest.raises(sa.SmoeError):
-        kernels.set_prefill_gemm(2)
-    kernels.set_prefill_gemm(1)
-    kernels.set_prefill_gemm(0)
+    for bad in (3, -1):
+        with pytest.raises(sa.SmoeError):
+            kernels.set_prefill_gemm(bad)
+    for ok in (2, 1, 0):
+        kernels.set_prefill_gemm(ok)
 
 
 def test_prefill_is_deterministic(kernels):

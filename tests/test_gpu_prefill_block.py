@@ -108,6 +108,26 @@ def test_prefill_block_matches_oracle(kernels, name, n, H, I, E, k, bits, group,
     assert err <= TOL and moe_err <= TOL
 
 
+DOWN_TILE_CASES = ["c4-a3b-shared", "c4-a3b-3bit-shared", "f32-x", "max-n1024-k16", "h4096"]
+
+
+@pytest.mark.parametrize("name", DOWN_TILE_CASES)
+def test_prefill_block_down_tile_option(kernels, name):
+    """SMOE_OPT_PREFILL_GEMM = 2 (the down GEMM on 32 x 32 tiles too, for
+    the 4-bit group-64 experts: routed, or the 4-bit shared expert's own
+    list beside 3-bit routed ones) meets the same bar as the default."""
+    c = next(c for c in CASES if c[0] == name)
+    kernels.set_prefill_gemm(2)
+    try:
+        got, want, h, _ = _block(kernels, *c[1:9], sum(map(ord, name)), *c[9:])
+    finally:
+        kernels.set_prefill_gemm(0)
+    err, moe_err = rel_err(got, want), rel_err(got - h, want - h)
+    print(f"prefill block {name} (32 x 32 down): rel_err={err:.3e} MoE part {moe_err:.3e}")
+    assert np.all(np.isfinite(got))
+    assert err <= TOL and moe_err <= TOL
+
+
 def test_prefill_block_in_place_and_deterministic(kernels):
     """hidden_out may alias h_mid; two runs give the same bits."""
     got, want, h, st = _block(kernels, 128, 2048, 512, 64, 8, 4, 64, True, 21, in_place=True)
