@@ -45,6 +45,7 @@ def _declare(L):
         "orc_expert_offsets": (None, [_U32, _U32, _U32, _U32, _U32, _P]),
         "orc_dequant_4bit": (None, [_P, _P, _P, _U32, _U32, _U32, _P]),
         "orc_dequant_matvec_4bit_gs": (C.c_int, [_P, _P, _P, _U32, _U32, _U32, _P, _P, C.c_int]),
+        "orc_dequant_matvec_8bit_gs": (C.c_int, [_P, _P, _P, _U32, _U32, _U32, _P, _P, C.c_int]),
         "orc_lm_head": (C.c_int, [_P, _P, _P, _U32, _U32, _U32, _P, _P]),
         "orc_f32_matvec": (None, [_P, _U32, _U32, _P, _P]),
         "orc_argmax": (_U32, [_P, _U32]),
@@ -96,6 +97,8 @@ class OrcLayer(C.Structure):
         ("hidden", _U32), ("inter", _U32), ("n_experts", _U32), ("k", _U32), ("group", _U32),
         ("bits", _U32), ("normalize", C.c_int), ("experts", _P), ("stride", C.c_uint64),
         ("router_w", _P), ("shared_blob", _P), ("shared_inter", _U32), ("shared_gate_w", _P),
+        ("router_q8", _P), ("router_s8", _P), ("router_b8", _P), ("gate_q8", _P), ("gate_s8", _P),
+        ("gate_b8", _P), ("group8", _U32),
     ]
 
 
@@ -134,6 +137,17 @@ def dequant_matvec_4bit_gs(packed, scales, biases, in_dim, out_dim, group, x, nt
     x = _c(x, np.float32)
     out = np.empty(out_dim, np.float32)
     rc = lib().orc_dequant_matvec_4bit_gs(_p(packed), _p(scales), _p(biases), in_dim, out_dim,
+                                          group, _p(x), _p(out), nthreads)
+    return rc, out
+
+
+def dequant_matvec_8bit_gs(packed, scales, biases, in_dim, out_dim, group, x, nthreads=0):
+    """packed: bytes [out_dim, in_dim] (or their u32 words, byte n of word i =
+    input 4i + n); scales / biases: bf16 [out_dim, in_dim / group]."""
+    packed, scales, biases = _words(packed), _c(scales, np.uint16), _c(biases, np.uint16)
+    x = _c(x, np.float32)
+    out = np.empty(out_dim, np.float32)
+    rc = lib().orc_dequant_matvec_8bit_gs(_p(packed), _p(scales), _p(biases), in_dim, out_dim,
                                           group, _p(x), _p(out), nthreads)
     return rc, out
 
@@ -249,15 +263,33 @@ def combine(expert_out, weights, h_mid, shared_out=None, shared_gate_score=float
 
 
 def moe_decode_layer(experts, stride, hidden, inter, n_experts, k, group, bits, normalize, router_w,
-                     x, h_mid, shared_blob=None, shared_gate_w=None, nthreads=0):
-    """One decode layer on the CPU; returns (hidden_out, idx, w, logits)."""
+                     x, h_mid, shared_blob=None, shared_gate_w=None, nthreads=0, router_q8=None,
+                     gate_q8=None):
+    """One decode layer on the CPU; returns (hidden_out, idx, w, logits).
+    router_q8 / gate_q8: an 8-bit affine router [n_experts, hidden] / shared
+    gate [1, hidden] as (codes uint8, scales bf16, biases bf16, group),
+    used instead of router_w / shared_gate_w."""
     experts = _c(experts, np.uint8)
-    router_w, x, h_mid = _c(router_w, np.float32), _c(x, np.float32), _c(h_mid, np.float32)
+    x, h_mid = _c(x, np.float32), _c(h_mid, np.float32)
+    router_w = None if router_w is None else _c(router_w, np.float32)
     sb = None if shared_blob is None else _c(shared_blob, np.uint8)
     sg = None if shared_gate_w is None else _c(shared_gate_w, np.float32)
+    keep = []
+
+    def q8(t):
+        if t is None:
+            return None, None, None, 0
+        q, s, b, g = _c(t[0], np.uint8), _c(t[1], np.uint16), _c(t[2], np.uint16), int(t[3])
+        keep.extend((q, s, b))
+        return q.ctypes.data, s.ctypes.data, b.ctypes.data, g
+    rq, rs, rb, rg = q8(router_q8)
+    gq, gs_, gb, gg = q8(gate_q8)
+    assert router_w is not None or rq is not None
+    assert not (rg and gg) or rg == gg
     L = OrcLayer(hidden, inter, n_experts, k, group, bits, int(normalize), experts.ctypes.data,
-                 stride, router_w.ctypes.data, None if sb is None else sb.ctypes.data, inter,
-                 None if sg is None else sg.ctypes.data)
+                 stride, None if router_w is None else router_w.ctypes.data,
+                 None if sb is None else sb.ctypes.data, inter, None if sg is None else sg.ctypes.data,
+                 rq, rs, rb, gq, gs_, gb, rg or gg)
     out = np.empty(hidden, np.float32)
     idx, w = np.empty(k, np.int32), np.empty(k, np.float32)
     logits = np.empty(n_experts, np.float32)

@@ -216,6 +216,48 @@ int orc_dequant_matvec_4bit_gs(const uint32_t* packed, const uint16_t* scales,
 }
 
 /* ------------------------------------------------------------------ */
+/* dequant_matvec_8bit_gs_cpu: cpu_matvec.rs:205-283.                   */
+/* Per row: acc = fma(fma(q, s, b), x, acc), input order, group by     */
+/* group, word by word, byte by byte (byte n of word i = input 4i + n). */
+/* ------------------------------------------------------------------ */
+static void mv8_rows(void* p, uint32_t r0, uint32_t r1) {
+  const mv4_ctx* c = (const mv4_ctx*)p;
+  uint32_t in_packed = c->in_dim / 4, in_groups = c->in_dim / c->group;
+  uint32_t ppg = c->group / 4;
+  for (uint32_t r = r0; r < r1; ++r) {
+    const uint32_t* prow = c->packed + (size_t)r * in_packed;
+    const uint16_t* srow = c->scales + (size_t)r * in_groups;
+    const uint16_t* brow = c->biases + (size_t)r * in_groups;
+    float acc = 0.0f;
+    for (uint32_t g = 0; g < in_groups; ++g) {
+      float scale = orc_bf16_to_f32(srow[g]);
+      float bias = orc_bf16_to_f32(brow[g]);
+      const uint32_t* gp = prow + (size_t)g * ppg;
+      const float* xg = c->x + (size_t)g * c->group;
+      for (uint32_t pp = 0; pp < ppg; ++pp) {
+        uint32_t word = gp[pp];
+        const float* xc = xg + pp * 4;
+        for (uint32_t n = 0; n < 4; ++n) {
+          float byte = (float)((word >> (n * 8)) & 0xFFu);
+          float w = fmaf(byte, scale, bias);
+          acc = fmaf(w, xc[n], acc);
+        }
+      }
+    }
+    c->out[r] = acc;
+  }
+}
+
+int orc_dequant_matvec_8bit_gs(const uint32_t* packed, const uint16_t* scales,
+                               const uint16_t* biases, uint32_t in_dim, uint32_t out_dim,
+                               uint32_t group, const float* x, float* out, int nthreads) {
+  if (group == 0 || group % 4 != 0 || in_dim % group != 0) return ORC_ERR_IN_DIM_NOT_MULTIPLE;
+  mv4_ctx c = {packed, scales, biases, in_dim, group, x, out};
+  parallel_rows(mv8_rows, &c, out_dim, nthreads);
+  return ORC_OK;
+}
+
+/* ------------------------------------------------------------------ */
 /* lm_head_cpu: lm_head.rs:66-122 — the same arithmetic and order as   */
 /* cpu_matvec.rs:150-171, single-threaded over rows.                   */
 /* ------------------------------------------------------------------ */
@@ -583,18 +625,29 @@ void orc_moe_combine_residual_n_tokens(const float* h_mid, const float* moe_sum,
 /* ------------------------------------------------------------------ */
 /* One decode layer, the per-token path (attn/linear_attn_forward.rs:  */
 /* 2123-2170 then moe_dispatch_per_token) restated on the CPU — router */
-/* logits (f32 matvec), moe_router_cpu_with, the routed                 */
+/* logits (f32 matvec, or the 8-bit affine matvec of cpu_matvec.rs:    */
+/* 205-283 for an 8-bit router), moe_router_cpu_with, the routed        */
 /* experts (run_packed_expert_swiglu per slot), the shared expert and   */
-/* its sigmoid gate (mlp_cpu.rs:78-117; gate logit = f32 dot), then     */
-/* cpu_combine.                                                         */
+/* its sigmoid gate (mlp_cpu.rs:78-117; gate logit = f32 dot or the     */
+/* 8-bit matvec), then cpu_combine.                                     */
 /* ------------------------------------------------------------------ */
 int orc_moe_decode_layer(const orc_layer* L, const float* x, const float* h_mid,
                          float* hidden_out, int32_t* idx_out, float* w_out, float* logits_out,
                          int nthreads) {
   if (L->k == 0 || L->k > L->n_experts || L->k > 16) return ORC_ERR_BAD_K;
   uint32_t H = L->hidden;
+  int rc0;
   float* scores = (float*)malloc(sizeof(float) * L->n_experts);
-  orc_f32_matvec_mt(L->router_w, H, L->n_experts, x, scores, nthreads);
+  if (L->router_q8) {
+    rc0 = orc_dequant_matvec_8bit_gs((const uint32_t*)L->router_q8, L->router_s8, L->router_b8, H,
+                                     L->n_experts, L->group8, x, scores, nthreads);
+    if (rc0) {
+      free(scores);
+      return rc0;
+    }
+  } else {
+    orc_f32_matvec_mt(L->router_w, H, L->n_experts, x, scores, nthreads);
+  }
   if (logits_out) memcpy(logits_out, scores, sizeof(float) * L->n_experts);
   int rc = orc_router(scores, L->n_experts, L->k, L->normalize, idx_out, w_out);
   free(scores);
@@ -614,7 +667,11 @@ int orc_moe_decode_layer(const orc_layer* L, const float* x, const float* h_mid,
   if (L->shared_blob) {
     shared = (float*)malloc(sizeof(float) * H);
     orc_expert_swiglu(L->shared_blob, 4, H, L->shared_inter, L->group, x, shared, nthreads);
-    if (L->shared_gate_w) orc_f32_matvec(L->shared_gate_w, H, 1, x, &score);
+    if (L->gate_q8)
+      orc_dequant_matvec_8bit_gs((const uint32_t*)L->gate_q8, L->gate_s8, L->gate_b8, H, 1, L->group8, x,
+                                 &score, 1);
+    else if (L->shared_gate_w)
+      orc_f32_matvec(L->shared_gate_w, H, 1, x, &score);
   }
   orc_combine(outs, w_out, L->k, h_mid, shared, score, H, hidden_out);
   free(outs);

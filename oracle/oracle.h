@@ -61,6 +61,11 @@ int orc_dequant_matvec_4bit_gs(const uint32_t* packed, const uint16_t* scales,
                                uint32_t group, const float* x, float* out, int nthreads);
 int orc_lm_head(const uint32_t* packed, const uint16_t* scales, const uint16_t* biases,
                 uint32_t hidden, uint32_t vocab, uint32_t group, const float* x, float* out);
+/* dequant_matvec_8bit_gs_cpu (cpu_matvec.rs:205-283): one byte per input,
+ * byte n of u32 word i = input 4i + n; group a multiple of 4. */
+int orc_dequant_matvec_8bit_gs(const uint32_t* packed, const uint16_t* scales,
+                               const uint16_t* biases, uint32_t in_dim, uint32_t out_dim,
+                               uint32_t group, const float* x, float* out, int nthreads);
 void orc_f32_matvec(const float* w, uint32_t in_dim, uint32_t out_dim, const float* x, float* out);
 void orc_f32_matvec_mt(const float* w, uint32_t in_dim, uint32_t out_dim, const float* x, float* out,
                        int nthreads);
@@ -102,6 +107,18 @@ typedef struct {
   const uint8_t* shared_blob;    /* 4-bit expert blob of inter_shared, or NULL */
   uint32_t shared_inter;
   const float* shared_gate_w;    /* [hidden] f32, or NULL = unscaled shared add */
+  /* 8-bit affine router and shared gate (the A3B mlp.gate.weight and
+   * mlp.shared_expert_gate.weight, linear_attn_forward.rs:1300-1301),
+   * used instead of router_w / shared_gate_w when router_q8 / gate_q8 is
+   * set: codes [rows, hidden] bytes, bf16 scales and biases [rows,
+   * hidden / group8]. */
+  const uint8_t* router_q8;
+  const uint16_t* router_s8;
+  const uint16_t* router_b8;
+  const uint8_t* gate_q8;
+  const uint16_t* gate_s8;
+  const uint16_t* gate_b8;
+  uint32_t group8;
 } orc_layer;
 
 int orc_moe_decode_layer(const orc_layer* L, const float* x, const float* h_mid,

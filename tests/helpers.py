@@ -16,6 +16,8 @@ def gen_quant_matrix(rng, out_dim, in_dim, group=64, bits=4, ssig=0.02, bsig=0.0
     if bits == 4:
         codes = rng.integers(0, 2**32, size=(out_dim, in_dim // 8), dtype=np.uint64).astype(np.uint32)
         codes = codes.view(np.uint8).reshape(out_dim, in_dim // 2)
+    elif bits == 8:
+        codes = rng.integers(0, 256, size=(out_dim, in_dim), dtype=np.uint8)
     else:
         codes = rng.integers(0, 256, size=(out_dim, in_dim * 3 // 8), dtype=np.uint8)
     scales = bf16(np.abs(rng.standard_normal((out_dim, n_groups))) * ssig)
