@@ -94,15 +94,55 @@ def stream_read_peak(dev, gib=4):
     return round(best, 1)
 
 
-def layer_bytes(c, tokens=1):
+def layer_bytes(c, tokens=1, router_bits=32):
     """Algorithmic bytes of one layer for `tokens` tokens decoded together:
     the router and the shared expert once, each token's k routed experts
-    (counted as distinct)."""
+    (counted as distinct). An 8-bit router: its codes plus bf16 scales and
+    biases per 64 inputs."""
     import streamoe_amd as sa
 
     routed = sa.ExpertLayout(c["H"], c["I"], c["bits"], 64).expert_size
     shared = sa.ExpertLayout(c["H"], c["I"], 4, 64).expert_size if c["shared"] else 0
-    return tokens * c["k"] * routed + shared + c["E"] * c["H"] * 4
+    router = c["E"] * c["H"] * 4 if router_bits == 32 else c["E"] * c["H"] + c["E"] * (c["H"] // 64) * 4
+    return tokens * c["k"] * routed + shared + router
+
+
+def q8_rows(rows, hidden, seed):
+    """A seeded 8-bit affine matrix [rows, hidden], group 64, with router-like
+    weights (codes uniform, scales |N(0, 2e-4)|, biases N(0, 0.02), both bf16
+    rounded): host (codes, scales, biases, 64) and its device QuantWeights
+    ([codes | scales | biases], 256-byte aligned regions)."""
+    import numpy as np
+    import torch
+
+    import streamoe_amd as sa
+
+    rng = np.random.default_rng(seed)
+    g = hidden // 64
+    q = rng.integers(0, 256, (rows, hidden), dtype=np.uint8)
+
+    def bf16(x):
+        b = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
+        return ((b + (((b >> 16) & 1) + 0x7FFF)) >> 16).astype(np.uint16)
+    s = bf16(np.abs(rng.standard_normal((rows, g))) * 2e-4)
+    b = bf16(rng.standard_normal((rows, g)) * 0.02)
+    pad = lambda n: (n + 255) // 256 * 256  # noqa: E731
+    so, bo = pad(q.size), pad(q.size) + pad(s.nbytes)
+    buf = np.zeros(bo + pad(b.nbytes), np.uint8)
+    buf[:q.size] = q.ravel()
+    buf[so:so + s.nbytes] = s.ravel().view(np.uint8)
+    buf[bo:bo + b.nbytes] = b.ravel().view(np.uint8)
+    dev = torch.from_numpy(buf).cuda()
+    return (q, s, b, 64), sa.QuantWeights(dev, 0, so, bo, 64, 8)
+
+
+def router_logits(oracle, r, x):
+    """Oracle router logits for an f32 router tensor or an 8-bit host tuple."""
+    if isinstance(r, tuple):
+        rc, y = oracle.dequant_matvec_8bit_gs(r[0], r[1], r[2], x.size, r[0].shape[0], r[3], x)
+        assert rc == 0
+        return y
+    return oracle.f32_matvec(r.cpu().numpy(), x)
 
 
 # LM head (config 1): decode tokens per timed graph replay.
@@ -155,13 +195,17 @@ def cpu_baseline_decode(c, arena_l0, router_l0, shared_l0, gate_l0, x, seconds):
     lay = sa.ExpertLayout(c["H"], c["I"], c["bits"], 64)
     th = cpu_threads()
     h_mid = np.zeros(c["H"], np.float32)
-    args = (arena_l0, lay.expert_size, c["H"], c["I"], c["E"], c["k"], 64, c["bits"], c["normalize"], router_l0)
-    oracle.moe_decode_layer(*args, x, h_mid, shared_l0, gate_l0, th)  # warm-up
+    q8 = isinstance(router_l0, tuple)
+    args = (arena_l0, lay.expert_size, c["H"], c["I"], c["E"], c["k"], 64, c["bits"], c["normalize"],
+            None if q8 else router_l0)
+    kw = dict(router_q8=router_l0 if q8 else None, gate_q8=gate_l0 if isinstance(gate_l0, tuple) else None)
+    gate_w = None if isinstance(gate_l0, tuple) else gate_l0
+    oracle.moe_decode_layer(*args, x, h_mid, shared_l0, gate_w, th, **kw)  # warm-up
     times = []
     t_end = time.perf_counter() + seconds
     while time.perf_counter() < t_end or len(times) < 5:
         t0 = time.perf_counter()
-        oracle.moe_decode_layer(*args, x, h_mid, shared_l0, gate_l0, th)
+        oracle.moe_decode_layer(*args, x, h_mid, shared_l0, gate_w, th, **kw)
         times.append(time.perf_counter() - t0)
     times.sort()
     med = times[len(times) // 2]
@@ -197,7 +241,7 @@ def decode_parity(kern, c, layers, arenas, routers, shareds, gates, norms, x0):
     for l in range(len(layers)):
         if l > 0:
             x = oracle.rms_norm_bf16(r, norms[l].cpu().numpy().view(np.uint16), 1e-6)
-        logits = oracle.f32_matvec(routers[l].cpu().numpy(), x)
+        logits = router_logits(oracle, routers[l], x)
         p = np.sort(oracle.softmax(logits))[::-1]
         min_gap = min(min_gap, float(p[k - 1] - p[k]))
         _, idx, w = oracle.router(logits, k, c["normalize"])
@@ -206,7 +250,7 @@ def decode_parity(kern, c, layers, arenas, routers, shareds, gates, norms, x0):
         sh = score = None
         if shareds[l] is not None:
             sh = oracle.expert_swiglu(shareds[l].cpu().numpy(), 4, H, I, 64, x)
-            score = float(oracle.f32_matvec(gates[l].cpu().numpy()[None, :], x)[0])
+            score = float(router_logits(oracle, gates[l] if isinstance(gates[l], tuple) else gates[l][None, :], x)[0])
         r = oracle.combine(outs, w, r, sh, float("nan") if score is None else score)
     chain_err = float(np.max(np.abs(got - r)) / np.max(np.abs(r)))
     # Layer 0 with idx / weights returned.
@@ -216,10 +260,13 @@ def decode_parity(kern, c, layers, arenas, routers, shareds, gates, norms, x0):
     w0 = torch.empty(k, dtype=torch.float32, device=x0.device)
     sa_check(kern.moe_decode_layer(layers[0], x0, zeros, out0, idx0, w0), "smoe_moe_decode_layer")
     torch.cuda.synchronize()
+    r8, g8 = isinstance(routers[0], tuple), isinstance(gates[0], tuple)
     want0, widx, ww, _ = oracle.moe_decode_layer(
-        arenas[0].cpu().numpy(), stride, H, I, c["E"], k, 64, bits, c["normalize"], routers[0].cpu().numpy(),
-        x0.cpu().numpy(), np.zeros(H, np.float32), None if shareds[0] is None else shareds[0].cpu().numpy(),
-        None if gates[0] is None else gates[0].cpu().numpy())
+        arenas[0].cpu().numpy(), stride, H, I, c["E"], k, 64, bits, c["normalize"],
+        None if r8 else routers[0].cpu().numpy(), x0.cpu().numpy(), np.zeros(H, np.float32),
+        None if shareds[0] is None else shareds[0].cpu().numpy(),
+        None if gates[0] is None or g8 else gates[0].cpu().numpy(), router_q8=routers[0] if r8 else None,
+        gate_q8=gates[0] if g8 else None)
     g0 = out0.cpu().numpy()
     return {"chain_rel_err": chain_err, "chain_layers": len(layers), "min_topk_prob_gap": min_gap,
             "layer0_rel_err": float(np.max(np.abs(g0 - want0)) / np.max(np.abs(want0))),
@@ -310,21 +357,33 @@ def run_decode(args, c):
     for l in range(nl):
         a = torch.empty(E * stride, dtype=torch.uint8, device=dev)
         sa.check(kern.synth_experts(a, E, stride, lay, 1000 + l), "synth")
-        r = torch.empty((E, H), dtype=torch.float32, device=dev)
-        sa.check(kern.synth_normal_f32(r, 2000 + l, 0.02), "synth")
+        rq = gq = None  # 8-bit router / gate (device QuantWeights)
+        if args.router_bits == 8:
+            r, rq = q8_rows(E, H, 2000 + l)
+        else:
+            r = torch.empty((E, H), dtype=torch.float32, device=dev)
+            sa.check(kern.synth_normal_f32(r, 2000 + l, 0.02), "synth")
         s = g = None
         if c["shared"]:
             s = torch.empty(slay.expert_size, dtype=torch.uint8, device=dev)
             sa.check(kern.synth_experts(s, 1, slay.expert_size, slay, 3000 + l), "synth")
-            g = torch.empty(H, dtype=torch.float32, device=dev)
-            sa.check(kern.synth_normal_f32(g, 4000 + l, 0.02), "synth")
+            if args.router_bits == 8:
+                g, gq = q8_rows(1, H, 4000 + l)
+            else:
+                g = torch.empty(H, dtype=torch.float32, device=dev)
+                sa.check(kern.synth_normal_f32(g, 4000 + l, 0.02), "synth")
         nw = torch.full((H,), 0x3F80, dtype=torch.int16, device=dev)  # bf16 1.0
         arenas.append(a)
         routers.append(r)
         shareds.append(s)
         gates.append(g)
         norms.append(nw)
-        layers.append(kern.layer(lay, a, stride, E, k, c["normalize"], r, s, g))
+        if rq is not None:
+            layers.append(kern.layer(lay, a, stride, E, k, c["normalize"], None, s, None, router_q=rq,
+                                     shared_gate_q=gq))
+            layers[-1]._keep_dev = (rq, gq)
+        else:
+            layers.append(kern.layer(lay, a, stride, E, k, c["normalize"], r, s, g))
     T = args.tokens
     x0 = torch.empty((T, H) if T > 1 else (H,), dtype=torch.float32, device=dev)
     sa.check(kern.synth_normal_f32(x0, 5000, 1.0), "synth")
@@ -367,7 +426,7 @@ def run_decode(args, c):
     if args.trace and T == 1:
         phases = trace_fused(kern, step, nl) if path in (0, 3) else None
 
-    nbytes = layer_bytes(c, T)
+    nbytes = layer_bytes(c, T, args.router_bits)
     achieved = nbytes / (us_layer * 1e-6) / 1e9
     out = {
         "metric": "4-bit MoE expert decode µs/layer + achieved HBM GB/s (% of peak), 1 GPU",
@@ -386,11 +445,12 @@ def run_decode(args, c):
                   "shared_gate": "4000 + layer", "x": 5000},
         "config": {"workload": c["name"], "hidden": H, "experts": E, "top_k": k, "inter": I, "bits": c["bits"],
                    "group": 64, "layers": nl, "shared_expert": c["shared"], "tokens": T,
+                   "router": "f32" if args.router_bits == 32 else "8-bit affine, group 64",
                    "mode": "hipgraph" if graph is not None else "eager"},
         "gbps": round(achieved, 1),
         "pct_of_hbm_peak": round(100 * achieved / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": MEASURED_TRAFFIC.get(c.get("key")) if path in (0, 3) and T == 1 else None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": MEASURED_TRAFFIC.get(c.get("key")) if path in (0, 3) and T == 1 and args.router_bits == 32 else None,
                      "unit_of_work": f"one layer, {T} token(s): {nbytes} algorithmic bytes",
                      "kernel": "decode layer: k_fa_route + k_fa_gateup + k_fa_down (one HIP graph)"
                                if path in (0, 3) else "decode layer (all launches)"},
@@ -405,9 +465,9 @@ def run_decode(args, c):
         out["parity"] = decode_parity(kern, c, layers, arenas, routers, shareds, gates, norms, x0)
     if not args.no_cpu and T == 1:
         a0 = arenas[0].cpu().numpy()
-        r0 = routers[0].cpu().numpy()
+        r0 = routers[0] if isinstance(routers[0], tuple) else routers[0].cpu().numpy()
         s0 = None if shareds[0] is None else shareds[0].cpu().numpy()
-        g0 = None if gates[0] is None else gates[0].cpu().numpy()
+        g0 = gates[0] if gates[0] is None or isinstance(gates[0], tuple) else gates[0].cpu().numpy()
         out["cpu_baseline"] = cpu_baseline_decode(c, a0, r0, s0, g0, x0.cpu().numpy(), args.cpu_seconds)
         out["cpu_baseline"]["gpu_speedup"] = round(out["cpu_baseline"]["value"] / us_layer, 1)
     kern.close()
@@ -674,6 +734,9 @@ def main():
     ap.add_argument("--no-parity", action="store_true", help="skip the parity check of the timed work after timing")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-stream-peak", action="store_true", help="skip the measured streaming-read peak")
+    ap.add_argument("--router-bits", type=int, default=32, choices=[32, 8],
+                    help="decode configs: f32 router and shared gate (BASELINE's configs), or 8-bit affine "
+                         "ones (group 64; the reference's A3B mlp.gate.weight / mlp.shared_expert_gate.weight)")
     ap.add_argument("--tokens", type=int, default=1, choices=[1, 2, 3, 4],
                     help="decode configs: tokens decoded together through the layers (value = us per layer "
                          "for all of them)")

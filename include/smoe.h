@@ -131,11 +131,16 @@ int smoe_set_option(smoe_handle* h, int option, int64_t value);
  * Mirrors QuantWeights (metal/lib.rs:339-351), plus the weight width. */
 typedef struct {
   const void* base;       /* device */
-  uint64_t packed_offset; /* byte offset of the codes, 16-byte aligned (4-bit) / 4-byte (3-bit) */
+  uint64_t packed_offset; /* byte offset of the codes, 16-byte aligned (4- and 8-bit) / 4-byte (3-bit) */
   uint64_t scales_offset; /* byte offset of bf16 scales [out_dim, in_dim/group], 2-byte aligned */
   uint64_t biases_offset; /* byte offset of bf16 biases, same shape */
   uint32_t group_size;    /* 32, 64 or 128 */
-  uint32_t bits;          /* 4, or 3 for the packed 3-bit layout */
+  uint32_t bits;          /* 4; 3 for the packed 3-bit layout; 8 for one byte per
+                             input (byte n of u32 word i = input 4i + n, the
+                             reference's 8-bit affine layout, cpu_matvec.rs:
+                             205-283; smoe_qmv, smoe_qmv_argmax and smoe_qmm,
+                             in_dim <= 8192, and the router / shared gate of
+                             smoe_layer) */
 } smoe_qweights;
 
 /* y[r] = sum_c (q[r,c] * s[r,c/g] + b[r,c/g]) * x[c] for r < out_dim,
@@ -302,10 +307,16 @@ int smoe_experts_decode(smoe_handle* h, const smoe_expert_shape* shape,
                         const float* input, const float* h_mid, const float* shared_out,
                         float shared_gate_score, float* hidden_out);
 
-/* One resident MoE layer: experts at base + e * stride (device), an f32
- * router [n_experts, hidden], an optional always-on 4-bit shared expert
- * (same hidden and inter as the routed ones) with an optional f32 gate
- * vector [hidden] (its sigmoid scales the shared output; NULL = unscaled). */
+/* One resident MoE layer: experts at base + e * stride (device), a router
+ * [n_experts, hidden] (f32, or 8-bit affine as the reference's A3B
+ * mlp.gate.weight, linear_attn_forward.rs:1300-1301), an optional
+ * always-on 4-bit shared expert (same hidden and inter as the routed ones)
+ * with an optional gate vector [hidden] (f32 or 8-bit affine; its sigmoid
+ * scales the shared output; none = unscaled). Exactly one of router_w /
+ * router_q is set, at most one of shared_gate / shared_gate_q. The 8-bit
+ * forms are smoe_qweights of bits 8 (host structs read during the call,
+ * device data; codes 16-byte aligned, hidden a multiple of the group); every
+ * weight is fma(q, s, b) as the reference's CPU matvec forms it. */
 typedef struct {
   smoe_expert_shape shape;
   const void* experts;       /* device, n_experts * stride bytes */
@@ -313,9 +324,11 @@ typedef struct {
   uint32_t n_experts;
   uint32_t k;                /* routed experts per token */
   int32_t normalize;         /* norm_topk_prob */
-  const float* router_w;     /* device f32[n_experts, hidden] */
+  const float* router_w;     /* device f32[n_experts, hidden], or NULL (router_q) */
   const void* shared_expert; /* device 4-bit blob, or NULL */
   const float* shared_gate;  /* device f32[hidden], or NULL */
+  const smoe_qweights* router_q;      /* 8-bit router [n_experts, hidden], or NULL */
+  const smoe_qweights* shared_gate_q; /* 8-bit shared gate [1, hidden], or NULL */
 } smoe_layer;
 
 /* Decode one token through one layer with routing on the device:

@@ -229,11 +229,19 @@ class Kernels:
     # -- one resident layer (moe_dispatch_per_token with device routing) --------
     @staticmethod
     def layer(layout: ExpertLayout, experts, stride, n_experts, k, normalize, router_w,
-              shared_expert=None, shared_gate=None):
-        return _abi.Layer(layout.shape(), experts.data_ptr(), stride, n_experts, k, int(normalize),
-                          router_w.data_ptr(),
-                          None if shared_expert is None else shared_expert.data_ptr(),
-                          None if shared_gate is None else shared_gate.data_ptr())
+              shared_expert=None, shared_gate=None, router_q=None, shared_gate_q=None):
+        """router_w: f32 router tensor, or None with router_q (an 8-bit
+        QuantWeights [n_experts, hidden]); shared_gate_q: an 8-bit shared gate
+        [1, hidden] in place of shared_gate."""
+        rq = None if router_q is None else router_q.c()
+        gq = None if shared_gate_q is None else shared_gate_q.c()
+        L = _abi.Layer(layout.shape(), experts.data_ptr(), stride, n_experts, k, int(normalize),
+                       None if router_w is None else router_w.data_ptr(),
+                       None if shared_expert is None else shared_expert.data_ptr(),
+                       None if shared_gate is None else shared_gate.data_ptr(),
+                       None if rq is None else C.addressof(rq), None if gq is None else C.addressof(gq))
+        L._keep = (rq, gq)  # the smoe_qweights structs the layer points to
+        return L
 
     def moe_decode_layer(self, layer, input, h_mid, hidden_out, idx_out=None, w_out=None):
         return _lib.smoe_moe_decode_layer(self.h, C.byref(layer), _ptr(input), _ptr(h_mid),

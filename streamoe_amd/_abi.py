@@ -79,6 +79,8 @@ class Layer(C.Structure):
         ("router_w", C.c_void_p),
         ("shared_expert", C.c_void_p),
         ("shared_gate", C.c_void_p),
+        ("router_q", C.c_void_p),        # const smoe_qweights* (8-bit router) or NULL
+        ("shared_gate_q", C.c_void_p),   # const smoe_qweights* (8-bit shared gate) or NULL
     ]
 
 

@@ -15,7 +15,7 @@ using namespace smoe;
 
 namespace {
 
-constexpr uint32_t kAbiVersion = 1;
+constexpr uint32_t kAbiVersion = 2;
 
 int hip_status(hipError_t e) { return e == hipSuccess ? SMOE_OK : SMOE_ERR_HIP; }
 
@@ -58,7 +58,8 @@ int reserve(smoe_handle* h, uint32_t H, uint32_t I, uint32_t E) {
   const size_t tab_b = al(T * sizeof(FfnTable));
   const size_t xl_b = al(T * (size_t)H / 32 * 32 * sizeof(uint32_t));
   const size_t arg_b = 2 * (size_t)kQmvMaxWaves * sizeof(uint32_t);
-  const size_t total = act_b + log_b + 256 + tab_b + xl_b + arg_b + 256;
+  const size_t grow_b = al((size_t)H * sizeof(float));  // an 8-bit shared gate's f32 weights
+  const size_t total = act_b + log_b + 256 + tab_b + xl_b + arg_b + 256 + grow_b;
   void* mem = nullptr;
   if (hipSetDevice(h->device) != hipSuccess) return SMOE_ERR_HIP;
   if (hipMalloc(&mem, total) != hipSuccess) return SMOE_ERR_HIP;
@@ -83,6 +84,7 @@ int reserve(smoe_handle* h, uint32_t H, uint32_t I, uint32_t E) {
   h->arg_i = (uint32_t*)(q + kQmvMaxWaves * sizeof(float));
   q += arg_b;
   h->err = (uint32_t*)q;
+  h->gate_row = (float*)(q + 256);
   h->lstride = (uint32_t)lstride;
   h->astride = (uint32_t)(kMaxSlotsHost * I);
   h->xstride = H / 32 * 32;
@@ -235,12 +237,13 @@ int smoe_set_option(smoe_handle* h, int option, int64_t value) {
   }
 }
 
-static int qview(const smoe_qweights* w, uint32_t in_dim, QView* v) {
+// allow8: the entry point takes 8-bit weights (one byte per input).
+static int qview(const smoe_qweights* w, uint32_t in_dim, QView* v, bool allow8 = false) {
   if (!w || !w->base || !in_dim) return SMOE_ERR_INVALID_ARG;
-  if (w->bits != 4 && w->bits != 3) return SMOE_ERR_UNSUPPORTED_BITS;
+  if (w->bits != 4 && w->bits != 3 && !(allow8 && w->bits == 8)) return SMOE_ERR_UNSUPPORTED_BITS;
   if (int rc = check_group(w->group_size)) return rc;
   if (in_dim % w->group_size) return SMOE_ERR_IN_DIM_NOT_MULTIPLE;
-  if (!aligned(w->base, w->packed_offset, w->bits == 4 ? 16 : 4) ||
+  if (!aligned(w->base, w->packed_offset, w->bits == 3 ? 4 : 16) ||
       !aligned(w->base, w->scales_offset, 2) || !aligned(w->base, w->biases_offset, 2))
     return SMOE_ERR_MISALIGNED;
   const uint8_t* b = (const uint8_t*)w->base;
@@ -256,7 +259,7 @@ int smoe_qmv(smoe_handle* h, const smoe_qweights* w, const float* x, float* y, u
              uint32_t in_dim) {
   if (!h || !x || !y || !out_dim) return SMOE_ERR_INVALID_ARG;
   QView v;
-  if (int rc = qview(w, in_dim, &v)) return rc;
+  if (int rc = qview(w, in_dim, &v, true)) return rc;
   if (!aligned(x, 0, 16)) return SMOE_ERR_MISALIGNED;
   if (int rc = use_device(h)) return rc;
   bool unsupported = false;
@@ -274,7 +277,7 @@ int smoe_qmm(smoe_handle* h, const smoe_qweights* w, const float* x, float* y, u
              uint32_t in_dim, uint32_t n_tokens, void* workspace, uint64_t workspace_bytes) {
   if (!h || !x || !y || !out_dim || !n_tokens || !workspace) return SMOE_ERR_INVALID_ARG;
   QView v;
-  if (int rc = qview(w, in_dim, &v)) return rc;
+  if (int rc = qview(w, in_dim, &v, true)) return rc;
   if (!qmm_supported(in_dim, out_dim, w->group_size, w->bits, n_tokens)) {
     // Shapes without GEMM tiles (in_dim or out_dim not a multiple of 256,
     // in_dim up to 8192): one k_qmv per token row, as smoe_qmv computes it.
@@ -325,8 +328,10 @@ int smoe_qmv_argmax(smoe_handle* h, const smoe_qweights* w, const float* x, floa
                     uint32_t in_dim, int32_t* out_index) {
   if (!h || !x || !y || !out_dim || !out_index) return SMOE_ERR_INVALID_ARG;
   QView v;
-  if (int rc = qview(w, in_dim, &v)) return rc;
+  if (int rc = qview(w, in_dim, &v, true)) return rc;
   if (!aligned(x, 0, 16)) return SMOE_ERR_MISALIGNED;
+  // 8-bit: the argmax reads y back (16-byte loads).
+  if (v.bits == 8 && !aligned(y, 0, 16)) return SMOE_ERR_MISALIGNED;
   if (!h->arg_v) return SMOE_ERR_SCRATCH_TOO_SMALL;
   if (int rc = use_device(h)) return rc;
   bool unsupported = false;
@@ -476,18 +481,45 @@ int smoe_experts_decode(smoe_handle* h, const smoe_expert_shape* shape,
   return hip_status(e);
 }
 
+// An 8-bit router or shared gate of a layer (bits 8, rows of `hidden`
+// inputs); null: r stays unused.
+static int q8_rows(const smoe_qweights* w, uint32_t hidden, Q8Rows* r) {
+  *r = Q8Rows{};
+  if (!w) return SMOE_OK;
+  if (w->bits != 8) return SMOE_ERR_UNSUPPORTED_BITS;
+  QView v;
+  if (int rc = qview(w, hidden, &v, true)) return rc;
+  r->q = v.codes;
+  r->s = v.scales;
+  r->b = v.biases;
+  r->group = v.group;
+  return SMOE_OK;
+}
+
+// The layer's router and (with a shared expert) shared gate in 8-bit form.
+static void layer_q8(const smoe_layer* L, Q8Rows* router, Q8Rows* gate) {
+  q8_rows(L->router_q, L->shape.hidden, router);
+  q8_rows(L->shared_expert ? L->shared_gate_q : nullptr, L->shape.hidden, gate);
+}
+
 // Arguments of one resident layer, independent of any reservation.
 static int check_layer_args(const smoe_layer* L) {
-  if (!L || !L->experts || !L->router_w) return SMOE_ERR_INVALID_ARG;
+  if (!L || !L->experts) return SMOE_ERR_INVALID_ARG;
+  // Exactly one router form, at most one gate form.
+  if ((L->router_w != nullptr) == (L->router_q != nullptr)) return SMOE_ERR_INVALID_ARG;
+  if (L->shared_gate && L->shared_gate_q) return SMOE_ERR_INVALID_ARG;
   if (int rc = check_shape(&L->shape)) return rc;
   if (int rc = check_router(1, L->n_experts, L->k)) return rc;
   if (L->stride < smoe_expert_bytes(&L->shape)) return SMOE_ERR_INVALID_ARG;
   if (!blob_aligned(L->experts, L->shape.bits) || L->stride % (L->shape.bits == 4 ? 16 : 4))
     return SMOE_ERR_MISALIGNED;
   if (L->shared_expert && !blob_aligned(L->shared_expert, 4)) return SMOE_ERR_MISALIGNED;
-  if (!aligned(L->router_w, 0, 16) || (L->shared_gate && !aligned(L->shared_gate, 0, 16)))
+  if ((L->router_w && !aligned(L->router_w, 0, 16)) || (L->shared_gate && !aligned(L->shared_gate, 0, 16)))
     return SMOE_ERR_MISALIGNED;
   if (L->shape.hidden % 4) return SMOE_ERR_UNSUPPORTED_SHAPE;
+  Q8Rows q;
+  if (int rc = q8_rows(L->router_q, L->shape.hidden, &q)) return rc;
+  if (int rc = q8_rows(L->shared_gate_q, L->shape.hidden, &q)) return rc;
   return SMOE_OK;
 }
 
@@ -506,9 +538,11 @@ static int decode_layer(smoe_handle* h, const smoe_layer* L, const float* input,
                         const float* h_mid, float* hidden_out, int32_t* idx_out, float* w_out,
                         const uint16_t* norm_w = nullptr, float eps = 0.f, float* x_norm = nullptr) {
   const smoe_expert_shape& s = L->shape;
+  Q8Rows rq, gq;
+  layer_q8(L, &rq, &gq);
   hipError_t e = launch_router_logits(L->router_w, L->shared_expert ? L->shared_gate : nullptr,
                                       input, 1, L->n_experts, s.hidden, h->logits, h->gate,
-                                      h->stream, norm_w, eps, x_norm);
+                                      h->stream, norm_w, eps, x_norm, rq, gq);
   if (norm_w) input = x_norm;
   if (e != hipSuccess) return SMOE_ERR_HIP;
   RouteOut ro{};
@@ -518,7 +552,7 @@ static int decode_layer(smoe_handle* h, const smoe_layer* L, const float* input,
   ro.experts = (const uint8_t*)L->experts;
   ro.stride = L->stride;
   ro.shared_blob = (const uint8_t*)L->shared_expert;
-  ro.gate_scores = (L->shared_expert && L->shared_gate) ? h->gate : nullptr;
+  ro.gate_scores = (L->shared_expert && (L->shared_gate || L->shared_gate_q)) ? h->gate : nullptr;
   e = launch_topk(h->logits, 1, L->n_experts, L->k, true, L->normalize != 0, ro, h->stream);
   if (e != hipSuccess) return SMOE_ERR_HIP;
   const BlobGeom g = blob_geom(s.hidden, s.inter, s.group, s.bits);
@@ -553,10 +587,12 @@ struct FaScratch {
   uint32_t lstride, astride, xstride;  // per-token strides (elements)
   uint64_t* trace;
   hipStream_t stream;
+  float* gate_row;  // [hidden] f32 weights of an 8-bit shared gate
 };
 
 static FaScratch handle_scratch(const smoe_handle* h) {
-  return FaScratch{h->xl, h->logits, h->act, h->table, h->lstride, h->astride, h->xstride, h->trace, h->stream};
+  return FaScratch{h->xl,      h->logits,  h->act,   h->table,  h->lstride,
+                   h->astride, h->xstride, h->trace, h->stream, h->gate_row};
 }
 
 static int decode_fused(const FaScratch& sc, const smoe_layer* L, const float* x_in, const float* resid,
@@ -571,9 +607,16 @@ static int decode_fused(const FaScratch& sc, const smoe_layer* L, const float* x
   a.norm = norm;
   a.eps = eps;
   a.xl = sc.xl;
-  a.router = L->router_w;
+  FaQ8 q;
+  layer_q8(L, &q.router, &q.gate);
+  // An 8-bit router: the limbs stand in for K_B's unused gate row.
+  a.router = L->router_w ? L->router_w : reinterpret_cast<const float*>(sc.xl);
   a.shared = (const uint8_t*)L->shared_expert;
   a.gate = L->shared_expert ? L->shared_gate : nullptr;
+  if (q.gate.q) {
+    q.gate_f32 = sc.gate_row;
+    a.gate = sc.gate_row;
+  }
   a.experts = (const uint8_t*)L->experts;
   a.stride = L->stride;
   a.routed = blob_geom(s.hidden, s.inter, s.group, s.bits);
@@ -593,7 +636,7 @@ static int decode_fused(const FaScratch& sc, const smoe_layer* L, const float* x
   a.lstride = sc.lstride;
   a.astride = sc.astride;
   a.xstride = sc.xstride;
-  return hip_status(launch_fused_layer(a, sc.stream));
+  return hip_status(launch_fused_layer(a, sc.stream, q));
 }
 
 // n_layers layers of one token on the three-kernel path: layer l reads x_l
@@ -686,7 +729,8 @@ int smoe_moe_decode_layers_noalloc(void* stream, const smoe_layer* layers, uint3
   const size_t act_b = al((size_t)kMaxSlotsHost * max_i * sizeof(float));
   const size_t tab_b = al(sizeof(FfnTable));
   const size_t xl_b = al((size_t)H / 32 * 32 * sizeof(uint32_t));
-  if (log_b + act_b + tab_b + xl_b > kNoAllocScratchBytes) return SMOE_ERR_SCRATCH_TOO_SMALL;
+  const size_t grow_b = al((size_t)H * sizeof(float));  // an 8-bit shared gate's f32 weights
+  if (log_b + act_b + tab_b + xl_b + grow_b > kNoAllocScratchBytes) return SMOE_ERR_SCRATCH_TOO_SMALL;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return SMOE_ERR_HIP;
   uint8_t* base = nullptr;
@@ -696,6 +740,7 @@ int smoe_moe_decode_layers_noalloc(void* stream, const smoe_layer* layers, uint3
   sc.act = (float*)(base + log_b);
   sc.table = (FfnTable*)(base + log_b + act_b);
   sc.xl = (uint32_t*)(base + log_b + act_b + tab_b);
+  sc.gate_row = (float*)(base + log_b + act_b + tab_b + xl_b);
   sc.lstride = (uint32_t)lstride;
   sc.astride = (uint32_t)(kMaxSlotsHost * max_i);
   sc.xstride = H / 32 * 32;

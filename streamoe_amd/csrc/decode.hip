@@ -283,9 +283,80 @@ static hipError_t qmv_bits(const QView& w, const float* x, float* y, uint32_t ro
   return hipSuccess;
 }
 
+// ---------------------------------------------------------------------------
+// 8-bit affine matvec (dequant_matvec_8bit_gs_cpu, cpu_matvec.rs:205-283;
+// the reference's GPU kernel is dequant_matvec_8bit_v3, shaders.metal:
+// 619-677): the small 8-bit projections of the A3B models (router, shared-
+// expert gate). Persistent waves, one row at a time; lane l takes the
+// 16-input pieces starting at 16 l + 1024 i (all of a row's pieces are
+// loaded before the first FMA), forms each weight as fma(q, s, b) and adds
+// it into one FMA chain, then the wave sum.
+// ---------------------------------------------------------------------------
+constexpr int kQ8Pieces = 8;  // 16-input pieces per lane: in_dim <= 8192
+
+__global__ __launch_bounds__(256) void k_qmv8(const uint8_t* __restrict__ codes,
+                                              const uint16_t* __restrict__ scales,
+                                              const uint16_t* __restrict__ biases,
+                                              const float* __restrict__ x, float* __restrict__ y,
+                                              uint32_t rows, uint32_t in_dim, uint32_t gsh, uint32_t n_waves) {
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
+  const uint32_t gpr = in_dim >> gsh;
+  for (uint32_t r = wave; r < rows; r += n_waves) {
+    u32x4 q[kQ8Pieces];
+    uint32_t s[kQ8Pieces], b[kQ8Pieces];
+#pragma unroll
+    for (int i = 0; i < kQ8Pieces; ++i) {
+      const uint32_t c = lane * 16 + 1024u * i;
+      if (c < in_dim) {
+        q[i] = *reinterpret_cast<const u32x4*>(codes + (size_t)r * in_dim + c);
+        const size_t gi = (size_t)r * gpr + (c >> gsh);
+        s[i] = scales[gi];
+        b[i] = biases[gi];
+      }
+    }
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < kQ8Pieces; ++i) {
+      const uint32_t c = lane * 16 + 1024u * i;
+      if (c < in_dim) {
+        const float sf = bf16f((uint16_t)s[i]), bf = bf16f((uint16_t)b[i]);
+        const uint32_t wd[4] = {q[i].x, q[i].y, q[i].z, q[i].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const f32x4 x4 = *reinterpret_cast<const f32x4*>(x + c + 4 * j);
+          const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
+#pragma unroll
+          for (int n = 0; n < 4; ++n)
+            acc = __builtin_fmaf(__builtin_fmaf((float)((wd[j] >> (8 * n)) & 0xFFu), sf, bf), xv[n], acc);
+        }
+      }
+    }
+    acc = group_sum<64>(acc);
+    if (lane == 0) y[r] = acc;
+  }
+}
+
+static hipError_t qmv8(const QView& w, const float* x, float* y, uint32_t rows, uint32_t in_dim,
+                       hipStream_t st, bool* unsupported, float* arg_v, uint32_t* arg_i, int32_t* arg_out) {
+  if (in_dim % 16 || in_dim > 1024u * kQ8Pieces || w.group < 16) {
+    *unsupported = true;
+    return hipSuccess;
+  }
+  const uint32_t wpb = 4;
+  uint32_t n_waves = rows < kQmvMaxWaves ? rows : kQmvMaxWaves;
+  const uint32_t blocks = (n_waves + wpb - 1) / wpb;
+  n_waves = blocks * wpb;
+  hipLaunchKernelGGL(k_qmv8, dim3(blocks), dim3(wpb * 64), 0, st, w.codes, w.scales, w.biases, x, y, rows,
+                     in_dim, (uint32_t)__builtin_ctz(w.group), n_waves);
+  if (arg_out) return launch_argmax(y, rows, arg_out, arg_v, arg_i, st);
+  return hipGetLastError();
+}
+
 hipError_t launch_qmv(const QView& w, const float* x, float* y, uint32_t out_dim, uint32_t in_dim,
                       hipStream_t st, bool* unsupported, float* arg_v, uint32_t* arg_i, int32_t* arg_out) {
   *unsupported = false;
+  if (w.bits == 8) return qmv8(w, x, y, out_dim, in_dim, st, unsupported, arg_v, arg_i, arg_out);
   if (in_dim % kChunk) {
     *unsupported = true;
     return hipSuccess;
@@ -436,6 +507,9 @@ hipError_t launch_argmax(const float* v, uint32_t n, int32_t* out, float* part_v
 // same sum in the same order), and block (0, t) stores the normalised row
 // in x_out for the expert kernels: one launch instead of a norm kernel
 // before the router.
+// An 8-bit router or gate (Wq / gq) has the same loop over 4-input pieces:
+// each weight is dequantized as fma(q, s, b) (dequant_matvec_8bit_gs_cpu,
+// cpu_matvec.rs:205-283) and then enters the same FMA chain.
 __global__ __launch_bounds__(256) void k_router_logits(const float* __restrict__ W,
                                                        const float* __restrict__ gate_w,
                                                        const float* __restrict__ x,
@@ -443,11 +517,14 @@ __global__ __launch_bounds__(256) void k_router_logits(const float* __restrict__
                                                        float* __restrict__ logits,
                                                        float* __restrict__ gate_scores,
                                                        const uint16_t* __restrict__ norm_w, float eps,
-                                                       float* __restrict__ x_out) {
+                                                       float* __restrict__ x_out, Q8Rows Wq, Q8Rows gq) {
   __shared__ float red[4];
   __shared__ float inv_sh;
   const uint32_t e = blockIdx.x, t = blockIdx.y;
   const float* row = e < n_experts ? W + (size_t)e * hidden : gate_w;
+  const Q8Rows rq = e < n_experts ? Wq : gq;
+  const uint32_t qrow = e < n_experts ? e : 0u;
+  const uint32_t gsh = rq.q ? __builtin_ctz(rq.group) : 0u;
   const float* xt = x + (size_t)t * hidden;
   float inv = 1.f;
   if (norm_w) {
@@ -468,7 +545,16 @@ __global__ __launch_bounds__(256) void k_router_logits(const float* __restrict__
   }
   float acc = 0.f;
   for (uint32_t c = threadIdx.x * 4; c < hidden; c += 1024) {
-    const f32x4 w4 = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(row + c));
+    f32x4 w4;
+    if (rq.q) {
+      const uint32_t q4 = *reinterpret_cast<const uint32_t*>(rq.q + (size_t)qrow * hidden + c);
+      const size_t gi = (size_t)qrow * (hidden >> gsh) + (c >> gsh);
+      const float s = bf16f(rq.s[gi]), b = bf16f(rq.b[gi]);
+      w4 = f32x4{__builtin_fmaf((float)(q4 & 0xFFu), s, b), __builtin_fmaf((float)((q4 >> 8) & 0xFFu), s, b),
+                 __builtin_fmaf((float)((q4 >> 16) & 0xFFu), s, b), __builtin_fmaf((float)(q4 >> 24), s, b)};
+    } else {
+      w4 = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(row + c));
+    }
     float4 x4 = *reinterpret_cast<const float4*>(xt + c);
     if (norm_w) {
       x4.x = x4.x * inv * bf16f(norm_w[c]);
@@ -497,10 +583,11 @@ __global__ __launch_bounds__(256) void k_router_logits(const float* __restrict__
 hipError_t launch_router_logits(const float* W, const float* gate_w, const float* x,
                                 uint32_t n_tokens, uint32_t n_experts, uint32_t hidden,
                                 float* logits, float* gate_scores, hipStream_t st,
-                                const uint16_t* norm_w, float eps, float* x_out) {
-  const uint32_t rows = n_experts + (gate_w ? 1 : 0);
+                                const uint16_t* norm_w, float eps, float* x_out, const Q8Rows& Wq,
+                                const Q8Rows& gq) {
+  const uint32_t rows = n_experts + (gate_w || gq.q ? 1 : 0);
   hipLaunchKernelGGL(k_router_logits, dim3(rows, n_tokens), dim3(256), 0, st, W, gate_w, x,
-                     n_experts, hidden, logits, gate_scores, norm_w, eps, x_out);
+                     n_experts, hidden, logits, gate_scores, norm_w, eps, x_out, Wq, gq);
   return hipGetLastError();
 }
 

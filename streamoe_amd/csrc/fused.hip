@@ -222,6 +222,47 @@ __device__ __forceinline__ void fa_row_load(const float* row, uint32_t lane, f32
   }
 }
 
+// An 8-bit row's chunks (chunk c = lane + 64 h): 32 code bytes and the
+// bf16 scale and bias of the chunk's group (a group holds whole chunks),
+// raw until fa_row_dequant_q8; loaded temporally like fa_row_load.
+template <int HC>
+struct FaQ8Row {
+  u32x4 q[HC][2];
+  uint32_t s[HC], b[HC];
+};
+
+template <int HC>
+__device__ __forceinline__ void fa_row_load_q8(const Q8Rows& m, uint32_t row, uint32_t lane, FaQ8Row<HC>& o) {
+  constexpr uint32_t K = HC * kFaH;
+  const uint32_t gsh = __builtin_ctz(m.group);
+#pragma unroll
+  for (int h = 0; h < HC; ++h) {
+    const uint32_t c = lane + 64 * h;
+    const u32x4* p = reinterpret_cast<const u32x4*>(m.q + (size_t)row * K + (size_t)c * kChunk);
+    o.q[h][0] = p[0];
+    o.q[h][1] = p[1];
+    const size_t gi = (size_t)row * (K >> gsh) + ((c * kChunk) >> gsh);
+    o.s[h] = m.s[gi];
+    o.b[h] = m.b[gi];
+  }
+}
+
+// The row's weights fma(q, s, b) (dequant_matvec_8bit_gs_cpu, cpu_matvec.rs:
+// 205-283; byte n of code word i is input 4 i + n) in fa_row_load's layout.
+template <int HC>
+__device__ __forceinline__ void fa_row_dequant_q8(const FaQ8Row<HC>& r, f32x4 (&wr)[HC][kChunk / 4]) {
+#pragma unroll
+  for (int h = 0; h < HC; ++h) {
+    const float s = bf16f((uint16_t)r.s[h]), b = bf16f((uint16_t)r.b[h]);
+#pragma unroll
+    for (int i = 0; i < kChunk / 4; ++i) {
+      const uint32_t w = r.q[h][i / 4][i % 4];
+      wr[h][i] = f32x4{__builtin_fmaf((float)(w & 0xFFu), s, b), __builtin_fmaf((float)((w >> 8) & 0xFFu), s, b),
+                       __builtin_fmaf((float)((w >> 16) & 0xFFu), s, b), __builtin_fmaf((float)(w >> 24), s, b)};
+    }
+  }
+}
+
 // row . x over the wave (valid in lane 63): four FMA chains per lane over
 // its chunks, then the wave sum.
 template <int HC>
@@ -242,10 +283,11 @@ __device__ __forceinline__ float fa_row_dot(const f32x4 (&wr)[HC][kChunk / 4], c
 // ---------------------------------------------------------------------------
 // K_A: router logits for T tokens: each wave reads its
 // router row once and applies it to every token's x. The last 4 HC T waves
-// write x of the tokens as integer limbs for K_B.
+// write x of the tokens as integer limbs for K_B. Q8: the router is 8-bit
+// (r8); its row is dequantized in registers after the loads.
 // ---------------------------------------------------------------------------
-template <int T, int HC>
-__global__ __launch_bounds__(64) void k_fa_route(FusedLayer a) {
+template <int T, int HC, bool Q8>
+__device__ __forceinline__ void fa_route(const FusedLayer& a, const Q8Rows& r8) {
   FA_ARGS_IN_SGPRS("s"(a.x_in), "s"(a.resid), "s"(a.norm), "s"(a.eps), "s"(a.router), "s"(a.E),
                    "s"(a.logits), "s"(a.xl), "s"(a.trace), "s"(a.lstride), "s"(a.xstride));
   FaClock clk;
@@ -280,12 +322,17 @@ __global__ __launch_bounds__(64) void k_fa_route(FusedLayer a) {
     return;
   }
   f32x4 wr[HC][kChunk / 4];
-  fa_row_load<HC>(a.router + (size_t)w * (HC * kFaH), lane, wr);
+  FaQ8Row<HC> wq;
+  if constexpr (Q8)
+    fa_row_load_q8<HC>(r8, w, lane, wq);
+  else
+    fa_row_load<HC>(a.router + (size_t)w * (HC * kFaH), lane, wr);
   FaX<HC> f[T];
 #pragma unroll
   for (int t = 0; t < T; ++t) fa_x_load<HC>(token_view<HC>(a, t), lane, f[t]);
   __builtin_amdgcn_sched_barrier(0);
   fa_stamp(a, clk, 3, true);
+  if constexpr (Q8) fa_row_dequant_q8<HC>(wq, wr);
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     const FusedLayer at = token_view<HC>(a, t);
@@ -321,6 +368,36 @@ __global__ __launch_bounds__(64) void k_fa_route(FusedLayer a) {
   fa_stamp(a, clk, 4, false);
   fa_stamp(a, clk, 5, true);
   fa_flush(a, clk, 0);
+}
+
+template <int T, int HC>
+__global__ __launch_bounds__(64) void k_fa_route(FusedLayer a) {
+  fa_route<T, HC, false>(a, Q8Rows{});
+}
+
+// K_A of a layer with an 8-bit router (Q8) and / or an 8-bit shared-expert
+// gate (g8.q set). Its own kernel, so that the f32 layers' kernels keep
+// their argument block. With g8, one more wave (the last block) writes the
+// gate row's weights fma(q, s, b) as f32 to gate_f32, which K_B's route
+// table wave reads as an f32 gate: the same values, so the same gate score
+// as a dot over the 8-bit row.
+template <int T, int HC, bool Q8>
+__global__ __launch_bounds__(64) void k_fa_route_q8(FusedLayer a, Q8Rows r8, Q8Rows g8, float* gate_f32) {
+  if (g8.q && blockIdx.x == gridDim.x - 1) {
+    const uint32_t lane = threadIdx.x;
+    FaQ8Row<HC> q;
+    fa_row_load_q8<HC>(g8, 0, lane, q);
+    f32x4 wr[HC][kChunk / 4];
+    fa_row_dequant_q8<HC>(q, wr);
+#pragma unroll
+    for (int h = 0; h < HC; ++h) {
+      f32x4* o = reinterpret_cast<f32x4*>(gate_f32 + ((size_t)lane + 64 * h) * kChunk);
+#pragma unroll
+      for (int i = 0; i < kChunk / 4; ++i) o[i] = wr[h][i];
+    }
+    return;
+  }
+  fa_route<T, HC, Q8>(a, r8);
 }
 
 // The E logits, P per lane (lane l holds [l*P, l*P + P)); positions >= E
@@ -803,37 +880,67 @@ static hipError_t launch_down_fa(const FusedLayer& a, hipStream_t st) {
                                      : launch_down_fa_h<BITS, LI, 1, HC>(a, st);
 }
 
+template <int HC, bool Q8>
+static void launch_route_q8(const FusedLayer& a, const FaQ8& q, uint32_t grid, hipStream_t st) {
+  switch (a.n_tokens) {
+    case 1:
+      hipLaunchKernelGGL((k_fa_route_q8<1, HC, Q8>), dim3(grid), dim3(64), 0, st, a, q.router, q.gate, q.gate_f32);
+      break;
+    case 2:
+      hipLaunchKernelGGL((k_fa_route_q8<2, HC, Q8>), dim3(grid), dim3(64), 0, st, a, q.router, q.gate, q.gate_f32);
+      break;
+    case 3:
+      if constexpr (HC == 1)
+        hipLaunchKernelGGL((k_fa_route_q8<3, HC, Q8>), dim3(grid), dim3(64), 0, st, a, q.router, q.gate,
+                           q.gate_f32);
+      break;
+    default:
+      if constexpr (HC == 1)
+        hipLaunchKernelGGL((k_fa_route_q8<4, HC, Q8>), dim3(grid), dim3(64), 0, st, a, q.router, q.gate,
+                           q.gate_f32);
+      break;
+  }
+}
+
 // K_A over a.n_tokens tokens. At hidden 4096 a router wave holds two
 // tokens' x at most (289 VGPRs), so 3 or 4 tokens take two launches of 2
 // and n - 2 tokens (the router rows are read twice, from the memory-side
 // cache the second time).
 template <int HC>
-static void launch_route_fa(const FusedLayer& a, hipStream_t st) {
+static void launch_route_fa(const FusedLayer& a, const FaQ8& q, hipStream_t st) {
   if (HC == 2 && a.n_tokens > 2) {
     FusedLayer lo = a, hi = token_view<HC>(a, 2);
     lo.n_tokens = 2;
     hi.n_tokens = a.n_tokens - 2;
-    launch_route_fa<HC>(lo, st);
-    launch_route_fa<HC>(hi, st);
+    launch_route_fa<HC>(lo, q, st);
+    launch_route_fa<HC>(hi, q, st);
     return;
   }
   const uint32_t ka = a.E + 4u * HC * a.n_tokens;
-  switch (a.n_tokens) {
-    case 1: hipLaunchKernelGGL((k_fa_route<1, HC>), dim3(ka), dim3(64), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((k_fa_route<2, HC>), dim3(ka), dim3(64), 0, st, a); break;
-    case 3:
-      if constexpr (HC == 1) hipLaunchKernelGGL((k_fa_route<3, HC>), dim3(ka), dim3(64), 0, st, a);
-      break;
-    default:
-      if constexpr (HC == 1) hipLaunchKernelGGL((k_fa_route<4, HC>), dim3(ka), dim3(64), 0, st, a);
-      break;
+  if (!q.router.q && !q.gate.q) {
+    switch (a.n_tokens) {
+      case 1: hipLaunchKernelGGL((k_fa_route<1, HC>), dim3(ka), dim3(64), 0, st, a); break;
+      case 2: hipLaunchKernelGGL((k_fa_route<2, HC>), dim3(ka), dim3(64), 0, st, a); break;
+      case 3:
+        if constexpr (HC == 1) hipLaunchKernelGGL((k_fa_route<3, HC>), dim3(ka), dim3(64), 0, st, a);
+        break;
+      default:
+        if constexpr (HC == 1) hipLaunchKernelGGL((k_fa_route<4, HC>), dim3(ka), dim3(64), 0, st, a);
+        break;
+    }
+    return;
   }
+  const uint32_t kq = ka + (q.gate.q ? 1u : 0u);
+  if (q.router.q)
+    launch_route_q8<HC, true>(a, q, kq, st);
+  else
+    launch_route_q8<HC, false>(a, q, kq, st);
 }
 
 template <int HC>
-static hipError_t launch_fused_layer_h(const FusedLayer& a, hipStream_t st) {
+static hipError_t launch_fused_layer_h(const FusedLayer& a, const FaQ8& q, hipStream_t st) {
   const uint32_t I = a.routed.inter;
-  launch_route_fa<HC>(a, st);
+  launch_route_fa<HC>(a, q, st);
   const uint32_t kb = (a.k + (a.shared ? 1u : 0u)) * (I / kFaRW) + 1u;
   if (a.routed.bits == 4)
     launch_gateup_fa<4, HC>(a, kb, st);
@@ -848,12 +955,12 @@ static hipError_t launch_fused_layer_h(const FusedLayer& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-hipError_t launch_fused_layer(const FusedLayer& a, hipStream_t st) {
+hipError_t launch_fused_layer(const FusedLayer& a, hipStream_t st, const FaQ8& q) {
   const uint32_t H = a.hidden;
   if ((H != kFaH && H != 2 * kFaH) || a.n_tokens < 1 || a.n_tokens > kMaxDecodeTokens ||
-      (a.trace && a.n_tokens != 1))
+      (a.trace && a.n_tokens != 1) || (q.gate.q && !q.gate_f32))
     return hipErrorInvalidValue;
-  return H == kFaH ? launch_fused_layer_h<1>(a, st) : launch_fused_layer_h<2>(a, st);
+  return H == kFaH ? launch_fused_layer_h<1>(a, q, st) : launch_fused_layer_h<2>(a, q, st);
 }
 
 }  // namespace smoe

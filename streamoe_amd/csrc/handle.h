@@ -22,6 +22,7 @@ struct smoe_handle {
   float* arg_v = nullptr;     // [kQmvMaxWaves] argmax partial values
   uint32_t* arg_i = nullptr;  // [kQmvMaxWaves] argmax partial indices
   uint32_t* err = nullptr;        // device error word (prefill routing errors)
+  float* gate_row = nullptr;  // [max_hidden] f32 weights of an 8-bit shared gate (three-kernel decode)
   uint32_t max_hidden = 0, max_inter = 0, max_experts = 0;
   // Per-token strides (elements) of logits, act and limbs in the scratch.
   uint32_t lstride = 0, astride = 0, xstride = 0;

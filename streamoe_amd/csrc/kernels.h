@@ -15,8 +15,19 @@ struct QView {
   const uint8_t* codes;
   const uint16_t* scales;
   const uint16_t* biases;
-  uint32_t bits;   // 4 or 3
+  uint32_t bits;   // 4, 3, or 8 (one byte per input: smoe_qmv / smoe_qmm only)
   uint32_t group;  // 32, 64, 128
+};
+
+// 8-bit affine rows (an 8-bit router or shared-expert gate): input c of row
+// r has code q[r * K + c] (byte n of u32 word i: input 4 i + n) and the bf16
+// scale / bias s / b[r * (K / group) + c / group]; its weight is
+// fma(q, s, b). q null: not used.
+struct Q8Rows {
+  const uint8_t* q = nullptr;
+  const uint16_t* s = nullptr;
+  const uint16_t* b = nullptr;
+  uint32_t group = 0;  // 32, 64 or 128
 };
 
 // Byte geometry of one expert blob [gate | up | down], each block
@@ -64,7 +75,9 @@ struct FusedLayer {
   float eps;
   uint32_t* xl;            // x as integer limbs for the expert kernel, hidden / 32 chunks
                            // of kXLimbWords dwords (written by the router kernel)
-  const float* router;     // f32 [E, hidden]
+  const float* router;     // f32 [E, hidden]; with an 8-bit router any readable
+                           // hidden floats (K_B's table wave loads one row as
+                           // a stand-in when there is no gate, and uses none)
   const float* gate;       // f32 [hidden] shared-expert gate, or null (unscaled)
   const uint8_t* experts;  // expert e at experts + e * stride
   uint64_t stride;
@@ -110,7 +123,14 @@ bool fused_supported(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t b
                      uint32_t n_experts, uint32_t k);
 // K_A (router + shared gate/up), K_B (top-k + routed gate/up), K_C (down +
 // combine) on `st`; no allocation, no memset (graph-capturable).
-hipError_t launch_fused_layer(const FusedLayer& a, hipStream_t st);
+// The 8-bit router and / or shared gate of a three-kernel layer (q null:
+// f32): K_A writes the gate's weights as f32 to gate_f32 (hidden floats),
+// which the layer's FusedLayer::gate then names.
+struct FaQ8 {
+  Q8Rows router, gate;
+  float* gate_f32 = nullptr;
+};
+hipError_t launch_fused_layer(const FusedLayer& a, hipStream_t st, const FaQ8& q = FaQ8{});
 
 // Prefill (prefill.hip): limits, arguments and workspace.
 constexpr uint32_t kPfMaxTokens = 1024;
@@ -202,13 +222,15 @@ hipError_t launch_argmax(const float* v, uint32_t n, int32_t* out, float* part_v
                          hipStream_t st);
 
 // logits[t, e] = W[e] . x[t] for e < n_experts; gate_scores[t] =
-// gate_w . x[t] when gate_w is not null.
+// gate_w . x[t] when gate_w is not null. Wq / gq (when their q is set):
+// 8-bit rows in place of W / gate_w.
 // With norm_w, x is the residual: the kernel applies the bf16-weighted
 // RMSNorm itself and writes the normalised rows to x_out.
 hipError_t launch_router_logits(const float* W, const float* gate_w, const float* x,
                                 uint32_t n_tokens, uint32_t n_experts, uint32_t hidden,
                                 float* logits, float* gate_scores, hipStream_t st,
-                                const uint16_t* norm_w = nullptr, float eps = 0.f, float* x_out = nullptr);
+                                const uint16_t* norm_w = nullptr, float eps = 0.f, float* x_out = nullptr,
+                                const Q8Rows& Wq = Q8Rows{}, const Q8Rows& gq = Q8Rows{});
 // Softmax (optional) + running-min top-k + optional renorm, one wave per token.
 hipError_t launch_topk(const float* scores, uint32_t n_tokens, uint32_t n, uint32_t k,
                        bool softmax, bool normalize, const RouteOut& out, hipStream_t st);

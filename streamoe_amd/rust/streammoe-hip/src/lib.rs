@@ -107,6 +107,16 @@ impl QuantWeights<'_> {
             bits: self.bits,
         })
     }
+
+    /// The C view of an 8-bit router or shared gate (`rows` x `hidden`,
+    /// bits 8) for [`MoeLayer::router_q8`] / [`MoeLayer::shared_gate_q8`],
+    /// after the same span checks.
+    pub fn rows_8bit(&self, rows: u32, hidden: u32) -> Result<sys::smoe_qweights, SmoeError> {
+        if self.bits != 8 {
+            return Err(SmoeError { status: sys::SMOE_ERR_UNSUPPORTED_BITS, what: "QuantWeights::rows_8bit" });
+        }
+        self.raw(rows, hidden, "QuantWeights::rows_8bit")
+    }
 }
 
 /// The compiled kernels and their scratch on one GPU (`Kernels` +
@@ -337,8 +347,12 @@ impl KernelCall for ExpertsDecodeCall<'_> {
     }
 }
 
-/// One resident MoE layer (experts at `experts + e * stride`, f32 router,
-/// optional 4-bit shared expert with an optional f32 gate).
+/// One resident MoE layer (experts at `experts + e * stride`, an f32 or
+/// 8-bit router, optional 4-bit shared expert with an optional f32 or 8-bit
+/// gate). Exactly one of `router_w` / `router_q8` is set, at most one of
+/// `shared_gate` / `shared_gate_q8` (the 8-bit forms from
+/// [`QuantWeights::rows_8bit`]; A3B's mlp.gate.weight and
+/// mlp.shared_expert_gate.weight, linear_attn_forward.rs:1300-1301).
 #[derive(Clone, Copy, Debug)]
 pub struct MoeLayer<'a> {
     pub shape: ExpertShape,
@@ -347,9 +361,11 @@ pub struct MoeLayer<'a> {
     pub n_experts: u32,
     pub k: u32,
     pub normalize: bool,
-    pub router_w: &'a BufferRef,
+    pub router_w: Option<&'a BufferRef>,
     pub shared_expert: Option<&'a BufferRef>,
     pub shared_gate: Option<&'a BufferRef>,
+    pub router_q8: Option<sys::smoe_qweights>,
+    pub shared_gate_q8: Option<sys::smoe_qweights>,
 }
 
 impl MoeLayer<'_> {
@@ -361,9 +377,12 @@ impl MoeLayer<'_> {
             n_experts: self.n_experts,
             k: self.k,
             normalize: self.normalize as i32,
-            router_w: self.router_w.ptr as *const f32,
+            router_w: self.router_w.map_or(ptr::null(), |b| b.ptr as *const f32),
             shared_expert: self.shared_expert.map_or(ptr::null(), |b| b.ptr as *const c_void),
             shared_gate: self.shared_gate.map_or(ptr::null(), |b| b.ptr as *const f32),
+            // Point into self: valid while the layer is borrowed for the call.
+            router_q: self.router_q8.as_ref().map_or(ptr::null(), |q| q as *const sys::smoe_qweights),
+            shared_gate_q: self.shared_gate_q8.as_ref().map_or(ptr::null(), |q| q as *const sys::smoe_qweights),
         }
     }
 }

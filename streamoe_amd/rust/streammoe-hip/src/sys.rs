@@ -72,6 +72,8 @@ pub struct smoe_layer {
     pub router_w: *const f32,
     pub shared_expert: *const c_void,
     pub shared_gate: *const f32,
+    pub router_q: *const smoe_qweights,
+    pub shared_gate_q: *const smoe_qweights,
 }
 
 #[repr(C)]
