@@ -43,6 +43,9 @@ extern "C" {
 #endif
 
 #define SMOE_MAX_K 16 /* expert_forward.rs:117 (MAX_K) */
+/* smoe_abi_version() of a library built from this header; 2: smoe_layer
+ * gained router_q / shared_gate_q. */
+#define SMOE_ABI_VERSION 2
 
 typedef enum {
   SMOE_OK = 0,

@@ -12,6 +12,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("SMOE_LIB") or os.path.join(HERE, "libsmoe.so")
 
 SMOE_MAX_K = 16
+SMOE_ABI_VERSION = 2  # the struct layouts below (include/smoe.h SMOE_ABI_VERSION)
 
 STATUS = {
     0: "SMOE_OK",
@@ -158,6 +159,9 @@ def load():
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
+    if lib.smoe_abi_version() != SMOE_ABI_VERSION:
+        raise ImportError(f"{LIB_PATH} has ABI version {lib.smoe_abi_version()}, these bindings "
+                          f"{SMOE_ABI_VERSION}; rebuild it (python streamoe_amd/build.py)")
     _lib = lib
     return lib
 

@@ -15,7 +15,7 @@ using namespace smoe;
 
 namespace {
 
-constexpr uint32_t kAbiVersion = 2;
+constexpr uint32_t kAbiVersion = SMOE_ABI_VERSION;
 
 int hip_status(hipError_t e) { return e == hipSuccess ? SMOE_OK : SMOE_ERR_HIP; }
 

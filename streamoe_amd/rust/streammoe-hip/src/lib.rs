@@ -130,6 +130,11 @@ unsafe impl Send for Kernels {}
 impl Kernels {
     /// `Kernels::new`: a handle on `device` enqueueing on `stream`.
     pub fn new(device: i32, stream: HipStream) -> Result<Kernels, SmoeError> {
+        // The library's struct layouts must be the ones sys.rs declares.
+        // SAFETY: no arguments.
+        if unsafe { sys::smoe_abi_version() } != sys::SMOE_ABI_VERSION {
+            return Err(SmoeError { status: sys::SMOE_ERR_INVALID_ARG, what: "smoe_abi_version" });
+        }
         let mut h = ptr::null_mut();
         // SAFETY: `h` is a valid out pointer.
         check(unsafe { sys::smoe_create(device, stream.0, &mut h) }, "smoe_create")?;

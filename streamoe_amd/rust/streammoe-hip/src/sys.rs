@@ -7,6 +7,7 @@
 use std::os::raw::{c_char, c_int, c_void};
 
 pub const SMOE_MAX_K: u32 = 16;
+pub const SMOE_ABI_VERSION: u32 = 2;
 
 pub const SMOE_OK: c_int = 0;
 pub const SMOE_ERR_INVALID_ARG: c_int = 1;

@@ -69,6 +69,7 @@ def header_api():
         structs[m.group(2)] = fields
     consts = {k: int(v) for k, v in re.findall(r"\b(SMOE_(?:OK|ERR_\w+|OPT_\w+))\s*=\s*(\d+)", src)}
     consts["SMOE_MAX_K"] = int(re.search(r"#define\s+SMOE_MAX_K\s+(\d+)", src).group(1))
+    consts["SMOE_ABI_VERSION"] = int(re.search(r"#define\s+SMOE_ABI_VERSION\s+(\d+)", src).group(1))
     return funcs, structs, consts
 
 
