@@ -1419,6 +1419,7 @@ struct Gu64 {
   static constexpr int NWC = 8, NWD = 4, NWT = NWC + NWD;  // compute, copy, all waves
   static constexpr int G = 64, KC = 256, CG = KC / G;       // inputs per chunk, groups per chunk
   static constexpr int NCOL = 128, ROWS = 2 * NCOL;         // output columns, weight rows per unit
+  static constexpr uint32_t SMALL = 16;                     // units of <= SMALL rows take 16-row tiles (gate/up)
   static constexpr int RB = KC / 2;                         // code bytes per row and chunk
   // Three rings: codes two chunks ahead; token rows and their group sums
   // one chunk ahead (they come from L2); scales and biases per chunk pair,
@@ -1449,6 +1450,18 @@ struct Gu64 {
   static_assert(EX <= BQ_SLOT, "exchange fits a code slot");
   static_assert(LDS <= 160 * 1024, "LDS per CU");
 };
+
+// The activation group sums of a finished gate/up unit from the row-sum
+// buffer: [column wave][32 rows] after 32 x 32 tiles, [column wave][k half]
+// [16 rows] after 16-row tiles; lane (m, gq) = (row, 64-column group).
+__device__ __forceinline__ void gu64_flush_asum(const float* ps, float* asum_out, uint32_t lane, uint32_t start,
+                                                uint32_t cnt, uint32_t cb, bool small, uint32_t groups) {
+  const uint32_t m = lane & 31, gq = lane >> 5;
+  if (m < cnt)
+    asum_out[(size_t)(start + m) * groups + cb * 2 + gq] =
+        small ? (ps[(4 * gq) * 16 + m] + ps[(4 * gq + 1) * 16 + m]) + (ps[(4 * gq + 2) * 16 + m] + ps[(4 * gq + 3) * 16 + m])
+              : ps[(2 * gq) * 32 + m] + ps[(2 * gq + 1) * 32 + m];
+}
 
 template <bool DOWN>
 __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint32_t* __restrict__ items,
@@ -1528,6 +1541,7 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
     uint32_t s;            // from the blob, copy 0
     uint32_t ar[C::N_A];   // from x_hi (token row + part)
     uint32_t xs;           // from xsum
+    bool small;            // a unit of <= 16 rows: rows 16-31 are not copied
   };
   auto srcc_of = [=](const Unit& u) {
     SrcC r;
@@ -1543,6 +1557,7 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
     const uint32_t mat = DOWN ? 0u : dw >= 2;
     const uint32_t row0 = DOWN ? u.cb * C::ROWS + 64 * dw : u.cb * C::NCOL + 64 * (dw & 1u);
     r.s = (uint32_t)((mat ? so1 : so0) + (lane & 1u) * bso) + (row0 + lane / 2) * ng * 2;
+    r.small = !DOWN && u.cnt <= C::SMALL;
     if constexpr (DOWN) {
       // Entry rows past the item's count repeat its last row.
       const uint32_t last = u.cnt - 1;
@@ -1576,9 +1591,11 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
   auto issue_a = [=](const SrcA& r, uint32_t c, uint32_t slot, bool pair, uint32_t sslot) {
     uint8_t* st = lds + C::OFF_A + slot * C::A_SLOT;
     const uint8_t* ab = xh + (size_t)c * C::KC * 2;
+    if (!r.small || dw < 2) {  // copy waves 2 and 3 hold rows 16-31
 #pragma unroll
-    for (int i = 0; i < C::N_A; ++i) dma16(ab + r.ar[i], st + (dw * C::N_A + i) * 64 * 16);
-    if (lane < 8) dma16(xsum + (size_t)c * C::CG * 4 + r.xs, st + C::A_BYTES + 8 * dw * 16);
+      for (int i = 0; i < C::N_A; ++i) dma16(ab + r.ar[i], st + (dw * C::N_A + i) * 64 * 16);
+      if (lane < 8) dma16(xsum + (size_t)c * C::CG * 4 + r.xs, st + C::A_BYTES + 8 * dw * 16);
+    }
     if (pair) {
       uint8_t* ss = lds + C::OFF_S + sslot * C::S_SLOT;
       const uint8_t* sb = r.blob + (size_t)c * C::CG * 2;
@@ -1588,46 +1605,39 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
     }
   };
 
-  f32x16 tot[2];
-  tot[0] = f32x16{};
-  tot[1] = f32x16{};
   // The first unit's token ids, visible to every wave before its copies.
   if (!DOWN && copier) token_dma(0, 0);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  // Issue positions: token rows and scales (unit au, chunk ac, token
-  // buffer apar) one chunk ahead of the compute position, codes (unit qu,
-  // chunk qc) two chunks ahead. The next unit's token ids are copied when
-  // the first issue position enters a unit.
-  uint32_t au = 0, ac = 0, apar = 0, aiss = 0;
-  uint32_t qu = 0, qc = 0, qiss = 0;
-  SrcA srca{};
-  SrcC srcc{};
-  uint32_t cc = 0, cu = 0;
-  Unit ucur = unit(0);
-  // Activation row sums of the last finished unit, written out by wave 0
-  // after the next block barrier.
-  bool ps_pend = false;
-  uint32_t ps_start = 0, ps_cnt = 0, ps_cb = 0;
-  // Iterations -2 and -1 only issue (the prologue); iteration j >= 0 waits
-  // for chunk j (its codes, issued two iterations earlier, and its token
-  // rows, issued one earlier before the next chunk's codes: N_BQ copies
-  // follow them), issues chunk j + 1's token rows and chunk j + 2's codes,
-  // and computes chunk j.
-  for (int jj = -2; jj < (int)total; ++jj) {
-    const uint32_t j = (uint32_t)jj;
-    if (jj >= 0) {
-      if (!copier)
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      else if (j + 1 < total)
-        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(C::N_BQ) : "memory");
-      else
-        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-      __builtin_amdgcn_s_barrier();
-      asm volatile("" ::: "memory");
-    }
-    if (copier) {
+  // The copy waves and the compute waves run loops of their own over the
+  // same chunk sequence and meet at the same block barriers: one per chunk
+  // j >= 0 (chunk j has landed), two more after a unit's last chunk (the K
+  // halves' exchange), one after the loop. Separate loops keep each role's
+  // loop-carried registers out of the other's.
+  if (copier) {
+    // Issue positions: token rows and scales (unit au, chunk ac, token
+    // buffer apar) one chunk ahead of the compute position, codes (unit
+    // qu, chunk qc) two chunks ahead. The next unit's token ids are copied
+    // when the first issue position enters a unit. Iterations -2 and -1
+    // only issue (the prologue); iteration j >= 0 waits for chunk j's
+    // copies (its codes, issued two iterations earlier, and its token rows,
+    // issued one earlier before the next chunk's codes: N_BQ copies follow
+    // them), then issues chunk j + 1's token rows and chunk j + 2's codes.
+    uint32_t au = 0, ac = 0, apar = 0, aiss = 0;
+    uint32_t qu = 0, qc = 0, qiss = 0, cc = 0;
+    SrcA srca{};
+    SrcC srcc{};
+    for (int jj = -2; jj < (int)total; ++jj) {
+      const uint32_t j = (uint32_t)jj;
+      if (jj >= 0) {
+        if (j + 1 < total)
+          asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(C::N_BQ) : "memory");
+        else
+          asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+      }
       bool tok_next = false;
       if (jj >= -1 && aiss < total) {
         if (ac == 0) {
@@ -1641,38 +1651,146 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
         issue_codes(srcc, qc, qiss % C::SC);
       }
       if (tok_next) token_dma(au + 1, apar ^ 1u);
-    }
-    if (jj >= -1 && aiss < total) {
-      ++aiss;
-      if (++ac == nch) {
-        ac = 0;
-        ++au;
-        apar ^= 1u;
+      if (jj >= -1 && aiss < total) {
+        ++aiss;
+        if (++ac == nch) {
+          ac = 0;
+          ++au;
+          apar ^= 1u;
+        }
+      }
+      if (qiss < total) {
+        ++qiss;
+        if (++qc == nch) {
+          qc = 0;
+          ++qu;
+        }
+      }
+      // The compute waves' exchange barriers after a unit's last chunk.
+      if (jj >= 0 && ++cc == nch) {
+        cc = 0;
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
       }
     }
-    if (qiss < total) {
-      ++qiss;
-      if (++qc == nch) {
-        qc = 0;
-        ++qu;
-      }
-    }
-    if (jj < 0) continue;
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    return;
+  }
+  f32x16 tot[2];
+  tot[0] = f32x16{};
+  tot[1] = f32x16{};
+  // Partial sums of the 16-row tiles (t, h) of a small unit.
+  f32x4 ts[2][2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) ts[t][h] = f32x4{0.f, 0.f, 0.f, 0.f};
+  uint32_t cc = 0, cu = 0;
+  Unit ucur = unit(0);
+  // Activation row sums of the last finished unit, written out by wave 0
+  // after the next block barrier.
+  bool ps_pend = false, ps_small = false;
+  uint32_t ps_start = 0, ps_cnt = 0, ps_cb = 0;
+  for (uint32_t j = 0; j < total; ++j) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
     if (ps_pend) {
-      if (wave == 0) {
-        const float* ps = reinterpret_cast<const float*>(lds + C::OFF_PS);
-        const uint32_t m = lane & 31, gq = lane >> 5;  // group of 64 columns within the unit
-        if (m < ps_cnt)
-          asum_out[(size_t)(ps_start + m) * (N / C::G) + ps_cb * 2 + gq] = ps[(2 * gq) * 32 + m] + ps[(2 * gq + 1) * 32 + m];
-      }
+      if (wave == 0)
+        gu64_flush_asum(reinterpret_cast<const float*>(lds + C::OFF_PS), asum_out, lane, ps_start, ps_cnt, ps_cb,
+                        ps_small, N / C::G);
       ps_pend = false;
     }
     const uint8_t* st = lds + C::OFF_BQ + (j % C::SC) * C::BQ_SLOT;      // codes
     const uint8_t* sa = lds + C::OFF_A + (j & 1u) * C::A_SLOT;            // token rows, x sums
     const uint8_t* ss = lds + C::OFF_S + ((j >> 1) & 1u) * C::S_SLOT;     // scales, biases
-    if (!copier) {
+    const bool small = !DOWN && ucur.cnt <= C::SMALL;
+    if (small) {
+      // A unit of <= 16 rows: v_mfma_f32_16x16x32_bf16 tiles (t, h) =
+      // columns 16 h .. 16 h + 15 of the wave's 32 in matrix t, rows 0-15;
+      // lane (c16, kb) = (A row / output column l % 16, 8-input block
+      // l / 16 of the 32 per step). The same codes and A parts as the
+      // 32 x 32 tiles, half the MFMA work; partial sums in ts[t][h][i]
+      // (row 4 kb + i). The lane's LDS offsets are formed here per chunk
+      // (the opaque lane value keeps the compiler from hoisting them out of
+      // the loop, where both tile paths' offsets would not fit in the
+      // registers together).
+      uint32_t lv = lane;
+      asm volatile("" : "+v"(lv));
+      const uint32_t c16 = lv & 15, kb = lv >> 4;
+      uint32_t sw[2][2], bw[2][2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t row = t * C::NCOL + 32 * cw + 16 * h + c16;
+          const uint32_t* sp = reinterpret_cast<const uint32_t*>(ss + row * 32 + 8 * (j & 1u) + 4 * kh);
+          sw[t][h] = sp[0];
+          bw[t][h] = sp[4];
+        }
+#pragma unroll
+      for (int gi = 0; gi < 2; ++gi) {
+        const uint32_t g = 2 * kh + gi;
+        u32x4 af[2];
+        uint32_t bq[2][2][2];
+        const uint8_t* ar = sa + c16 * (C::KC * 2);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) af[u] = *reinterpret_cast<const u32x4*>(ar + (((8 * g + 4 * u + kb) ^ c16) * 16));
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const uint32_t row = t * C::NCOL + 32 * cw + 16 * h + c16;
+              bq[u][t][h] = *reinterpret_cast<const uint32_t*>(st + row * C::RB + (((2 * g + u) ^ (row & 7u)) * 16) + 4 * kb);
+            }
+        f32x4 acc[2][2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) acc[t][h] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) acc[t][h] = mfma(af[u], codes_bf16_4p(bq[u][t][h], c43), acc[t][h]);
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const float s = bf16f((uint16_t)(sw[t][h] >> (16 * gi)));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) ts[t][h][i] = __builtin_fmaf(s, acc[t][h][i], ts[t][h][i]);
+          }
+      }
+      // Dequant term: one v_mfma_f32_16x16x4_f32 per tile over the chunk's
+      // four groups, lane (., kb) supplying group kb; the other k half's two
+      // groups enter as zeros.
+      const bool mine = (kb >> 1) == kh;
+      const float xa = mine ? reinterpret_cast<const float*>(sa + C::A_BYTES)[c16 * C::CG + kb] : 0.f;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t sh = 16 * (kb & 1u);
+          const float cbv =
+              mine ? __builtin_fmaf(-128.0f, bf16f((uint16_t)(sw[t][h] >> sh)), bf16f((uint16_t)(bw[t][h] >> sh))) : 0.f;
+          ts[t][h] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, cbv, ts[t][h], 0, 0, 0);
+        }
+    } else {
       // Scales and biases of this wave's two groups for both tiles: bf16
-      // pairs (group 2 kh, 2 kh + 1).
+      // pairs (group 2 kh, 2 kh + 1). Lane offsets formed per chunk, as in
+      // the 16-row path.
+      uint32_t lv = lane;
+      asm volatile("" : "+v"(lv));
+      const uint32_t c32 = lv & 31, kq = lv >> 5;
       uint32_t sw[2], bw[2];
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
@@ -1732,7 +1850,14 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
       float* ex = reinterpret_cast<float*>(const_cast<uint8_t*>(st));
-      if (!copier) {
+      if (small) {
+        // 16-row tiles: wave kh finishes column half kh of both matrices.
+        float* xo = ex + (cw * 2 + (kh ^ 1u)) * 16 * 64 + lane;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) xo[(t * 4 + i) * 64] = kh ? ts[t][0][i] : ts[t][1][i];
+      } else {
         float* xo = ex + (cw * 2 + (kh ^ 1u)) * 16 * 64 + lane;
         const uint32_t vo = 8 * (kh ^ 1u);
 #pragma unroll
@@ -1743,7 +1868,7 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
-      if (DOWN && !copier) {
+      if (DOWN) {
         const float* xi = ex + (cw * 2 + kh) * 16 * 64 + lane;
         const uint32_t vm = 8 * kh;
         const uint32_t col = cb * C::ROWS + 32 * cw + c32;
@@ -1757,7 +1882,33 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
             o[C::NCOL] = tot[1][v] + xi[(8 + i) * 64];
           }
         }
-      } else if (!copier) {
+      } else if (small) {
+        const float* xi = ex + (cw * 2 + kh) * 16 * 64 + lane;
+        uint32_t lv = lane;
+        asm volatile("" : "+v"(lv));
+        const uint32_t c16 = lv & 15, kb = lv >> 4;
+        const uint32_t col = cb * C::NCOL + 32 * cw + 16 * kh + c16;
+        const uint32_t pc = (col & ~7u) + perm8_pos(col & 7u);
+        float rs[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t m = 4 * kb + i;
+          const float g = (kh ? ts[0][1][i] : ts[0][0][i]) + xi[i * 64];
+          const float u = (kh ? ts[1][1][i] : ts[1][0][i]) + xi[(4 + i) * 64];
+          const _Float16 h = (_Float16)silu_mul(g, u);
+          if (m < cnt) act_out[(size_t)(start + m) * N + pc] = __builtin_bit_cast(uint16_t, h);
+          rs[i] = (float)h;
+        }
+        // Row sums over the wave's 16 columns (a 16-lane row), into
+        // [column wave][k half][16 rows].
+#pragma unroll
+        for (int i = 0; i < 4; ++i) rs[i] = row_sum16_all(rs[i]);
+        if (c16 == 0) {
+          float* ps = reinterpret_cast<float*>(lds + C::OFF_PS) + (cw * 2 + kh) * 16;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) ps[4 * kb + i] = rs[i];
+        }
+      } else {
         const float* xi = ex + (cw * 2 + kh) * 16 * 64 + lane;
         const uint32_t vm = 8 * kh;
         const uint32_t col = cb * C::NCOL + 32 * cw + c32;
@@ -1788,23 +1939,25 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
         }
       }
       ps_pend = !DOWN;
+      ps_small = small;
       ps_start = start;
       ps_cnt = cnt;
       ps_cb = cb;
       tot[0] = f32x16{};
       tot[1] = f32x16{};
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) ts[t][h] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
   }
-  // The last unit's sums (every wave leaves the loop after the same chunk).
+  // The last unit's sums (every wave leaves its loop after the same chunk).
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  if (ps_pend && wave == 0) {
-    const float* ps = reinterpret_cast<const float*>(lds + C::OFF_PS);
-    const uint32_t m = lane & 31, gq = lane >> 5;
-    if (m < ps_cnt)
-      asum_out[(size_t)(ps_start + m) * (N / C::G) + ps_cb * 2 + gq] = ps[(2 * gq) * 32 + m] + ps[(2 * gq + 1) * 32 + m];
-  }
+  if (ps_pend && wave == 0)
+    gu64_flush_asum(reinterpret_cast<const float*>(lds + C::OFF_PS), asum_out, lane, ps_start, ps_cnt, ps_cb, ps_small,
+                    N / C::G);
 }
 
 // Group sums of the fp16 activations per entry; one block per entry.
