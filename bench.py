@@ -63,7 +63,7 @@ CONFIGS = {
 # profiles/prefill_c4_a3b_4bit.md (the four prefill launches of one layer).
 # None where no counter pass was taken (multi-token decode, per-phase path).
 MEASURED_TRAFFIC = {"c0": 29_732_534, "c2": 18_897_532, "c3": 15_786_871, "c1": 175_922_937,
-                    "c4": 571_822_881, "c5": 87_783_971}
+                    "c4": 558_268_246, "c5": 87_783_971}
 
 
 def stream_read_peak(dev, gib=4):
@@ -633,14 +633,18 @@ def run_prefill(args, c):
         sa.check(_sync_status(kern), "smoe_sync")
         return e0.elapsed_time(e1) * 1e3 / args.steps, graph
 
-    # The other gate/up tile on the same inputs (its own graph), for
+    # The other tile choices on the same inputs (their own graphs), for
     # comparison; timed first, so that the reported value does not carry
     # the clock ramp of the first timed loop.
-    kern.set_prefill_gemm(0 if args.prefill_gemm == "16x16" else 1)
-    us_other, _ = time_steps(step)
-    kern.set_prefill_gemm(1 if args.prefill_gemm == "16x16" else 0)
+    main_opt = 1 if args.prefill_gemm == "16x16" else 0
+    us_other = {}
+    for opt, label in ((0, "32x32"), (1, "16x16"), (2, "32x32 gate/up, 16x16 down")):
+        if opt != main_opt and not args.main_only:
+            kern.set_prefill_gemm(opt)
+            us_other[label] = round(time_steps(step)[0], 2)
+    kern.set_prefill_gemm(main_opt)
     us, graph = time_steps(step)
-    us_blk, _ = time_steps(step_block)
+    us_blk = None if args.main_only else time_steps(step_block)[0]
     hit = np.unique(idx)
     nbytes = len(hit) * stride + n * H * 2 + n * H * 4  # weights of hit experts + bf16 X + f32 Y
     flops = 2 * n * k * (2 * H * I + I * H)
@@ -663,16 +667,20 @@ def run_prefill(args, c):
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": MEASURED_TRAFFIC.get("c4"),
                      "unit_of_work": f"one layer: {nbytes} algorithmic bytes ({len(hit)} hit experts x {stride} "
                                      f"+ X + Y), {flops} flops",
-                     "kernel": ("prefill layer: k_pf_route (+ per-token x preparation) + k_pf_gu64 (gate/up on 32x32 tiles, "
-                                "with the activation group sums) + k_pf_mm (down) + k_pf_combine (one HIP graph)")
+                     "kernel": ("prefill layer: k_pf_route (+ per-token x preparation) + k_pf_gu64<false> (gate/up on "
+                                "32x32 tiles, 16x16 for units of <= 16 rows, with the activation group sums) + "
+                                "k_pf_gu64<true> (down, the same tiles) + k_pf_combine (one HIP graph)")
                                if args.prefill_gemm == "auto" else
                                ("prefill layer: k_pf_route (+ per-token x preparation) + k_pf_mm (gate/up on 16x16 "
                                 "tiles, with the activation group sums) + k_pf_mm (down) + k_pf_combine (one HIP graph)")},
-        "gate_up_tile": "32x32" if args.prefill_gemm == "auto" else "16x16",
-        "other_tile_us_per_layer": {"16x16" if args.prefill_gemm == "auto" else "32x32": round(us_other, 2)},
+        "gemm_tiles": "32x32" if args.prefill_gemm == "auto" else "16x16",
+        "other_tiles_us_per_layer": us_other,
     }
     blk_bytes = nbytes + slay.expert_size + 2 * n * H * 4  # + shared expert, h_mid read, gate
     blk_flops = flops + 2 * n * (2 * H * I + I * H)
+    if args.main_only:
+        kern.close()
+        return out_d
     out_d["block_variant"] = {
         "what": "smoe_moe_prefill_block: the same routed experts plus a 4-bit shared expert over all tokens (extra "
                 "work items of the same grouped GEMMs), its f32 sigmoid gate and the residual "
@@ -726,8 +734,11 @@ def main():
                     help="decode path: auto (three-kernel where supported), kernels (one per phase), "
                          "fused (three-kernel only)")
     ap.add_argument("--prefill-gemm", default="auto", choices=["auto", "16x16"],
-                    help="c4: the default gate/up tile (32x32 where it applies) or the 16x16 one "
-                         "(SMOE_OPT_PREFILL_GEMM = 1); the other one is timed beside it")
+                    help="c4: the default GEMM tiles (32x32 where they apply) or the 16x16 ones "
+                         "(SMOE_OPT_PREFILL_GEMM = 1); the other choices are timed beside it")
+    ap.add_argument("--main-only", action="store_true",
+                    help="c4: time the default tiles only (no other tiles, no block variant, no CPU leg): for "
+                         "profiler runs whose per-kernel figures must come from the reported configuration")
     ap.add_argument("--eager", action="store_true", help="launch every step eagerly instead of replaying a HIP graph")
     ap.add_argument("--trace", action="store_true", help="report per-phase times from in-kernel timestamps")
     ap.add_argument("--no-cpu", action="store_true")

@@ -75,14 +75,15 @@ typedef enum {
                                 words (kernel, block, point); prefill: 8 words
                                 (phase ends of the bucketing kernel). Diagnostics
                                 only. */
-  SMOE_OPT_PREFILL_GEMM = 3  /* prefill GEMM tiles: 0 auto (default: gate/up on
-                                32 x 32 MFMA tiles over 128-column units for
-                                4-bit group-64 experts over bf16 x, else 16 x
-                                16 tiles over 64-column units; down on 16 x 16
-                                tiles), 1 the 16 x 16 tiles always, 2 as 0
-                                with the down GEMM also on 32 x 32 tiles
-                                (256-column units; 4-bit group-64 experts,
-                                inter a multiple of 512). All give the same
+  SMOE_OPT_PREFILL_GEMM = 3  /* prefill GEMM tiles: 0 auto (default: for 4-bit
+                                group-64 experts, gate/up on 32 x 32 MFMA tiles
+                                over 128-column units (bf16 x, hidden a
+                                multiple of 512) and down on 32 x 32 tiles over
+                                256-column units (inter a multiple of 512),
+                                units of <= 16 rows on 16 x 16 tiles; else
+                                16 x 16 tiles over 64-column units), 1 the
+                                16 x 16 tiles always, 2 as 0 with the down
+                                GEMM on the 16 x 16 tiles. All give the same
                                 results up to fp32 rounding order. */
 } smoe_option;
 

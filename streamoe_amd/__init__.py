@@ -153,8 +153,8 @@ class Kernels:
         self.set_option(_abi.SMOE_OPT_DECODE_PATH, path)
 
     def set_prefill_gemm(self, path):
-        """0 auto (32 x 32 gate/up tiles where they apply), 1 k_pf_mm only, 2 as 0 with the down GEMM on
-        32 x 32 tiles too (SMOE_OPT_PREFILL_GEMM)."""
+        """0 auto (32 x 32 gate/up and down tiles where they apply), 1 k_pf_mm only, 2 as 0 with the down
+        GEMM on k_pf_mm (SMOE_OPT_PREFILL_GEMM)."""
         self.set_option(_abi.SMOE_OPT_PREFILL_GEMM, path)
 
     def reserve(self, max_hidden, max_inter, max_experts):

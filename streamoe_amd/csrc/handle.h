@@ -29,7 +29,7 @@ struct smoe_handle {
   // Options.
   int decode_path = 0;  // 0 auto, 1 per-phase kernels, 3 three-kernel
   uint64_t* trace = nullptr;
-  int prefill_gemm = 0;  // 0 the 32 x 32 gate/up tile where it applies, 1 k_pf_mm only
+  int prefill_gemm = 0;  // SMOE_OPT_PREFILL_GEMM: 0 the 32 x 32 tiles where they apply, 1 k_pf_mm only, 2 down on k_pf_mm
   // File loader: two pinned host staging buffers (allocated on first use,
   // freed by smoe_destroy) and the events that say when a copy out of
   // each has finished.

@@ -179,7 +179,7 @@ struct PfArgs {
   uint32_t* sn_items;
   uint32_t* sitem_tok;
   uint32_t* sxr;
-  int gemm_path;           // 0: the 32 x 32 gate/up tile where it applies, 1: k_pf_mm only, 2: 32 x 32 gate/up and down tiles
+  int gemm_path;           // 0: the 32 x 32 gate/up and down tiles where they apply, 1: k_pf_mm only, 2: down on k_pf_mm
 };
 
 // Workspace bytes for these sizes; with `a` and `base`, also points a's

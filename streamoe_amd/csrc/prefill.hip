@@ -1419,7 +1419,7 @@ struct Gu64 {
   static constexpr int NWC = 8, NWD = 4, NWT = NWC + NWD;  // compute, copy, all waves
   static constexpr int G = 64, KC = 256, CG = KC / G;       // inputs per chunk, groups per chunk
   static constexpr int NCOL = 128, ROWS = 2 * NCOL;         // output columns, weight rows per unit
-  static constexpr uint32_t SMALL = 16;                     // units of <= SMALL rows take 16-row tiles (gate/up)
+  static constexpr uint32_t SMALL = 16;                     // units of <= SMALL rows take 16-row tiles
   static constexpr int RB = KC / 2;                         // code bytes per row and chunk
   // Three rings: codes two chunks ahead; token rows and their group sums
   // one chunk ahead (they come from L2); scales and biases per chunk pair,
@@ -1557,7 +1557,7 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
     const uint32_t mat = DOWN ? 0u : dw >= 2;
     const uint32_t row0 = DOWN ? u.cb * C::ROWS + 64 * dw : u.cb * C::NCOL + 64 * (dw & 1u);
     r.s = (uint32_t)((mat ? so1 : so0) + (lane & 1u) * bso) + (row0 + lane / 2) * ng * 2;
-    r.small = !DOWN && u.cnt <= C::SMALL;
+    r.small = u.cnt <= C::SMALL;
     if constexpr (DOWN) {
       // Entry rows past the item's count repeat its last row.
       const uint32_t last = u.cnt - 1;
@@ -1709,9 +1709,9 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
     const uint8_t* st = lds + C::OFF_BQ + (j % C::SC) * C::BQ_SLOT;      // codes
     const uint8_t* sa = lds + C::OFF_A + (j & 1u) * C::A_SLOT;            // token rows, x sums
     const uint8_t* ss = lds + C::OFF_S + ((j >> 1) & 1u) * C::S_SLOT;     // scales, biases
-    const bool small = !DOWN && ucur.cnt <= C::SMALL;
+    const bool small = ucur.cnt <= C::SMALL;
     if (small) {
-      // A unit of <= 16 rows: v_mfma_f32_16x16x32_bf16 tiles (t, h) =
+      // A unit of <= 16 rows: 16 x 16 x 32 MFMA tiles (bf16; down: f16) (t, h) =
       // columns 16 h .. 16 h + 15 of the wave's 32 in matrix t, rows 0-15;
       // lane (c16, kb) = (A row / output column l % 16, 8-input block
       // l / 16 of the 32 per step). The same codes and A parts as the
@@ -1760,12 +1760,17 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
 #pragma unroll
           for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int h = 0; h < 2; ++h) acc[t][h] = mfma(af[u], codes_bf16_4p(bq[u][t][h], c43), acc[t][h]);
+            for (int h = 0; h < 2; ++h) {
+              if constexpr (DOWN)
+                acc[t][h] = mfma_f16(af[u], codes_f16_4p(bq[u][t][h]), acc[t][h]);
+              else
+                acc[t][h] = mfma(af[u], codes_bf16_4p(bq[u][t][h], c43), acc[t][h]);
+            }
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
-            const float s = bf16f((uint16_t)(sw[t][h] >> (16 * gi)));
+            const float s = (DOWN ? 64.0f : 1.0f) * bf16f((uint16_t)(sw[t][h] >> (16 * gi)));
 #pragma unroll
             for (int i = 0; i < 4; ++i) ts[t][h][i] = __builtin_fmaf(s, acc[t][h][i], ts[t][h][i]);
           }
@@ -1781,7 +1786,8 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
         for (int h = 0; h < 2; ++h) {
           const uint32_t sh = 16 * (kb & 1u);
           const float cbv =
-              mine ? __builtin_fmaf(-128.0f, bf16f((uint16_t)(sw[t][h] >> sh)), bf16f((uint16_t)(bw[t][h] >> sh))) : 0.f;
+              mine ? __builtin_fmaf(DOWN ? -64.0f : -128.0f, bf16f((uint16_t)(sw[t][h] >> sh)), bf16f((uint16_t)(bw[t][h] >> sh)))
+                   : 0.f;
           ts[t][h] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, cbv, ts[t][h], 0, 0, 0);
         }
     } else {
@@ -1868,7 +1874,22 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
-      if (DOWN) {
+      if (DOWN && small) {
+        const float* xi = ex + (cw * 2 + kh) * 16 * 64 + lane;
+        uint32_t lv = lane;
+        asm volatile("" : "+v"(lv));
+        const uint32_t c16 = lv & 15, kb = lv >> 4;
+        const uint32_t col = cb * C::ROWS + 32 * cw + 16 * kh + c16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t m = 4 * kb + i;
+          if (m < cnt) {
+            float* o = down_out + (size_t)(start + m) * N + col;
+            o[0] = (kh ? ts[0][1][i] : ts[0][0][i]) + xi[i * 64];
+            o[C::NCOL] = (kh ? ts[1][1][i] : ts[1][0][i]) + xi[(4 + i) * 64];
+          }
+        }
+      } else if (DOWN) {
         const float* xi = ex + (cw * 2 + kh) * 16 * 64 + lane;
         const uint32_t vm = 8 * kh;
         const uint32_t col = cb * C::ROWS + 32 * cw + c32;
@@ -2152,8 +2173,8 @@ static hipError_t launch_gemms(const PfArgs& a, uint32_t row0, uint32_t n_rows, 
   const uint32_t gu_units = a.max_items * (a.g.inter / 64);
   hipError_t e;
   // The 32 x 32 tiles take the chunks of a unit in pairs (their scales
-  // come per pair): K a multiple of 512. Gate/up on them by default, down
-  // on them with gemm_path 2.
+  // come per pair): K a multiple of 512. Gate/up and down on them by
+  // default; gemm_path 2 keeps the down GEMM on k_pf_mm.
   const bool tiles32 = BITS == 4 && G == 64 && a.gemm_path != 1;
   if (tiles32 && a.x_bf16 && a.g.inter % Gu64::NCOL == 0 && a.g.hidden % (2 * Gu64::KC) == 0)
     e = launch_gu64<false>(a, a.max_items * (a.g.inter / Gu64::NCOL), n_cu, st);
@@ -2167,7 +2188,7 @@ static hipError_t launch_gemms(const PfArgs& a, uint32_t row0, uint32_t n_rows, 
   // With G <= 64 the gate/up GEMM writes the activation group sums itself.
   if (G > 64) hipLaunchKernelGGL(k_pf_act_sum, dim3(n_rows), dim3(256), 0, st, a, row0);
   const uint32_t dn_units = a.max_items * (a.g.hidden / 256);
-  if (tiles32 && a.gemm_path == 2 && a.g.hidden % Gu64::ROWS == 0 && a.g.inter % (2 * Gu64::KC) == 0)
+  if (tiles32 && a.gemm_path != 2 && a.g.hidden % Gu64::ROWS == 0 && a.g.inter % (2 * Gu64::KC) == 0)
     return launch_gu64<true>(a, a.max_items * (a.g.hidden / Gu64::ROWS), n_cu, st);
   if (G == 64 && a.g.inter == 512) return launch_mm<BITS, G, 2, false, G == 64 ? 512 : 0>(a, dn_units, n_cu, st);
   return launch_mm<BITS, G, 2, false, 0>(a, dn_units, n_cu, st);

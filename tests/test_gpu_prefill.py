@@ -103,15 +103,15 @@ def test_prefill_matches_oracle(kernels, name, n, H, I, E, k, bits, group, x_bf1
     ("hot-expert", 200, 2048, 512, 64, 8, "hot"),
     ("olmoe-inter1024", 64, 2048, 1024, 64, 8, "zipf"),
     ("h1024-k4", 40, 1024, 512, 32, 4, "zipf"),
-    ("inter768", 48, 2048, 768, 32, 8, "zipf"),  # down on 16 x 16 tiles under every option
+    ("inter768", 48, 2048, 768, 32, 8, "zipf"),  # down on k_pf_mm under every option
 ])
 def test_prefill_gate_up_tiles_agree(kernels, name, n, H, I, E, k, routing):
     """The GEMM tile choices of SMOE_OPT_PREFILL_GEMM on the same inputs:
-    0 (gate/up on 32 x 32 tiles, the default for 4-bit group-64 experts
-    over bf16 x), 1 (16 x 16 tiles only) and 2 (gate/up and down on 32 x 32
-    tiles) each meet the oracle bar and agree with each other to fp32
-    rounding-order differences (and the fp16 rounding of the activations
-    they feed)."""
+    0 (gate/up and down on 32 x 32 tiles, units of <= 16 rows on 16 x 16
+    ones: the default for 4-bit group-64 experts over bf16 x), 1 (k_pf_mm's
+    16 x 16 tiles only) and 2 (down on k_pf_mm) each meet the oracle bar and
+    agree with each other to fp32 rounding-order differences (and the fp16
+    rounding of the activations they feed)."""
     seed = sum(map(ord, name)) + 3
     got = {}
     try:

@@ -113,9 +113,10 @@ DOWN_TILE_CASES = ["c4-a3b-shared", "c4-a3b-3bit-shared", "f32-x", "max-n1024-k1
 
 @pytest.mark.parametrize("name", DOWN_TILE_CASES)
 def test_prefill_block_down_tile_option(kernels, name):
-    """SMOE_OPT_PREFILL_GEMM = 2 (the down GEMM on 32 x 32 tiles too, for
-    the 4-bit group-64 experts: routed, or the 4-bit shared expert's own
-    list beside 3-bit routed ones) meets the same bar as the default."""
+    """SMOE_OPT_PREFILL_GEMM = 2 (the down GEMM on k_pf_mm's 16 x 16 tiles
+    instead of the default 32 x 32 ones, for the 4-bit group-64 experts:
+    routed, or the 4-bit shared expert's own list beside 3-bit routed ones)
+    meets the same bar as the default."""
     c = next(c for c in CASES if c[0] == name)
     kernels.set_prefill_gemm(2)
     try:
@@ -123,7 +124,7 @@ def test_prefill_block_down_tile_option(kernels, name):
     finally:
         kernels.set_prefill_gemm(0)
     err, moe_err = rel_err(got, want), rel_err(got - h, want - h)
-    print(f"prefill block {name} (32 x 32 down): rel_err={err:.3e} MoE part {moe_err:.3e}")
+    print(f"prefill block {name} (16 x 16 down): rel_err={err:.3e} MoE part {moe_err:.3e}")
     assert np.all(np.isfinite(got))
     assert err <= TOL and moe_err <= TOL
 
