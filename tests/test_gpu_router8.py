@@ -256,6 +256,25 @@ def test_q8_layer_matches_oracle(kernels, path, name, H, I, E, k, router, gate):
         kernels.set_decode_path(0)
 
 
+@pytest.mark.parametrize("name,H,I,E,k", [("flash-next-q8", 2560, 640, 512, 10), ("tiny-q8", 256, 64, 8, 3)])
+def test_q8_layer_other_shapes_per_phase(kernels, name, H, I, E, k):
+    """Shapes without a three-kernel instance (the default path takes the
+    per-phase kernels for them): the 8-bit router and gate against the
+    oracle."""
+    seed = sum(map(ord, name)) * 3
+    L, d, keep = _layer(kernels, H, I, E, k, seed)
+    x, h_mid = _inputs(kernels, H, seed)
+    got, gi, gw = _run(kernels, L, H, k, x, h_mid)
+    want, wi, ww, logits = oracle.moe_decode_layer(
+        host(d["arena"]), d["stride"], H, I, E, k, 64, 4, True, None, host(x), host(h_mid), host(d["shared"]), None,
+        router_q8=d["router_q8"], gate_q8=d["gate_q8"])
+    err = rel_err(got, want)
+    print(f"q8 layer {name}: idx gpu={list(gi)} cpu={list(wi)} rel_err={err:.3e}")
+    assert np.array_equal(gi, wi)
+    assert np.max(np.abs(gw - ww)) <= 1e-5 * np.max(np.abs(ww))
+    assert err <= TOL
+
+
 def _q8_chain(kernels, NL, H, I, E, k, seed):
     """NL layers with 8-bit routers and gates, bf16 RMSNorm weights."""
     torch = _torch()
