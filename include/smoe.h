@@ -192,8 +192,10 @@ int smoe_qmm(smoe_handle* h, const smoe_qweights* w, const float* x, float* y, u
 /* Dequantize rows [row0, row0 + n_rows) of `w` into device
  * f32[n_rows, in_dim]: w = fma(q, s, b), one rounding, exactly the value
  * the reference CPU path forms (crates/streammoe/src/riir/backend/cpu/
- * cpu_matvec.rs:164-165). Verification entry point: the decode kernels
- * use the same code-unpacking routine and never materialise w. */
+ * cpu_matvec.rs:164-165; 8-bit rows: cpu_matvec.rs:205-283). Verification
+ * and load-time entry point (bits 4, 3 or 8): the decode kernels use the
+ * same code-unpacking routine and never materialise w; a prefill block's
+ * f32 shared-expert gate is one 8-bit row dequantized here once. */
 int smoe_dequant(smoe_handle* h, const smoe_qweights* w, uint32_t in_dim, uint32_t row0,
                  uint32_t n_rows, float* out);
 

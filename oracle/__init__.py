@@ -44,6 +44,7 @@ def _declare(L):
         "orc_expert_bytes": (C.c_size_t, [_U32, _U32, _U32, _U32]),
         "orc_expert_offsets": (None, [_U32, _U32, _U32, _U32, _U32, _P]),
         "orc_dequant_4bit": (None, [_P, _P, _P, _U32, _U32, _U32, _P]),
+        "orc_dequant_8bit": (None, [_P, _P, _P, _U32, _U32, _U32, _P]),
         "orc_dequant_matvec_4bit_gs": (C.c_int, [_P, _P, _P, _U32, _U32, _U32, _P, _P, C.c_int]),
         "orc_dequant_matvec_8bit_gs": (C.c_int, [_P, _P, _P, _U32, _U32, _U32, _P, _P, C.c_int]),
         "orc_lm_head": (C.c_int, [_P, _P, _P, _U32, _U32, _U32, _P, _P]),
@@ -129,6 +130,14 @@ def dequant_4bit(packed, scales, biases, in_dim, out_dim, group):
     packed, scales, biases = _words(packed), _c(scales, np.uint16), _c(biases, np.uint16)
     out = np.empty((out_dim, in_dim), np.float32)
     lib().orc_dequant_4bit(_p(packed), _p(scales), _p(biases), in_dim, out_dim, group, _p(out))
+    return out
+
+
+def dequant_8bit(packed, scales, biases, in_dim, out_dim, group):
+    """packed: bytes [out_dim, in_dim] (or their u32 words)."""
+    packed, scales, biases = _words(packed), _c(scales, np.uint16), _c(biases, np.uint16)
+    out = np.empty((out_dim, in_dim), np.float32)
+    lib().orc_dequant_8bit(_p(packed), _p(scales), _p(biases), in_dim, out_dim, group, _p(out))
     return out
 
 

@@ -74,6 +74,22 @@ void orc_dequant_4bit(const uint32_t* packed, const uint16_t* scales, const uint
   }
 }
 
+/* 8-bit rows (cpu_matvec.rs:205-283's weight, before the multiply by x):
+ * byte n of u32 word i is input 4i + n; w = fma(q, s, b). */
+void orc_dequant_8bit(const uint32_t* packed, const uint16_t* scales, const uint16_t* biases,
+                      uint32_t in_dim, uint32_t out_dim, uint32_t group, float* w_out) {
+  uint32_t in_packed = in_dim / 4, in_groups = in_dim / group;
+  for (uint32_t r = 0; r < out_dim; ++r) {
+    for (uint32_t c = 0; c < in_dim; ++c) {
+      uint32_t word = packed[(size_t)r * in_packed + c / 4];
+      float q = (float)((word >> ((c % 4) * 8)) & 0xFFu);
+      float s = orc_bf16_to_f32(scales[(size_t)r * in_groups + c / group]);
+      float b = orc_bf16_to_f32(biases[(size_t)r * in_groups + c / group]);
+      w_out[(size_t)r * in_dim + c] = fmaf(q, s, b);
+    }
+  }
+}
+
 /* ------------------------------------------------------------------ */
 /* Row-parallel worker pool (rayon's par_iter_mut over output rows,    */
 /* cpu_matvec.rs:150). Rows are independent, so the result does not   */

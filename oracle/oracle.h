@@ -56,6 +56,9 @@ void orc_expert_offsets(uint32_t hidden, uint32_t inter, uint32_t bits, uint32_t
 /* ---- dequant / matvec --------------------------------------------- */
 void orc_dequant_4bit(const uint32_t* packed, const uint16_t* scales, const uint16_t* biases,
                       uint32_t in_dim, uint32_t out_dim, uint32_t group, float* w_out);
+/* 8-bit rows: w = fma(q, s, b), byte n of word i = input 4i + n. */
+void orc_dequant_8bit(const uint32_t* packed, const uint16_t* scales, const uint16_t* biases,
+                      uint32_t in_dim, uint32_t out_dim, uint32_t group, float* w_out);
 int orc_dequant_matvec_4bit_gs(const uint32_t* packed, const uint16_t* scales,
                                const uint16_t* biases, uint32_t in_dim, uint32_t out_dim,
                                uint32_t group, const float* x, float* out, int nthreads);

@@ -351,7 +351,7 @@ int smoe_dequant(smoe_handle* h, const smoe_qweights* w, uint32_t in_dim, uint32
                  uint32_t n_rows, float* out) {
   if (!h || !out || !n_rows) return SMOE_ERR_INVALID_ARG;
   QView v;
-  if (int rc = qview(w, in_dim, &v)) return rc;
+  if (int rc = qview(w, in_dim, &v, true)) return rc;
   if (in_dim % 32) return SMOE_ERR_UNSUPPORTED_SHAPE;
   if (int rc = use_device(h)) return rc;
   return hip_status(launch_dequant(v, in_dim, row0, n_rows, out, h->stream));

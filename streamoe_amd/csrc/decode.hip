@@ -387,8 +387,35 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ cod
   for (int j = 0; j < kChunk; ++j) o[j] = __builtin_fmaf((float)code_at(raw, j), s, b);
 }
 
+// 8-bit rows: one thread per 16 consecutive inputs (byte n of word i is
+// input 4i + n); in_dim is a multiple of the group (>= 32), so a piece never
+// straddles a group.
+__global__ __launch_bounds__(256) void k_dequant8(const uint8_t* __restrict__ codes,
+                                                  const uint16_t* __restrict__ scales,
+                                                  const uint16_t* __restrict__ biases,
+                                                  uint32_t in_dim, uint32_t group, uint32_t row0,
+                                                  uint32_t n_rows, float* __restrict__ out) {
+  const uint32_t ppr = in_dim / 16;
+  const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (uint64_t)n_rows * ppr) return;
+  const uint32_t r = row0 + (uint32_t)(t / ppr), c = (uint32_t)(t % ppr) * 16;
+  const u32x4 q = *reinterpret_cast<const u32x4*>(codes + (size_t)r * in_dim + c);
+  const size_t gi = (size_t)r * (in_dim / group) + c / group;
+  const float s = bf16f(scales[gi]), b = bf16f(biases[gi]);
+  const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
+  float* o = out + (size_t)(r - row0) * in_dim + c;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) o[j] = __builtin_fmaf((float)((wd[j >> 2] >> (8 * (j & 3))) & 0xFFu), s, b);
+}
+
 hipError_t launch_dequant(const QView& w, uint32_t in_dim, uint32_t row0, uint32_t n_rows,
                           float* out, hipStream_t st) {
+  if (w.bits == 8) {
+    const uint64_t n = (uint64_t)n_rows * (in_dim / 16);
+    hipLaunchKernelGGL(k_dequant8, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, st, w.codes,
+                       w.scales, w.biases, in_dim, w.group, row0, n_rows, out);
+    return hipGetLastError();
+  }
   const uint64_t n = (uint64_t)n_rows * (in_dim / kChunk);
   const uint32_t blocks = (uint32_t)((n + 255) / 256);
   if (w.bits == 4)

@@ -104,6 +104,22 @@ def test_qmv8_argmax_and_qmm(kernels):
     assert np.array_equal(host(ym).view(np.uint32), np.stack(ys).view(np.uint32))
 
 
+@pytest.mark.parametrize("rows,in_dim,group,row0", [
+    (7, 2048, 64, 2), (1, 2048, 64, 0), (64, 1024, 32, 5), (3, 8192, 128, 1), (1, 32, 32, 0),
+])
+def test_dequant8_bit_exact(kernels, rows, in_dim, group, row0):
+    """smoe_dequant on 8-bit rows (the load-time f32 form of an 8-bit
+    shared-expert gate): every weight fma(q, s, b) bit for bit against the
+    oracle, from row row0 on."""
+    rng = np.random.default_rng(rows * 7 + in_dim + group)
+    q, s, b = _q8(rng, rows + row0, in_dim, group)
+    torch = _torch()
+    out = torch.empty((rows, in_dim), dtype=torch.float32, device="cuda")
+    assert kernels.dequant(qweights(q, s, b, group, 8), in_dim, row0, rows, out) == 0
+    want = oracle.dequant_8bit(q, s, b, in_dim, rows + row0, group)[row0:]
+    assert np.array_equal(host(out).view(np.uint32), want.view(np.uint32))
+
+
 def test_qmv8_argument_errors(kernels):
     import streamoe_amd as sa
     from streamoe_amd import _abi
@@ -114,7 +130,7 @@ def test_qmv8_argument_errors(kernels):
     y = torch.zeros(16, dtype=torch.float32, device="cuda")
     w = sa.QuantWeights(buf, 0, 1 << 18, 1 << 19, 64, 8)
     assert kernels.qmv(w, x, y, 2, 16384) == _abi.CODES["SMOE_ERR_UNSUPPORTED_SHAPE"]
-    assert kernels.dequant(w, 2048, 0, 1, x) == _abi.CODES["SMOE_ERR_UNSUPPORTED_BITS"]
+    assert kernels.dequant(w, 2048 + 16, 0, 1, x) == _abi.CODES["SMOE_ERR_IN_DIM_NOT_MULTIPLE"]
     w = sa.QuantWeights(buf, 4, 1 << 18, 1 << 19, 64, 8)
     assert kernels.qmv(w, x, y, 2, 2048) == _abi.CODES["SMOE_ERR_MISALIGNED"]
     w = sa.QuantWeights(buf, 0, 1 << 18, 1 << 19, 64, 8)

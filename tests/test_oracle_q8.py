@@ -34,6 +34,27 @@ def test_q8_byte_order_one_hot():
         assert np.array_equal(y, want), (r, j, y)
 
 
+@pytest.mark.parametrize("group", [32, 64, 128])
+def test_q8_dequant_rows(group):
+    """orc_dequant_8bit: each weight fma(q, s, b) with one rounding. Pinned
+    two ways: column j equals the matvec against the unit vector e_j (whose
+    byte order the one-hot test fixes), and every weight equals q s + b
+    formed exactly in float64 (q s has at most 16 significant bits and the
+    exponents here are close, so the sum is exact) rounded once to f32."""
+    O, I = 5, 256
+    rng = np.random.default_rng(group)
+    q, s, b = gen_quant_matrix(rng, O, I, group, 8)
+    w = oracle.dequant_8bit(q, s, b, I, O, group)
+    assert w.shape == (O, I) and w.dtype == np.float32
+    assert np.array_equal(w, _dequant_f64(q, s, b, group).astype(np.float32))
+    for j in (0, 3, 4, group - 1, group, I - 1):
+        e = np.zeros(I, np.float32)
+        e[j] = 1.0
+        rc, y = oracle.dequant_matvec_8bit_gs(q, s, b, I, O, group, e)
+        assert rc == 0
+        assert np.array_equal(y.view(np.uint32), np.ascontiguousarray(w[:, j]).view(np.uint32)), j
+
+
 def test_q8_closed_form_constant_codes():
     """Codes c everywhere, per-group scale s_g and bias b_g: row = sum_g
     (c s_g + b_g) sum_{j in g} x_j, exact with small integers and powers of
