@@ -5,12 +5,13 @@
 // combine), whose CPU statement is build_expert_buckets (moe_router.rs:
 // 374-436) + moe_permute_fuse_cpu (moe_cpu.rs:282-339).
 //
-//   k_pf_route    block 0, one thread per token: bucket the n*k
-//                 assignments by expert (stable in token order), per-token
-//                 entry positions in ascending expert order, a work list of
-//                 (expert, <= kPfMC entries) items, so a hot expert is spread
-//                 over many waves, and the token of each item row. Blocks
-//                 1..: each token's x row in the MFMA k-order (bf16, or f32
+//   k_pf_route    blocks 0..nb-1 (nb <= 8), one thread per token: bucket
+//                 the n*k assignments by expert (stable in token order),
+//                 per-token entry positions in ascending expert order, a work
+//                 list of (expert, <= kPfMC entries) items, so a hot expert
+//                 is spread over many waves, and the token of each item row
+//                 (every block buckets, each stores a share). Blocks
+//                 nb..: each token's x row in the MFMA k-order (bf16, or f32
 //                 split into bf16 hi + lo) and its group sums (the per-group
 //                 terms of the dequant epilogue), once per token.
 //   k_pf_mm       persistent pipelined grouped GEMM on MFMA
@@ -167,16 +168,24 @@ __device__ __forceinline__ u32x4 codes_bf16(uint32_t w) {
 }
 
 // ---------------------------------------------------------------------------
-// Bucketing (block 0 of k_pf_route, 1024 threads) and the per-token x
-// preparation (blocks 1.., four tokens each), in one launch: the
-// preparation runs on other CUs while the single bucketing block works.
+// Bucketing (blocks 0..nb-1 of k_pf_route, 1024 threads) and the per-token
+// x preparation (blocks nb.., four tokens each), in one launch: the
+// preparation runs on other CUs while the bucketing blocks work.
 // ---------------------------------------------------------------------------
 #define PF_STAMP(i)                                                         \
   do {                                                                      \
-    if (a.trace && threadIdx.x == 0) a.trace[i] = __builtin_amdgcn_s_memrealtime(); \
+    if (a.trace && threadIdx.x == 0 && blockIdx.x == 0) a.trace[i] = __builtin_amdgcn_s_memrealtime(); \
   } while (0)
 
 constexpr uint32_t kPfPrepTokens = 4;                    // tokens per preparation block (256 threads each)
+
+// Bucketing blocks: each computes the whole bucketing (bitmaps, counts,
+// scans) from the routing input and stores one share of its results (a
+// wave of tokens' entries, every nb-th expert's items), so the scattered
+// stores spread over nb CUs instead of queueing on one.
+__host__ __device__ constexpr uint32_t pf_bucket_blocks(uint32_t n) {
+  return (n + 63) / 64 < 8 ? (n + 63) / 64 : 8;
+}
 constexpr uint32_t kPfPart8 = kPfMaxGroupsK * 128 / 8;   // 8-input partial sums of one row (H <= 16384)
 
 // Token t's x row -> MFMA-ready bf16 hi (and lo for fp32 input) and its
@@ -277,11 +286,93 @@ __device__ __forceinline__ uint32_t wave_scan_incl(uint32_t v) {
   return v;
 }
 
+// Per-expert counts from the column bitmaps: tpe threads per expert
+// (adjacent lanes), each over PER >= ceil(cw / tpe) words. Every word read
+// is issued unconditionally (addresses clamped into the bitmap, values
+// masked), so the reads overlap instead of one LDS round trip each.
+template <uint32_t PER>
+__device__ __forceinline__ void pf_count_words(const uint32_t* col, uint16_t* pre, uint32_t* scnt, uint32_t* snch,
+                                               uint32_t E, uint32_t cw, uint32_t tpe, uint32_t tid) {
+  const uint32_t e = tid / tpe, j = tid % tpe, per = (cw + tpe - 1) / tpe;
+  const uint32_t ec = e < E ? e : E - 1u;
+  uint32_t pc[PER], loc = 0;
+#pragma unroll
+  for (uint32_t i = 0; i < PER; ++i) {
+    const uint32_t c = j * per + i;
+    const uint32_t v = col[ec * cw + (c < cw ? c : cw - 1u)];
+    pc[i] = (e < E && i < per && c < cw) ? __popc(v) : 0u;
+    loc += pc[i];
+  }
+  // Inclusive scan over the tpe lanes of the expert (aligned groups of 2
+  // or 4 within a 16-lane row): DPP shifts by 1 and 2.
+  uint32_t incl = loc;
+  const uint32_t t1 = dpp_shr_u<0x111>(incl);
+  if (j >= 1) incl += t1;
+  if (tpe == 4) {
+    const uint32_t t2 = dpp_shr_u<0x112>(incl);
+    if (j >= 2) incl += t2;
+  }
+  if (e < E) {
+    uint32_t run = incl - loc;
+#pragma unroll
+    for (uint32_t i = 0; i < PER; ++i) {
+      const uint32_t c = j * per + i;
+      if (i < per && c < cw) pre[e * cw + c] = (uint16_t)run;
+      run += pc[i];
+    }
+    if (j == tpe - 1) {
+      scnt[e] = incl;
+      snch[e] = (incl + kPfMC - 1) / kPfMC;
+    }
+  }
+}
+
+// Work-list index of routed item i: the routed items in expert order, cut
+// into 8 XCD ranges [nr x / 8, nr (x + 1) / 8); with ns shared-expert
+// items in the list, range x's shared items follow its routed ones.
+__device__ __forceinline__ uint32_t pf_fidx(uint32_t i, uint32_t nr, uint32_t ns) {
+  return i + ns * ((8u * (i + 1u) - 1u) / nr) / 8u;
+}
+
+struct PfPlace {
+  const uint32_t* col;
+  const uint16_t* pre;
+  const uint32_t* offs;
+  const uint32_t* sibase;
+  uint32_t E, cw, k, nr, ns;
+};
+
+// Token tid's entries (slots s < KM, ids past k are INT32_MAX): position =
+// the expert's offset + the tokens before tid that chose the same expert
+// (its row in the expert's items); rank among the token's experts in
+// ascending expert order = how many of its ids are smaller. Stores the
+// (position, weight) pair at the rank and the token id into its item row.
+template <uint32_t KM, bool SHARED>
+__device__ __forceinline__ void pf_place(const PfArgs& a, const PfPlace& p, const int32_t (&ex)[kPfMaxK],
+                                         const float (&wt)[kPfMaxK], uint32_t tid) {
+#pragma unroll
+  for (uint32_t s = 0; s < KM; ++s) {
+    const int32_t e = ex[s];
+    if (s >= p.k || e < 0 || (uint32_t)e >= p.E) continue;
+    const uint32_t ci = e * p.cw + (tid >> 5);
+    const uint32_t row = p.pre[ci] + __popc(p.col[ci] & ((1u << (tid & 31)) - 1u));
+    const uint32_t pos = p.offs[e] + row;
+    uint32_t r = 0;
+#pragma unroll
+    for (uint32_t q = 0; q < KM; ++q) r += ex[q] < e ? 1u : 0u;
+    r = min(r, p.k - 1);  // a duplicated expert (already reported) stays in range
+    a.tok_pw[tid * p.k + r] = make_uint2(pos, __float_as_uint(wt[s]));
+    const uint32_t it = p.sibase[e] + row / kPfMC;
+    a.item_tok[(SHARED ? pf_fidx(it, p.nr, p.ns) : it) * kPfMC + row % kPfMC] = tid;
+  }
+}
+
 __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t pf_dyn[];
   const uint32_t tid = threadIdx.x;
-  if (blockIdx.x > 0) {
-    const uint32_t sub = tid >> 8, t = (blockIdx.x - 1) * kPfPrepTokens + sub;
+  const uint32_t nb = pf_bucket_blocks(a.n_tokens), bb = blockIdx.x;
+  if (bb >= nb) {
+    const uint32_t sub = tid >> 8, t = (bb - nb) * kPfPrepTokens + sub;
     pf_prep_token(a, t, t < a.n_tokens, tid & 255u, reinterpret_cast<float*>(pf_dyn) + sub * kPfPart8);
     return;
   }
@@ -303,7 +394,7 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
   bool bad = false;
 #pragma unroll
   for (uint32_t s = 0; s < kPfMaxK; ++s) {
-    ex[s] = -1;
+    ex[s] = INT32_MAX;  // past k: above every expert id (out of range, never smaller)
     wt[s] = 0.f;
   }
   const bool vec = (k & 3) == 0 && ((reinterpret_cast<uintptr_t>(a.idx) | reinterpret_cast<uintptr_t>(a.w)) & 15) == 0;
@@ -337,8 +428,9 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
 #pragma unroll
     for (uint32_t s = 0; s < kPfMaxK; ++s) {
       if (s >= k || ex[s] < 0 || (uint32_t)ex[s] >= E) continue;
-      const uint32_t old = atomicOr(&col[ex[s] * cw + (tid >> 5)], 1u << (tid & 31));
-      bad |= (old >> (tid & 31)) & 1u;  // an expert twice in one token
+      // No returned value: an expert twice in one token shows as a bitmap
+      // total below n k (checked with the scans).
+      atomicOr(&col[ex[s] * cw + (tid >> 5)], 1u << (tid & 31));
     }
     if (bad) *a.err = 2u;
   }
@@ -352,38 +444,13 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
     // each word.
     static_assert(kPfMaxTokens / 32 <= 2 * 16 && 2 * kPfMaxExperts <= 1024 && 4 * 256 <= 1024, "count split");
     const uint32_t tpe = E <= 256 ? 4u : 2u;
-    const uint32_t e = tid / tpe, j = tid % tpe, per = (cw + tpe - 1) / tpe;
-    uint32_t pc[16], loc = 0;
-#pragma unroll
-    for (uint32_t i = 0; i < 16; ++i) {
-      const uint32_t c = j * per + i;
-      pc[i] = (e < E && i < per && c < cw) ? __popc(col[e * cw + c]) : 0u;
-      loc += pc[i];
-    }
-    // Inclusive scan over the TPE lanes of the expert (aligned groups of
-    // 2 or 4 within a 16-lane row): DPP shifts by 1 and 2.
-    uint32_t incl = loc;
-    const uint32_t t1 = dpp_shr_u<0x111>(incl);
-    if (j >= 1) incl += t1;
-    if (tpe == 4) {
-      const uint32_t t2 = dpp_shr_u<0x112>(incl);
-      if (j >= 2) incl += t2;
-    }
-    if (e < E) {
-      uint32_t run = incl - loc;
-#pragma unroll
-      for (uint32_t i = 0; i < 16; ++i) {
-        const uint32_t c = j * per + i;
-        if (i < per && c < cw) {
-          pre[e * cw + c] = (uint16_t)run;
-          run += pc[i];
-        }
-      }
-      if (j == tpe - 1) {
-        scnt[e] = incl;
-        snch[e] = (incl + kPfMC - 1) / kPfMC;
-      }
-    }
+    const uint32_t per = (cw + tpe - 1) / tpe;
+    if (per <= 4)
+      pf_count_words<4>(col, pre, scnt, snch, E, cw, tpe, tid);
+    else if (per <= 8)
+      pf_count_words<8>(col, pre, scnt, snch, E, cw, tpe, tid);
+    else
+      pf_count_words<16>(col, pre, scnt, snch, E, cw, tpe, tid);
   }
   __syncthreads();
   PF_STAMP(3);
@@ -412,7 +479,10 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
       co += c8[q];
       no += n8[q];
     }
-    if (tid == 63) s_nr = ni;
+    if (tid == 63) {
+      s_nr = ni;
+      if (bb == 0 && ci != n * k) *a.err = 2u;  // a duplicated (or invalid) expert id
+    }
   }
   __syncthreads();
   PF_STAMP(4);
@@ -423,10 +493,10 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
   // routed items, so that no XCD takes all of them.
   const uint32_t nr = s_nr;
   const uint32_t ns = a.shared && a.shared_in_list ? (n + kPfMC - 1) / kPfMC : 0u;
-  auto fidx = [=](uint32_t i) { return i + ns * ((8u * (i + 1u) - 1u) / nr) / 8u; };
-  if (tid < 9) a.xr[tid] = nr * tid / 8u + ns * tid / 8u;
-  if (tid == 0) *a.n_items = nr + ns;
-  for (uint32_t j = tid; j < ns; j += blockDim.x) {
+  auto fidx = [=](uint32_t i) { return pf_fidx(i, nr, ns); };
+  if (bb == 0 && tid < 9) a.xr[tid] = nr * tid / 8u + ns * tid / 8u;
+  if (bb == 0 && tid == 0) *a.n_items = nr + ns;
+  for (uint32_t j = bb + nb * tid; j < ns; j += nb * blockDim.x) {
     const uint32_t x = (8u * (j + 1u) - 1u) / ns, f = nr * (x + 1u) / 8u + j;
     const uint32_t cnt = min(kPfMC, n - j * kPfMC);
     a.items[2 * f] = E;
@@ -436,20 +506,21 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
   if (a.shared && !a.shared_in_list) {
     // A list of its own for 4-bit GEMM launches (routed bits 3).
     const uint32_t ms = (n + kPfMC - 1) / kPfMC;
-    for (uint32_t j = tid; j < ms; j += blockDim.x) {
+    for (uint32_t j = bb + nb * tid; j < ms; j += nb * blockDim.x) {
       const uint32_t cnt = min(kPfMC, n - j * kPfMC);
       a.sitems[2 * j] = 0;
       a.sitems[2 * j + 1] = (n * k + j * kPfMC) | (cnt << 16);
       for (uint32_t r = 0; r < cnt; ++r) a.sitem_tok[j * kPfMC + r] = j * kPfMC + r;
     }
-    if (tid < 9) a.sxr[tid] = ms * tid / 8u;
-    if (tid == 0) *a.sn_items = ms;
+    if (bb == 0 && tid < 9) a.sxr[tid] = ms * tid / 8u;
+    if (bb == 0 && tid == 0) *a.sn_items = ms;
   }
-  if (tid < E) {
-    const uint32_t cnt = scnt[tid], nch = snch[tid], off = offs[tid], ibase = sibase[tid];
+  if (bb + nb * tid < E) {
+    const uint32_t e = bb + nb * tid;
+    const uint32_t cnt = scnt[e], nch = snch[e], off = offs[e], ibase = sibase[e];
     for (uint32_t c = 0; c < nch; ++c) {
       const uint32_t f = fidx(ibase + c);
-      a.items[2 * f] = tid;
+      a.items[2 * f] = e;
       a.items[2 * f + 1] = (off + c * kPfMC) | (min(kPfMC, cnt - c * kPfMC) << 16);
     }
     // Rows past the count of the expert's last item are not written: the
@@ -461,20 +532,15 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
   // rank r among t's experts in ascending expert order = how many of t's
   // experts are smaller. The token writes its entry positions and weights
   // in that order (token-major), and its id into its items' row slots.
-  if (tok) {
-#pragma unroll
-    for (uint32_t s = 0; s < kPfMaxK; ++s) {
-      const int32_t e = ex[s];
-      if (s >= k || e < 0 || (uint32_t)e >= E) continue;
-      const uint32_t ci = e * cw + (tid >> 5);
-      const uint32_t row = pre[ci] + __popc(col[ci] & ((1u << (tid & 31)) - 1u));
-      const uint32_t pos = offs[e] + row;
-      uint32_t r = 0;
-#pragma unroll
-      for (uint32_t q = 0; q < kPfMaxK; ++q) r += (q < k && ex[q] < e) ? 1u : 0u;
-      r = min(r, k - 1);  // a duplicated expert (already reported) stays in range
-      a.tok_pw[tid * k + r] = make_uint2(pos, __float_as_uint(wt[s]));
-      a.item_tok[fidx(sibase[e] + row / kPfMC) * kPfMC + row % kPfMC] = tid;
+  // Block bb places the tokens of waves bb, bb + nb, ...
+  if (tok && (tid >> 6) % nb == bb) {
+    const PfPlace p{col, pre, offs, sibase, E, cw, k, nr, ns};
+    if (k <= 8) {
+      if (ns) pf_place<8, true>(a, p, ex, wt, tid);
+      else pf_place<8, false>(a, p, ex, wt, tid);
+    } else {
+      if (ns) pf_place<kPfMaxK, true>(a, p, ex, wt, tid);
+      else pf_place<kPfMaxK, false>(a, p, ex, wt, tid);
     }
   }
   PF_STAMP(5);
@@ -2201,7 +2267,8 @@ hipError_t launch_prefill(const PfArgs& a, uint32_t n_cu, hipStream_t st) {
     const hipError_t e = raise_lds_limit(reinterpret_cast<const void*>(&k_pf_route), (int)pf_route_lds(kPfMaxExperts, kPfMaxTokens), raised);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(k_pf_route, dim3(1 + (a.n_tokens + kPfPrepTokens - 1) / kPfPrepTokens), dim3(1024), route_lds, st, a);
+  hipLaunchKernelGGL(k_pf_route, dim3(pf_bucket_blocks(a.n_tokens) + (a.n_tokens + kPfPrepTokens - 1) / kPfPrepTokens),
+                     dim3(1024), route_lds, st, a);
   const uint32_t G = a.g.group, nk = a.n_tokens * a.k;
   const uint32_t rows = nk + (a.shared && a.shared_in_list ? a.n_tokens : 0u);
   hipError_t e;
