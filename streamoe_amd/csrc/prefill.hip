@@ -350,20 +350,31 @@ struct PfPlace {
 template <uint32_t KM, bool SHARED>
 __device__ __forceinline__ void pf_place(const PfArgs& a, const PfPlace& p, const int32_t (&ex)[kPfMaxK],
                                          const float (&wt)[kPfMaxK], uint32_t tid) {
+  // Every slot's LDS reads first (an invalid slot reads expert 0's words
+  // and stores nothing), so they take one round trip, not one per slot.
+  bool ok[KM];
+  uint32_t pv[KM], cv[KM], ov[KM], sv[KM];
 #pragma unroll
   for (uint32_t s = 0; s < KM; ++s) {
-    const int32_t e = ex[s];
-    if (s >= p.k || e < 0 || (uint32_t)e >= p.E) continue;
-    const uint32_t ci = e * p.cw + (tid >> 5);
-    const uint32_t row = p.pre[ci] + __popc(p.col[ci] & ((1u << (tid & 31)) - 1u));
-    const uint32_t pos = p.offs[e] + row;
+    ok[s] = s < p.k && ex[s] >= 0 && (uint32_t)ex[s] < p.E;
+    const uint32_t e = ok[s] ? (uint32_t)ex[s] : 0u, ci = e * p.cw + (tid >> 5);
+    pv[s] = p.pre[ci];
+    cv[s] = p.col[ci];
+    ov[s] = p.offs[e];
+    sv[s] = p.sibase[e];
+  }
+#pragma unroll
+  for (uint32_t s = 0; s < KM; ++s) {
+    const uint32_t row = pv[s] + __popc(cv[s] & ((1u << (tid & 31)) - 1u));
     uint32_t r = 0;
 #pragma unroll
-    for (uint32_t q = 0; q < KM; ++q) r += ex[q] < e ? 1u : 0u;
+    for (uint32_t q = 0; q < KM; ++q) r += ex[q] < ex[s] ? 1u : 0u;
     r = min(r, p.k - 1);  // a duplicated expert (already reported) stays in range
-    a.tok_pw[tid * p.k + r] = make_uint2(pos, __float_as_uint(wt[s]));
-    const uint32_t it = p.sibase[e] + row / kPfMC;
-    a.item_tok[(SHARED ? pf_fidx(it, p.nr, p.ns) : it) * kPfMC + row % kPfMC] = tid;
+    const uint32_t it = sv[s] + row / kPfMC;
+    if (ok[s]) {
+      a.tok_pw[tid * p.k + r] = make_uint2(ov[s] + row, __float_as_uint(wt[s]));
+      a.item_tok[(SHARED ? pf_fidx(it, p.nr, p.ns) : it) * kPfMC + row % kPfMC] = tid;
+    }
   }
 }
 
@@ -494,9 +505,14 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
   const uint32_t nr = s_nr;
   const uint32_t ns = a.shared && a.shared_in_list ? (n + kPfMC - 1) / kPfMC : 0u;
   auto fidx = [=](uint32_t i) { return pf_fidx(i, nr, ns); };
+  // Shared-expert items on wave wi + 1 and routed items on wave wi (threads
+  // rotated so that the wave holds the block's first 64 of them): when
+  // nb > 1 neither places tokens (the waves bb, bb + nb, ... do).
+  const uint32_t wi = (bb + nb / 2) & 15u, it = (tid + 1024u - 64u * wi) & 1023u;
+  const uint32_t is = (tid + 1024u - 64u * ((wi + 1u) & 15u)) & 1023u;
   if (bb == 0 && tid < 9) a.xr[tid] = nr * tid / 8u + ns * tid / 8u;
   if (bb == 0 && tid == 0) *a.n_items = nr + ns;
-  for (uint32_t j = bb + nb * tid; j < ns; j += nb * blockDim.x) {
+  for (uint32_t j = bb + nb * is; j < ns; j += nb * blockDim.x) {
     const uint32_t x = (8u * (j + 1u) - 1u) / ns, f = nr * (x + 1u) / 8u + j;
     const uint32_t cnt = min(kPfMC, n - j * kPfMC);
     a.items[2 * f] = E;
@@ -506,7 +522,7 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
   if (a.shared && !a.shared_in_list) {
     // A list of its own for 4-bit GEMM launches (routed bits 3).
     const uint32_t ms = (n + kPfMC - 1) / kPfMC;
-    for (uint32_t j = bb + nb * tid; j < ms; j += nb * blockDim.x) {
+    for (uint32_t j = bb + nb * is; j < ms; j += nb * blockDim.x) {
       const uint32_t cnt = min(kPfMC, n - j * kPfMC);
       a.sitems[2 * j] = 0;
       a.sitems[2 * j + 1] = (n * k + j * kPfMC) | (cnt << 16);
@@ -515,8 +531,8 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
     if (bb == 0 && tid < 9) a.sxr[tid] = ms * tid / 8u;
     if (bb == 0 && tid == 0) *a.sn_items = ms;
   }
-  if (bb + nb * tid < E) {
-    const uint32_t e = bb + nb * tid;
+  if (bb + nb * it < E) {
+    const uint32_t e = bb + nb * it;
     const uint32_t cnt = scnt[e], nch = snch[e], off = offs[e], ibase = sibase[e];
     for (uint32_t c = 0; c < nch; ++c) {
       const uint32_t f = fidx(ibase + c);
