@@ -257,13 +257,16 @@ __device__ __forceinline__ void pf_prep_token(const PfArgs& a, uint32_t t, bool 
   }
 }
 
-// LDS of the bucketing block: col [E, cw] u32 then pre [E, cw] u16
-// (cw = ceil(n / 32)); the preparation blocks use the same memory as
-// kPfPrepTokens rows of part sums.
+// LDS of a bucketing block: col [E, cws] u32 (row stride cws = cw | 1,
+// odd, so that the words of different experts spread over the LDS banks)
+// then pre [E, cw] u16 (cw = ceil(n / 32)); the preparation blocks use the
+// same memory as kPfPrepTokens rows of part sums.
+__host__ __device__ constexpr uint32_t pf_route_bucket_lds(uint32_t E, uint32_t n) {
+  return (E * (((n + 31) / 32) | 1u) * 4 + E * ((n + 31) / 32) * 2 + 15) / 16 * 16;
+}
 __host__ __device__ constexpr uint32_t pf_route_lds(uint32_t E, uint32_t n) {
-  return (E * ((n + 31) / 32) * 6 + 15) / 16 * 16 > kPfPrepTokens * kPfPart8 * 4
-             ? (E * ((n + 31) / 32) * 6 + 15) / 16 * 16
-             : kPfPrepTokens * kPfPart8 * 4;
+  return pf_route_bucket_lds(E, n) > kPfPrepTokens * kPfPart8 * 4 ? pf_route_bucket_lds(E, n)
+                                                                  : kPfPrepTokens * kPfPart8 * 4;
 }
 
 // Lane l - d's value (DPP row shift right; row_shr:d = 0x110 + d), 0 where
@@ -292,14 +295,14 @@ __device__ __forceinline__ uint32_t wave_scan_incl(uint32_t v) {
 // masked), so the reads overlap instead of one LDS round trip each.
 template <uint32_t PER>
 __device__ __forceinline__ void pf_count_words(const uint32_t* col, uint16_t* pre, uint32_t* scnt, uint32_t* snch,
-                                               uint32_t E, uint32_t cw, uint32_t tpe, uint32_t tid) {
+                                               uint32_t E, uint32_t cw, uint32_t cws, uint32_t tpe, uint32_t tid) {
   const uint32_t e = tid / tpe, j = tid % tpe, per = (cw + tpe - 1) / tpe;
   const uint32_t ec = e < E ? e : E - 1u;
   uint32_t pc[PER], loc = 0;
 #pragma unroll
   for (uint32_t i = 0; i < PER; ++i) {
     const uint32_t c = j * per + i;
-    const uint32_t v = col[ec * cw + (c < cw ? c : cw - 1u)];
+    const uint32_t v = col[ec * cws + (c < cw ? c : cw - 1u)];
     pc[i] = (e < E && i < per && c < cw) ? __popc(v) : 0u;
     loc += pc[i];
   }
@@ -339,7 +342,7 @@ struct PfPlace {
   const uint16_t* pre;
   const uint32_t* offs;
   const uint32_t* sibase;
-  uint32_t E, cw, k, nr, ns;
+  uint32_t E, cw, cws, k, nr, ns;
 };
 
 // Token tid's entries (slots s < KM, ids past k are INT32_MAX): position =
@@ -357,9 +360,9 @@ __device__ __forceinline__ void pf_place(const PfArgs& a, const PfPlace& p, cons
 #pragma unroll
   for (uint32_t s = 0; s < KM; ++s) {
     ok[s] = s < p.k && ex[s] >= 0 && (uint32_t)ex[s] < p.E;
-    const uint32_t e = ok[s] ? (uint32_t)ex[s] : 0u, ci = e * p.cw + (tid >> 5);
-    pv[s] = p.pre[ci];
-    cv[s] = p.col[ci];
+    const uint32_t e = ok[s] ? (uint32_t)ex[s] : 0u;
+    pv[s] = p.pre[e * p.cw + (tid >> 5)];
+    cv[s] = p.col[e * p.cws + (tid >> 5)];
     ov[s] = p.offs[e];
     sv[s] = p.sibase[e];
   }
@@ -389,14 +392,14 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
   }
   PF_STAMP(0);
   const uint32_t n = a.n_tokens, k = a.k, E = a.E;
-  const uint32_t cw = (n + 31) / 32;
+  const uint32_t cw = (n + 31) / 32, cws = cw | 1u;
   // col[e][c]: bit (t & 31) set when token 32c + (t & 31) chose expert e;
   // pre[e][c]: tokens before 32c that chose e.
   uint32_t* const col = reinterpret_cast<uint32_t*>(pf_dyn);
-  uint16_t* const pre = reinterpret_cast<uint16_t*>(pf_dyn + E * cw * 4);
+  uint16_t* const pre = reinterpret_cast<uint16_t*>(pf_dyn + E * cws * 4);
   __shared__ uint32_t offs[kPfMaxExperts];
   __shared__ uint32_t s_nr;  // routed work items
-  for (uint32_t i = tid; i < E * cw; i += blockDim.x) col[i] = 0;
+  for (uint32_t i = tid; i < E * cws; i += blockDim.x) col[i] = 0;
   // Thread t owns token t: its k experts and weights stay in registers
   // (one read of the routing input), validated here.
   int32_t ex[kPfMaxK];
@@ -435,13 +438,32 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
     if (tok && s < k) bad |= ex[s] < 0 || (uint32_t)ex[s] >= E;
   __syncthreads();
   PF_STAMP(1);
-  if (tok) {
+  // No returned value: an expert twice in one token shows as a bitmap
+  // total below n k (checked with the scans).
+  if (tok && k <= 8) {
+    // Lane l starts at slot l mod 8 (slots past k hold INT32_MAX), so the
+    // lanes that hit one word together (the same expert in the same slot,
+    // such as a hot expert in slot 0) are spread over the 8 instructions.
+    int32_t rx[8];
+#pragma unroll
+    for (uint32_t s = 0; s < 8; ++s) rx[s] = ex[s];
+#pragma unroll
+    for (uint32_t b = 1; b < 8; b <<= 1) {
+      const bool sh = (tid & b) != 0;
+      int32_t t[8];
+#pragma unroll
+      for (uint32_t s = 0; s < 8; ++s) t[s] = sh ? rx[(s + b) & 7] : rx[s];
+#pragma unroll
+      for (uint32_t s = 0; s < 8; ++s) rx[s] = t[s];
+    }
+#pragma unroll
+    for (uint32_t s = 0; s < 8; ++s)
+      if (rx[s] >= 0 && (uint32_t)rx[s] < E) atomicOr(&col[rx[s] * cws + (tid >> 5)], 1u << (tid & 31));
+  } else if (tok) {
 #pragma unroll
     for (uint32_t s = 0; s < kPfMaxK; ++s) {
       if (s >= k || ex[s] < 0 || (uint32_t)ex[s] >= E) continue;
-      // No returned value: an expert twice in one token shows as a bitmap
-      // total below n k (checked with the scans).
-      atomicOr(&col[ex[s] * cw + (tid >> 5)], 1u << (tid & 31));
+      atomicOr(&col[ex[s] * cws + (tid >> 5)], 1u << (tid & 31));
     }
     if (bad) *a.err = 2u;
   }
@@ -457,11 +479,11 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
     const uint32_t tpe = E <= 256 ? 4u : 2u;
     const uint32_t per = (cw + tpe - 1) / tpe;
     if (per <= 4)
-      pf_count_words<4>(col, pre, scnt, snch, E, cw, tpe, tid);
+      pf_count_words<4>(col, pre, scnt, snch, E, cw, cws, tpe, tid);
     else if (per <= 8)
-      pf_count_words<8>(col, pre, scnt, snch, E, cw, tpe, tid);
+      pf_count_words<8>(col, pre, scnt, snch, E, cw, cws, tpe, tid);
     else
-      pf_count_words<16>(col, pre, scnt, snch, E, cw, tpe, tid);
+      pf_count_words<16>(col, pre, scnt, snch, E, cw, cws, tpe, tid);
   }
   __syncthreads();
   PF_STAMP(3);
@@ -550,7 +572,7 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
   // in that order (token-major), and its id into its items' row slots.
   // Block bb places the tokens of waves bb, bb + nb, ...
   if (tok && (tid >> 6) % nb == bb) {
-    const PfPlace p{col, pre, offs, sibase, E, cw, k, nr, ns};
+    const PfPlace p{col, pre, offs, sibase, E, cw, cws, k, nr, ns};
     if (k <= 8) {
       if (ns) pf_place<8, true>(a, p, ex, wt, tid);
       else pf_place<8, false>(a, p, ex, wt, tid);
