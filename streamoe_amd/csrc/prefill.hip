@@ -383,6 +383,15 @@ __device__ __forceinline__ void pf_place(const PfArgs& a, const PfPlace& p, cons
 
 __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t pf_dyn[];
+  // Every argument either role reads, in scalar registers in one batch
+  // before the role branch (the compiler would otherwise load them lazily,
+  // a dependent round trip per branch level; the argument block is not in
+  // the cache when the kernel starts).
+  asm volatile("" ::"s"(a.n_tokens), "s"(a.k), "s"(a.E), "s"(a.idx), "s"(a.w), "s"(a.err), "s"(a.trace),
+               "s"(a.items), "s"(a.n_items), "s"(a.item_tok), "s"(a.tok_pw), "s"(a.xr), "s"(a.shared),
+               "s"(a.shared_in_list));
+  asm volatile("" ::"s"(a.g.hidden), "s"(a.g.group), "s"(a.x_bf16), "s"(a.x), "s"(a.gate), "s"(a.x_hi),
+               "s"(a.x_lo), "s"(a.xsum), "s"(a.gscore));
   const uint32_t tid = threadIdx.x;
   const uint32_t nb = pf_bucket_blocks(a.n_tokens), bb = blockIdx.x;
   if (bb >= nb) {
@@ -399,7 +408,6 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
   uint16_t* const pre = reinterpret_cast<uint16_t*>(pf_dyn + E * cws * 4);
   __shared__ uint32_t offs[kPfMaxExperts];
   __shared__ uint32_t s_nr;  // routed work items
-  for (uint32_t i = tid; i < E * cws; i += blockDim.x) col[i] = 0;
   // Thread t owns token t: its k experts and weights stay in registers
   // (one read of the routing input), validated here.
   int32_t ex[kPfMaxK];
@@ -433,6 +441,9 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
         wt[s] = a.w[tid * k + s];
       }
   }
+  // The bitmaps cleared while the routing input is in flight (the block
+  // size is the launch bound: no kernel-argument load for blockDim).
+  for (uint32_t i = tid; i < E * cws; i += 1024u) col[i] = 0;
 #pragma unroll
   for (uint32_t s = 0; s < kPfMaxK; ++s)
     if (tok && s < k) bad |= ex[s] < 0 || (uint32_t)ex[s] >= E;
@@ -534,7 +545,7 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
   const uint32_t is = (tid + 1024u - 64u * ((wi + 1u) & 15u)) & 1023u;
   if (bb == 0 && tid < 9) a.xr[tid] = nr * tid / 8u + ns * tid / 8u;
   if (bb == 0 && tid == 0) *a.n_items = nr + ns;
-  for (uint32_t j = bb + nb * is; j < ns; j += nb * blockDim.x) {
+  for (uint32_t j = bb + nb * is; j < ns; j += nb * 1024u) {
     const uint32_t x = (8u * (j + 1u) - 1u) / ns, f = nr * (x + 1u) / 8u + j;
     const uint32_t cnt = min(kPfMC, n - j * kPfMC);
     a.items[2 * f] = E;
@@ -544,7 +555,7 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
   if (a.shared && !a.shared_in_list) {
     // A list of its own for 4-bit GEMM launches (routed bits 3).
     const uint32_t ms = (n + kPfMC - 1) / kPfMC;
-    for (uint32_t j = bb + nb * is; j < ms; j += nb * blockDim.x) {
+    for (uint32_t j = bb + nb * is; j < ms; j += nb * 1024u) {
       const uint32_t cnt = min(kPfMC, n - j * kPfMC);
       a.sitems[2 * j] = 0;
       a.sitems[2 * j + 1] = (n * k + j * kPfMC) | (cnt << 16);
@@ -2119,6 +2130,10 @@ __global__ __launch_bounds__(256) void k_pf_act_sum(PfArgs a, uint32_t row0) {
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(512) void k_pf_combine(PfArgs a) {
 #pragma clang fp contract(off)
+  // Every argument in scalar registers in one batch (lazily loaded, they
+  // would cost a dependent round trip per branch level).
+  asm volatile("" ::"s"(a.g.hidden), "s"(a.k), "s"(a.n_tokens), "s"(a.down), "s"(a.out), "s"(a.h_mid),
+               "s"(a.shared), "s"(a.gate), "s"(a.gscore), "s"(a.tok_pw));
   const uint32_t t = blockIdx.x;
   const uint32_t H = a.g.hidden, k = a.k;
   const float* const down = a.down;
@@ -2131,16 +2146,21 @@ __global__ __launch_bounds__(512) void k_pf_combine(PfArgs a) {
   uint32_t pos[kPfMaxK];
   float wt[kPfMaxK];
   const uint32_t nk = a.n_tokens * k;
+  // The token's (position, weight) words in one load: lane r < k reads
+  // slot r (later lanes reread slot k - 1), and every slot is broadcast
+  // from its lane; the gate score's load goes out with it.
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint2 mine = a.tok_pw[t * k + (lane < k ? lane : k - 1u)];
+  const float gs = shared && a.gate ? a.gscore[t] : 0.f;
 #pragma unroll
   for (uint32_t r = 0; r < kPfMaxK; ++r) {
-    const uint2 pw = r < k ? a.tok_pw[t * k + r] : make_uint2(0u, 0u);
     // In range even when bucketing rejected the input (then *err is set).
-    pos[r] = min(pw.x, nk - 1);
-    wt[r] = __uint_as_float(pw.y);
+    pos[r] = min((uint32_t)__builtin_amdgcn_readlane((int)mine.x, (int)r), nk - 1);
+    wt[r] = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)mine.y, (int)r));
   }
-  const float sg = shared && a.gate ? sigmoid_ref(a.gscore[t]) : 1.0f;
+  const float sg = shared && a.gate ? sigmoid_ref(gs) : 1.0f;
   const float* const sh_row = down + (size_t)(nk + t) * H;
-  for (uint32_t h = threadIdx.x * 4; h < H; h += blockDim.x * 4) {
+  for (uint32_t h = threadIdx.x * 4; h < H; h += 512u * 4u) {  // 512 threads (the launch bound)
     float4 d[kPfMaxK];
 #pragma unroll
     for (uint32_t r = 0; r < kPfMaxK; ++r)
