@@ -1513,10 +1513,13 @@ __global__ __launch_bounds__(64 * (8 + NWD)) void k_pf_mm(PfArgs a, const uint32
 // Down (DOWN = true): the same rings over one matrix, a unit = (item, 256
 // output columns) = 256 rows of the down matrix, A = the item's entry rows
 // of the fp16 activations (rows start .. start + cnt - 1, no token ids) with
-// their group sums. Tile t of wave (cw, kh) is columns 128 t + 32 cw ..
-// + 31; codes enter the fp16 MFMA as 1 + q / 64, so the scale is 64 s and
-// the dequant term (b - 64 s) * sum a. The unit's end stores the f32 sums
-// per entry (the combine reads them).
+// their group sums. Wave (cw, kh) owns one tile, columns 128 kh + 32 cw ..
+// + 31, over the whole K of every chunk (its four groups; two dequant-term
+// MFMAs per chunk), so a unit's sums are complete in each wave and need no
+// exchange (the waves read every A fragment, twice the A reads of a K
+// split, which the LDS absorbs); codes enter the fp16 MFMA as 1 + q / 64,
+// so the scale is 64 s and the dequant term (b - 64 s) * sum a. The unit's
+// end stores the f32 sums per entry (the combine reads them).
 // ---------------------------------------------------------------------------
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -1825,7 +1828,96 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
     const uint8_t* sa = lds + C::OFF_A + (j & 1u) * C::A_SLOT;            // token rows, x sums
     const uint8_t* ss = lds + C::OFF_S + ((j >> 1) & 1u) * C::S_SLOT;     // scales, biases
     const bool small = ucur.cnt <= C::SMALL;
-    if (small) {
+    if constexpr (DOWN) {
+      // Down: wave (cw, kh) owns one 32-column tile, columns kh * 128 +
+      // 32 cw .. + 31 of the unit, over the chunk's whole K (its four
+      // groups), so a unit's sums need no exchange between waves.
+      uint32_t lv = lane;
+      asm volatile("" : "+v"(lv));
+      const uint32_t* scp = reinterpret_cast<const uint32_t*>(ss + 8 * (j & 1u));
+      if (small) {
+        // 16 x 16 x 32 f16 tiles h = columns 16 h .. 16 h + 15 of the wave's
+        // 32, rows 0-15; lane (c16, kb) as in the gate/up 16-row tiles.
+        const uint32_t c16 = lv & 15, kb = lv >> 4;
+        uint32_t sw[2][2], bw[2][2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t row = kh * C::NCOL + 32 * cw + 16 * h + c16;
+#pragma unroll
+          for (int p = 0; p < 2; ++p) {
+            sw[h][p] = scp[row * 8 + p];
+            bw[h][p] = scp[row * 8 + 4 + p];
+          }
+        }
+        const uint8_t* ar = sa + c16 * (C::KC * 2);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          u32x4 af[2];
+          uint32_t bq[2][2];
+#pragma unroll
+          for (int u = 0; u < 2; ++u) af[u] = *reinterpret_cast<const u32x4*>(ar + (((8 * g + 4 * u + kb) ^ c16) * 16));
+#pragma unroll
+          for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const uint32_t row = kh * C::NCOL + 32 * cw + 16 * h + c16;
+              bq[u][h] = *reinterpret_cast<const uint32_t*>(st + row * C::RB + (((2 * g + u) ^ (row & 7u)) * 16) + 4 * kb);
+            }
+          f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+          for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) acc[h] = mfma_f16(af[u], codes_f16_4p(bq[u][h]), acc[h]);
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const float sc = 64.0f * bf16f((uint16_t)(sw[h][g >> 1] >> (16 * (g & 1))));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) ts[0][h][i] = __builtin_fmaf(sc, acc[h][i], ts[0][h][i]);
+          }
+        }
+        // Dequant term: one v_mfma_f32_16x16x4_f32 per tile over the four
+        // groups, lane (., kb) supplying group kb.
+        const float xa = reinterpret_cast<const float*>(sa + C::A_BYTES)[c16 * C::CG + kb];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t sh = 16 * (kb & 1u);
+          const float cbv = __builtin_fmaf(-64.0f, bf16f((uint16_t)(sw[h][kb >> 1] >> sh)), bf16f((uint16_t)(bw[h][kb >> 1] >> sh)));
+          ts[0][h] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, cbv, ts[0][h], 0, 0, 0);
+        }
+      } else {
+        const uint32_t c32 = lv & 31, kq = lv >> 5;
+        const uint32_t row = kh * C::NCOL + 32 * cw + c32;
+        uint32_t sw[2], bw[2];
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          sw[p] = scp[row * 8 + p];
+          bw[p] = scp[row * 8 + 4 + p];
+        }
+        const uint8_t* ar = sa + c32 * (C::KC * 2);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          u32x4 af[4];
+#pragma unroll
+          for (int s = 0; s < 4; ++s) af[s] = *reinterpret_cast<const u32x4*>(ar + (((8 * g + 4 * kq + s) ^ (c32 & 15u)) * 16));
+          const u32x4 bq = *reinterpret_cast<const u32x4*>(st + row * C::RB + (((2 * g + kq) ^ (row & 7u)) * 16));
+          f32x16 acc = f32x16{};
+#pragma unroll
+          for (int s = 0; s < 4; ++s) acc = mfma32_f16(af[s], codes_f16_4p(bq[s]), acc);
+          const float sc = 64.0f * bf16f((uint16_t)(sw[g >> 1] >> (16 * (g & 1))));
+#pragma unroll
+          for (int v = 0; v < 16; ++v) tot[0][v] = __builtin_fmaf(sc, acc[v], tot[0][v]);
+        }
+        // Dequant term: A = the entry rows' group sums [32 rows x 2 groups],
+        // B = (b - 64 s) [2 groups x 32 columns], one MFMA per group pair.
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const float xa = reinterpret_cast<const float*>(sa + C::A_BYTES)[c32 * C::CG + 2 * p + kq];
+          const uint32_t sh = 16 * kq;
+          const float cb = __builtin_fmaf(-64.0f, bf16f((uint16_t)(sw[p] >> sh)), bf16f((uint16_t)(bw[p] >> sh)));
+          tot[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa, cb, tot[0], 0, 0, 0);
+        }
+      }
+    } else if (small) {
       // A unit of <= 16 rows: 16 x 16 x 32 MFMA tiles (bf16; down: f16) (t, h) =
       // columns 16 h .. 16 h + 15 of the wave's 32 in matrix t, rows 0-15;
       // lane (c16, kb) = (A row / output column l % 16, 8-input block
@@ -1965,13 +2057,15 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
       cc = 0;
       const uint32_t start = ucur.start, cnt = ucur.cnt, cb = ucur.cb;
       if (++cu < my_units) ucur = unit(cu);
-      // Every wave is done reading this code slot; the K halves swap the
+      // Every wave is done reading this code slot; the gate/up K halves swap the
       // rows the other one finishes (values 8 kh' .. 8 kh' + 7 of each tile).
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
       float* ex = reinterpret_cast<float*>(const_cast<uint8_t*>(st));
-      if (small) {
+      if (DOWN) {
+        // Down: every wave holds whole sums (no exchange).
+      } else if (small) {
         // 16-row tiles: wave kh finishes column half kh of both matrices.
         float* xo = ex + (cw * 2 + (kh ^ 1u)) * 16 * 64 + lane;
 #pragma unroll
@@ -1990,33 +2084,25 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
       if (DOWN && small) {
-        const float* xi = ex + (cw * 2 + kh) * 16 * 64 + lane;
         uint32_t lv = lane;
         asm volatile("" : "+v"(lv));
         const uint32_t c16 = lv & 15, kb = lv >> 4;
-        const uint32_t col = cb * C::ROWS + 32 * cw + 16 * kh + c16;
+        const uint32_t col = cb * C::ROWS + kh * C::NCOL + 32 * cw + c16;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const uint32_t m = 4 * kb + i;
           if (m < cnt) {
             float* o = down_out + (size_t)(start + m) * N + col;
-            o[0] = (kh ? ts[0][1][i] : ts[0][0][i]) + xi[i * 64];
-            o[C::NCOL] = (kh ? ts[1][1][i] : ts[1][0][i]) + xi[(4 + i) * 64];
+            o[0] = ts[0][0][i];
+            o[16] = ts[0][1][i];
           }
         }
       } else if (DOWN) {
-        const float* xi = ex + (cw * 2 + kh) * 16 * 64 + lane;
-        const uint32_t vm = 8 * kh;
-        const uint32_t col = cb * C::ROWS + 32 * cw + c32;
+        const uint32_t col = cb * C::ROWS + kh * C::NCOL + 32 * cw + c32;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const uint32_t v = vm + i;
+        for (int v = 0; v < 16; ++v) {
           const uint32_t m = 8 * (v / 4) + 4 * kq + (v % 4);
-          if (m < cnt) {
-            float* o = down_out + (size_t)(start + m) * N + col;
-            o[0] = tot[0][v] + xi[i * 64];
-            o[C::NCOL] = tot[1][v] + xi[(8 + i) * 64];
-          }
+          if (m < cnt) down_out[(size_t)(start + m) * N + col] = tot[0][v];
         }
       } else if (small) {
         const float* xi = ex + (cw * 2 + kh) * 16 * 64 + lane;
