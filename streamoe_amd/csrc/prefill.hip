@@ -419,6 +419,7 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
     ex[s] = INT32_MAX;  // past k: above every expert id (out of range, never smaller)
     wt[s] = 0.f;
   }
+  const bool per_entry = k <= 8;  // entries placed one lane each (below); else per token
   const bool vec = (k & 3) == 0 && ((reinterpret_cast<uintptr_t>(a.idx) | reinterpret_cast<uintptr_t>(a.w)) & 15) == 0;
   if (tok && vec) {
     // A token's k ids / weights are contiguous and 16-byte aligned: read
@@ -429,17 +430,47 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
     for (uint32_t q = 0; q < kPfMaxK / 4; ++q)
       if (4 * q < k) {
         const int4 iv = ip[q];
-        const float4 wv = wp[q];
         ex[4 * q] = iv.x, ex[4 * q + 1] = iv.y, ex[4 * q + 2] = iv.z, ex[4 * q + 3] = iv.w;
-        wt[4 * q] = wv.x, wt[4 * q + 1] = wv.y, wt[4 * q + 2] = wv.z, wt[4 * q + 3] = wv.w;
+        if (!per_entry) {  // the per-token placement's weights
+          const float4 wv = wp[q];
+          wt[4 * q] = wv.x, wt[4 * q + 1] = wv.y, wt[4 * q + 2] = wv.z, wt[4 * q + 3] = wv.w;
+        }
       }
   } else if (tok) {
 #pragma unroll
     for (uint32_t s = 0; s < kPfMaxK; ++s)
       if (s < k) {
         ex[s] = a.idx[tid * k + s];
-        wt[s] = a.w[tid * k + s];
+        if (!per_entry) wt[s] = a.w[tid * k + s];
       }
+  }
+  // Entry placement for k <= 8, one lane per (token, slot): thread tid
+  // places slot pslot of token ptok (token wave bb + nb (tid / 512), eight
+  // lanes per token); its id and weight and its token's ids (for the rank)
+  // are loaded here with the rest of the routing input.
+  const uint32_t ptok = 64u * (bb + nb * (tid >> 9)) + ((tid & 511u) >> 3), pslot = tid & 7u;
+  const bool plive = per_entry && ptok < n && pslot < k;
+  int32_t pid[8];
+  int32_t pex = INT32_MAX;
+  float pwt = 0.f;
+#pragma unroll
+  for (uint32_t q = 0; q < 8; ++q) pid[q] = INT32_MAX;
+  if (plive) {
+    pex = a.idx[ptok * k + pslot];
+    pwt = a.w[ptok * k + pslot];
+    if (vec) {
+      const int4* ip = reinterpret_cast<const int4*>(a.idx + ptok * k);
+#pragma unroll
+      for (uint32_t q = 0; q < 2; ++q)
+        if (4 * q < k) {
+          const int4 iv = ip[q];
+          pid[4 * q] = iv.x, pid[4 * q + 1] = iv.y, pid[4 * q + 2] = iv.z, pid[4 * q + 3] = iv.w;
+        }
+    } else {
+#pragma unroll
+      for (uint32_t q = 0; q < 8; ++q)
+        if (q < k) pid[q] = a.idx[ptok * k + q];
+    }
   }
   // The bitmaps cleared while the routing input is in flight (the block
   // size is the launch bound: no kernel-argument load for blockDim).
@@ -581,16 +612,24 @@ __global__ __launch_bounds__(1024) void k_pf_route(PfArgs a) {
   // rank r among t's experts in ascending expert order = how many of t's
   // experts are smaller. The token writes its entry positions and weights
   // in that order (token-major), and its id into its items' row slots.
-  // Block bb places the tokens of waves bb, bb + nb, ...
-  if (tok && (tid >> 6) % nb == bb) {
-    const PfPlace p{col, pre, offs, sibase, E, cw, cws, k, nr, ns};
-    if (k <= 8) {
-      if (ns) pf_place<8, true>(a, p, ex, wt, tid);
-      else pf_place<8, false>(a, p, ex, wt, tid);
-    } else {
-      if (ns) pf_place<kPfMaxK, true>(a, p, ex, wt, tid);
-      else pf_place<kPfMaxK, false>(a, p, ex, wt, tid);
+  // Block bb places the tokens of waves bb, bb + nb, ...: for k <= 8 one
+  // lane per entry, else one thread per token.
+  if (per_entry) {
+    if (plive && pex >= 0 && (uint32_t)pex < E) {
+      const uint32_t e = (uint32_t)pex, wv = ptok >> 5;
+      const uint32_t row = pre[e * cw + wv] + __popc(col[e * cws + wv] & ((1u << (ptok & 31)) - 1u));
+      uint32_t r = 0;
+#pragma unroll
+      for (uint32_t q = 0; q < 8; ++q) r += pid[q] < pex ? 1u : 0u;
+      r = min(r, k - 1);  // a duplicated expert (already reported) stays in range
+      a.tok_pw[ptok * k + r] = make_uint2(offs[e] + row, __float_as_uint(pwt));
+      const uint32_t it = sibase[e] + row / kPfMC;
+      a.item_tok[(ns ? fidx(it) : it) * kPfMC + row % kPfMC] = ptok;
     }
+  } else if (tok && (tid >> 6) % nb == bb) {
+    const PfPlace p{col, pre, offs, sibase, E, cw, cws, k, nr, ns};
+    if (ns) pf_place<kPfMaxK, true>(a, p, ex, wt, tid);
+    else pf_place<kPfMaxK, false>(a, p, ex, wt, tid);
   }
   PF_STAMP(5);
   __syncthreads();
