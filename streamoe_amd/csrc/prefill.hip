@@ -1933,18 +1933,29 @@ __global__ __launch_bounds__(64 * Gu64::NWT) void k_pf_gu64(PfArgs a, const uint
           bw[p] = scp[row * 8 + 4 + p];
         }
         const uint8_t* ar = sa + c32 * (C::KC * 2);
+        // Groups in pairs: two independent accumulator chains (one per
+        // group) interleaved, so one's MFMAs run while the other's wait.
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          u32x4 af[4];
+        for (int gp = 0; gp < 2; ++gp) {
+          u32x4 af[2][4], bq[2];
 #pragma unroll
-          for (int s = 0; s < 4; ++s) af[s] = *reinterpret_cast<const u32x4*>(ar + (((8 * g + 4 * kq + s) ^ (c32 & 15u)) * 16));
-          const u32x4 bq = *reinterpret_cast<const u32x4*>(st + row * C::RB + (((2 * g + kq) ^ (row & 7u)) * 16));
-          f32x16 acc = f32x16{};
+          for (int q = 0; q < 2; ++q) {
+            const int g = 2 * gp + q;
 #pragma unroll
-          for (int s = 0; s < 4; ++s) acc = mfma32_f16(af[s], codes_f16_4p(bq[s]), acc);
-          const float sc = 64.0f * bf16f((uint16_t)(sw[g >> 1] >> (16 * (g & 1))));
+            for (int s = 0; s < 4; ++s) af[q][s] = *reinterpret_cast<const u32x4*>(ar + (((8 * g + 4 * kq + s) ^ (c32 & 15u)) * 16));
+            bq[q] = *reinterpret_cast<const u32x4*>(st + row * C::RB + (((2 * g + kq) ^ (row & 7u)) * 16));
+          }
+          f32x16 acc[2] = {f32x16{}, f32x16{}};
 #pragma unroll
-          for (int v = 0; v < 16; ++v) tot[0][v] = __builtin_fmaf(sc, acc[v], tot[0][v]);
+          for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) acc[q] = mfma32_f16(af[q][s], codes_f16_4p(bq[q][s]), acc[q]);
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            const float sc = 64.0f * bf16f((uint16_t)(sw[gp] >> (16 * q)));
+#pragma unroll
+            for (int v = 0; v < 16; ++v) tot[0][v] = __builtin_fmaf(sc, acc[q][v], tot[0][v]);
+          }
         }
         // Dequant term: A = the entry rows' group sums [32 rows x 2 groups],
         // B = (b - 64 s) [2 groups x 32 columns], one MFMA per group pair.
