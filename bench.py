@@ -63,7 +63,7 @@ CONFIGS = {
 # profiles/prefill_c4_a3b_4bit.md (the four prefill launches of one layer).
 # None where no counter pass was taken (multi-token decode, per-phase path).
 MEASURED_TRAFFIC = {"c0": 29_732_534, "c2": 18_897_532, "c3": 15_786_871, "c1": 175_922_937,
-                    "c4": 558_553_195, "c5": 87_783_971}
+                    "c4": 558_463_070, "c5": 87_783_971}
 
 
 def stream_read_peak(dev, gib=4):
