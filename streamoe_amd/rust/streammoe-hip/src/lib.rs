@@ -248,6 +248,29 @@ impl KernelCall for MatvecCall<'_> {
     }
 }
 
+/// Rows `[row0, row0 + n_rows)` of quantized weights (4-, 3- or 8-bit) as
+/// f32 `[n_rows, in_dim]`, each weight `fma(q, s, b)` (`smoe_dequant`): the
+/// load-time f32 form of an 8-bit shared-expert gate for the prefill block,
+/// or a read-back for verification.
+pub struct DequantCall<'a> {
+    pub weights: QuantWeights<'a>,
+    pub in_dim: u32,
+    pub row0: u32,
+    pub n_rows: u32,
+    pub output: &'a BufferRef,
+    pub output_offset: u64,
+}
+
+impl KernelCall for DequantCall<'_> {
+    fn encode(&self, k: &Kernels) -> Result<(), SmoeError> {
+        let what = "smoe_dequant";
+        let rows = self.row0.checked_add(self.n_rows).ok_or(SmoeError { status: sys::SMOE_ERR_INVALID_ARG, what })?;
+        let w = self.weights.raw(rows, self.in_dim, what)?;
+        let out = self.output.f32_span(self.output_offset, self.n_rows as u64 * self.in_dim as u64, what)?;
+        check(unsafe { sys::smoe_dequant(k.h, &w, self.in_dim, self.row0, self.n_rows, out) }, what)
+    }
+}
+
 /// LM head with the greedy pick (io/gpu_lm_head.rs:130-193): logits and
 /// the first index of their maximum, both left on the device.
 pub struct LmHeadCall<'a> {
